@@ -1,0 +1,128 @@
+/*
+ * mnemo_kernels.h -- C ABI of the MI355X (gfx950) quantized-matmul library.
+ *
+ * Drop-in for MnemoCUDA's kernel entry points: the functions named cuda_* keep the
+ * reference's names, argument lists and semantics (forward.c declares them extern at
+ * forward.c:23-152; they are defined in kernels.cu / gemm_q4k.cu at the lines cited per
+ * declaration), with cudaStream_t replaced by hipStream_t.  The mnemo_* functions are
+ * additions the reference lacks.
+ *
+ * Conventions shared by every entry point:
+ *  - All pointers are device pointers owned by the caller; nothing here allocates.
+ *  - Weights are raw GGUF bytes, row-major, ceil(n_cols/256) super-blocks per row:
+ *    Q4_K 144 B (type id 12), Q6_K 210 B (type id 14), F32 router (type id 0).
+ *  - Every call is asynchronous on `stream` and capture-safe (no sync, no malloc,
+ *    no attribute changes at launch), so calls can be recorded into a hipGraph.
+ *  - Errors: like the reference (KERNEL_LAUNCH_CHECK, kernels.cu:1062-1067) failures
+ *    are printed to stderr and the call returns without launching; in addition the
+ *    code is kept for mnemo_last_error().  Argument checks that the reference does not
+ *    make (null pointers, non-positive sizes, K not a multiple of 256 for GEMMs) are
+ *    reported the same way.
+ */
+#ifndef MNEMO_KERNELS_H
+#define MNEMO_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- errors */
+#define MNEMO_OK 0
+#define MNEMO_ERR_BAD_ARG 1
+#define MNEMO_ERR_LAUNCH 2
+#define MNEMO_ERR_UNSUPPORTED_TYPE 3
+
+/* Last error recorded by any entry point on this host thread (MNEMO_OK if none);
+ * reading it clears it. */
+int mnemo_last_error(void);
+const char *mnemo_last_error_string(void);
+
+/* Library version string, e.g. "mnemo-mi355x 0.1 gfx950". */
+const char *mnemo_version(void);
+
+/* Replaces cuda_kernels_init (kernels.cu:2217-2240, called once at load,
+ * engine.c:1203-1207).  Nothing needs raising on gfx950 (every kernel stays within the
+ * default LDS limit); the call checks that the current device is gfx950. */
+void cuda_kernels_init(void);
+
+/* ---------------------------------------------------------------- decode GEMVs */
+/* y = W x, W Q4_K [n_rows][n_cols]                       (kernels.cu:66, :1071-1079) */
+void cuda_matvec_q4k(const void *weights, const float *x, float *y, int n_rows, int n_cols,
+                     hipStream_t stream);
+/* y = W x + residual (O-proj + skip)                      (kernels.cu:149, :1094-1102) */
+void cuda_matvec_q4k_add(const void *weights, const float *x, const float *residual, float *y,
+                         int n_rows, int n_cols, hipStream_t stream);
+/* Q, K, V projections of one x in one launch              (kernels.cu:205, :1081-1092) */
+void cuda_matvec_q4k_qkv(const void *w_q, const void *w_k, const void *w_v, const float *x,
+                         float *out_q, float *out_k, float *out_v, int q_rows, int kv_rows,
+                         int n_cols, hipStream_t stream);
+/* y_a = A x, y_b = B x (K+V, gate+up), both Q4_K         (kernels.cu:278, :1104-1113) */
+void cuda_matvec_q4k_dual(const void *wa, const void *wb, const float *x, float *ya, float *yb,
+                          int n_rows, int n_cols, hipStream_t stream);
+/* y += scale * (W x), W Q4_K (expert down-proj)           (kernels.cu:358, :1115-1124) */
+void cuda_matvec_q4k_scaled_add(const void *weights, const float *x, float *y, int n_rows,
+                                int n_cols, float scale, hipStream_t stream);
+/* y = W x, W Q6_K                                          (kernels.cu:427, :1126-1135) */
+void cuda_matvec_q6k(const void *weights, const float *x, float *y, int n_rows, int n_cols,
+                     hipStream_t stream);
+
+/* New: y += scale * (W x), W Q6_K, in one launch.  Replaces the reference's
+ * cuda_matvec_q6k + cuda_scaled_add pair (forward.c:1137-1140). */
+void mnemo_matvec_q6k_scaled_add(const void *weights, const float *x, float *y, int n_rows,
+                                 int n_cols, float scale, hipStream_t stream);
+/* New: y_a = A x, y_b = B x with independent GGUF types (12 or 14) for A and B, e.g. the
+ * Q4_K K-proj + Q6_K V-proj of Q4_K_M models, which the reference runs as two launches
+ * (forward.c:714-718). */
+void mnemo_matvec_dual(const void *wa, int type_a, const void *wb, int type_b, const float *x,
+                       float *ya, float *yb, int n_rows, int n_cols, hipStream_t stream);
+/* New: fused expert down projection of one expert:
+ * y += scale * (W_down (silu(gate) * up)), W_down Q4_K or Q6_K [n_rows][n_cols].
+ * Replaces cuda_swiglu + (cuda_matvec_q4k_scaled_add | cuda_matvec_q6k + cuda_scaled_add)
+ * in expert_fwd (forward.c:1130-1141). */
+void mnemo_matvec_swiglu_scaled_add(const void *w_down, int type_down, const float *gate,
+                                    const float *up, float *y, int n_rows, int n_cols, float scale,
+                                    hipStream_t stream);
+
+/* ---------------------------------------------------------------- router */
+/* y = W x, W fp32 row-major [n_rows][n_cols]               (kernels.cu:859, :1275-1281) */
+void cuda_matvec_f32(const float *weights, const float *x, float *y, int n_rows, int n_cols,
+                     hipStream_t stream);
+/* top-k of n_experts scores, softmax over the k winners    (kernels.cu:993, :1301-1305)
+ * k <= 16, n_experts <= 1024.  Winners are written in (score desc, index asc) order; the
+ * reference writes them in an unspecified slot order, so consumers must only rely on the
+ * (index, weight) pairing, which is what forward.c does. */
+void cuda_topk_softmax(const float *scores, int *indices, float *weights, int n_experts, int k,
+                       hipStream_t stream);
+
+/* ---------------------------------------------------------------- glue */
+/* out = silu(gate) * up                                    (kernels.cu:677, :1170-1176) */
+void cuda_swiglu(const float *gate, const float *up, float *out, int n, hipStream_t stream);
+/* out += scale * x                                         (kernels.cu:980, :1293-1299) */
+void cuda_scaled_add(float *out, const float *x, float scale, int n, hipStream_t stream);
+
+/* ---------------------------------------------------------------- prefill GEMM */
+/* fp32 [N][K] -> Q8_1 MMQ blocks [N][K/128] x 144 B        (gemm_q4k.cu:327-364)
+ * Byte-identical to the reference (including ds.y = half(d * sum(x))).  K % 128 == 0;
+ * src and dst 16-byte aligned. */
+void cuda_quantize_mmq_q8_1(const float *src, void *dst, int K, int N, hipStream_t stream);
+/* out[j*M + i] = sum_k deq(W)[i][k] * deq(act)[j][k]      (gemm_q4k.cu:202, :272-324)
+ * W Q4_K [M][K], act from cuda_quantize_mmq_q8_1 with N columns, out column-major [N][M].
+ * K % 256 == 0. */
+void cuda_gemm_q4k(const void *weights, const void *act_q8, float *output, int M, int K, int N,
+                   hipStream_t stream);
+/* New: the same for Q6_K weights (Q4_K_M expert down projections). */
+void mnemo_gemm_q6k(const void *weights, const void *act_q8, float *output, int M, int K, int N,
+                    hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MNEMO_KERNELS_H */

@@ -1,0 +1,72 @@
+"""Builds the gfx950 kernel library in-tree: mnemocuda_amd/libmnemo_hip.so.
+
+HIP sources are compiled with hipcc for gfx950 only; the C host composition
+(csrc/host/mnemo_host.c) with the system C compiler; both link into one shared library
+whose exported symbols are exactly the declarations of include/mnemo_kernels.h and
+include/mnemo_host.h.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = ROOT / "_build"
+LIB = PKG / "libmnemo_hip.so"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+HIP_SOURCES = ["abi.hip", "gemv.hip", "router.hip", "gemm.hip"]
+C_SOURCES = ["host/mnemo_host.c"]
+
+HIPCC_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
+    # no packed-fp32 VALU code anywhere in this library
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless
+    noise = "is not a recognized feature for this target"
+    msg = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l and l.strip())
+    if msg:
+        print(msg, file=sys.stderr)
+
+
+def build(jobs: int = 4) -> Path:
+    hipcc = str(ROCM / "bin" / "hipcc")
+    cc = shutil.which(os.environ.get("CC", "gcc")) or "gcc"
+    BUILD.mkdir(exist_ok=True)
+    objs: list[Path] = []
+    cmds: list[list[str]] = []
+    for src in HIP_SOURCES:
+        obj = BUILD / (Path(src).stem + ".hip.o")
+        cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    for src in C_SOURCES:
+        obj = BUILD / (Path(src).stem + ".c.o")
+        cmds.append([cc, "-O2", "-std=c11", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+                     f"-I{ROCM / 'include'}", "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_run, cmds))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([hipcc, "-shared", "-fPIC", "--offload-arch=gfx950", *map(str, objs), "-o", str(tmp),
+          f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"])
+    tmp.replace(LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build())

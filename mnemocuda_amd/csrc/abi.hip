@@ -1,0 +1,199 @@
+// abi.hip -- extern "C" entry points declared in include/mnemo_kernels.h.
+//
+// Each wrapper validates its arguments, fills a launch descriptor and returns; errors are
+// printed (as the reference's KERNEL_LAUNCH_CHECK does, kernels.cu:1062-1067) and kept
+// per host thread for mnemo_last_error().
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "mnemo_common.hpp"
+#include "mnemo_internal.hpp"
+#include "../../include/mnemo_kernels.h"
+
+namespace mnemo {
+
+static thread_local int g_err = kOk;
+static thread_local char g_msg[256];
+
+int set_error(int code, const char *fmt, ...) {
+    g_err = code;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_msg, sizeof g_msg, fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "[mnemo] %s\n", g_msg);
+    return code;
+}
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(kErrLaunch, "kernel launch error in %s: %s", what, hipGetErrorString(e));
+    return kOk;
+}
+
+int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s);
+int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k, hipStream_t s);
+int launch_swiglu(const float *g, const float *u, float *out, int n, hipStream_t s);
+int launch_scaled_add(float *out, const float *x, float sc, int n, hipStream_t s);
+int launch_quantize_q8_1(const float *src, void *dst, int K, int N, hipStream_t s);
+int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M, int K, int N, hipStream_t s);
+
+static bool type_ok(int t) { return t == kTypeQ4K || t == kTypeQ6K; }
+
+// Builds a GEMV launch over up to three matrices sharing x (all with n_cols columns).
+struct GemvBuilder {
+    GemvArgs a;
+    GemvBuilder(const float *x, int n_cols) {
+        memset(&a, 0, sizeof a);
+        a.x = x;
+        a.n_cols = n_cols;
+        a.off[0] = 0;
+        a.off[1] = a.off[2] = INT_MAX;
+    }
+    void add(const void *w, int type, float *y, int rows, int mode, const float *res = nullptr,
+             float scale = 0.0f) {
+        GemvMat &m = a.m[a.nmat];
+        m.w = w; m.type = type; m.y = y; m.rows = rows; m.mode = mode; m.res = res; m.scale = scale;
+        a.off[a.nmat] = a.total_rows;
+        a.total_rows += rows;
+        a.nmat++;
+    }
+    int run(const char *what, hipStream_t s) {
+        if (!a.x || a.n_cols < 4 || a.n_cols > kMaxGemvCols)
+            return set_error(kErrBadArg, "%s: need x != NULL and 4 <= n_cols <= %d", what, kMaxGemvCols);
+        for (int i = 0; i < a.nmat; i++) {
+            const GemvMat &m = a.m[i];
+            if (!m.w || !m.y || m.rows <= 0 || (m.mode == kEpiResidual && !m.res))
+                return set_error(kErrBadArg, "%s: bad pointer or row count for matrix %d", what, i);
+            if (!type_ok(m.type)) return set_error(kErrUnsupportedType, "%s: unsupported GGUF type %d", what, m.type);
+        }
+        for (int i = a.nmat; i < 3; i++) a.off[i] = INT_MAX;
+        return launch_gemv(a, s);
+    }
+};
+
+}  // namespace mnemo
+
+using namespace mnemo;
+
+extern "C" {
+
+int mnemo_last_error(void) {
+    int e = g_err;
+    g_err = kOk;
+    return e;
+}
+const char *mnemo_last_error_string(void) { return g_msg; }
+const char *mnemo_version(void) { return "mnemo-mi355x 0.1 gfx950"; }
+
+void cuda_kernels_init(void) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        set_error(kErrLaunch, "cuda_kernels_init: no HIP device");
+        return;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        set_error(kErrLaunch, "cuda_kernels_init: built for gfx950, device is %s", prop.gcnArchName);
+}
+
+void cuda_matvec_q4k(const void *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(w, kTypeQ4K, y, n_rows, kEpiStore);
+    b.run("cuda_matvec_q4k", s);
+}
+
+void cuda_matvec_q4k_add(const void *w, const float *x, const float *res, float *y, int n_rows, int n_cols,
+                         hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(w, kTypeQ4K, y, n_rows, kEpiResidual, res);
+    b.run("cuda_matvec_q4k_add", s);
+}
+
+void cuda_matvec_q4k_qkv(const void *wq, const void *wk, const void *wv, const float *x, float *oq, float *ok,
+                         float *ov, int q_rows, int kv_rows, int n_cols, hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(wq, kTypeQ4K, oq, q_rows, kEpiStore);
+    b.add(wk, kTypeQ4K, ok, kv_rows, kEpiStore);
+    b.add(wv, kTypeQ4K, ov, kv_rows, kEpiStore);
+    b.run("cuda_matvec_q4k_qkv", s);
+}
+
+void cuda_matvec_q4k_dual(const void *wa, const void *wb, const float *x, float *ya, float *yb, int n_rows,
+                          int n_cols, hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(wa, kTypeQ4K, ya, n_rows, kEpiStore);
+    b.add(wb, kTypeQ4K, yb, n_rows, kEpiStore);
+    b.run("cuda_matvec_q4k_dual", s);
+}
+
+void cuda_matvec_q4k_scaled_add(const void *w, const float *x, float *y, int n_rows, int n_cols, float scale,
+                                hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(w, kTypeQ4K, y, n_rows, kEpiScaledAdd, nullptr, scale);
+    b.run("cuda_matvec_q4k_scaled_add", s);
+}
+
+void cuda_matvec_q6k(const void *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(w, kTypeQ6K, y, n_rows, kEpiStore);
+    b.run("cuda_matvec_q6k", s);
+}
+
+void mnemo_matvec_q6k_scaled_add(const void *w, const float *x, float *y, int n_rows, int n_cols, float scale,
+                                 hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(w, kTypeQ6K, y, n_rows, kEpiScaledAdd, nullptr, scale);
+    b.run("mnemo_matvec_q6k_scaled_add", s);
+}
+
+void mnemo_matvec_dual(const void *wa, int ta, const void *wb, int tb, const float *x, float *ya, float *yb,
+                       int n_rows, int n_cols, hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(wa, ta, ya, n_rows, kEpiStore);
+    b.add(wb, tb, yb, n_rows, kEpiStore);
+    b.run("mnemo_matvec_dual", s);
+}
+
+void mnemo_matvec_swiglu_scaled_add(const void *w, int type, const float *gate, const float *up, float *y,
+                                    int n_rows, int n_cols, float scale, hipStream_t s) {
+    GemvBuilder b(gate, n_cols);
+    b.a.x2 = up;
+    b.a.xmode = 1;
+    if (!up) {
+        set_error(kErrBadArg, "mnemo_matvec_swiglu_scaled_add: up == NULL");
+        return;
+    }
+    b.add(w, type, y, n_rows, kEpiScaledAdd, nullptr, scale);
+    b.run("mnemo_matvec_swiglu_scaled_add", s);
+}
+
+void cuda_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s) {
+    launch_matvec_f32(w, x, y, n_rows, n_cols, s);
+}
+
+void cuda_topk_softmax(const float *scores, int *idx, float *wts, int n_experts, int k, hipStream_t s) {
+    launch_topk_softmax(scores, idx, wts, n_experts, k, s);
+}
+
+void cuda_swiglu(const float *g, const float *u, float *out, int n, hipStream_t s) { launch_swiglu(g, u, out, n, s); }
+
+void cuda_scaled_add(float *out, const float *x, float scale, int n, hipStream_t s) {
+    launch_scaled_add(out, x, scale, n, s);
+}
+
+void cuda_quantize_mmq_q8_1(const float *src, void *dst, int K, int N, hipStream_t s) {
+    launch_quantize_q8_1(src, dst, K, N, s);
+}
+
+void cuda_gemm_q4k(const void *w, const void *act, float *out, int M, int K, int N, hipStream_t s) {
+    launch_gemm_q8_1(kTypeQ4K, w, act, out, M, K, N, s);
+}
+
+void mnemo_gemm_q6k(const void *w, const void *act, float *out, int M, int K, int N, hipStream_t s) {
+    launch_gemm_q8_1(kTypeQ6K, w, act, out, M, K, N, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,487 @@
+// gemv.hip -- dequant-fused Q4_K / Q6_K matrix-vector products for decode (gfx950).
+//
+// One kernel serves every GEMV entry point of the reference (MnemoCUDA kernels.cu:66
+// matvec_q4k, :149 _add, :205 _qkv, :278 _dual, :358 _scaled_add, :427 matvec_q6k):
+// up to three weight matrices that share one input vector x are processed as one
+// concatenated row space, each with its own GGUF type and epilogue
+// (store | store + residual | y += scale * acc).
+//
+// Design (CDNA4, wave64):
+//  * x is re-expressed per 32-element sub-block as two int8 digits,
+//      x ~= u * (254*d1 + d2),  u = amax/(127*254),  |x - xhat| <= ~amax/64516,
+//    held in LDS together with fp32 sums of x per 32 and per 16 elements.  Each
+//    workgroup (512 threads, two per CU) builds this image once for all of its rows.
+//    Weight nibbles / 6-bit values are multiplied with v_dot4_i32_i8 (4 MACs per
+//    instruction, two per digit) and the integer partial of each sub-block is rescaled
+//    in fp32:
+//      Q4_K: w = d*sc*q - dmin*m   ->  acc += d*sc*u*I - dmin*m*sum32(x)
+//      Q6_K: w = d*sc*(q-32)       ->  acc += d*sc*(u*I - 32*sum16(x))
+//  * A lane owns one half super-block of a row (128 weights: 64 B of Q4_K nibbles plus the
+//    16 B header, or 64 B ql + 32 B qh + 8 scale bytes + d of Q6_K), loaded with 16-byte
+//    global loads; a row spans LPR = pow2ceil(K/128) <= 64 lanes, short rows put
+//    P = 64/LPR rows in one wave pass.  The row sum is a DPP reduction.
+//  * The x loads go out first, then the weight loads of the wave's first two passes, so
+//    the x image is built while the weights are in flight.  Every load sits on a
+//    branch-free path (addresses clamped, results masked) so that the compiler's waits
+//    count exactly the loads a value depends on.
+#include <climits>
+
+#include "mnemo_common.hpp"
+#include "mnemo_internal.hpp"
+
+namespace mnemo {
+
+constexpr int kGemvThreads = 512;
+
+// ------------------------------------------------------------------ x preparation
+// LDS image of x for a padded length kp (multiple of 256):
+//   int8 d1[kp] | int8 d2[kp] | float u[kp/32] | float s32[kp/32] | float s16[kp/16]
+struct XLds {
+    int8_t *d1;
+    int8_t *d2;
+    float *u;
+    float *s32;
+    float *s16;
+    __device__ XLds(uint8_t *base, int kp)
+        : d1((int8_t *)base), d2((int8_t *)(base + kp)), u((float *)(base + 2 * kp)),
+          s32((float *)(base + 2 * kp + kp / 8)), s16((float *)(base + 2 * kp + kp / 4)) {}
+};
+
+__host__ __device__ constexpr size_t xlds_bytes(int kp) { return (size_t)2 * kp + kp / 2; }
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    // silu(g) * u, the reference's expression (kernels.cu:686-687)
+    return g / (1.0f + expf(-g)) * u;
+}
+
+template <int XPT>  // float4 of x per thread: kp <= 4 * XPT * kGemvThreads
+struct XRegs {
+    float4 v[XPT];
+};
+
+// One 16-byte load per 4 elements from e clamped to n-4 (x may be unaligned; the host
+// rejects n < 4), so the instruction sequence is fixed.
+template <int XPT, bool SWI>
+__device__ __forceinline__ void load_x(const float *__restrict__ x0, const float *__restrict__ x1, int n,
+                                       XRegs<XPT> &R, XRegs<XPT> &R2) {
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int e = 4 * (threadIdx.x + i * kGemvThreads);
+        const int ec = min(e, n - 4);
+        __builtin_memcpy(&R.v[i], x0 + ec, 16);
+        if (SWI) __builtin_memcpy(&R2.v[i], x1 + ec, 16);
+    }
+}
+
+__device__ __forceinline__ uint32_t umax_dpp8(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor2, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowHalfMirror, 0xF, 0xF, false));
+    return v;
+}
+
+// Builds the LDS image; every thread of the block must call this (it ends in a barrier).
+// Elements at or past n (loaded from clamped addresses) are zeroed here, after the
+// weight loads have been issued, so that waiting for x does not wait for the weights.
+template <int XPT, bool SWI>
+__device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, XLds X) {
+    const int lane = lane_id();
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23: adding it rounds to an integer (RNE)
+    const bool ragged = (n & 3) != 0;      // uniform
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        // computed unconditionally (a load used only under a branch would be sunk into it,
+        // behind the weight loads); only the stores are guarded
+        const int e4 = threadIdx.x + i * kGemvThreads;
+        const bool store = 4 * e4 < kp;  // uniform per 8-lane group: kp is a multiple of 256
+        const int e = 4 * e4;
+        float v[4] = {R.v[i].x, R.v[i].y, R.v[i].z, R.v[i].w};
+        if (SWI) {
+            const float g[4] = {R2.v[i].x, R2.v[i].y, R2.v[i].z, R2.v[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = silu_mul(v[j], g[j]);
+        }
+        if (ragged) {
+            // element e+j sits at v[j + sh], sh = e - min(e, n-4) (non-zero only in the last
+            // partial group); elements >= n are zero
+            const int sh = e - min(e, n - 4);
+            float t[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int k = min(j + sh, 3);
+                float a = v[3];
+                a = k == 2 ? v[2] : a;
+                a = k == 1 ? v[1] : a;
+                a = k == 0 ? v[0] : a;
+                t[j] = e + j < n ? a : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = t[j];
+        } else {
+            const uint32_t keep = e < n ? ~0u : 0u;
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[j] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[j]) & keep);
+        }
+        // |v| as unsigned bits orders like |v|; max over the 8 lanes of the sub-block
+        uint32_t ab = max(max(__builtin_bit_cast(uint32_t, v[0]) & 0x7FFFFFFFu,
+                              __builtin_bit_cast(uint32_t, v[1]) & 0x7FFFFFFFu),
+                          max(__builtin_bit_cast(uint32_t, v[2]) & 0x7FFFFFFFu,
+                              __builtin_bit_cast(uint32_t, v[3]) & 0x7FFFFFFFu));
+        const float amax = __builtin_bit_cast(float, umax_dpp8(ab));
+        const float s = amax * (1.0f / 127.0f);
+        const float u = s * (1.0f / 254.0f);
+        const float inv1 = amax > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.0f;
+        const float inv2 = inv1 * 254.0f;
+        // d1 = rne(v * inv1), d2 = rne((v - d1*s) * inv2); |v * inv1| <= 127 (1 + 2^-22) and
+        // |r * inv2| <= 127 (1 + 2^-21), so both land in [-127, 127] without a clamp.  The
+        // low byte of (t + magic) is the digit in two's complement.
+        uint32_t b1[4], b2[4];
+        float s4 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float t1 = fmaf(v[j], inv1, kMagic);
+            const float a = t1 - kMagic;
+            const float r = fmaf(-a, s, v[j]);
+            const float t2 = fmaf(r, inv2, kMagic);
+            b1[j] = __builtin_bit_cast(uint32_t, t1);
+            b2[j] = __builtin_bit_cast(uint32_t, t2);
+            s4 += v[j];
+        }
+        // gather the low bytes: selector byte k picks byte sel_k of {src0 (4..7), src1 (0..3)}
+        const uint32_t w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0C0C0400u) |
+                            __builtin_amdgcn_perm(b1[3], b1[2], 0x04000C0Cu);
+        const uint32_t w2 = __builtin_amdgcn_perm(b2[1], b2[0], 0x0C0C0400u) |
+                            __builtin_amdgcn_perm(b2[3], b2[2], 0x04000C0Cu);
+        const float s16 = sum4(s4);                             // 4 lanes x 4 = 16 elements
+        const float s32 = s16 + dpp_f<kDppRowHalfMirror>(s16);  // 8 lanes = 32 elements
+        if (store) {
+            ((uint32_t *)X.d1)[e4] = w1;
+            ((uint32_t *)X.d2)[e4] = w2;
+            if ((lane & 7) == 0) {
+                X.u[e >> 5] = u;
+                X.s32[e >> 5] = s32;
+            }
+            if ((lane & 3) == 0) X.s16[e >> 4] = s16;
+        }
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ weight units
+// Raw bytes of one half super-block (128 weights), loaded ahead of use.
+//   Q4_K: h = header (d, dmin, 12 scale bytes), q[0..3] = the 64 nibble bytes of the half
+//   Q6_K: h = the 16 scale bytes, q[0..3] = 64 ql bytes, qh[0..1] = 32 qh bytes, dd = f16 d
+struct RawH {
+    uint4 h;
+    uint4 q[4];
+    uint4 qh[2];
+    uint32_t dd;
+};
+
+// Q4_K half hf of super-block blk: qs bytes [64hf, +64), sub-blocks 4hf .. 4hf+3
+// (kernels.cu:114-136: qs pair g holds sub-block 2g in low, 2g+1 in high nibbles).
+__device__ __forceinline__ void load_q4k(const uint8_t *__restrict__ blk, int hf, RawH &r) {
+    r.h = ld16(blk);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.q[i] = ld16(blk + 16 + 64 * hf + 16 * i);
+}
+
+// Q6_K half hf: ql bytes [64hf, +64), qh bytes [128 + 32hf, +32), the 16 scale bytes at
+// 192 (the half uses 8hf .. 8hf+7), d at 208 (kernels.cu:427-491;
+// validate_dequant.py:253-319).
+__device__ __forceinline__ void load_q6k(const uint8_t *__restrict__ blk, int hf, RawH &r) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.q[i] = ld16(blk + 64 * hf + 16 * i);
+    r.qh[0] = ld16(blk + 128 + 32 * hf);
+    r.qh[1] = ld16(blk + 144 + 32 * hf);
+    r.h = ld16(blk + 192);
+    uint16_t dd;
+    __builtin_memcpy(&dd, blk + 208, 2);
+    r.dd = dd;
+}
+
+// Mixed-type launches issue one instruction sequence for both types (offsets chosen with
+// selects), so that no branch separates the loads of one pass from those of the next.
+__device__ __forceinline__ void load_any(const uint8_t *__restrict__ blk, int hf, bool q4, RawH &r) {
+    r.h = ld16(blk + (q4 ? 0 : 192));
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.q[i] = ld16(blk + (q4 ? 16 + 64 * hf : 64 * hf) + 16 * i);
+    r.qh[0] = ld16(blk + (q4 ? 0 : 128 + 32 * hf));
+    r.qh[1] = ld16(blk + (q4 ? 0 : 144 + 32 * hf));
+    uint16_t dd;
+    __builtin_memcpy(&dd, blk + (q4 ? 0 : 208), 2);
+    r.dd = dd;
+}
+
+__device__ __forceinline__ int dot16(const uint32_t (&q)[4], const int4 &d, int acc) {
+    acc = sdot4((int)q[0], d.x, acc);
+    acc = sdot4((int)q[1], d.y, acc);
+    acc = sdot4((int)q[2], d.z, acc);
+    acc = sdot4((int)q[3], d.w, acc);
+    return acc;
+}
+
+// Sum over the 128 weights of a Q4_K half super-block whose first column is c.
+// Sub-block t of the half: nibble t%2 of qs dwords 8(t/2) .. +7.
+__device__ __forceinline__ float q4k_dot(const RawH &r, int hf, int c, const XLds &X) {
+    int I[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int4 d1a = *(const int4 *)(X.d1 + c + 32 * t), d1b = *(const int4 *)(X.d1 + c + 32 * t + 16);
+        const int4 d2a = *(const int4 *)(X.d2 + c + 32 * t), d2b = *(const int4 *)(X.d2 + c + 32 * t + 16);
+        const uint4 qa = r.q[2 * (t >> 1)], qb = r.q[2 * (t >> 1) + 1];
+        const int sh = 4 * (t & 1);
+        const uint32_t na[4] = {(qa.x >> sh) & 0x0F0F0F0Fu, (qa.y >> sh) & 0x0F0F0F0Fu,
+                                (qa.z >> sh) & 0x0F0F0F0Fu, (qa.w >> sh) & 0x0F0F0F0Fu};
+        const uint32_t nb[4] = {(qb.x >> sh) & 0x0F0F0F0Fu, (qb.y >> sh) & 0x0F0F0F0Fu,
+                                (qb.z >> sh) & 0x0F0F0F0Fu, (qb.w >> sh) & 0x0F0F0F0Fu};
+        const int a1 = dot16(nb, d1b, dot16(na, d1a, 0));
+        const int a2 = dot16(nb, d2b, dot16(na, d2a, 0));
+        I[t] = 254 * a1 + a2;
+        // keep the scheduler from hoisting every sub-block's digit reads at once (that
+        // costs ~64 VGPRs and halves occupancy); other waves hide the LDS latency
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // four 6-bit scales and mins per dword: the packed form of get_scale_min_k4
+    // (kernels.cu:45-53), the same unpacking as gemm_q4k.cu:53-56
+    const uint32_t S0 = r.h.y, S1 = r.h.z, S2 = r.h.w;
+    const uint32_t sc = hf ? ((S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u)) : (S0 & 0x3F3F3F3Fu);
+    const uint32_t mm = hf ? (((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) : (S1 & 0x3F3F3F3Fu);
+    const float4 u = *(const float4 *)(X.u + (c >> 5));
+    const float4 sx = *(const float4 *)(X.s32 + (c >> 5));
+    const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+    float a = (float)(sc & 0xFF) * (u.x * (float)I[0]);
+    a = fmaf((float)((sc >> 8) & 0xFF), u.y * (float)I[1], a);
+    a = fmaf((float)((sc >> 16) & 0xFF), u.z * (float)I[2], a);
+    a = fmaf((float)(sc >> 24), u.w * (float)I[3], a);
+    float m = (float)(mm & 0xFF) * sx.x;
+    m = fmaf((float)((mm >> 8) & 0xFF), sx.y, m);
+    m = fmaf((float)((mm >> 16) & 0xFF), sx.z, m);
+    m = fmaf((float)(mm >> 24), sx.w, m);
+    return fmaf(d, a, -dmin * m);
+}
+
+// Sum over the 128 weights of a Q6_K half super-block (values 32g + l of the half,
+// g = 0..3) whose first column is c.
+__device__ __forceinline__ float q6k_dot(const RawH &r, int hf, int c, const XLds &X) {
+    const uint32_t H[8] = {r.qh[0].x, r.qh[0].y, r.qh[0].z, r.qh[0].w, r.qh[1].x, r.qh[1].y, r.qh[1].z, r.qh[1].w};
+    const float4 u = *(const float4 *)(X.u + (c >> 5));
+    const float4 s16a = *(const float4 *)(X.s16 + (c >> 4));
+    const float4 s16b = *(const float4 *)(X.s16 + (c >> 4) + 4);
+    const float uu[4] = {u.x, u.y, u.z, u.w};
+    const float ss[8] = {s16a.x, s16a.y, s16a.z, s16a.w, s16b.x, s16b.y, s16b.z, s16b.w};
+    float acc = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        // group g: low nibbles of ql bytes 32(g&1) .. +31 (high nibbles for g >= 2), top
+        // two bits at 2g of qh bytes 0..31, moved to bits 4-5 of each byte
+        const uint4 la = r.q[2 * (g & 1)], lb = r.q[2 * (g & 1) + 1];
+        const uint32_t L[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
+        uint32_t q[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t lo = (g >= 2 ? (L[k] >> 4) : L[k]) & 0x0F0F0F0Fu;
+            const uint32_t hi = (2 * g <= 4 ? (H[k] << (4 - 2 * g)) : (H[k] >> (2 * g - 4))) & 0x30303030u;
+            q[k] = lo | hi;
+        }
+        const int4 d1a = *(const int4 *)(X.d1 + c + 32 * g), d1b = *(const int4 *)(X.d1 + c + 32 * g + 16);
+        const int4 d2a = *(const int4 *)(X.d2 + c + 32 * g), d2b = *(const int4 *)(X.d2 + c + 32 * g + 16);
+        const uint32_t qa[4] = {q[0], q[1], q[2], q[3]}, qb[4] = {q[4], q[5], q[6], q[7]};
+        const int i0 = 254 * dot16(qa, d1a, 0) + dot16(qa, d2a, 0);
+        const int i1 = 254 * dot16(qb, d1b, 0) + dot16(qb, d2b, 0);
+        // scale bytes 8hf + 2g, 8hf + 2g + 1 (the 16-value groups of group g)
+        const uint32_t sw = hf ? (g < 2 ? r.h.z : r.h.w) : (g < 2 ? r.h.x : r.h.y);
+        const int sc0 = (int8_t)(sw >> (16 * (g & 1)));
+        const int sc1 = (int8_t)(sw >> (16 * (g & 1) + 8));
+        acc = fmaf((float)sc0, fmaf(uu[g], (float)i0, -32.0f * ss[2 * g]), acc);
+        acc = fmaf((float)sc1, fmaf(uu[g], (float)i1, -32.0f * ss[2 * g + 1]), acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return h2f(r.dd) * acc;
+}
+
+// ------------------------------------------------------------------ the kernel
+template <int LPR>
+__device__ __forceinline__ float reduce_rows(float v) {
+    if constexpr (LPR == 64) return sum64_lane63(v);
+    else if constexpr (LPR == 32) return sum32_lane31(v);
+    else if constexpr (LPR == 16) return sum16(v);
+    else if constexpr (LPR == 8) {
+        v = sum4(v);
+        return v + dpp_f<kDppRowHalfMirror>(v);
+    } else if constexpr (LPR == 4) return sum4(v);
+    else return v + dpp_f<kDppXor1>(v);
+}
+
+// One wave pass: P = 64/LPR rows, each lane holding UPL half super-blocks of its row.
+template <int UPL>
+struct Pass {
+    RawH q[UPL];
+    int lrow;  // row of this lane within its matrix (clamped)
+    bool valid;
+};
+
+// Matrices start at multiples of P rows in the concatenated row space (launch_gemv pads),
+// so a pass never straddles two matrices and its matrix index is wave-uniform.
+__device__ __forceinline__ int pass_matrix(const GemvArgs &args, int base) {
+    return (base >= args.off[1]) + (base >= args.off[2]);
+}
+
+// TM: types present in the launch -- 1 Q4_K only, 2 Q6_K only, 3 both.
+template <int LPR, int UPL, int TM>
+__device__ __forceinline__ void load_pass(const GemvArgs &args, int base, int bpr, Pass<UPL> &ps) {
+    const int lane = lane_id();
+    const int ul = lane % LPR;
+    const int uph = bpr * 2;  // half super-blocks per row
+    const int mi = pass_matrix(args, base);
+    const GemvMat &M = args.m[mi];
+    const int lrow = base - args.off[mi] + lane / LPR;
+    // branch-free: a row past the end of its matrix re-loads the last row, dropped later
+    ps.valid = lrow < M.rows;
+    ps.lrow = min(lrow, M.rows - 1);
+    const bool q4 = TM == 1 || (TM == 3 && M.type == kTypeQ4K);  // uniform
+    const int bb = q4 ? kQ4KBytes : kQ6KBytes;
+    const uint8_t *wrow = (const uint8_t *)M.w + (size_t)ps.lrow * bpr * bb;
+#pragma unroll
+    for (int j = 0; j < UPL; j++) {
+        const int u = min(ul + j * LPR, uph - 1);
+        const uint8_t *blk = wrow + (size_t)(u >> 1) * bb;
+        if (TM == 1) load_q4k(blk, u & 1, ps.q[j]);
+        else if (TM == 2) load_q6k(blk, u & 1, ps.q[j]);
+        else load_any(blk, u & 1, q4, ps.q[j]);
+    }
+}
+
+template <int LPR, int UPL, int TM>
+__device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int bpr, const Pass<UPL> &ps,
+                                            const XLds &X) {
+    const int lane = lane_id();
+    const int ul = lane % LPR;
+    const int uph = bpr * 2;
+    const GemvMat &M = args.m[pass_matrix(args, base)];
+    const bool q4 = TM == 1 || (TM == 3 && M.type == kTypeQ4K);  // uniform
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < UPL; j++) {
+        const int u = ul + j * LPR;
+        const int uc = min(u, uph - 1);
+        float v;
+        if (TM == 1) v = q4k_dot(ps.q[j], uc & 1, uc * 128, X);
+        else if (TM == 2) v = q6k_dot(ps.q[j], uc & 1, uc * 128, X);
+        else v = q4 ? q4k_dot(ps.q[j], uc & 1, uc * 128, X) : q6k_dot(ps.q[j], uc & 1, uc * 128, X);
+        acc += u < uph ? v : 0.0f;
+    }
+    acc = reduce_rows<LPR>(acc);
+    if (ul == LPR - 1 && ps.valid) {
+        if (M.mode == kEpiStore) M.y[ps.lrow] = acc;
+        else if (M.mode == kEpiResidual) M.y[ps.lrow] = acc + M.res[ps.lrow];
+        else M.y[ps.lrow] += M.scale * acc;
+    }
+}
+
+// R wave passes per wave, all loaded before the x image is built.  The grid covers the
+// row space exactly once (no loop), so the loads of every pass are issued back to back.
+template <int LPR, int UPL, int XPT, bool SWI, int TM, int R>
+__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int kp = (args.n_cols + 255) & ~255;
+    const int bpr = kp / 256;
+    XLds X(smem, kp);
+    constexpr int P = 64 / LPR;
+    constexpr int wpb = kGemvThreads / 64;
+    const int wave = blockIdx.x * wpb + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * wpb;
+    const int base0 = __builtin_amdgcn_readfirstlane(wave * P);  // wave-uniform
+    const int last = args.total_rows - P;
+
+    XRegs<XPT> xr, xr2;
+    load_x<XPT, SWI>(args.x, args.x2, args.n_cols, xr, xr2);
+    // pass r of this wave starts at row base0 + r * nwaves * P; a start past the end is
+    // clamped to the last pass (loaded again, dropped) so every wave issues the same loads
+    Pass<UPL> ps[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) load_pass<LPR, UPL, TM>(args, min(base0 + r * nwaves * P, last), bpr, ps[r]);
+    finish_x<XPT, SWI>(xr, xr2, args.n_cols, kp, X);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int base = base0 + r * nwaves * P;
+        if (base < args.total_rows) finish_pass<LPR, UPL, TM>(args, base, bpr, ps[r], X);
+    }
+}
+
+template <int LPR, int UPL, int XPT, int TM>
+static void launch_tm(const GemvArgs &a, int blocks, int R, size_t lds, hipStream_t stream) {
+#define MNEMO_GEMV_LAUNCH(SWI_, R_)                                                                          \
+    hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, SWI_, TM, R_>), dim3(blocks), dim3(kGemvThreads), lds, \
+                       stream, a)
+    if (a.xmode == 1) {
+        if (R == 1) MNEMO_GEMV_LAUNCH(true, 1);
+        else MNEMO_GEMV_LAUNCH(true, 2);
+    } else {
+        if (R == 1) MNEMO_GEMV_LAUNCH(false, 1);
+        else MNEMO_GEMV_LAUNCH(false, 2);
+    }
+#undef MNEMO_GEMV_LAUNCH
+}
+
+template <int LPR, int UPL, int XPT>
+static void launch(const GemvArgs &a, int blocks, int R, size_t lds, hipStream_t stream) {
+    int tm = 0;
+    for (int i = 0; i < a.nmat; i++) tm |= a.m[i].type == kTypeQ4K ? 1 : 2;
+    if (tm == 1) launch_tm<LPR, UPL, XPT, 1>(a, blocks, R, lds, stream);
+    else if (tm == 2) launch_tm<LPR, UPL, XPT, 2>(a, blocks, R, lds, stream);
+    else launch_tm<LPR, UPL, XPT, 3>(a, blocks, R, lds, stream);
+}
+
+static int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+int launch_gemv(GemvArgs a, hipStream_t stream) {
+    if (a.n_cols < 4 || a.n_cols > kMaxGemvCols) return kErrBadArg;
+    const int kp = (a.n_cols + 255) & ~255;
+    // half super-blocks per row -> lanes per row (pow2, <= 64) and rows per wave pass
+    const int uph = kp / 128;
+    int lpr = 2;
+    while (lpr < uph && lpr < 64) lpr <<= 1;
+    const int P = 64 / lpr;
+    constexpr int wpb = kGemvThreads / 64;
+    // each matrix starts at a multiple of P rows so that no wave pass spans two matrices
+    int off = 0;
+    for (int i = 0; i < a.nmat; i++) {
+        a.off[i] = off;
+        off += (a.m[i].rows + P - 1) / P * P;
+    }
+    for (int i = a.nmat; i < 3; i++) a.off[i] = INT_MAX;
+    a.total_rows = off;
+    const int passes = a.total_rows / P;
+    // One pass per wave while the whole grid fits on the chip at once (2 workgroups per
+    // CU), else two passes per wave; the hardware queues any further workgroups.
+    const int resident = 2 * device_cus() * wpb;
+    const int R = passes > resident ? 2 : 1;
+    const int blocks = (passes + wpb * R - 1) / (wpb * R);
+    const size_t lds = xlds_bytes(kp);
+    // XPT = float4 of x per thread = kp / (4 * kGemvThreads), rounded up
+    switch (lpr) {
+    case 2: launch<2, 1, 1>(a, blocks, R, lds, stream); break;
+    case 4: launch<4, 1, 1>(a, blocks, R, lds, stream); break;
+    case 8: launch<8, 1, 1>(a, blocks, R, lds, stream); break;
+    case 16: launch<16, 1, 1>(a, blocks, R, lds, stream); break;
+    case 32: launch<32, 1, 2>(a, blocks, R, lds, stream); break;
+    default:
+        if (kp <= 8192) launch<64, 1, 4>(a, blocks, R, lds, stream);
+        else launch<64, 2, 8>(a, blocks, R, lds, stream);
+    }
+    return check_launch("gemv");
+}
+
+}  // namespace mnemo

@@ -1,0 +1,76 @@
+"""ctypes binding of libmnemo_hip.so (include/mnemo_kernels.h + include/mnemo_host.h).
+
+Every exported symbol is declared here with its C signature; ``EXPORTS`` is the list the
+CPU test compares against the headers.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmnemo_hip.so"
+
+vp, fp, ip = C.c_void_p, C.c_void_p, C.c_void_p  # device pointers travel as void*
+i32, f32, sz = C.c_int, C.c_float, C.c_size_t
+stream_t = C.c_void_p
+
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple] = {
+    "mnemo_last_error": (i32, []),
+    "mnemo_last_error_string": (C.c_char_p, []),
+    "mnemo_version": (C.c_char_p, []),
+    "cuda_kernels_init": (None, []),
+    "cuda_matvec_q4k": (None, [vp, fp, fp, i32, i32, stream_t]),
+    "cuda_matvec_q4k_add": (None, [vp, fp, fp, fp, i32, i32, stream_t]),
+    "cuda_matvec_q4k_qkv": (None, [vp, vp, vp, fp, fp, fp, fp, i32, i32, i32, stream_t]),
+    "cuda_matvec_q4k_dual": (None, [vp, vp, fp, fp, fp, i32, i32, stream_t]),
+    "cuda_matvec_q4k_scaled_add": (None, [vp, fp, fp, i32, i32, f32, stream_t]),
+    "cuda_matvec_q6k": (None, [vp, fp, fp, i32, i32, stream_t]),
+    "mnemo_matvec_q6k_scaled_add": (None, [vp, fp, fp, i32, i32, f32, stream_t]),
+    "mnemo_matvec_dual": (None, [vp, i32, vp, i32, fp, fp, fp, i32, i32, stream_t]),
+    "mnemo_matvec_swiglu_scaled_add": (None, [vp, i32, fp, fp, fp, i32, i32, f32, stream_t]),
+    "cuda_matvec_f32": (None, [fp, fp, fp, i32, i32, stream_t]),
+    "cuda_topk_softmax": (None, [fp, ip, fp, i32, i32, stream_t]),
+    "cuda_swiglu": (None, [fp, fp, fp, i32, stream_t]),
+    "cuda_scaled_add": (None, [fp, fp, f32, i32, stream_t]),
+    "cuda_quantize_mmq_q8_1": (None, [fp, vp, i32, i32, stream_t]),
+    "cuda_gemm_q4k": (None, [vp, vp, fp, i32, i32, i32, stream_t]),
+    "mnemo_gemm_q6k": (None, [vp, vp, fp, i32, i32, i32, stream_t]),
+    # host composition (mnemo_host.h)
+    "mnemo_matvec": (i32, [vp, fp, fp, i32, i32, i32, stream_t]),
+    "mnemo_down_type_id": (i32, [sz, i32, i32]),
+    "mnemo_expert_fwd": (i32, [vp, sz, sz, i32, i32, i32, f32, fp, fp, fp, fp, stream_t]),
+}
+EXPORTS = sorted(SIGNATURES)
+
+
+class MnemoError(RuntimeError):
+    pass
+
+
+_lib: C.CDLL | None = None
+
+
+def load_library(path: Path | str | None = None) -> C.CDLL:
+    """Load libmnemo_hip.so and declare every signature.  Raises if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise MnemoError(f"{p} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                         "or `python mnemocuda_amd/build.py`")
+    lib = C.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def check(lib: C.CDLL, what: str) -> None:
+    e = lib.mnemo_last_error()
+    if e:
+        raise MnemoError(f"{what}: error {e}: {lib.mnemo_last_error_string().decode()}")

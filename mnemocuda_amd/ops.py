@@ -1,0 +1,186 @@
+"""Torch-tensor wrappers over the C ABI (one call = one C entry point).
+
+Tensors must be CUDA (HIP) tensors on the current device; weights are uint8 tensors that
+hold raw GGUF blocks.  Calls are enqueued on torch's current stream.  Nothing here
+computes on the host: a missing library or a CPU tensor raises MnemoError.
+"""
+from __future__ import annotations
+
+import torch
+
+from .lib import MnemoError, check, load_library
+
+TYPE_F32, TYPE_Q4K, TYPE_Q6K = 0, 12, 14
+BLOCK_BYTES = {TYPE_Q4K: 144, TYPE_Q6K: 210}
+
+
+def _dev(t: torch.Tensor, name: str, dtype: torch.dtype | None = None) -> int:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise MnemoError(f"{name} must be a GPU tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise MnemoError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise MnemoError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def row_bytes(type_id: int, n_cols: int) -> int:
+    if type_id == TYPE_F32:
+        return 4 * n_cols
+    return (n_cols + 255) // 256 * BLOCK_BYTES[type_id]
+
+
+def _check_w(w: torch.Tensor, type_id: int, rows: int, cols: int, name: str = "W") -> int:
+    p = _dev(w, name)
+    need = rows * row_bytes(type_id, cols)
+    if w.numel() * w.element_size() < need:
+        raise MnemoError(f"{name}: {w.numel() * w.element_size()} bytes < {need} needed for "
+                         f"{rows}x{cols} type {type_id}")
+    return p
+
+
+def init() -> None:
+    lib = load_library()
+    lib.cuda_kernels_init()
+    check(lib, "cuda_kernels_init")
+
+
+def matvec(w, x, y, rows, cols, type_id):
+    """Reference dispatcher matvec() (forward.c:160-173) via mnemo_matvec."""
+    lib = load_library()
+    _check_w(w, type_id, rows, cols)
+    e = lib.mnemo_matvec(w.data_ptr(), _dev(x, "x", torch.float32), _dev(y, "y", torch.float32),
+                         rows, cols, type_id, _stream())
+    if e:
+        raise MnemoError(f"mnemo_matvec: error {e}: {lib.mnemo_last_error_string().decode()}")
+
+
+def matvec_q4k(w, x, y, rows, cols):
+    lib = load_library()
+    lib.cuda_matvec_q4k(_check_w(w, TYPE_Q4K, rows, cols), _dev(x, "x", torch.float32),
+                        _dev(y, "y", torch.float32), rows, cols, _stream())
+    check(lib, "cuda_matvec_q4k")
+
+
+def matvec_q6k(w, x, y, rows, cols):
+    lib = load_library()
+    lib.cuda_matvec_q6k(_check_w(w, TYPE_Q6K, rows, cols), _dev(x, "x", torch.float32),
+                        _dev(y, "y", torch.float32), rows, cols, _stream())
+    check(lib, "cuda_matvec_q6k")
+
+
+def matvec_q4k_add(w, x, residual, y, rows, cols):
+    lib = load_library()
+    lib.cuda_matvec_q4k_add(_check_w(w, TYPE_Q4K, rows, cols), _dev(x, "x", torch.float32),
+                            _dev(residual, "residual", torch.float32), _dev(y, "y", torch.float32),
+                            rows, cols, _stream())
+    check(lib, "cuda_matvec_q4k_add")
+
+
+def matvec_q4k_qkv(wq, wk, wv, x, q, k, v, q_rows, kv_rows, cols):
+    lib = load_library()
+    lib.cuda_matvec_q4k_qkv(_check_w(wq, TYPE_Q4K, q_rows, cols, "wq"),
+                            _check_w(wk, TYPE_Q4K, kv_rows, cols, "wk"),
+                            _check_w(wv, TYPE_Q4K, kv_rows, cols, "wv"), _dev(x, "x", torch.float32),
+                            _dev(q, "q", torch.float32), _dev(k, "k", torch.float32),
+                            _dev(v, "v", torch.float32), q_rows, kv_rows, cols, _stream())
+    check(lib, "cuda_matvec_q4k_qkv")
+
+
+def matvec_q4k_dual(wa, wb, x, ya, yb, rows, cols):
+    lib = load_library()
+    lib.cuda_matvec_q4k_dual(_check_w(wa, TYPE_Q4K, rows, cols, "wa"), _check_w(wb, TYPE_Q4K, rows, cols, "wb"),
+                             _dev(x, "x", torch.float32), _dev(ya, "ya", torch.float32),
+                             _dev(yb, "yb", torch.float32), rows, cols, _stream())
+    check(lib, "cuda_matvec_q4k_dual")
+
+
+def matvec_dual(wa, ta, wb, tb, x, ya, yb, rows, cols):
+    lib = load_library()
+    lib.mnemo_matvec_dual(_check_w(wa, ta, rows, cols, "wa"), ta, _check_w(wb, tb, rows, cols, "wb"), tb,
+                          _dev(x, "x", torch.float32), _dev(ya, "ya", torch.float32),
+                          _dev(yb, "yb", torch.float32), rows, cols, _stream())
+    check(lib, "mnemo_matvec_dual")
+
+
+def matvec_q4k_scaled_add(w, x, y, rows, cols, scale):
+    lib = load_library()
+    lib.cuda_matvec_q4k_scaled_add(_check_w(w, TYPE_Q4K, rows, cols), _dev(x, "x", torch.float32),
+                                   _dev(y, "y", torch.float32), rows, cols, float(scale), _stream())
+    check(lib, "cuda_matvec_q4k_scaled_add")
+
+
+def matvec_q6k_scaled_add(w, x, y, rows, cols, scale):
+    lib = load_library()
+    lib.mnemo_matvec_q6k_scaled_add(_check_w(w, TYPE_Q6K, rows, cols), _dev(x, "x", torch.float32),
+                                    _dev(y, "y", torch.float32), rows, cols, float(scale), _stream())
+    check(lib, "mnemo_matvec_q6k_scaled_add")
+
+
+def matvec_swiglu_scaled_add(w, type_id, gate, up, y, rows, cols, scale):
+    lib = load_library()
+    lib.mnemo_matvec_swiglu_scaled_add(_check_w(w, type_id, rows, cols), type_id,
+                                       _dev(gate, "gate", torch.float32), _dev(up, "up", torch.float32),
+                                       _dev(y, "y", torch.float32), rows, cols, float(scale), _stream())
+    check(lib, "mnemo_matvec_swiglu_scaled_add")
+
+
+def matvec_f32(w, x, y, rows, cols):
+    lib = load_library()
+    lib.cuda_matvec_f32(_dev(w, "W", torch.float32), _dev(x, "x", torch.float32), _dev(y, "y", torch.float32),
+                        rows, cols, _stream())
+    check(lib, "cuda_matvec_f32")
+
+
+def topk_softmax(scores, idx, w, n_experts, k):
+    lib = load_library()
+    lib.cuda_topk_softmax(_dev(scores, "scores", torch.float32), _dev(idx, "idx", torch.int32),
+                          _dev(w, "w", torch.float32), n_experts, k, _stream())
+    check(lib, "cuda_topk_softmax")
+
+
+def swiglu(g, u, out, n):
+    lib = load_library()
+    lib.cuda_swiglu(_dev(g, "g", torch.float32), _dev(u, "u", torch.float32), _dev(out, "out", torch.float32),
+                    n, _stream())
+    check(lib, "cuda_swiglu")
+
+
+def scaled_add(out, x, scale, n):
+    lib = load_library()
+    lib.cuda_scaled_add(_dev(out, "out", torch.float32), _dev(x, "x", torch.float32), float(scale), n, _stream())
+    check(lib, "cuda_scaled_add")
+
+
+def quantize_q8_1(src, dst, K, N):
+    lib = load_library()
+    if dst.numel() * dst.element_size() < N * (K // 128) * 144:
+        raise MnemoError("quantize_q8_1: dst too small")
+    lib.cuda_quantize_mmq_q8_1(_dev(src, "src", torch.float32), _dev(dst, "dst"), K, N, _stream())
+    check(lib, "cuda_quantize_mmq_q8_1")
+
+
+def gemm(w, type_id, act, out, M, K, N):
+    lib = load_library()
+    _check_w(w, type_id, M, K)
+    if act.numel() * act.element_size() < N * (K // 128) * 144:
+        raise MnemoError("gemm: activation buffer too small")
+    if out.numel() < M * N:
+        raise MnemoError("gemm: output too small")
+    fn = lib.cuda_gemm_q4k if type_id == TYPE_Q4K else lib.mnemo_gemm_q6k
+    fn(w.data_ptr(), _dev(act, "act"), _dev(out, "out", torch.float32), M, K, N, _stream())
+    check(lib, "gemm")
+
+
+def expert_fwd(expert, gate_sz, up_sz, H, EFF, down_type, weight, x, gate_buf, up_buf, moe_out):
+    lib = load_library()
+    e = lib.mnemo_expert_fwd(_dev(expert, "expert"), gate_sz, up_sz, H, EFF, down_type, float(weight),
+                             _dev(x, "x", torch.float32), _dev(gate_buf, "gate_buf", torch.float32),
+                             _dev(up_buf, "up_buf", torch.float32), _dev(moe_out, "moe_out", torch.float32),
+                             _stream())
+    if e:
+        raise MnemoError(f"mnemo_expert_fwd: error {e}: {lib.mnemo_last_error_string().decode()}")

@@ -1,0 +1,143 @@
+"""CPU oracle for the quantized-matmul hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use this
+package; the product library never loads it.  ``load()`` returns the C restatement
+(mnemo_oracle.c) with typed numpy-friendly wrappers; ``oracle_np`` is the independent
+numpy restatement the C code is cross-checked against.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "libmnemo_oracle.so"
+
+
+def build() -> Path:
+    r = subprocess.run(["make", "-C", str(HERE)], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{r.stdout}\n{r.stderr}")
+    return LIB
+
+
+class Oracle:
+    def __init__(self, path: Path = LIB):
+        if not path.exists():
+            build()
+        L = C.CDLL(str(path))
+        P = C.c_void_p
+        L.mo_f16_to_f32.restype = C.c_float
+        L.mo_f16_to_f32.argtypes = [C.c_uint16]
+        L.mo_f32_to_f16.restype = C.c_uint16
+        L.mo_f32_to_f16.argtypes = [C.c_float]
+        L.mo_get_scale_min_k4.argtypes = [C.c_int, P, P, P]
+        for n in ("mo_dequant_q4k", "mo_dequant_q6k"):
+            getattr(L, n).argtypes = [P, P, C.c_int, C.c_int]
+        L.mo_dequant.restype = C.c_int
+        L.mo_dequant.argtypes = [C.c_int, P, P, C.c_int, C.c_int]
+        L.mo_gemv.restype = C.c_int
+        L.mo_gemv.argtypes = [C.c_int, P, P, P, C.c_int, C.c_int]
+        L.mo_gemv_f32acc.restype = C.c_int
+        L.mo_gemv_f32acc.argtypes = [C.c_int, P, P, P, C.c_int, C.c_int, C.c_int]
+        L.mo_matvec_f32.argtypes = [P, P, P, C.c_int, C.c_int]
+        L.mo_topk_softmax.argtypes = [P, C.c_int, C.c_int, P, P]
+        L.mo_swiglu.argtypes = [P, P, P, C.c_int]
+        L.mo_scaled_add.argtypes = [P, P, C.c_float, C.c_int]
+        L.mo_quantize_q8_1_mmq.argtypes = [P, P, C.c_int, C.c_int]
+        L.mo_dequant_q8_1_mmq.argtypes = [P, P, C.c_int, C.c_int]
+        L.mo_gemm_q8_1.restype = C.c_int
+        L.mo_gemm_q8_1.argtypes = [C.c_int, P, P, P, C.c_int, C.c_int, C.c_int]
+        self.L = L
+
+    @staticmethod
+    def _p(a: np.ndarray):
+        return a.ctypes.data_as(C.c_void_p)
+
+    def f16_to_f32(self, h: int) -> float:
+        return self.L.mo_f16_to_f32(h)
+
+    def f32_to_f16(self, f: float) -> int:
+        return self.L.mo_f32_to_f16(f)
+
+    def scale_min_k4(self, j: int, scales12: np.ndarray) -> tuple[int, int]:
+        s = np.ascontiguousarray(scales12, np.uint8)
+        sc, m = np.zeros(1, np.uint8), np.zeros(1, np.uint8)
+        self.L.mo_get_scale_min_k4(j, self._p(s), self._p(sc), self._p(m))
+        return int(sc[0]), int(m[0])
+
+    def dequant(self, type_id: int, w: np.ndarray, rows: int, cols: int) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.uint8)
+        out = np.zeros((rows, cols), np.float32)
+        if self.L.mo_dequant(type_id, self._p(w), self._p(out), rows, cols):
+            raise ValueError(type_id)
+        return out
+
+    def gemv(self, type_id: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(rows, np.float64)
+        if self.L.mo_gemv(type_id, self._p(w), self._p(x), self._p(y), rows, cols):
+            raise ValueError(type_id)
+        return y
+
+    def gemv_f32acc(self, type_id, w, x, rows, cols, nthreads=0) -> np.ndarray:
+        y = np.zeros(rows, np.float32)
+        if self.L.mo_gemv_f32acc(type_id, self._p(w), self._p(x), self._p(y), rows, cols, nthreads):
+            raise ValueError(type_id)
+        return y
+
+    def matvec_f32(self, w: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(rows, np.float64)
+        self.L.mo_matvec_f32(self._p(w), self._p(x), self._p(y), rows, cols)
+        return y
+
+    def topk_softmax(self, scores: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
+        s = np.ascontiguousarray(scores, np.float32)
+        idx = np.zeros(k, np.int32)
+        w = np.zeros(k, np.float32)
+        self.L.mo_topk_softmax(self._p(s), s.size, k, self._p(idx), self._p(w))
+        return idx, w
+
+    def swiglu(self, g: np.ndarray, u: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        out = np.zeros_like(g)
+        self.L.mo_swiglu(self._p(g), self._p(u), self._p(out), g.size)
+        return out
+
+    def quantize_q8_1(self, src: np.ndarray) -> np.ndarray:
+        src = np.ascontiguousarray(src, np.float32)
+        n, k = src.shape
+        out = np.zeros((n, k // 128, 144), np.uint8)
+        self.L.mo_quantize_q8_1_mmq(self._p(src), self._p(out), k, n)
+        return out
+
+    def dequant_q8_1(self, blocks: np.ndarray, k: int, n: int) -> np.ndarray:
+        b = np.ascontiguousarray(blocks, np.uint8)
+        out = np.zeros((n, k), np.float32)
+        self.L.mo_dequant_q8_1_mmq(self._p(b), self._p(out), k, n)
+        return out
+
+    def gemm(self, type_id: int, w: np.ndarray, act: np.ndarray, M: int, K: int, N: int) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.uint8)
+        a = np.ascontiguousarray(act, np.uint8)
+        out = np.zeros((N, M), np.float64)
+        if self.L.mo_gemm_q8_1(type_id, self._p(w), self._p(a), self._p(out), M, K, N):
+            raise ValueError(type_id)
+        return out
+
+
+_oracle: Oracle | None = None
+
+
+def load() -> Oracle:
+    global _oracle
+    if _oracle is None:
+        _oracle = Oracle()
+    return _oracle

@@ -1,0 +1,78 @@
+/*
+ * mnemo_oracle.h -- CPU restatement of MnemoCUDA's quantized-matmul hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP kernels are
+ * compared against; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it.  The product library (mnemocuda_amd/libmnemo_hip.so) never links,
+ * loads or falls back to it.
+ *
+ * Every routine cites the reference file:line whose arithmetic it restates
+ * (paths relative to the MnemoCUDA source tree).
+ *
+ * Pinning (what fixes each routine independently of this code; see tests/test_oracle.py):
+ *   mo_f16_to_f32        exhaustive over all 65536 patterns vs numpy float16 and x86 F16C.
+ *   mo_f32_to_f16        edge cases + 2^20 random floats vs numpy astype(float16) (RNE).
+ *   mo_get_scale_min_k4  exhaustive round trip through an independent packer, and the
+ *                        packed-int form of gemm_q4k.cu:53-56 restated in numpy.
+ *   mo_dequant_q4k/q6k   one-hot brute force over all 256 positions, closed forms
+ *                        (all-zero / all-max quants), linearity in d and dmin, and an
+ *                        independent numpy restatement written from the layout text.
+ *   mo_gemv_*            fp64 brute force of numpy-dequantised weights.
+ *   mo_quantize_q8_1     closed forms per block (zero block, +-amax maps to +-127,
+ *                        round-half-even ties) and an independent numpy restatement.
+ *   mo_topk_softmax      numpy argsort (stable) + fp64 softmax.
+ *   mo_gemm_*            numpy fp64 matmul of the dequantised operands.
+ */
+#ifndef MNEMO_ORACLE_H
+#define MNEMO_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MO_QK_K 256
+#define MO_Q4K_BYTES 144
+#define MO_Q6K_BYTES 210
+#define MO_Q8_1_MMQ_BYTES 144 /* 4 x half2 + 128 int8, covers 128 values */
+
+/* GGUF type ids used by the reference dispatcher (forward.c:160-173). */
+#define MO_TYPE_F32 0
+#define MO_TYPE_Q4K 12
+#define MO_TYPE_Q6K 14
+
+float mo_f16_to_f32(uint16_t h);
+uint16_t mo_f32_to_f16(float f);
+void mo_get_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m);
+
+/* Dequantise n_rows x n_cols (row-major, ceil(n_cols/256) blocks per row). */
+void mo_dequant_q4k(const void *w, float *out, int n_rows, int n_cols);
+void mo_dequant_q6k(const void *w, float *out, int n_rows, int n_cols);
+int mo_dequant(int type_id, const void *w, float *out, int n_rows, int n_cols);
+
+/* y = W x accumulated in fp64 over fp32 dequantised weights. */
+int mo_gemv(int type_id, const void *w, const float *x, double *y, int n_rows, int n_cols);
+
+/* CPU baseline: the reference GPU kernel's arithmetic (fp32 dequant, fp32 accumulate),
+ * rows split over nthreads OpenMP threads. */
+int mo_gemv_f32acc(int type_id, const void *w, const float *x, float *y, int n_rows,
+                   int n_cols, int nthreads);
+
+void mo_matvec_f32(const float *w, const float *x, double *y, int n_rows, int n_cols);
+void mo_topk_softmax(const float *scores, int n_experts, int k, int *idx, float *wts);
+void mo_swiglu(const float *g, const float *u, float *out, int n);
+void mo_scaled_add(float *out, const float *x, float scale, int n);
+
+/* Q8_1 "MMQ" activation blocks, [N][K/128] blocks of 144 B. */
+void mo_quantize_q8_1_mmq(const float *src, void *dst, int K, int N);
+void mo_dequant_q8_1_mmq(const void *src, float *out, int K, int N);
+
+/* out[j*M + i] = sum_k deq(W)[i][k] * deq(A)[j][k] in fp64 (column-major [N][M]). */
+int mo_gemm_q8_1(int type_id, const void *w, const void *act, double *out, int M, int K, int N);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,156 @@
+"""GPU parity of the decode GEMV family against the CPU oracle (fp64 of fp32-dequantised
+weights).  Bar: relative L2 <= 1e-3; the int8-digit x encoding is
+expected to land near 1e-5, which is also recorded."""
+import numpy as np
+import pytest
+import torch
+
+from mnemocuda_amd import synth
+from tests.conftest import rel_l2
+from tests.gpu_util import case, dev, host
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _mk(rng, type_id, rows, cols):
+    w = synth.weights(rng, type_id, rows, cols)
+    return w, dev(w)
+
+
+SHAPES = [
+    (12, 4096, 4096), (12, 8192, 4096), (12, 512, 4096), (12, 1536, 4096), (12, 4096, 1536),
+    (12, 4096, 8192), (14, 512, 4096), (14, 4096, 1536), (14, 333, 4096),
+    (12, 1, 256), (14, 3, 512), (12, 7, 300), (14, 5, 1000), (12, 2, 16384),
+]
+
+
+@pytest.mark.parametrize("type_id,rows,cols", SHAPES)
+def test_matvec(gpu, oracle, type_id, rows, cols):
+    rng = np.random.default_rng(rows * 31 + cols + type_id)
+    w, wd = _mk(rng, type_id, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    case(f"matvec type={type_id} {rows}x{cols}")
+    (gpu.ops.matvec_q4k if type_id == 12 else gpu.ops.matvec_q6k)(wd, dev(x), y, rows, cols)
+    err = rel_l2(host(y), oracle.gemv(type_id, w, x, rows, cols))
+    print(f"rel_l2={err:.2e}")
+    assert err < TOL
+
+
+def test_dispatcher_matvec(gpu, oracle):
+    rng = np.random.default_rng(7)
+    for t, rows, cols in [(12, 64, 1024), (14, 64, 1024)]:
+        w, wd = _mk(rng, t, rows, cols)
+        x = rng.standard_normal(cols).astype(np.float32)
+        y = torch.zeros(rows, device="cuda")
+        case(f"mnemo_matvec type={t}")
+        gpu.ops.matvec(wd, dev(x), y, rows, cols, t)
+        assert rel_l2(host(y), oracle.gemv(t, w, x, rows, cols)) < TOL
+    wr = rng.standard_normal((128, 4096)).astype(np.float32)
+    x = rng.standard_normal(4096).astype(np.float32)
+    y = torch.zeros(128, device="cuda")
+    case("mnemo_matvec type=0 (router)")
+    gpu.ops.matvec(dev(wr), dev(x), y, 128, 4096, 0)
+    assert rel_l2(host(y), oracle.matvec_f32(wr, x, 128, 4096)) < 1e-6
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 8192), (100, 4096), (33, 512)])
+def test_matvec_add_residual(gpu, oracle, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    w, wd = _mk(rng, 12, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    res = rng.standard_normal(rows).astype(np.float32)
+    y = torch.zeros(rows, device="cuda")
+    case(f"matvec_q4k_add {rows}x{cols}")
+    gpu.ops.matvec_q4k_add(wd, dev(x), dev(res), y, rows, cols)
+    assert rel_l2(host(y), oracle.gemv(12, w, x, rows, cols) + res) < TOL
+
+
+@pytest.mark.parametrize("q_rows,kv_rows,cols", [(8192, 512, 4096), (64, 6, 512), (40, 3, 1024)])
+def test_qkv(gpu, oracle, q_rows, kv_rows, cols):
+    rng = np.random.default_rng(q_rows + kv_rows)
+    ws = [_mk(rng, 12, r, cols) for r in (q_rows, kv_rows, kv_rows)]
+    x = rng.standard_normal(cols).astype(np.float32)
+    outs = [torch.zeros(r, device="cuda") for r in (q_rows, kv_rows, kv_rows)]
+    case(f"qkv {q_rows}/{kv_rows}x{cols}")
+    gpu.ops.matvec_q4k_qkv(ws[0][1], ws[1][1], ws[2][1], dev(x), *outs, q_rows, kv_rows, cols)
+    for (w, _), o, r in zip(ws, outs, (q_rows, kv_rows, kv_rows)):
+        assert rel_l2(host(o), oracle.gemv(12, w, x, r, cols)) < TOL
+
+
+@pytest.mark.parametrize("ta,tb,rows,cols", [(12, 12, 1536, 4096), (12, 14, 512, 4096), (14, 12, 77, 768),
+                                             (14, 14, 64, 1536)])
+def test_dual(gpu, oracle, ta, tb, rows, cols):
+    rng = np.random.default_rng(ta * tb + rows)
+    wa, wad = _mk(rng, ta, rows, cols)
+    wb, wbd = _mk(rng, tb, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    ya, yb = torch.zeros(rows, device="cuda"), torch.zeros(rows, device="cuda")
+    case(f"dual {ta}/{tb} {rows}x{cols}")
+    if ta == tb == 12:
+        gpu.ops.matvec_q4k_dual(wad, wbd, dev(x), ya, yb, rows, cols)
+    else:
+        gpu.ops.matvec_dual(wad, ta, wbd, tb, dev(x), ya, yb, rows, cols)
+    assert rel_l2(host(ya), oracle.gemv(ta, wa, x, rows, cols)) < TOL
+    assert rel_l2(host(yb), oracle.gemv(tb, wb, x, rows, cols)) < TOL
+
+
+@pytest.mark.parametrize("type_id,rows,cols", [(12, 4096, 1536), (14, 4096, 1536), (14, 100, 4096)])
+def test_scaled_add(gpu, oracle, type_id, rows, cols):
+    rng = np.random.default_rng(rows * type_id)
+    w, wd = _mk(rng, type_id, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    y = dev(y0.copy())
+    s = 0.37
+    case(f"scaled_add type={type_id} {rows}x{cols}")
+    (gpu.ops.matvec_q4k_scaled_add if type_id == 12 else gpu.ops.matvec_q6k_scaled_add)(wd, dev(x), y, rows, cols, s)
+    exp = y0 + s * oracle.gemv(type_id, w, x, rows, cols)
+    assert rel_l2(host(y) - y0, exp - y0) < TOL
+
+
+@pytest.mark.parametrize("type_id", [12, 14])
+def test_swiglu_fused_down(gpu, oracle, type_id):
+    rng = np.random.default_rng(99 + type_id)
+    H, EFF = 4096, 1536
+    w, wd = _mk(rng, type_id, H, EFF)
+    g = rng.standard_normal(EFF).astype(np.float32)
+    u = rng.standard_normal(EFF).astype(np.float32)
+    y0 = rng.standard_normal(H).astype(np.float32)
+    y = dev(y0.copy())
+    case(f"swiglu_scaled_add type={type_id}")
+    gpu.ops.matvec_swiglu_scaled_add(wd, type_id, dev(g), dev(u), y, H, EFF, 0.25)
+    exp = 0.25 * oracle.gemv(type_id, w, oracle.swiglu(g, u), H, EFF)
+    assert rel_l2(host(y) - y0, exp) < TOL
+
+
+def test_expert_fwd_host_composition(gpu, oracle):
+    """mnemo_expert_fwd (forward.c:1122-1142 composition): blob [gate][up][down Q6_K]."""
+    rng = np.random.default_rng(5)
+    H, EFF = 4096, 1536
+    gate, up = synth.weights(rng, 12, EFF, H), synth.weights(rng, 12, EFF, H)
+    down = synth.weights(rng, 14, H, EFF)
+    blob = np.concatenate([gate, up, down])
+    x = rng.standard_normal(H).astype(np.float32)
+    acc0 = rng.standard_normal(H).astype(np.float32)
+    acc = dev(acc0.copy())
+    gb, ub = torch.zeros(EFF, device="cuda"), torch.zeros(EFF, device="cuda")
+    case("expert_fwd")
+    gpu.ops.expert_fwd(dev(blob), gate.size, up.size, H, EFF, 14, 0.6, dev(x), gb, ub, acc)
+    gy = oracle.gemv(12, gate, x, EFF, H).astype(np.float32)
+    uy = oracle.gemv(12, up, x, EFF, H).astype(np.float32)
+    exp = 0.6 * oracle.gemv(14, down, oracle.swiglu(gy, uy), H, EFF)
+    assert rel_l2(host(acc) - acc0, exp) < TOL
+
+
+def test_repeat_calls_are_deterministic(gpu):
+    rng = np.random.default_rng(3)
+    w, wd = _mk(rng, 12, 2048, 4096)
+    x = dev(rng.standard_normal(4096).astype(np.float32))
+    ys = []
+    for _ in range(3):
+        y = torch.zeros(2048, device="cuda")
+        gpu.ops.matvec_q4k(wd, x, y, 2048, 4096)
+        ys.append(host(y))
+    assert all(np.array_equal(ys[0], t) for t in ys[1:])
