@@ -35,19 +35,29 @@ constexpr int kGemvThreads = 512;
 
 // ------------------------------------------------------------------ x preparation
 // LDS image of x for a padded length kp (multiple of 256):
-//   int8 d1[kp] | int8 d2[kp] | float u[kp/32] | float s32[kp/32] | float s16[kp/16]
+//   int8 d1[kp + 128] | int8 d2[kp + 128] | float u[kp/32] | float s32[kp/32] | float s16[kp/16]
+// The digit planes are stored in 16-byte words, interleaved by 128-column chunk: column c
+// lives in word ((c % 128) / 16) * (kp/128 + 1) + c / 128.  Lane ul reads chunk ul, so the
+// 16-byte reads of one instruction hit consecutive words (no bank conflicts); the +1
+// skew keeps the 4-byte writes of the preparation conflict-free as well.
 struct XLds {
     int8_t *d1;
     int8_t *d2;
     float *u;
     float *s32;
     float *s16;
+    int nch1;  // 128-column chunks + 1
     __device__ XLds(uint8_t *base, int kp)
-        : d1((int8_t *)base), d2((int8_t *)(base + kp)), u((float *)(base + 2 * kp)),
-          s32((float *)(base + 2 * kp + kp / 8)), s16((float *)(base + 2 * kp + kp / 4)) {}
+        : d1((int8_t *)base), d2((int8_t *)(base + kp + 128)), u((float *)(base + 2 * kp + 256)),
+          s32((float *)(base + 2 * kp + 256 + kp / 8)), s16((float *)(base + 2 * kp + 256 + kp / 4)),
+          nch1(kp / 128 + 1) {}
+    // byte offset of column c (c % 16 == 0 gives a 16-byte aligned word)
+    __device__ __forceinline__ int off(int c) const {
+        return ((((c & 127) >> 4) * nch1 + (c >> 7)) << 4) + (c & 15);
+    }
 };
 
-__host__ __device__ constexpr size_t xlds_bytes(int kp) { return (size_t)2 * kp + kp / 2; }
+__host__ __device__ constexpr size_t xlds_bytes(int kp) { return (size_t)2 * kp + 256 + kp / 2; }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
     // silu(g) * u, the reference's expression (kernels.cu:686-687)
@@ -155,8 +165,9 @@ __device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &
         const float s16 = sum4(s4);                             // 4 lanes x 4 = 16 elements
         const float s32 = s16 + dpp_f<kDppRowHalfMirror>(s16);  // 8 lanes = 32 elements
         if (store) {
-            ((uint32_t *)X.d1)[e4] = w1;
-            ((uint32_t *)X.d2)[e4] = w2;
+            const int o = X.off(e);
+            *(uint32_t *)(X.d1 + o) = w1;
+            *(uint32_t *)(X.d2 + o) = w2;
             if ((lane & 7) == 0) {
                 X.u[e >> 5] = u;
                 X.s32[e >> 5] = s32;
@@ -227,8 +238,9 @@ __device__ __forceinline__ float q4k_dot(const RawH &r, int hf, int c, const XLd
     int I[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const int4 d1a = *(const int4 *)(X.d1 + c + 32 * t), d1b = *(const int4 *)(X.d1 + c + 32 * t + 16);
-        const int4 d2a = *(const int4 *)(X.d2 + c + 32 * t), d2b = *(const int4 *)(X.d2 + c + 32 * t + 16);
+        const int oa = X.off(c + 32 * t), ob = X.off(c + 32 * t + 16);
+        const int4 d1a = *(const int4 *)(X.d1 + oa), d1b = *(const int4 *)(X.d1 + ob);
+        const int4 d2a = *(const int4 *)(X.d2 + oa), d2b = *(const int4 *)(X.d2 + ob);
         const uint4 qa = r.q[2 * (t >> 1)], qb = r.q[2 * (t >> 1) + 1];
         const int sh = 4 * (t & 1);
         const uint32_t na[4] = {(qa.x >> sh) & 0x0F0F0F0Fu, (qa.y >> sh) & 0x0F0F0F0Fu,
@@ -284,8 +296,9 @@ __device__ __forceinline__ float q6k_dot(const RawH &r, int hf, int c, const XLd
             const uint32_t hi = (2 * g <= 4 ? (H[k] << (4 - 2 * g)) : (H[k] >> (2 * g - 4))) & 0x30303030u;
             q[k] = lo | hi;
         }
-        const int4 d1a = *(const int4 *)(X.d1 + c + 32 * g), d1b = *(const int4 *)(X.d1 + c + 32 * g + 16);
-        const int4 d2a = *(const int4 *)(X.d2 + c + 32 * g), d2b = *(const int4 *)(X.d2 + c + 32 * g + 16);
+        const int oa = X.off(c + 32 * g), ob = X.off(c + 32 * g + 16);
+        const int4 d1a = *(const int4 *)(X.d1 + oa), d1b = *(const int4 *)(X.d1 + ob);
+        const int4 d2a = *(const int4 *)(X.d2 + oa), d2b = *(const int4 *)(X.d2 + ob);
         const uint32_t qa[4] = {q[0], q[1], q[2], q[3]}, qb[4] = {q[4], q[5], q[6], q[7]};
         const int i0 = 254 * dot16(qa, d1a, 0) + dot16(qa, d2a, 0);
         const int i1 = 254 * dot16(qb, d1b, 0) + dot16(qb, d2b, 0);
@@ -464,7 +477,7 @@ int launch_gemv(GemvArgs a, hipStream_t stream) {
     for (int i = a.nmat; i < 3; i++) a.off[i] = INT_MAX;
     a.total_rows = off;
     const int passes = a.total_rows / P;
-    // One pass per wave while the whole grid fits on the chip at once (2 workgroups per
+    // One pass per wave while the whole grid fits on the chip at once (two workgroups per
     // CU), else two passes per wave; the hardware queues any further workgroups.
     const int resident = 2 * device_cus() * wpb;
     const int R = passes > resident ? 2 : 1;
