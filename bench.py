@@ -52,6 +52,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     return ap.parse_args()
 
 
@@ -143,7 +144,40 @@ def gpu_bench(args):
                 ops_ = 2.0 * M_TOK * N_ * H
                 res_g[name] = {"us": d * 1e6, "tops": ops_ / d / 1e12, "frac_int8_peak": ops_ / d / 1e12 / INT8_PEAK_TOPS}
             gemm = res_g
-    return dict(step_s=step_s, wall=wall, d_q=d_q, d_kv=d_kv, d_o=d_o, gemm=gemm)
+
+        moe = None
+        if not args.no_moe:
+            moe = moe_prefill_bench(gen, s)
+    return dict(step_s=step_s, wall=wall, d_q=d_q, d_kv=d_kv, d_o=d_o, gemm=gemm, moe=moe)
+
+
+def moe_prefill_bench(gen, stream):
+    """grouped-expert prefill, 512 tokens x top-8 of 128 experts (Zipf 1.1),
+    gate+up Q4_K 4096->1536, down Q6_K 1536->4096, router-weighted scatter-add."""
+    import numpy as np
+    import torch
+    from mnemocuda_amd import ops, synth
+    T, E, k, EFF = 512, 128, 8, 1536
+    idx, w = synth.zipf_routing(np.random.default_rng(7), T, E, k)
+    table = synth.expert_table_torch(gen, E, H, EFF, Q6K, "cuda")
+    stride, g_off, u_off, d_off = synth.expert_layout(H, EFF, Q6K)
+    x = torch.randn(T, H, device="cuda", generator=gen)
+    out = torch.zeros(T, H, device="cuda")
+    idx_d, w_d = torch.from_numpy(idx).cuda(), torch.from_numpy(w).cuda()
+    ws = torch.empty(ops.moe_prefill_workspace_bytes(T, H, EFF, E, k), dtype=torch.uint8, device="cuda")
+
+    def run(_i):
+        ops.moe_prefill(table, stride, g_off, u_off, d_off, Q6K, x, idx_d, w_d, T, H, EFF, E, k, ws, out)
+
+    for i in range(3):
+        run(i)
+    d = time_launches(run, 10, stream)
+    active = int(np.unique(idx).size)
+    flops = 2.0 * T * k * 3 * H * EFF
+    wbytes = active * (stride)
+    return {"us": round(d * 1e6, 1), "tops": round(flops / d / 1e12, 1),
+            "frac_int8_peak": round(flops / d / 1e12 / INT8_PEAK_TOPS, 4),
+            "active_experts": active, "expert_weight_GBps": round(wbytes / d / 1e9, 1)}
 
 
 def cpu_baseline(seconds):
@@ -219,6 +253,7 @@ def main():
             "per_kernel_us": {"q_proj": round(r["d_q"] * 1e6, 2), "kv_dual": round(r["d_kv"] * 1e6, 2),
                               "o_proj_res": round(r["d_o"] * 1e6, 2)},
             "gemm_q4k_m512": r["gemm"],
+            "moe_prefill_cfg4": r["moe"],
             "wall_s_timed": round(r["wall"], 3),
         },
     }

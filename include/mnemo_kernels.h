@@ -122,6 +122,25 @@ void cuda_gemm_q4k(const void *weights, const void *act_q8, float *output, int M
 void mnemo_gemm_q6k(const void *weights, const void *act_q8, float *output, int M, int K, int N,
                     hipStream_t stream);
 
+/* ---- Grouped-expert prefill (no reference counterpart) ---------------------------------
+ * The reference prefills MoE layers token by token through the decode chain
+ * (src/forward.c:1783-1830; per expert src/forward.c:876-893).  This entry point computes
+ * the same composition for T tokens at once:
+ *   out[t] += sum_slot topk_w[t][slot] * W_down[e] (silu(W_gate[e] x_t) * W_up[e] x_t),
+ *   e = topk_idx[t][slot]
+ * with x_t and the SwiGLU activations quantized to Q8_1 (the GEMM semantics above).
+ * Expert e's matrices sit at experts + e*expert_stride + {gate,up,down}_off, gate/up Q4_K
+ * [eff][hidden], down Q4_K or Q6_K [hidden][eff] (the reference's expert file layout,
+ * src/forward.c:866-872).  topk_idx / topk_w are [n_tokens][k] (cuda_topk_softmax's output
+ * per token); ids outside [0, n_experts) are skipped.  hidden, eff % 256 == 0,
+ * n_experts <= 512.  workspace: device memory of at least
+ * mnemo_moe_prefill_workspace_bytes(...) bytes, 16-byte aligned. */
+size_t mnemo_moe_prefill_workspace_bytes(int n_tokens, int hidden, int eff, int n_experts, int k);
+int mnemo_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off, size_t up_off,
+                      size_t down_off, int down_type, const float *x, const int *topk_idx,
+                      const float *topk_w, int n_tokens, int hidden, int eff, int n_experts, int k,
+                      void *workspace, size_t workspace_bytes, float *out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,18 +4,22 @@
 //   out[j*M + i] = sum_k deq(W)[i][k] * deq(A)[j][k]
 // with W GGUF blocks [M][K] and A the Q8_1 MMQ activations [N][K/128] x 144 B.
 //
-// Design: both operands are dequantised on the fly into f16 tiles in LDS and multiplied
-// with v_mfma_f32_16x16x32_f16 (fp32 accumulate).  The per-32 scales of both operands are
-// thereby folded into the values, so the MFMA accumulates across the whole K without a
-// per-sub-block fp32 rescale (an int8 MFMA would need one cvt + two FMAs per output per
-// 32-K step, several times the MFMA time in VALU work).
-//   * W value w = d*sc*q - dmin*m (Q4_K) or d*sc*(q-32) (Q6_K) is computed exactly in fp32
-//     and rounded once to f16; A value d8*q8 is formed in packed f16 arithmetic
-//     (q8 exact, one rounding of the product).  Expected relative L2 error vs the fp64
-//     product: ~4e-4 (two independent f16 roundings).
+// Design: both operands become f16 tiles in LDS multiplied with v_mfma_f32_16x16x32_f16
+// (fp32 accumulate).  The per-32 scales of both operands are folded into the values, so
+// the MFMA accumulates across the whole K without a per-sub-block fp32 rescale (an int8
+// MFMA would need one cvt + two FMAs per output per 32-K step, several times the MFMA
+// time in VALU work).
+//   * Activations are staged once per call (stage_* kernels) as f16 rows holding
+//     d8*q8*2^-e_row, e_row an exact power of two chosen per row so that the values stay
+//     inside the f16 range (127*max d8*2^-e <= 2^15); the epilogue multiplies by 2^e.  The
+//     GEMM then copies activation tiles instead of converting them once per weight tile.
+//   * Weights are dequantised on the fly in packed f16 arithmetic: a quant q placed under
+//     the exponent byte 0x64 is the f16 1024 + q; subtracting 1024 (or 1056 for Q6_K's
+//     q - 32) is exact; then one fma with (f16(d*sc), f16(-dmin*m)) (Q4_K) or one multiply
+//     by f16(d*sc) (Q6_K).  Expected relative L2 error vs the fp64 product: ~4e-4.
 //   * Workgroup tile 128 weight rows x 128 tokens (4 waves of 64 x 64 = 4 x 4 MFMA tiles),
-//     K step 64 (one Q4_K nibble group, one Q6_K ql group, half a Q8_1 block).  The raw
-//     blocks of each step are prefetched three steps ahead into registers; f16 tiles are
+//     K step 64 (one Q4_K nibble group, one Q6_K ql group).  Raw weight blocks and
+//     activation chunks are prefetched three steps ahead into registers; f16 tiles are
 //     double-buffered in LDS (XOR-swizzled, conflict-free); one barrier per step.
 //   * When the tile grid covers less than half of the CUs, K is split across workgroups
 //     and the partial tiles are summed with fp32 atomics into the output, which a small
@@ -46,8 +50,7 @@ struct RawW {
     uint32_t s, dd;    // Q6_K: two int8 scales, f16 d
 };
 struct RawA {
-    uint4 a, b;   // 32 int8
-    uint32_t ds;  // half2 (d, d*sum)
+    uint4 a, b, c, d;  // 32 f16 activation values
 };
 
 // Q4_K step ks = super-block ks/4, nibble group g = ks%4 (qs bytes 32g..32g+31); half h
@@ -76,13 +79,13 @@ __device__ __forceinline__ void load_w_q6k(const uint8_t *__restrict__ wrow, int
 }
 
 // Activations of step ks, half h: values 64ks + 32h .. +31 = one Q8_1 sub-block.
-__device__ __forceinline__ void load_a(const uint8_t *__restrict__ arow, int ks, int h, RawA &r) {
-    const int v0 = ks * kKS + 32 * h;
-    const uint8_t *blk = arow + (size_t)(v0 >> 7) * kQ81Bytes;
-    const int sub = (v0 >> 5) & 3;
-    r.ds = *(const uint32_t *)(blk + 4 * sub);
-    r.a = ld16(blk + 16 + 32 * sub);
-    r.b = ld16(blk + 32 + 32 * sub);
+// Half h of step ks: f16 activations ks*64 + 32h .. +31 of the staged row.
+__device__ __forceinline__ void load_a(const _Float16 *__restrict__ arow, int ks, int h, RawA &r) {
+    const _Float16 *p = arow + ks * kKS + 32 * h;
+    r.a = ld16((const uint8_t *)(p));
+    r.b = ld16((const uint8_t *)(p + 8));
+    r.c = ld16((const uint8_t *)(p + 16));
+    r.d = ld16((const uint8_t *)(p + 24));
 }
 
 // ------------------------------------------------------------------ LDS tiles
@@ -97,6 +100,16 @@ __device__ __forceinline__ void put16(_Float16 *tile, int row, int chunk, uint32
 }
 
 // ------------------------------------------------------------------ conversion to LDS
+// Two byte-sized quants (bytes selected by `sel` from v) as the f16 pair 1024 + q.
+__device__ __forceinline__ h2 magic_pair(uint32_t v, uint32_t sel) {
+    return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, sel));
+}
+// (q - 1024 + 1024) * a + b for two quants, in packed f16 (exact subtraction, one rounding)
+__device__ __forceinline__ uint32_t dq_fma(uint32_t v, uint32_t sel, h2 a, h2 b) {
+    const h2 off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2 q = magic_pair(v, sel) + off;
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a, b));
+}
 // Q4_K: half h of step ks holds 16 weights of sub-block 2g (K columns 16h .. 16h+15 of the
 // step: chunks 2h, 2h+1) and 16 of sub-block 2g+1 (columns 32+16h ..: chunks 4+2h, 5+2h).
 __device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int h, _Float16 *tile, int row) {
@@ -115,18 +128,18 @@ __device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int h, _Float
         m1 = ((s2 >> (sh + 12)) & 15) | (((s1 >> (sh + 14)) & 3) << 4);
     }
     const float d = h2f(r.a.x & 0xFFFFu), dmin = h2f(r.a.x >> 16);
-    const float a0 = d * (float)sc0, b0 = dmin * (float)m0;
-    const float a1 = d * (float)sc1, b1 = dmin * (float)m1;
+    const _Float16 a0 = (_Float16)(d * (float)sc0), b0 = (_Float16)(-dmin * (float)m0);
+    const _Float16 a1 = (_Float16)(d * (float)sc1), b1 = (_Float16)(-dmin * (float)m1);
+    const h2 A0 = {a0, a0}, B0 = {b0, b0}, A1 = {a1, a1}, B1 = {b1, b1};
     const uint32_t w[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
     uint32_t lo[8], hi[8];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const uint32_t ml = w[k] & 0x0F0F0F0Fu, mh = (w[k] >> 4) & 0x0F0F0F0Fu;
-        // (float)(byte j of a masked dword) compiles to v_cvt_f32_ubyte{j}
-        lo[2 * k] = pack_h2(fmaf(a0, (float)(ml & 0xFF), -b0), fmaf(a0, (float)((ml >> 8) & 0xFF), -b0));
-        lo[2 * k + 1] = pack_h2(fmaf(a0, (float)((ml >> 16) & 0xFF), -b0), fmaf(a0, (float)(ml >> 24), -b0));
-        hi[2 * k] = pack_h2(fmaf(a1, (float)(mh & 0xFF), -b1), fmaf(a1, (float)((mh >> 8) & 0xFF), -b1));
-        hi[2 * k + 1] = pack_h2(fmaf(a1, (float)((mh >> 16) & 0xFF), -b1), fmaf(a1, (float)(mh >> 24), -b1));
+        lo[2 * k] = dq_fma(ml, 0x04010400u, A0, B0);
+        lo[2 * k + 1] = dq_fma(ml, 0x04030402u, A0, B0);
+        hi[2 * k] = dq_fma(mh, 0x04010400u, A1, B1);
+        hi[2 * k + 1] = dq_fma(mh, 0x04030402u, A1, B1);
     }
     put16(tile, row, 2 * h, lo[0], lo[1], lo[2], lo[3]);
     put16(tile, row, 2 * h + 1, lo[4], lo[5], lo[6], lo[7]);
@@ -138,7 +151,9 @@ __device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int h, _Float
 __device__ __forceinline__ void store_w_q6k(const RawW &r, int ks, int h, _Float16 *tile, int row) {
     const int grp = 2 * (ks & 1) + h;
     const float d = h2f(r.dd);
-    const float s0 = d * (float)(int8_t)(r.s & 0xFF), s1 = d * (float)(int8_t)(r.s >> 8);
+    const _Float16 s0 = (_Float16)(d * (float)(int8_t)(r.s & 0xFF)), s1 = (_Float16)(d * (float)(int8_t)(r.s >> 8));
+    const h2 S0 = {s0, s0}, S1 = {s1, s1};
+    const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
     const uint32_t ql[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
     const uint32_t qh[8] = {r.c.x, r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w};
     const int shl = grp >= 2 ? 4 : 0;
@@ -149,34 +164,20 @@ __device__ __forceinline__ void store_w_q6k(const RawW &r, int ks, int h, _Float
         const uint32_t lo = (ql[k] >> shl) & 0x0F0F0F0Fu;
         const uint32_t hi = (2 * grp <= 4 ? (qh[k] << (4 - 2 * grp)) : (qh[k] >> (2 * grp - 4))) & 0x30303030u;
         const uint32_t q = lo | hi;
-        const float s = k < 4 ? s0 : s1;
-        o[2 * k] = pack_h2(s * (float)((int)(q & 0xFF) - 32), s * (float)((int)((q >> 8) & 0xFF) - 32));
-        o[2 * k + 1] = pack_h2(s * (float)((int)((q >> 16) & 0xFF) - 32), s * (float)((int)(q >> 24) - 32));
+        const h2 S = k < 4 ? S0 : S1;
+        o[2 * k] = __builtin_bit_cast(uint32_t, (magic_pair(q, 0x04010400u) + off) * S);
+        o[2 * k + 1] = __builtin_bit_cast(uint32_t, (magic_pair(q, 0x04030402u) + off) * S);
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) put16(tile, row, 4 * h + k, o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
 }
 
-// d8 * q8 in packed f16: q8 ^ 0x80 placed under the exponent byte 0x64 is 1024 + q8 + 128
-// exactly; subtracting 1152 gives q8 exactly; the product with d8 is rounded once.
-// Half h: K columns 32h .. 32h+31 (chunks 4h .. 4h+3).
+// Half h: K columns 32h .. 32h+31 (chunks 4h .. 4h+3) of the staged activation row.
 __device__ __forceinline__ void store_a(const RawA &r, int h, _Float16 *tile, int row) {
-    const h2 d2 = {__builtin_bit_cast(_Float16, (uint16_t)(r.ds & 0xFFFF)),
-                   __builtin_bit_cast(_Float16, (uint16_t)(r.ds & 0xFFFF))};
-    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-    uint32_t o[16];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const uint32_t u = w[k] ^ 0x80808080u;
-        const uint32_t e01 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [u0, 64, u1, 64]
-        const uint32_t e23 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [u2, 64, u3, 64]
-        const h2 q01 = __builtin_bit_cast(h2, e01) + off, q23 = __builtin_bit_cast(h2, e23) + off;
-        o[2 * k] = __builtin_bit_cast(uint32_t, q01 * d2);
-        o[2 * k + 1] = __builtin_bit_cast(uint32_t, q23 * d2);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) put16(tile, row, 4 * h + k, o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+    put16(tile, row, 4 * h, r.a.x, r.a.y, r.a.z, r.a.w);
+    put16(tile, row, 4 * h + 1, r.b.x, r.b.y, r.b.z, r.b.w);
+    put16(tile, row, 4 * h + 2, r.c.x, r.c.y, r.c.z, r.c.w);
+    put16(tile, row, 4 * h + 3, r.d.x, r.d.y, r.d.z, r.d.w);
 }
 
 // ------------------------------------------------------------------ kernel
@@ -192,7 +193,7 @@ constexpr int kBM = 128, kBN = 128;
 constexpr int kPF = 4;
 
 template <int TYPE>
-__device__ __forceinline__ void load_step(const uint8_t *wrow, const uint8_t *arow, int ks, int h, RawW &rw,
+__device__ __forceinline__ void load_step(const uint8_t *wrow, const _Float16 *arow, int ks, int h, RawW &rw,
                                           RawA &ra) {
     if (TYPE == kTypeQ4K) load_w_q4k(wrow, ks, h, rw);
     else load_w_q6k(wrow, ks, h, rw);
@@ -227,27 +228,79 @@ __device__ __forceinline__ void mfma_step(const _Float16 *as, const _Float16 *bs
     }
 }
 
-template <int TYPE, bool ATOMIC>
-__global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(const uint8_t *__restrict__ W,
-                                                              const uint8_t *__restrict__ A,
-                                                              float *__restrict__ out, int M, int K, int N,
-                                                              int splits) {
+// Epilogue / operand-addressing modes of the kernel:
+//   kModePlain   : W [M][K], activations rows j = token, out[j*M + i] (column-major [N][M])
+//   kModeSwiGLU  : grouped experts; a tile covers 64 features with 64 gate rows and 64 up
+//                  rows interleaved; activation rows are tokens gathered through perm[];
+//                  out[q*ld + f] = silu(gate) * up for expert-sorted row q
+//   kModeGrouped : grouped experts; activation rows are the expert-sorted rows q themselves;
+//                  out[q*ld + i]
+enum GemmMode : int { kModePlain = 0, kModeSwiGLU = 1, kModeGrouped = 2 };
+
+struct GemmArgs {
+    const uint8_t *W;  // plain: weights; grouped: expert table base
+    const _Float16 *A;       // staged activation rows (K values each)
+    const float *a_unscale;  // per staged row: 2^e
+    float *out;
+    int M, K, N, splits;
+    int out_ld;
+    // grouped modes
+    size_t expert_stride, w_off, w_off2;  // expert e's matrix at W + e*stride + w_off (up: w_off2)
+    const int *counts;                   // [n_experts] rows per expert
+    const int *offsets;                  // [n_experts] first expert-sorted row
+    const int *perm;                     // [rows] expert-sorted row -> token (SwiGLU gather)
+    const int *tiles;                    // [max_tiles] (expert << 16) | n_tile; tiles[-1] = count
+};
+
+template <int TYPE, int MODE, bool ATOMIC>
+__global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     __shared__ __align__(16) _Float16 lds[2][2][kBM * kKS];  // [buffer][weights | tokens]
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int i0 = blockIdx.x * kBM, j0 = blockIdx.y * kBN;
+    const int K = g.K;
     const int wi = (wave & 1) * 64, wj = (wave >> 1) * 64;
     const size_t wrow_bytes = (size_t)(K / 256) * (TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
-    const size_t arow_bytes = (size_t)(K / 128) * kQ81Bytes;
     const int nks_all = K / kKS;
-    const int ks0 = (int)((long)nks_all * blockIdx.z / splits);
-    const int ks1 = (int)((long)nks_all * (blockIdx.z + 1) / splits);
+    const int ks0 = (int)((long)nks_all * blockIdx.z / g.splits);
+    const int ks1 = (int)((long)nks_all * (blockIdx.z + 1) / g.splits);
     const int last = ks1 - 1;
 
-    // loader role: thread -> (row/token lr, half lh); rows past the end re-read the last
+    // tile coordinates: weights i0 (features for SwiGLU), activation rows j0 .. j0+127 of
+    // [row_base, row_base + n_rows)
+    int i0, j0, n_rows, row_base = 0;
+    const uint8_t *Wm = g.W, *Wm2 = g.W;
+    if (MODE == kModePlain) {
+        i0 = blockIdx.x * kBM;
+        j0 = blockIdx.y * kBN;
+        n_rows = g.N;
+    } else {
+        if ((int)blockIdx.y >= g.tiles[-1]) return;  // uniform: past the tile list
+        const int t = g.tiles[blockIdx.y];
+        const int e = t >> 16, nt = t & 0xFFFF;
+        n_rows = g.counts[e];
+        row_base = g.offsets[e];
+        j0 = nt * kBN;
+        i0 = blockIdx.x * (MODE == kModeSwiGLU ? kBM / 2 : kBM);
+        Wm = g.W + (size_t)e * g.expert_stride + g.w_off;
+        Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
+    }
+
+    // loader role: thread -> (LDS row lr, half lh); rows past the end re-read the last
     const int lr = tid >> 1, lh = tid & 1;
-    const uint8_t *wrow = W + (size_t)min(i0 + lr, M - 1) * wrow_bytes;
-    const uint8_t *arow = A + (size_t)min(j0 + lr, N - 1) * arow_bytes;
+    const uint8_t *wrow;
+    if (MODE == kModeSwiGLU) {
+        // LDS rows 64w .. 64w+31 = gate features i0 + 32w + (0..31), 64w+32 .. = up features
+        const int w = lr >> 6, rr = lr & 63;
+        const int f = min(i0 + 32 * w + (rr & 31), g.M - 1);
+        wrow = (rr < 32 ? Wm : Wm2) + (size_t)f * wrow_bytes;
+    } else {
+        wrow = Wm + (size_t)min(i0 + lr, g.M - 1) * wrow_bytes;
+    }
+    const int jr = min(j0 + lr, n_rows - 1);
+    const int arow_idx = MODE == kModePlain ? jr : MODE == kModeSwiGLU ? g.perm[row_base + jr] : row_base + jr;
+    const _Float16 *arow = g.A + (size_t)arow_idx * K;
+    __shared__ float row_unscale[kBN];
+    if (lh == 0) row_unscale[lr] = g.a_unscale[arow_idx];
 
     f4 acc[4][4];
 #pragma unroll
@@ -280,27 +333,175 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(const uint8_t *__re
         }
     }
     // D layout (16x16 f32): lane l holds rows 4*(l/16)+e, column l%16.  Rows index
-    // weights i (A operand), columns tokens j (B operand).
+    // weights (A operand), columns activation rows (B operand).
+    if (MODE == kModeSwiGLU) {
+        // gate tile a pairs with up tile a+2: feature i0 + 32*(wave&1) + 16a + 4*(l/16) + e
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int j = j0 + wj + 16 * b + (lane & 15);
+                const int f = i0 + 32 * (wave & 1) + 16 * a + 4 * (lane >> 4);
+                if (j >= n_rows) continue;
+                const float us = row_unscale[wj + 16 * b + (lane & 15)];
+                float *o = g.out + (size_t)(row_base + j) * g.out_ld + f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float gt = acc[a][b][e] * us, up = acc[a + 2][b][e] * us;
+                    if (f + e < g.M) o[e] = gt / (1.0f + expf(-gt)) * up;
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             const int j = j0 + wj + 16 * b + (lane & 15);
             const int ib = i0 + wi + 16 * a + 4 * (lane >> 4);
-            if (j >= N) continue;
-            float *o = out + (size_t)j * M + ib;
+            if (j >= n_rows) continue;
+            const float us = row_unscale[wj + 16 * b + (lane & 15)];
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[a][b][e] *= us;
+            float *o = g.out + (size_t)(row_base + j) * g.out_ld + ib;
             if (ATOMIC) {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    if (ib + e < M) __hip_atomic_fetch_add(o + e, acc[a][b][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else if (ib + 3 < M && ((M & 3) == 0)) {
+                    if (ib + e < g.M) __hip_atomic_fetch_add(o + e, acc[a][b][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else if (ib + 3 < g.M && ((g.out_ld & 3) == 0)) {
                 *(f4 *)o = acc[a][b];
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
-                    if (ib + e < M) o[e] = acc[a][b][e];
+                    if (ib + e < g.M) o[e] = acc[a][b][e];
             }
         }
+}
+
+// ------------------------------------------------------------------ activation staging
+// One wave per activation row, 4 rows per 256-thread block.
+constexpr int kStageThreads = 256;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Row exponent e >= 0 with 127 * dmax * 2^-e <= 2^15 (dmax = largest |d8| of the row).
+__device__ __forceinline__ int row_exponent(float dmax) {
+    int ex = 0;
+    frexpf(dmax * 127.0f, &ex);  // 127 * dmax < 2^ex
+    return max(0, ex - 15);
+}
+
+// 8 int8 quants (two dwords) times the f16 scale d: q8 ^ 0x80 under the exponent byte 0x64
+// is 1024 + q8 + 128 exactly; subtracting 1152 gives q8; the product is rounded once.
+__device__ __forceinline__ void q8x4_to_f16(uint32_t v, h2 d2, uint32_t &o0, uint32_t &o1) {
+    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t u = v ^ 0x80808080u;
+    o0 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04010400u) + off) * d2);
+    o1 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04030402u) + off) * d2);
+}
+
+// Q8_1 MMQ rows [N][K/128] x 144 B -> f16 rows d8*q8*2^-e, unscale[row] = 2^e.
+__global__ void __launch_bounds__(kStageThreads) stage_q8_1_kernel(const uint8_t *__restrict__ A, int K, int N,
+                                                                   _Float16 *__restrict__ out,
+                                                                   float *__restrict__ unscale) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kStageThreads / 64) + (threadIdx.x >> 6);
+    if (row >= N) return;
+    const uint8_t *ar = A + (size_t)row * (K / 128) * kQ81Bytes;
+    float dmax = 0.0f;
+    for (int b = lane; b < K / 128; b += 64) {
+        const uint4 hd = ld16(ar + (size_t)b * kQ81Bytes);
+        dmax = fmaxf(dmax, fmaxf(fmaxf(fabsf(h2f(hd.x & 0xFFFF)), fabsf(h2f(hd.y & 0xFFFF))),
+                                 fmaxf(fabsf(h2f(hd.z & 0xFFFF)), fabsf(h2f(hd.w & 0xFFFF)))));
+    }
+    const int e = row_exponent(wave_max(dmax));
+    const float as = ldexpf(1.0f, -e);
+    if (lane == 0) unscale[row] = ldexpf(1.0f, e);
+    _Float16 *orow = out + (size_t)row * K;
+    for (int c = lane; c < K / 16; c += 64) {  // 16 values per chunk
+        const uint8_t *blk = ar + (size_t)(c >> 3) * kQ81Bytes;
+        uint16_t dbits;
+        __builtin_memcpy(&dbits, blk + 4 * ((c & 7) >> 1), 2);
+        const _Float16 d = (_Float16)(h2f(dbits) * as);  // exact: power-of-two scaling
+        const h2 d2 = {d, d};
+        const uint4 q = ld16(blk + 16 + 16 * (c & 7));
+        uint4 o0, o1;
+        q8x4_to_f16(q.x, d2, o0.x, o0.y);
+        q8x4_to_f16(q.y, d2, o0.z, o0.w);
+        q8x4_to_f16(q.z, d2, o1.x, o1.y);
+        q8x4_to_f16(q.w, d2, o1.z, o1.w);
+        *(uint4 *)(orow + 16 * c) = o0;
+        *(uint4 *)(orow + 16 * c + 8) = o1;
+    }
+}
+
+// fp32 rows [N][K] -> the same staged form as stage_q8_1_kernel applied to
+// cuda_quantize_mmq_q8_1's output: per 32 values d = f16(amax/127), q = rint(x*127/amax)
+// clamped to +-127 (gemm_q4k.cu:327-358), staged value f16(d*2^-e) * q.
+__global__ void __launch_bounds__(kStageThreads) stage_f32_kernel(const float *__restrict__ x, int K, int N,
+                                                                  _Float16 *__restrict__ out,
+                                                                  float *__restrict__ unscale) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (kStageThreads / 64) + (threadIdx.x >> 6);
+    if (row >= N) return;
+    const float4 *xr = (const float4 *)(x + (size_t)row * K);
+    float dmax = 0.0f;
+    for (int b = lane; b < K / 32; b += 64) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = xr[8 * b + i];
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        float d = amax / 127.0f;
+        asm volatile("" : "+v"(d));  // round d to fp32 before the f16 conversion
+        dmax = fmaxf(dmax, (float)(_Float16)d);
+    }
+    const int e = row_exponent(wave_max(dmax));
+    const float as = ldexpf(1.0f, -e);
+    if (lane == 0) unscale[row] = ldexpf(1.0f, e);
+    _Float16 *orow = out + (size_t)row * K;
+    for (int b = lane; b < K / 32; b += 64) {
+        float xv[32];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 v = xr[8 * b + i];
+            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        float d = amax / 127.0f;
+        asm volatile("" : "+v"(d));
+        const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
+        const _Float16 ds = (_Float16)((float)(_Float16)d * as);
+        uint32_t o[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float r0 = fminf(fmaxf(rintf(xv[2 * i] * id), -127.0f), 127.0f);
+            const float r1 = fminf(fmaxf(rintf(xv[2 * i + 1] * id), -127.0f), 127.0f);
+            const h2 q = {(_Float16)r0, (_Float16)r1};
+            const h2 d2 = {ds, ds};
+            o[i] = __builtin_bit_cast(uint32_t, q * d2);
+        }
+        uint4 *dst = (uint4 *)(orow + 32 * b);
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
+}
+
+int launch_stage_q8_1(const void *act, int K, int N, _Float16 *out, float *unscale, hipStream_t s) {
+    hipLaunchKernelGGL(stage_q8_1_kernel, dim3((N + 3) / 4), dim3(kStageThreads), 0, s, (const uint8_t *)act, K, N,
+                       out, unscale);
+    return check_launch("stage_q8_1");
+}
+
+int launch_stage_f32(const float *x, int K, int N, _Float16 *out, float *unscale, hipStream_t s) {
+    hipLaunchKernelGGL(stage_f32_kernel, dim3((N + 3) / 4), dim3(kStageThreads), 0, s, x, K, N, out, unscale);
+    return check_launch("stage_f32");
 }
 
 __global__ void zero_kernel(float4 *__restrict__ p, long n4) {
@@ -321,6 +522,19 @@ static int device_cus_gemm() {
     return cus;
 }
 
+template <int MODE>
+static void launch_mode(int type, bool atomic, dim3 grid, const GemmArgs &g, hipStream_t stream) {
+#define MNEMO_GEMM_LAUNCH(T_, A_) hipLaunchKernelGGL((gemm_q8_1_kernel<T_, MODE, A_>), grid, dim3(kThreads), 0, stream, g)
+    if (type == kTypeQ4K) {
+        if (atomic) MNEMO_GEMM_LAUNCH(kTypeQ4K, true);
+        else MNEMO_GEMM_LAUNCH(kTypeQ4K, false);
+    } else {
+        if (atomic) MNEMO_GEMM_LAUNCH(kTypeQ6K, true);
+        else MNEMO_GEMM_LAUNCH(kTypeQ6K, false);
+    }
+#undef MNEMO_GEMM_LAUNCH
+}
+
 int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M, int K, int N,
                      hipStream_t stream) {
     if (!w || !act || !out || M <= 0 || N <= 0 || K <= 0 || K % 256 != 0)
@@ -334,26 +548,66 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
     const int nks = K / kKS;
     int splits = 1;
     while (2 * tm * tn * splits < device_cus_gemm() && nks / (splits * 2) >= 16) splits *= 2;
-    const size_t lds = 0;
-    dim3 grid(tm, tn, splits);
-    if (splits > 1) {
+    if (((long)M * N) % 4 != 0) splits = 1;  // the fill kernel clears float4s
+    // stage the activations (stream-ordered scratch: N*K f16 + N unscale factors)
+    const size_t a16_bytes = ((size_t)N * K * 2 + 255) & ~(size_t)255;
+    void *stage = nullptr;
+    if (hipMallocAsync(&stage, a16_bytes + (size_t)N * 4, stream) != hipSuccess || !stage) {
+        (void)hipGetLastError();
+        return set_error(kErrLaunch, "gemm: cannot allocate %zu bytes of staging memory", a16_bytes + (size_t)N * 4);
+    }
+    _Float16 *a16 = (_Float16 *)stage;
+    float *unscale = (float *)((uint8_t *)stage + a16_bytes);
+    int rc = launch_stage_q8_1(act, K, N, a16, unscale, stream);
+    GemmArgs g{};
+    g.W = (const uint8_t *)w;
+    g.A = a16;
+    g.a_unscale = unscale;
+    g.out = out;
+    g.M = M;
+    g.K = K;
+    g.N = N;
+    g.splits = splits;
+    g.out_ld = M;
+    if (!rc && splits > 1) {
         const long n = (long)M * N;
-        if (n % 4 != 0) return set_error(kErrBadArg, "gemm: M*N must be a multiple of 4 for split-K");
         hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<long>((n / 4 + 255) / 256, 4096)), dim3(256), 0,
                            stream, (float4 *)out, n / 4);
     }
-#define MNEMO_GEMM_LAUNCH(T_, A_)                                                                          \
-    hipLaunchKernelGGL((gemm_q8_1_kernel<T_, A_>), grid, dim3(kThreads), lds, stream, (const uint8_t *)w, \
-                       (const uint8_t *)act, out, M, K, N, splits)
-    if (type == kTypeQ4K) {
-        if (splits > 1) MNEMO_GEMM_LAUNCH(kTypeQ4K, true);
-        else MNEMO_GEMM_LAUNCH(kTypeQ4K, false);
-    } else {
-        if (splits > 1) MNEMO_GEMM_LAUNCH(kTypeQ6K, true);
-        else MNEMO_GEMM_LAUNCH(kTypeQ6K, false);
+    if (!rc) {
+        launch_mode<kModePlain>(type, splits > 1, dim3(tm, tn, splits), g, stream);
+        rc = check_launch("gemm_q8_1");
     }
-#undef MNEMO_GEMM_LAUNCH
-    return check_launch("gemm_q8_1");
+    (void)hipFreeAsync(stage, stream);
+    return rc;
+}
+
+// Grouped launches used by the MoE prefill path (moe.hip): tiles[] and the routing arrays
+// live in device memory, the grid covers max_tiles tile-list entries.
+int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert_stride, size_t w_off,
+                        size_t w_off2, const _Float16 *act, const float *act_unscale, const int *counts, const int *offsets, const int *perm,
+                        const int *tiles, int max_tiles, float *out, int out_ld, int M, int K,
+                        hipStream_t stream) {
+    GemmArgs g{};
+    g.W = (const uint8_t *)experts;
+    g.A = act;
+    g.a_unscale = act_unscale;
+    g.out = out;
+    g.M = M;
+    g.K = K;
+    g.N = 0;
+    g.splits = 1;
+    g.out_ld = out_ld;
+    g.expert_stride = expert_stride;
+    g.w_off = w_off;
+    g.w_off2 = w_off2;
+    g.counts = counts;
+    g.offsets = offsets;
+    g.perm = perm;
+    g.tiles = tiles;
+    if (swiglu) launch_mode<kModeSwiGLU>(type, false, dim3((M + kBM / 2 - 1) / (kBM / 2), max_tiles, 1), g, stream);
+    else launch_mode<kModeGrouped>(type, false, dim3((M + kBM - 1) / kBM, max_tiles, 1), g, stream);
+    return check_launch("gemm_grouped");
 }
 
 }  // namespace mnemo

@@ -1,0 +1,232 @@
+// moe.hip -- grouped-expert prefill: route T tokens x k experts into expert-sorted rows,
+// run every active expert's gate+up (SwiGLU fused) and down projections as grouped
+// Q4_K/Q6_K x Q8_1 GEMMs, then scatter-add the router-weighted rows back per token.
+//
+// The reference has no batched MoE path: its prefill runs the decode chain token by
+// token (src/forward.c:1783-1830), i.e. per token and selected expert
+//   gate = W_g x, up = W_u x (Q4_K, src/forward.c:876-882)
+//   act = silu(gate) * up (src/kernels.cu:1310-1313)
+//   out += w_slot * W_d act (Q4_K or Q6_K down, src/forward.c:884-893)
+// This file computes the same composition with the activations quantized to Q8_1 blocks
+// (x once per token, act once per token-expert pair), the semantics the GEMMs implement;
+// the quantized rows are staged directly in the GEMM's f16 operand form.
+//
+// Workspace layout (each part 256-byte aligned), sizes for T tokens, k slots, E experts:
+//   xs      T staged rows of x: f16 values of Q8_1(x) scaled by 2^-e_row; xun: 2^e_row
+//   counts  E ints, offsets E ints
+//   rank    T*k ints   (rank of a pair within its expert; -1 for dropped slots)
+//   inv     T*k ints   (pair -> expert-sorted row, -1 for dropped slots)
+//   perm    T*k ints   (expert-sorted row -> token)
+//   tiles   1 + E + ceil(T*k/128) ints (count, then (expert << 16) | token tile)
+//   act     T*k rows of eff fp32 (SwiGLU output)
+//   acts    T*k staged rows of Q8_1(act), actun: their 2^e_row
+//   down    T*k rows of hidden fp32
+#include <algorithm>
+
+#include "mnemo_common.hpp"
+#include "mnemo_internal.hpp"
+
+namespace mnemo {
+
+int launch_stage_f32(const float *x, int K, int N, _Float16 *out, float *unscale, hipStream_t s);
+int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert_stride, size_t w_off,
+                        size_t w_off2, const _Float16 *act, const float *act_unscale, const int *counts,
+                        const int *offsets, const int *perm, const int *tiles, int max_tiles, float *out,
+                        int out_ld, int M, int K, hipStream_t stream);
+
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / 64;
+constexpr int kMaxMoeExperts = 512;
+constexpr int kMoeTileRows = 128;  // token rows per GEMM tile (kBN of gemm.hip)
+
+struct MoeLayout {
+    size_t xs, xun, counts, offsets, rank, inv, perm, tiles, act, acts, actun, down, total;
+    int max_tiles;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static MoeLayout moe_layout(int T, int hidden, int eff, int E, int k) {
+    MoeLayout L{};
+    const size_t pairs = (size_t)T * k;
+    L.max_tiles = E + (int)((pairs + kMoeTileRows - 1) / kMoeTileRows);
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        size_t at = o;
+        o = align256(o + bytes);
+        return at;
+    };
+    L.xs = take((size_t)T * hidden * 2);
+    L.xun = take((size_t)T * 4);
+    L.counts = take((size_t)E * 4);
+    L.offsets = take((size_t)E * 4);
+    L.rank = take(pairs * 4);
+    L.inv = take(pairs * 4);
+    L.perm = take(pairs * 4);
+    L.tiles = take((size_t)(1 + L.max_tiles) * 4);
+    L.act = take(pairs * eff * 4);
+    L.acts = take(pairs * eff * 2);
+    L.actun = take(pairs * 4);
+    L.down = take(pairs * hidden * 4);
+    L.total = o;
+    return L;
+}
+
+// Wave-wide "match any": mask of the lanes whose value equals this lane's (v < 2^bits).
+__device__ inline uint64_t match_mask(int v, int bits) {
+    uint64_t m = ~0ull;
+    for (int b = 0; b < bits; b++) {
+        const bool bit = (v >> b) & 1;
+        const uint64_t bal = __ballot(bit);
+        m &= bit ? bal : ~bal;
+    }
+    return m;
+}
+
+// One block of 1024 threads.  Pass 1 walks the pairs in chunks of 1024 (pair order = token
+// major, slot minor) and gives each pair its rank among the earlier pairs of the same
+// expert, so the expert-sorted order is deterministic: token ascending within an expert.
+// Pass 2 scans the counts, places the pairs and writes the tile list.
+__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const int *__restrict__ topk_idx, int pairs, int E,
+                                                                  int bits, int *__restrict__ counts,
+                                                                  int *__restrict__ offsets, int *__restrict__ rank,
+                                                                  int *__restrict__ inv, int *__restrict__ perm,
+                                                                  int *__restrict__ tiles, int k) {
+    __shared__ int running[kMaxMoeExperts];
+    __shared__ int wave_cnt[kRouteWaves][kMaxMoeExperts];
+    __shared__ int tile_base[kMaxMoeExperts];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < E; e += kRouteThreads) running[e] = 0;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+
+    for (int c0 = 0; c0 < pairs; c0 += kRouteThreads) {
+        for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wave_cnt[i / E][i % E] = 0;
+        __syncthreads();
+        const int p = c0 + tid;
+        int e = p < pairs ? topk_idx[p] : -1;
+        if (e >= E) e = -1;  // out-of-range expert ids are dropped like empty slots
+        const int key = e < 0 ? E : e;  // E = "dropped" bucket, matched like any value
+        const uint64_t m = match_mask(key, bits);
+        const int r_wave = __popcll(m & lt);
+        if (e >= 0 && r_wave == 0) wave_cnt[wave][e] = __popcll(m);
+        __syncthreads();
+        if (e >= 0) {
+            int r = running[e] + r_wave;
+            for (int w = 0; w < wave; w++) r += wave_cnt[w][e];
+            rank[p] = r;
+        } else if (p < pairs) {
+            rank[p] = -1;
+        }
+        __syncthreads();
+        for (int ex = tid; ex < E; ex += kRouteThreads) {
+            int s = 0;
+            for (int w = 0; w < kRouteWaves; w++) s += wave_cnt[w][ex];
+            running[ex] += s;
+        }
+        __syncthreads();
+    }
+    // exclusive scans of counts and of tiles per expert (E <= 512: one thread does it)
+    if (tid == 0) {
+        int acc = 0, tacc = 0;
+        for (int ex = 0; ex < E; ex++) {
+            const int c = running[ex];
+            counts[ex] = c;
+            offsets[ex] = acc;
+            tile_base[ex] = tacc;
+            acc += c;
+            tacc += (c + kMoeTileRows - 1) / kMoeTileRows;
+        }
+        tiles[0] = tacc;
+    }
+    __syncthreads();
+    for (int ex = 0; ex < E; ex++) {  // tiles of each expert, in expert order
+        const int nt = (running[ex] + kMoeTileRows - 1) / kMoeTileRows;
+        for (int j = tid; j < nt; j += kRouteThreads) tiles[1 + tile_base[ex] + j] = (ex << 16) | j;
+    }
+    for (int p = tid; p < pairs; p += kRouteThreads) {
+        const int r = rank[p];
+        if (r < 0) {
+            inv[p] = -1;
+            continue;
+        }
+        const int q = offsets[topk_idx[p]] + r;
+        inv[p] = q;
+        perm[q] = p / k;
+    }
+}
+
+// out[t][i] += sum over slots (in slot order) of w[t][slot] * down[inv[t][slot]][i]
+__global__ void __launch_bounds__(256) moe_combine_kernel(const float *__restrict__ down, const int *__restrict__ inv,
+                                                          const float *__restrict__ topk_w, float *__restrict__ out,
+                                                          int T, int hidden, int k) {
+    const long n4 = (long)T * hidden / 4;
+    const int h4 = hidden / 4;
+    for (long v = (long)blockIdx.x * blockDim.x + threadIdx.x; v < n4; v += (long)gridDim.x * blockDim.x) {
+        const int t = (int)(v / h4), i4 = (int)(v % h4);
+        float4 acc = ((float4 *)out)[v];
+        for (int s = 0; s < k; s++) {
+            const int q = inv[t * k + s];
+            if (q < 0) continue;
+            const float w = topk_w[t * k + s];
+            const float4 d = ((const float4 *)(down + (size_t)q * hidden))[i4];
+            acc.x += w * d.x;
+            acc.y += w * d.y;
+            acc.z += w * d.z;
+            acc.w += w * d.w;
+        }
+        ((float4 *)out)[v] = acc;
+    }
+}
+
+size_t moe_prefill_workspace_bytes(int T, int hidden, int eff, int E, int k) {
+    if (T <= 0 || hidden <= 0 || eff <= 0 || E <= 0 || k <= 0) return 0;
+    return moe_layout(T, hidden, eff, E, k).total;
+}
+
+int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off, size_t up_off, size_t down_off,
+                       int down_type, const float *x, const int *topk_idx, const float *topk_w, int T, int hidden,
+                       int eff, int E, int k, void *ws, size_t ws_bytes, float *out, hipStream_t s) {
+    if (!experts || !x || !topk_idx || !topk_w || !ws || !out || T <= 0 || k <= 0 || k > 64 || E <= 0)
+        return set_error(kErrBadArg, "moe_prefill: null pointer or non-positive size");
+    if (E > kMaxMoeExperts) return set_error(kErrBadArg, "moe_prefill: at most %d experts", kMaxMoeExperts);
+    if (hidden % 256 != 0 || eff % 256 != 0)
+        return set_error(kErrBadArg, "moe_prefill: hidden and eff must be multiples of 256");
+    if ((long)T * k > (long)1 << 24) return set_error(kErrBadArg, "moe_prefill: too many token-expert pairs");
+    if (down_type != kTypeQ4K && down_type != kTypeQ6K)
+        return set_error(kErrUnsupportedType, "moe_prefill: unsupported down type %d", down_type);
+    if ((((uintptr_t)ws | (uintptr_t)x | (uintptr_t)out) & 15) != 0)
+        return set_error(kErrBadArg, "moe_prefill: workspace, x and out must be 16-byte aligned");
+    const MoeLayout L = moe_layout(T, hidden, eff, E, k);
+    if (ws_bytes < L.total)
+        return set_error(kErrBadArg, "moe_prefill: workspace of %zu bytes, need %zu", ws_bytes, L.total);
+    uint8_t *w8 = (uint8_t *)ws;
+    int *counts = (int *)(w8 + L.counts), *offsets = (int *)(w8 + L.offsets);
+    int *rank = (int *)(w8 + L.rank), *inv = (int *)(w8 + L.inv), *perm = (int *)(w8 + L.perm);
+    int *tiles = (int *)(w8 + L.tiles);
+    float *act = (float *)(w8 + L.act), *down = (float *)(w8 + L.down);
+    const int pairs = T * k;
+    int bits = 1;
+    while ((1 << bits) <= E) bits++;
+
+    _Float16 *xs = (_Float16 *)(w8 + L.xs), *acts = (_Float16 *)(w8 + L.acts);
+    float *xun = (float *)(w8 + L.xun), *actun = (float *)(w8 + L.actun);
+    int rc = launch_stage_f32(x, hidden, T, xs, xun, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, s, topk_idx, pairs, E, bits, counts,
+                       offsets, rank, inv, perm, tiles, k);
+    if ((rc = check_launch("moe_route"))) return rc;
+    // gate + up, SwiGLU fused: act[q][f]
+    rc = launch_gemm_grouped(kTypeQ4K, 1, experts, expert_stride, gate_off, up_off, xs, xun, counts, offsets, perm,
+                             tiles + 1, L.max_tiles, act, eff, eff, hidden, s);
+    if (rc) return rc;
+    if ((rc = launch_stage_f32(act, eff, pairs, acts, actun, s))) return rc;
+    rc = launch_gemm_grouped(down_type, 0, experts, expert_stride, down_off, down_off, acts, actun, counts, offsets,
+                             nullptr, tiles + 1, L.max_tiles, down, hidden, hidden, eff, s);
+    if (rc) return rc;
+    const long n4 = (long)T * hidden / 4;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<long>((n4 + 255) / 256, 8192)), dim3(256), 0, s,
+                       down, inv, topk_w, out, T, hidden, k);
+    return check_launch("moe_combine");
+}
+
+}  // namespace mnemo

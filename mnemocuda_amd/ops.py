@@ -43,6 +43,14 @@ def _check_w(w: torch.Tensor, type_id: int, rows: int, cols: int, name: str = "W
     return p
 
 
+def _check_rc(lib, rc: int, what: str) -> None:
+    """Raise for a non-zero return code; also consumes the library's per-thread error slot
+    so that a later call does not report this error again."""
+    lib.mnemo_last_error()
+    if rc:
+        raise MnemoError(f"{what}: error {rc}: {lib.mnemo_last_error_string().decode()}")
+
+
 def init() -> None:
     lib = load_library()
     lib.cuda_kernels_init()
@@ -55,8 +63,7 @@ def matvec(w, x, y, rows, cols, type_id):
     _check_w(w, type_id, rows, cols)
     e = lib.mnemo_matvec(w.data_ptr(), _dev(x, "x", torch.float32), _dev(y, "y", torch.float32),
                          rows, cols, type_id, _stream())
-    if e:
-        raise MnemoError(f"mnemo_matvec: error {e}: {lib.mnemo_last_error_string().decode()}")
+    _check_rc(lib, e, "mnemo_matvec")
 
 
 def matvec_q4k(w, x, y, rows, cols):
@@ -182,5 +189,26 @@ def expert_fwd(expert, gate_sz, up_sz, H, EFF, down_type, weight, x, gate_buf, u
                              _dev(x, "x", torch.float32), _dev(gate_buf, "gate_buf", torch.float32),
                              _dev(up_buf, "up_buf", torch.float32), _dev(moe_out, "moe_out", torch.float32),
                              _stream())
-    if e:
-        raise MnemoError(f"mnemo_expert_fwd: error {e}: {lib.mnemo_last_error_string().decode()}")
+    _check_rc(lib, e, "mnemo_expert_fwd")
+
+
+def moe_prefill_workspace_bytes(T, hidden, eff, n_experts, k) -> int:
+    return int(load_library().mnemo_moe_prefill_workspace_bytes(T, hidden, eff, n_experts, k))
+
+
+def moe_prefill(experts, expert_stride, gate_off, up_off, down_off, down_type, x, topk_idx, topk_w,
+                T, hidden, eff, n_experts, k, workspace, out):
+    """Grouped-expert prefill: out[t] += sum_slot w * down(silu(gate x_t) * up x_t)."""
+    lib = load_library()
+    need = expert_stride * (n_experts - 1) + down_off + row_bytes(down_type, eff) * hidden \
+        if down_type in BLOCK_BYTES else 0  # an unknown type is reported by the library
+    if experts.numel() * experts.element_size() < need:
+        raise MnemoError("moe_prefill: expert table too small")
+    if topk_idx.numel() < T * k or topk_w.numel() < T * k or x.numel() < T * hidden or out.numel() < T * hidden:
+        raise MnemoError("moe_prefill: routing, x or out too small")
+    e = lib.mnemo_moe_prefill(_dev(experts, "experts"), expert_stride, gate_off, up_off, down_off, down_type,
+                              _dev(x, "x", torch.float32), _dev(topk_idx, "topk_idx", torch.int32),
+                              _dev(topk_w, "topk_w", torch.float32), T, hidden, eff, n_experts, k,
+                              _dev(workspace, "workspace"), workspace.numel() * workspace.element_size(),
+                              _dev(out, "out", torch.float32), _stream())
+    _check_rc(lib, e, "mnemo_moe_prefill")

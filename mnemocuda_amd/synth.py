@@ -71,3 +71,53 @@ def weights_torch(gen, type_id: int, rows: int, cols: int, device):
     if type_id == 14:
         return q6k_blocks_torch(gen, rows * bpr, device).reshape(-1)
     raise ValueError(type_id)
+
+
+# ------------------------------------------------------------------ MoE routing / expert tables
+def expert_layout(hidden: int, eff: int, down_type: int) -> tuple[int, int, int, int]:
+    """(stride, gate_off, up_off, down_off) of one expert's [gate | up | down] record, the
+    order of the reference's per-expert files (gate Q4_K, up Q4_K, down Q4_K or Q6_K)."""
+    g = eff * ((hidden + 255) // 256) * Q4K_BYTES
+    d = hidden * ((eff + 255) // 256) * (Q6K_BYTES if down_type == 14 else Q4K_BYTES)
+    stride = (2 * g + d + 255) // 256 * 256
+    return stride, 0, g, 2 * g
+
+
+def expert_table(rng: np.random.Generator, n_experts: int, hidden: int, eff: int, down_type: int) -> np.ndarray:
+    stride, _, up_off, down_off = expert_layout(hidden, eff, down_type)
+    t = np.zeros((n_experts, stride), dtype=np.uint8)
+    for e in range(n_experts):
+        t[e, :up_off] = weights(rng, 12, eff, hidden)
+        t[e, up_off:down_off] = weights(rng, 12, eff, hidden)
+        dw = weights(rng, down_type, hidden, eff)
+        t[e, down_off:down_off + dw.size] = dw
+    return t.reshape(-1)
+
+
+def expert_table_torch(gen, n_experts: int, hidden: int, eff: int, down_type: int, device):
+    import torch
+    stride, _, up_off, down_off = expert_layout(hidden, eff, down_type)
+    t = torch.zeros((n_experts, stride), dtype=torch.uint8, device=device)
+    for e in range(n_experts):
+        t[e, :up_off] = weights_torch(gen, 12, eff, hidden, device)
+        t[e, up_off:down_off] = weights_torch(gen, 12, eff, hidden, device)
+        dw = weights_torch(gen, down_type, hidden, eff, device)
+        t[e, down_off:down_off + dw.numel()] = dw
+    return t.reshape(-1)
+
+
+def zipf_routing(rng: np.random.Generator, n_tokens: int, n_experts: int, k: int, s: float = 1.1):
+    """Top-k routing per token: k distinct experts drawn without replacement with
+    P(expert of popularity rank r) ~ r^-s (rank order itself a random permutation), router
+    weights = softmax over the k selected logits (normalised top-k).  Returns int32
+    [n_tokens][k] ids and fp32 [n_tokens][k] weights."""
+    p = 1.0 / np.arange(1, n_experts + 1) ** s
+    p /= p.sum()
+    order = rng.permutation(n_experts)
+    idx = np.empty((n_tokens, k), dtype=np.int32)
+    for t in range(n_tokens):
+        idx[t] = order[rng.choice(n_experts, size=k, replace=False, p=p)]
+    logits = np.sort(rng.standard_normal((n_tokens, k)), axis=1)[:, ::-1]
+    w = np.exp(logits - logits[:, :1])
+    w /= w.sum(axis=1, keepdims=True)
+    return idx, w.astype(np.float32)

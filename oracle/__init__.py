@@ -132,6 +132,33 @@ class Oracle:
             raise ValueError(type_id)
         return out
 
+    def moe_prefill(self, table: np.ndarray, stride: int, gate_off: int, up_off: int, down_off: int,
+                    down_type: int, x: np.ndarray, idx: np.ndarray, w: np.ndarray, hidden: int, eff: int,
+                    n_experts: int) -> np.ndarray:
+        """sum over slots of w * down(silu(gate x) * up x) per token, with x and the SwiGLU
+        activations quantized to Q8_1: the reference's token-sequential MoE prefill
+        (src/forward.c:1783-1830, per expert src/forward.c:876-893) in the GEMM semantics
+        (mo_gemm_q8_1).  Pairs are grouped per expert only to batch the oracle GEMMs; each
+        output row depends on its own token alone.  Returns the fp64 delta [T][hidden]."""
+        T, k = idx.shape
+        xq = self.quantize_q8_1(np.ascontiguousarray(x, np.float32).reshape(T, hidden))
+        out = np.zeros((T, hidden), np.float64)
+        gsz = up_off - gate_off
+        for e in range(n_experts):
+            tok, slot = np.nonzero(idx == e)
+            if tok.size == 0:
+                continue
+            base = e * stride
+            wg = table[base + gate_off: base + gate_off + gsz]
+            wu = table[base + up_off: base + up_off + gsz]
+            wd = table[base + down_off: base + stride]
+            g = self.gemm(12, wg, xq[tok], eff, hidden, tok.size).astype(np.float32)
+            u = self.gemm(12, wu, xq[tok], eff, hidden, tok.size).astype(np.float32)
+            act = self.swiglu(g, u).reshape(tok.size, eff)
+            d = self.gemm(down_type, wd, self.quantize_q8_1(act), hidden, eff, tok.size)
+            np.add.at(out, tok, w[tok, slot][:, None].astype(np.float64) * d)
+        return out
+
 
 _oracle: Oracle | None = None
 

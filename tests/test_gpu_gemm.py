@@ -68,3 +68,22 @@ def test_gemm_baseline_shapes(gpu, oracle, type_id, M, K, N):
     a2[:, :, :16] = ds.view(torch.uint8).reshape(N, K // 128, 16)
     out2 = _run(gpu, type_id, dev(w), a2.reshape(-1), M, K, N)
     assert rel_l2(host(out2), 2 * host(out)) < 1e-6
+
+
+@pytest.mark.parametrize("type_id", [12, 14])
+def test_gemm_large_activations(gpu, oracle, type_id):
+    """Activations whose Q8_1 values d8*q8 exceed the f16 range (|x| up to ~5e6; d8 itself
+    still fits f16, as the Q8_1 format requires) and rows of very different magnitude."""
+    M, K, N = 192, 1024, 48
+    rng = np.random.default_rng(11 + type_id)
+    w = synth.weights(rng, type_id, M, K)
+    x = rng.standard_normal((N, K)).astype(np.float32)
+    x *= np.logspace(-3, 6, N, dtype=np.float32)[:, None]
+    act = oracle.quantize_q8_1(x)
+    case(f"gemm large activations type={type_id}")
+    out = _run(gpu, type_id, dev(w), dev(act), M, K, N)
+    got, ref = host(out), oracle.gemm(type_id, w, act, M, K, N)
+    assert np.all(np.isfinite(got))
+    # per token row: rows span 9 decades, so compare each on its own scale
+    for j in range(N):
+        assert rel_l2(got[j], ref[j]) < TOL, j

@@ -1,0 +1,134 @@
+"""GPU parity of the grouped-expert prefill (mnemo_moe_prefill).
+
+Two references for the added delta out - out0:
+ * the per-expert composition of the plain entry points (cuda_quantize_mmq_q8_1,
+   cuda_gemm_q4k / mnemo_gemm_q6k, SwiGLU in fp32), each oracle-tested on its own:
+   relative L2 <= 1e-3 (the GEMM bar; the two differ only in the SwiGLU's exp rounding);
+ * Oracle.moe_prefill, the fp64 per-token composition of the reference's expert chain
+   (src/forward.c:876-893, applied token by token as src/forward.c:1783-1830 does) in the
+   Q8_1 GEMM semantics: relative L2 <= 1e-2.  The chain re-quantizes the SwiGLU output to
+   Q8_1, and an input error of r ~ 5e-4 (two f16-operand GEMMs) flips the rounding of about
+   r*|q| ~ 2% of the int8 values (|q| ~ 40), an error of 1 step each: sqrt(0.02)/40 ~ 4e-3
+   relative, which the bound covers with margin while a wrong expert, slot or weight
+   (an O(1) error) fails it.
+Routing edge cases: experts with no tokens, an expert spanning several 128-row tiles,
+dropped slots (id -1 or >= n_experts), one token.  The benchmark shape (512 tokens, 128
+experts, top-8 Zipf) is checked against the plain composition and for bitwise run-to-run
+determinism."""
+import numpy as np
+import pytest
+import torch
+
+from mnemocuda_amd import synth
+from tests.conftest import rel_l2
+from tests.gpu_util import case, dev, host
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+TOL_ORACLE = 1e-2
+
+
+def _run(gpu, table, lay, down_type, x, idx, w, T, H, EFF, E, k, out0):
+    stride, g_off, u_off, d_off = lay
+    ws = torch.empty(gpu.ops.moe_prefill_workspace_bytes(T, H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    out = out0.clone()
+    gpu.ops.moe_prefill(table, stride, g_off, u_off, d_off, down_type, x, idx, w, T, H, EFF, E, k, ws, out)
+    return out
+
+
+def _compose_plain(gpu, table, lay, DT, x, idx, w, T, H, EFF, out0):
+    """out0 + sum_slot w * down(silu(gate x) * up x) through the plain GPU entry points."""
+    stride, g_off, u_off, d_off = lay
+    ops = gpu.ops
+    xq = torch.empty(T * (H // 128) * 144, dtype=torch.uint8, device="cuda")
+    ops.quantize_q8_1(x, xq, H, T)
+    xq = xq.view(T, -1)
+    ref = out0.clone().double().view(T, H)
+    for e in np.unique(idx):
+        tok, slot = np.nonzero(idx == e)
+        if e < 0 or e * stride >= table.numel():
+            continue
+        n = tok.size
+        a = xq[torch.from_numpy(tok).cuda()].contiguous()
+        base = int(e) * stride
+        g = torch.empty(n, EFF, device="cuda")
+        u = torch.empty(n, EFF, device="cuda")
+        ops.gemm(table[base + g_off: base + u_off], 12, a, g, EFF, H, n)
+        ops.gemm(table[base + u_off: base + d_off], 12, a, u, EFF, H, n)
+        act = (g / (1 + torch.exp(-g)) * u).contiguous()
+        aq = torch.empty(n * (EFF // 128) * 144, dtype=torch.uint8, device="cuda")
+        ops.quantize_q8_1(act, aq, EFF, n)
+        d = torch.empty(n, H, device="cuda")
+        ops.gemm(table[base + d_off: base + stride], DT, aq, d, H, EFF, n)
+        ref.index_add_(0, torch.from_numpy(tok).cuda(),
+                       d.double() * torch.from_numpy(w[tok, slot]).cuda()[:, None].double())
+    return ref
+
+
+@pytest.mark.parametrize("T,H,EFF,E,k,down_type,skew", [
+    (64, 512, 256, 16, 4, 14, 1.1),
+    (300, 256, 512, 4, 2, 12, 3.0),    # expert 0 spans several tiles
+    (1, 256, 256, 8, 8, 14, 1.1),      # one token, every expert once
+    (37, 768, 256, 32, 3, 14, 0.0),    # most experts empty or single-row
+])
+def test_moe_prefill_vs_oracle(gpu, oracle, T, H, EFF, E, k, down_type, skew):
+    rng = np.random.default_rng(T * 1000 + E)
+    table = synth.expert_table(rng, E, H, EFF, down_type)
+    lay = synth.expert_layout(H, EFF, down_type)
+    idx, w = synth.zipf_routing(rng, T, E, k, s=skew)
+    if T > 4:  # dropped slots: an unfilled top-k slot (-1) and an id past the table
+        idx[1, -1] = -1
+        idx[3, 0] = E + 5
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    out0 = rng.standard_normal((T, H)).astype(np.float32)
+    case(f"moe_prefill T={T} H={H} EFF={EFF} E={E} k={k} down={down_type}")
+    out = _run(gpu, dev(table), lay, down_type, dev(x), dev(idx), dev(w), T, H, EFF, E, k, dev(out0))
+    got_delta = host(out).astype(np.float64).reshape(T, H) - out0
+    comp = host(_compose_plain(gpu, dev(table), lay, down_type, dev(x), idx, w, T, H, EFF, dev(out0))) - out0
+    ref_delta = oracle.moe_prefill(table, *lay, down_type, x, idx, w, H, EFF, E)
+    err_c, err_o = rel_l2(got_delta, comp), rel_l2(got_delta, ref_delta)
+    print(f"rel_l2 vs plain composition={err_c:.2e} vs oracle={err_o:.2e} "
+          f"(plain composition vs oracle {rel_l2(comp, ref_delta):.2e})")
+    assert err_c < TOL
+    assert err_o < TOL_ORACLE
+
+
+def test_moe_prefill_bad_args(gpu):
+    T, H, EFF, E, k = 4, 256, 256, 4, 2
+    x = torch.zeros(T * H, device="cuda")
+    idx = torch.zeros(T * k, dtype=torch.int32, device="cuda")
+    w = torch.zeros(T * k, device="cuda")
+    out = torch.zeros(T * H, device="cuda")
+    table = torch.zeros(E * synth.expert_layout(H, EFF, 14)[0], dtype=torch.uint8, device="cuda")
+    lay = synth.expert_layout(H, EFF, 14)
+    small = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    with pytest.raises(gpu.MnemoError, match="workspace"):
+        gpu.ops.moe_prefill(table, *lay, 14, x, idx, w, T, H, EFF, E, k, small, out)
+    ws = torch.zeros(gpu.ops.moe_prefill_workspace_bytes(T, H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    with pytest.raises(gpu.MnemoError, match="down type"):
+        gpu.ops.moe_prefill(table, *lay, 3, x, idx, w, T, H, EFF, E, k, ws, out)
+
+
+def test_moe_prefill_baseline_shape(gpu):
+    """512 tokens, hidden 4096, eff 1536, 128 experts, top-8 Zipf(1.1), Q6_K down."""
+    T, H, EFF, E, k, DT = 512, 4096, 1536, 128, 8, 14
+    rng = np.random.default_rng(5)
+    idx, w = synth.zipf_routing(rng, T, E, k)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    case("moe_prefill baseline shape: building expert table")
+    table = synth.expert_table_torch(gen, E, H, EFF, DT, "cuda")
+    lay = synth.expert_layout(H, EFF, DT)
+    stride, g_off, u_off, d_off = lay
+    x = torch.randn(T, H, device="cuda", generator=gen)
+    out0 = torch.randn(T, H, device="cuda", generator=gen)
+    idx_d, w_d = dev(idx), dev(w)
+    case("moe_prefill baseline shape: grouped run x2")
+    out = _run(gpu, table, lay, DT, x, idx_d, w_d, T, H, EFF, E, k, out0)
+    out_b = _run(gpu, table, lay, DT, x, idx_d, w_d, T, H, EFF, E, k, out0)
+    assert torch.equal(out, out_b), "grouped prefill is not deterministic"
+
+    case("moe_prefill baseline shape: per-expert composition of the plain GEMMs")
+    ref = _compose_plain(gpu, table, lay, DT, x, idx, w, T, H, EFF, out0)
+    err = rel_l2(host(out).astype(np.float64) - host(out0), host(ref) - host(out0))
+    print(f"rel_l2 vs composition={err:.2e}")
+    assert err < TOL
