@@ -83,6 +83,13 @@ void mnemo_matvec_q6k_scaled_add(const void *weights, const float *x, float *y, 
  * (forward.c:714-718). */
 void mnemo_matvec_dual(const void *wa, int type_a, const void *wb, int type_b, const float *x,
                        float *ya, float *yb, int n_rows, int n_cols, hipStream_t stream);
+/* New: cuda_matvec_q4k_qkv with a GGUF type per matrix.  Q4_K_M stores V as Q6_K, for
+ * which the reference falls back to separate matvec() launches (src/forward.c:699-718);
+ * this replaces that whole branch:
+ * Q [q_rows], K and V [kv_rows] from one x, one launch. */
+void mnemo_matvec_qkv(const void *wq, int tq, const void *wk, int tk, const void *wv, int tv,
+                      const float *x, float *oq, float *ok, float *ov, int q_rows, int kv_rows,
+                      int n_cols, hipStream_t stream);
 /* New: fused expert down projection of one expert:
  * y += scale * (W_down (silu(gate) * up)), W_down Q4_K or Q6_K [n_rows][n_cols].
  * Replaces cuda_swiglu + (cuda_matvec_q4k_scaled_add | cuda_matvec_q6k + cuda_scaled_add)

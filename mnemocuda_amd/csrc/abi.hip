@@ -161,6 +161,15 @@ void mnemo_matvec_dual(const void *wa, int ta, const void *wb, int tb, const flo
     b.run("mnemo_matvec_dual", s);
 }
 
+void mnemo_matvec_qkv(const void *wq, int tq, const void *wk, int tk, const void *wv, int tv, const float *x,
+                      float *oq, float *ok, float *ov, int q_rows, int kv_rows, int n_cols, hipStream_t s) {
+    GemvBuilder b(x, n_cols);
+    b.add(wq, tq, oq, q_rows, kEpiStore);
+    b.add(wk, tk, ok, kv_rows, kEpiStore);
+    b.add(wv, tv, ov, kv_rows, kEpiStore);
+    b.run("mnemo_matvec_qkv", s);
+}
+
 void mnemo_matvec_swiglu_scaled_add(const void *w, int type, const float *gate, const float *up, float *y,
                                     int n_rows, int n_cols, float scale, hipStream_t s) {
     GemvBuilder b(gate, n_cols);

@@ -188,6 +188,9 @@ __device__ __forceinline__ void store_a(const RawA &r, int h, _Float16 *tile, in
 // compiler inserts count exactly the outstanding steps).  With splits > 1 the partial
 // tiles are added into the (pre-zeroed) output with fp32 atomics, in an order that may
 // differ from run to run.
+#ifndef MNEMO_GEMM_SCHED
+#define MNEMO_GEMM_SCHED 0
+#endif
 constexpr int kThreads = 256;
 constexpr int kBM = 128, kBN = 128;
 constexpr int kPF = 4;
@@ -325,9 +328,26 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
                                 ra[(p + kPF - 1) % kPF]);
                 const int cur = (ks - ks0) & 1;
                 mfma_step(lds[cur][0], lds[cur][1], wi, wj, lane, acc);
-                if (ks + 1 < ks1)
-                    store_step<TYPE>(rw[(p + 1) % kPF], ra[(p + 1) % kPF], ks + 1, lh, lds[cur ^ 1][0],
-                                     lds[cur ^ 1][1], lr);
+                // after the last step this fills the idle buffer with data nobody reads
+                store_step<TYPE>(rw[(p + 1) % kPF], ra[(p + 1) % kPF], ks + 1, lh, lds[cur ^ 1][0],
+                                 lds[cur ^ 1][1], lr);
+#if MNEMO_GEMM_SCHED
+                // interleave the conversion of the next step with this step's MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);  // global loads
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // LDS reads (first half)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, MNEMO_GEMM_SCHED, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // LDS reads (second half)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, MNEMO_GEMM_SCHED, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);  // LDS writes
+#endif
                 __syncthreads();
             }
         }

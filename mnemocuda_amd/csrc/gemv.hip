@@ -31,7 +31,11 @@
 
 namespace mnemo {
 
-constexpr int kGemvThreads = 512;
+#ifndef MNEMO_GEMV_THREADS
+#define MNEMO_GEMV_THREADS 512
+#endif
+constexpr int kGemvThreads = MNEMO_GEMV_THREADS;
+static_assert(kGemvThreads >= 512 && kGemvThreads <= 1024 && kGemvThreads % 64 == 0, "x image staging assumes 512..1024 threads");
 
 // ------------------------------------------------------------------ x preparation
 // LDS image of x for a padded length kp (multiple of 256):
@@ -313,6 +317,74 @@ __device__ __forceinline__ float q6k_dot(const RawH &r, int hf, int c, const XLd
     return h2f(r.dd) * acc;
 }
 
+// Mixed-type launches (Q4_K and Q6_K matrices in one grid): one code path for both types
+// so that the LDS digit reads are not duplicated per type (which would keep both sets of
+// reads live and halve occupancy).  Per 16-value group k of the half super-block:
+//   sum = A_k * u * i_k - B_k * s16_k,  i_k = 254 * <q, d1> + <q, d2>
+// Q4_K: A = d*sc, B = dmin*m (both 16-groups of a sub-block share them);
+// Q6_K: A = d*sc_k, B = 32*d*sc_k (the -32 offset of the 6-bit quants).
+__device__ __forceinline__ float mixed_dot(const RawH &r, int hf, int c, const XLds &X, bool q4) {
+    uint32_t q[4][8];
+    float A[8], B[8];
+    if (q4) {
+        const uint32_t S0 = r.h.y, S1 = r.h.z, S2 = r.h.w;
+        const uint32_t sc = hf ? ((S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u)) : (S0 & 0x3F3F3F3Fu);
+        const uint32_t mm = hf ? (((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) : (S1 & 0x3F3F3F3Fu);
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            A[2 * t] = A[2 * t + 1] = d * (float)((sc >> (8 * t)) & 0xFF);
+            B[2 * t] = B[2 * t + 1] = dmin * (float)((mm >> (8 * t)) & 0xFF);
+            const int sh = 4 * (t & 1);
+            const uint4 qa = r.q[2 * (t >> 1)], qb = r.q[2 * (t >> 1) + 1];
+            const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int k = 0; k < 8; k++) q[t][k] = (w[k] >> sh) & 0x0F0F0F0Fu;
+        }
+    } else {
+        const float d = h2f(r.dd);
+        const uint32_t H[8] = {r.qh[0].x, r.qh[0].y, r.qh[0].z, r.qh[0].w,
+                               r.qh[1].x, r.qh[1].y, r.qh[1].z, r.qh[1].w};
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint32_t sw = hf ? (g < 2 ? r.h.z : r.h.w) : (g < 2 ? r.h.x : r.h.y);
+            A[2 * g] = d * (float)(int)(int8_t)(sw >> (16 * (g & 1)));
+            A[2 * g + 1] = d * (float)(int)(int8_t)(sw >> (16 * (g & 1) + 8));
+            B[2 * g] = 32.0f * A[2 * g];
+            B[2 * g + 1] = 32.0f * A[2 * g + 1];
+            const uint4 la = r.q[2 * (g & 1)], lb = r.q[2 * (g & 1) + 1];
+            const uint32_t L[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t lo = (g >= 2 ? (L[k] >> 4) : L[k]) & 0x0F0F0F0Fu;
+                const uint32_t hi = (2 * g <= 4 ? (H[k] << (4 - 2 * g)) : (H[k] >> (2 * g - 4))) & 0x30303030u;
+                q[g][k] = lo | hi;
+            }
+        }
+    }
+    const float4 u = *(const float4 *)(X.u + (c >> 5));
+    const float4 s16a = *(const float4 *)(X.s16 + (c >> 4));
+    const float4 s16b = *(const float4 *)(X.s16 + (c >> 4) + 4);
+    const float uu[4] = {u.x, u.y, u.z, u.w};
+    const float ss[8] = {s16a.x, s16a.y, s16a.z, s16a.w, s16b.x, s16b.y, s16b.z, s16b.w};
+    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int oa = X.off(c + 32 * t), ob = X.off(c + 32 * t + 16);
+        const int4 d1a = *(const int4 *)(X.d1 + oa), d1b = *(const int4 *)(X.d1 + ob);
+        const int4 d2a = *(const int4 *)(X.d2 + oa), d2b = *(const int4 *)(X.d2 + ob);
+        const uint32_t qa[4] = {q[t][0], q[t][1], q[t][2], q[t][3]}, qb[4] = {q[t][4], q[t][5], q[t][6], q[t][7]};
+        const int i0 = 254 * dot16(qa, d1a, 0) + dot16(qa, d2a, 0);
+        const int i1 = 254 * dot16(qb, d1b, 0) + dot16(qb, d2b, 0);
+        acc = fmaf(A[2 * t], uu[t] * (float)i0, acc);
+        acc = fmaf(A[2 * t + 1], uu[t] * (float)i1, acc);
+        acc = fmaf(-B[2 * t], ss[2 * t], acc);
+        acc = fmaf(-B[2 * t + 1], ss[2 * t + 1], acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return acc;
+}
+
 // ------------------------------------------------------------------ the kernel
 template <int LPR>
 __device__ __forceinline__ float reduce_rows(float v) {
@@ -381,7 +453,7 @@ __device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int 
         float v;
         if (TM == 1) v = q4k_dot(ps.q[j], uc & 1, uc * 128, X);
         else if (TM == 2) v = q6k_dot(ps.q[j], uc & 1, uc * 128, X);
-        else v = q4 ? q4k_dot(ps.q[j], uc & 1, uc * 128, X) : q6k_dot(ps.q[j], uc & 1, uc * 128, X);
+        else v = mixed_dot(ps.q[j], uc & 1, uc * 128, X, q4);
         acc += u < uph ? v : 0.0f;
     }
     acc = reduce_rows<LPR>(acc);
@@ -395,7 +467,10 @@ __device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int 
 // R wave passes per wave, all loaded before the x image is built.  The grid covers the
 // row space exactly once (no loop), so the loads of every pass are issued back to back.
 template <int LPR, int UPL, int XPT, bool SWI, int TM, int R>
-__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs args) {
+#ifndef MNEMO_GEMV_MINW
+#define MNEMO_GEMV_MINW 1
+#endif
+__global__ void __launch_bounds__(kGemvThreads, MNEMO_GEMV_MINW) gemv_kernel(GemvArgs args) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int kp = (args.n_cols + 255) & ~255;
     const int bpr = kp / 256;
@@ -427,13 +502,9 @@ static void launch_tm(const GemvArgs &a, int blocks, int R, size_t lds, hipStrea
 #define MNEMO_GEMV_LAUNCH(SWI_, R_)                                                                          \
     hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, SWI_, TM, R_>), dim3(blocks), dim3(kGemvThreads), lds, \
                        stream, a)
-    if (a.xmode == 1) {
-        if (R == 1) MNEMO_GEMV_LAUNCH(true, 1);
-        else MNEMO_GEMV_LAUNCH(true, 2);
-    } else {
-        if (R == 1) MNEMO_GEMV_LAUNCH(false, 1);
-        else MNEMO_GEMV_LAUNCH(false, 2);
-    }
+    (void)R;
+    if (a.xmode == 1) MNEMO_GEMV_LAUNCH(true, 1);
+    else MNEMO_GEMV_LAUNCH(false, 1);
 #undef MNEMO_GEMV_LAUNCH
 }
 
@@ -477,22 +548,24 @@ int launch_gemv(GemvArgs a, hipStream_t stream) {
     for (int i = a.nmat; i < 3; i++) a.off[i] = INT_MAX;
     a.total_rows = off;
     const int passes = a.total_rows / P;
-    // One pass per wave while the whole grid fits on the chip at once (two workgroups per
-    // CU), else two passes per wave; the hardware queues any further workgroups.
-    const int resident = 2 * device_cus() * wpb;
-    const int R = passes > resident ? 2 : 1;
-    const int blocks = (passes + wpb * R - 1) / (wpb * R);
+    // One pass per wave: the loads of a wave are issued back to back and the hardware queues
+    // the workgroups beyond what fits on the chip.  (Two passes per wave once the grid
+    // exceeds the chip measured slower at every size: fewer waves in flight.)
+    const int R = 1;
+    const int blocks = (passes + wpb - 1) / wpb;
     const size_t lds = xlds_bytes(kp);
     // XPT = float4 of x per thread = kp / (4 * kGemvThreads), rounded up
+    constexpr int T4 = 4 * kGemvThreads;
+    constexpr int X4K = (4096 + T4 - 1) / T4, X8K = (8192 + T4 - 1) / T4, X16K = (16384 + T4 - 1) / T4;
     switch (lpr) {
     case 2: launch<2, 1, 1>(a, blocks, R, lds, stream); break;
     case 4: launch<4, 1, 1>(a, blocks, R, lds, stream); break;
     case 8: launch<8, 1, 1>(a, blocks, R, lds, stream); break;
     case 16: launch<16, 1, 1>(a, blocks, R, lds, stream); break;
-    case 32: launch<32, 1, 2>(a, blocks, R, lds, stream); break;
+    case 32: launch<32, 1, X4K>(a, blocks, R, lds, stream); break;
     default:
-        if (kp <= 8192) launch<64, 1, 4>(a, blocks, R, lds, stream);
-        else launch<64, 2, 8>(a, blocks, R, lds, stream);
+        if (kp <= 8192) launch<64, 1, X8K>(a, blocks, R, lds, stream);
+        else launch<64, 2, X16K>(a, blocks, R, lds, stream);
     }
     return check_launch("gemv");
 }

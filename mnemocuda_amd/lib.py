@@ -28,6 +28,7 @@ SIGNATURES: dict[str, tuple] = {
     "cuda_matvec_q6k": (None, [vp, fp, fp, i32, i32, stream_t]),
     "mnemo_matvec_q6k_scaled_add": (None, [vp, fp, fp, i32, i32, f32, stream_t]),
     "mnemo_matvec_dual": (None, [vp, i32, vp, i32, fp, fp, fp, i32, i32, stream_t]),
+    "mnemo_matvec_qkv": (None, [vp, i32, vp, i32, vp, i32, fp, fp, fp, fp, i32, i32, i32, stream_t]),
     "mnemo_matvec_swiglu_scaled_add": (None, [vp, i32, fp, fp, fp, i32, i32, f32, stream_t]),
     "cuda_matvec_f32": (None, [fp, fp, fp, i32, i32, stream_t]),
     "cuda_topk_softmax": (None, [fp, ip, fp, i32, i32, stream_t]),

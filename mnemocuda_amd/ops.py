@@ -114,6 +114,15 @@ def matvec_dual(wa, ta, wb, tb, x, ya, yb, rows, cols):
     check(lib, "mnemo_matvec_dual")
 
 
+def matvec_qkv(wq, tq, wk, tk, wv, tv, x, oq, ok, ov, q_rows, kv_rows, cols):
+    lib = load_library()
+    lib.mnemo_matvec_qkv(_check_w(wq, tq, q_rows, cols, "wq"), tq, _check_w(wk, tk, kv_rows, cols, "wk"), tk,
+                         _check_w(wv, tv, kv_rows, cols, "wv"), tv, _dev(x, "x", torch.float32),
+                         _dev(oq, "oq", torch.float32), _dev(ok, "ok", torch.float32),
+                         _dev(ov, "ov", torch.float32), q_rows, kv_rows, cols, _stream())
+    check(lib, "mnemo_matvec_qkv")
+
+
 def matvec_q4k_scaled_add(w, x, y, rows, cols, scale):
     lib = load_library()
     lib.cuda_matvec_q4k_scaled_add(_check_w(w, TYPE_Q4K, rows, cols), _dev(x, "x", torch.float32),

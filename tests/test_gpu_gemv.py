@@ -79,6 +79,21 @@ def test_qkv(gpu, oracle, q_rows, kv_rows, cols):
         assert rel_l2(host(o), oracle.gemv(12, w, x, r, cols)) < TOL
 
 
+@pytest.mark.parametrize("types,q_rows,kv_rows,cols", [((12, 12, 14), 8192, 512, 4096), ((14, 12, 14), 70, 9, 768),
+                                                       ((12, 14, 12), 33, 64, 1000)])
+def test_qkv_mixed(gpu, oracle, types, q_rows, kv_rows, cols):
+    rng = np.random.default_rng(q_rows * 3 + kv_rows)
+    rows = (q_rows, kv_rows, kv_rows)
+    ws = [_mk(rng, t, r, cols) for t, r in zip(types, rows)]
+    x = rng.standard_normal(cols).astype(np.float32)
+    outs = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    case(f"qkv mixed {types} {q_rows}/{kv_rows}x{cols}")
+    gpu.ops.matvec_qkv(ws[0][1], types[0], ws[1][1], types[1], ws[2][1], types[2], dev(x), *outs,
+                       q_rows, kv_rows, cols)
+    for (w, _), t, o, r in zip(ws, types, outs, rows):
+        assert rel_l2(host(o), oracle.gemv(t, w, x, r, cols)) < TOL
+
+
 @pytest.mark.parametrize("ta,tb,rows,cols", [(12, 12, 1536, 4096), (12, 14, 512, 4096), (14, 12, 77, 768),
                                              (14, 14, 64, 1536)])
 def test_dual(gpu, oracle, ta, tb, rows, cols):
