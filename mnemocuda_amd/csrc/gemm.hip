@@ -9,10 +9,12 @@
 // the MFMA accumulates across the whole K without a per-sub-block fp32 rescale (an int8
 // MFMA would need one cvt + two FMAs per output per 32-K step, several times the MFMA
 // time in VALU work).
-//   * Activations are staged once per call (stage_* kernels) as f16 rows holding
-//     d8*q8*2^-e_row, e_row an exact power of two chosen per row so that the values stay
-//     inside the f16 range (127*max d8*2^-e <= 2^15); the epilogue multiplies by 2^e.  The
-//     GEMM then copies activation tiles instead of converting them once per weight tile.
+//   * Activation values d8*q8 are held in f16 scaled per row by 2^-e_row, an exact power
+//     of two chosen so that they stay inside the f16 range (127*max d8*2^-e <= 2^15); the
+//     epilogue multiplies by 2^e.  The reference entry points (cuda_gemm_q4k,
+//     mnemo_gemm_q6k) convert Q8_1 blocks per tile and allocate nothing; the grouped
+//     expert path stages each activation row once in that f16 form (stage_* kernels, in
+//     the caller's workspace) and copies tiles.
 //   * Weights are dequantised on the fly in packed f16 arithmetic: a quant q placed under
 //     the exponent byte 0x64 is the f16 1024 + q; subtracting 1024 (or 1056 for Q6_K's
 //     q - 32) is exact; then one fma with (f16(d*sc), f16(-dmin*m)) (Q4_K) or one multiply
@@ -49,8 +51,15 @@ struct RawW {
     uint4 a, b, c, d;  // Q4_K: a = header, b = 16 qs bytes;  Q6_K: a,b = 32 ql, c,d = 32 qh
     uint32_t s, dd;    // Q6_K: two int8 scales, f16 d
 };
+// Activation chunk of one step half: staged f16 values, or a raw Q8_1 sub-block.
+template <bool Q8>
 struct RawA {
-    uint4 a, b, c, d;  // 32 f16 activation values
+    uint4 a, b, c, d;  // 32 f16 values
+};
+template <>
+struct RawA<true> {
+    uint4 a, b;   // 32 int8
+    uint32_t ds;  // half2 (d, d*sum) of the 32
 };
 
 // Q4_K step ks = super-block ks/4, nibble group g = ks%4 (qs bytes 32g..32g+31); half h
@@ -79,13 +88,22 @@ __device__ __forceinline__ void load_w_q6k(const uint8_t *__restrict__ wrow, int
 }
 
 // Activations of step ks, half h: values 64ks + 32h .. +31 = one Q8_1 sub-block.
-// Half h of step ks: f16 activations ks*64 + 32h .. +31 of the staged row.
-__device__ __forceinline__ void load_a(const _Float16 *__restrict__ arow, int ks, int h, RawA &r) {
-    const _Float16 *p = arow + ks * kKS + 32 * h;
+// Half h of step ks: activations ks*64 + 32h .. +31 of the row (staged f16 row, or the
+// row's Q8_1 MMQ blocks: block v/128, sub-block (v/32)%4).
+__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int h, RawA<false> &r) {
+    const _Float16 *p = (const _Float16 *)arow + ks * kKS + 32 * h;
     r.a = ld16((const uint8_t *)(p));
     r.b = ld16((const uint8_t *)(p + 8));
     r.c = ld16((const uint8_t *)(p + 16));
     r.d = ld16((const uint8_t *)(p + 24));
+}
+__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int h, RawA<true> &r) {
+    const int v0 = ks * kKS + 32 * h;
+    const uint8_t *blk = (const uint8_t *)arow + (size_t)(v0 >> 7) * kQ81Bytes;
+    const int sub = (v0 >> 5) & 3;
+    __builtin_memcpy(&r.ds, blk + 4 * sub, 4);
+    r.a = ld16(blk + 16 + 32 * sub);
+    r.b = ld16(blk + 32 + 32 * sub);
 }
 
 // ------------------------------------------------------------------ LDS tiles
@@ -110,6 +128,29 @@ __device__ __forceinline__ uint32_t dq_fma(uint32_t v, uint32_t sel, h2 a, h2 b)
     const h2 q = magic_pair(v, sel) + off;
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a, b));
 }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Row exponent e >= 0 with 127 * dmax * 2^-e <= 2^15 (dmax = largest |d8| of the row).
+__device__ __forceinline__ int row_exponent(float dmax) {
+    int ex = 0;
+    frexpf(dmax * 127.0f, &ex);  // 127 * dmax < 2^ex
+    return max(0, ex - 15);
+}
+
+// 8 int8 quants (two dwords) times the f16 scale d: q8 ^ 0x80 under the exponent byte 0x64
+// is 1024 + q8 + 128 exactly; subtracting 1152 gives q8; the product is rounded once.
+__device__ __forceinline__ void q8x4_to_f16(uint32_t v, h2 d2, uint32_t &o0, uint32_t &o1) {
+    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t u = v ^ 0x80808080u;
+    o0 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04010400u) + off) * d2);
+    o1 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04030402u) + off) * d2);
+}
+
 // Q4_K: half h of step ks holds 16 weights of sub-block 2g (K columns 16h .. 16h+15 of the
 // step: chunks 2h, 2h+1) and 16 of sub-block 2g+1 (columns 32+16h ..: chunks 4+2h, 5+2h).
 __device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int h, _Float16 *tile, int row) {
@@ -172,12 +213,23 @@ __device__ __forceinline__ void store_w_q6k(const RawW &r, int ks, int h, _Float
     for (int k = 0; k < 4; k++) put16(tile, row, 4 * h + k, o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
 }
 
-// Half h: K columns 32h .. 32h+31 (chunks 4h .. 4h+3) of the staged activation row.
-__device__ __forceinline__ void store_a(const RawA &r, int h, _Float16 *tile, int row) {
+// Half h: K columns 32h .. 32h+31 (chunks 4h .. 4h+3) of the activation row.
+__device__ __forceinline__ void store_a(const RawA<false> &r, int h, _Float16 *tile, int row, float) {
     put16(tile, row, 4 * h, r.a.x, r.a.y, r.a.z, r.a.w);
     put16(tile, row, 4 * h + 1, r.b.x, r.b.y, r.b.z, r.b.w);
     put16(tile, row, 4 * h + 2, r.c.x, r.c.y, r.c.z, r.c.w);
     put16(tile, row, 4 * h + 3, r.d.x, r.d.y, r.d.z, r.d.w);
+}
+// Raw Q8_1: d8 * 2^-e (exact) times q8, as the staging kernel computes it.
+__device__ __forceinline__ void store_a(const RawA<true> &r, int h, _Float16 *tile, int row, float as) {
+    const _Float16 d = (_Float16)(h2f(r.ds & 0xFFFF) * as);
+    const h2 d2 = {d, d};
+    const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    uint32_t o[16];
+#pragma unroll
+    for (int k = 0; k < 8; k++) q8x4_to_f16(w[k], d2, o[2 * k], o[2 * k + 1]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) put16(tile, row, 4 * h + k, o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
 }
 
 // ------------------------------------------------------------------ kernel
@@ -195,20 +247,20 @@ constexpr int kThreads = 256;
 constexpr int kBM = 128, kBN = 128;
 constexpr int kPF = 4;
 
-template <int TYPE>
-__device__ __forceinline__ void load_step(const uint8_t *wrow, const _Float16 *arow, int ks, int h, RawW &rw,
-                                          RawA &ra) {
+template <int TYPE, bool Q8>
+__device__ __forceinline__ void load_step(const uint8_t *wrow, const void *arow, int ks, int h, RawW &rw,
+                                          RawA<Q8> &ra) {
     if (TYPE == kTypeQ4K) load_w_q4k(wrow, ks, h, rw);
     else load_w_q6k(wrow, ks, h, rw);
     load_a(arow, ks, h, ra);
 }
 
-template <int TYPE>
-__device__ __forceinline__ void store_step(const RawW &rw, const RawA &ra, int ks, int h, _Float16 *at,
-                                           _Float16 *bt, int row) {
+template <int TYPE, bool Q8>
+__device__ __forceinline__ void store_step(const RawW &rw, const RawA<Q8> &ra, int ks, int h, _Float16 *at,
+                                           _Float16 *bt, int row, float as) {
     if (TYPE == kTypeQ4K) store_w_q4k(rw, ks, h, at, row);
     else store_w_q6k(rw, ks, h, at, row);
-    store_a(ra, h, bt, row);
+    store_a(ra, h, bt, row, as);
 }
 
 __device__ __forceinline__ void mfma_step(const _Float16 *as, const _Float16 *bs, int wi, int wj, int lane,
@@ -242,8 +294,8 @@ enum GemmMode : int { kModePlain = 0, kModeSwiGLU = 1, kModeGrouped = 2 };
 
 struct GemmArgs {
     const uint8_t *W;  // plain: weights; grouped: expert table base
-    const _Float16 *A;       // staged activation rows (K values each)
-    const float *a_unscale;  // per staged row: 2^e
+    const void *A;           // activation rows: staged f16 (K values) or Q8_1 MMQ blocks
+    const float *a_unscale;  // staged rows: 2^e per row
     float *out;
     int M, K, N, splits;
     int out_ld;
@@ -255,7 +307,7 @@ struct GemmArgs {
     const int *tiles;                    // [max_tiles] (expert << 16) | n_tile; tiles[-1] = count
 };
 
-template <int TYPE, int MODE, bool ATOMIC>
+template <int TYPE, int MODE, bool ATOMIC, bool Q8>
 __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     __shared__ __align__(16) _Float16 lds[2][2][kBM * kKS];  // [buffer][weights | tokens]
     const int tid = threadIdx.x;
@@ -301,9 +353,29 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     }
     const int jr = min(j0 + lr, n_rows - 1);
     const int arow_idx = MODE == kModePlain ? jr : MODE == kModeSwiGLU ? g.perm[row_base + jr] : row_base + jr;
-    const _Float16 *arow = g.A + (size_t)arow_idx * K;
     __shared__ float row_unscale[kBN];
-    if (lh == 0) row_unscale[lr] = g.a_unscale[arow_idx];
+    float a_scale = 1.0f;
+    const void *arow;
+    if constexpr (Q8) {
+        // f16 staging of d8*q8 overflows once |d8*q8| > 65504: scale the row by an exact
+        // power of two 2^-e from its largest d8 (127 * max d8 * 2^-e <= 2^15) and undo it
+        // in the epilogue (the staging kernels do the same for staged rows)
+        const uint8_t *ar = (const uint8_t *)g.A + (size_t)arow_idx * (K / 128) * kQ81Bytes;
+        arow = ar;
+        float dmax = 0.0f;
+        for (int b = lh; b < K / 128; b += 2) {
+            const uint4 hd = ld16(ar + (size_t)b * kQ81Bytes);
+            dmax = fmaxf(dmax, fmaxf(fmaxf(fabsf(h2f(hd.x & 0xFFFF)), fabsf(h2f(hd.y & 0xFFFF))),
+                                     fmaxf(fabsf(h2f(hd.z & 0xFFFF)), fabsf(h2f(hd.w & 0xFFFF)))));
+        }
+        dmax = fmaxf(dmax, __shfl_xor(dmax, 1));
+        const int e = row_exponent(dmax);
+        a_scale = ldexpf(1.0f, -e);
+        if (lh == 0) row_unscale[lr] = ldexpf(1.0f, e);
+    } else {
+        arow = (const _Float16 *)g.A + (size_t)arow_idx * K;
+        if (lh == 0) row_unscale[lr] = g.a_unscale[arow_idx];
+    }
 
     f4 acc[4][4];
 #pragma unroll
@@ -312,11 +384,11 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
         for (int b = 0; b < 4; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
 
     RawW rw[kPF];
-    RawA ra[kPF];
+    RawA<Q8> ra[kPF];
     // prologue: steps ks0 .. ks0+kPF-2 in flight (clamped to the last step, unconditional)
 #pragma unroll
-    for (int p = 0; p < kPF - 1; p++) load_step<TYPE>(wrow, arow, min(ks0 + p, last), lh, rw[p], ra[p]);
-    store_step<TYPE>(rw[0], ra[0], ks0, lh, lds[0][0], lds[0][1], lr);
+    for (int p = 0; p < kPF - 1; p++) load_step<TYPE, Q8>(wrow, arow, min(ks0 + p, last), lh, rw[p], ra[p]);
+    store_step<TYPE, Q8>(rw[0], ra[0], ks0, lh, lds[0][0], lds[0][1], lr, a_scale);
     __syncthreads();
 
     for (int kb = ks0; kb < ks1; kb += kPF) {
@@ -324,13 +396,13 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
         for (int p = 0; p < kPF; p++) {
             const int ks = kb + p;
             if (ks < ks1) {  // uniform
-                load_step<TYPE>(wrow, arow, min(ks + kPF - 1, last), lh, rw[(p + kPF - 1) % kPF],
+                load_step<TYPE, Q8>(wrow, arow, min(ks + kPF - 1, last), lh, rw[(p + kPF - 1) % kPF],
                                 ra[(p + kPF - 1) % kPF]);
                 const int cur = (ks - ks0) & 1;
                 mfma_step(lds[cur][0], lds[cur][1], wi, wj, lane, acc);
                 // after the last step this fills the idle buffer with data nobody reads
-                store_step<TYPE>(rw[(p + 1) % kPF], ra[(p + 1) % kPF], ks + 1, lh, lds[cur ^ 1][0],
-                                 lds[cur ^ 1][1], lr);
+                store_step<TYPE, Q8>(rw[(p + 1) % kPF], ra[(p + 1) % kPF], ks + 1, lh, lds[cur ^ 1][0],
+                                     lds[cur ^ 1][1], lr, a_scale);
 #if MNEMO_GEMM_SCHED
                 // interleave the conversion of the next step with this step's MFMAs
                 __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);  // global loads
@@ -401,28 +473,6 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
 // ------------------------------------------------------------------ activation staging
 // One wave per activation row, 4 rows per 256-thread block.
 constexpr int kStageThreads = 256;
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
-// Row exponent e >= 0 with 127 * dmax * 2^-e <= 2^15 (dmax = largest |d8| of the row).
-__device__ __forceinline__ int row_exponent(float dmax) {
-    int ex = 0;
-    frexpf(dmax * 127.0f, &ex);  // 127 * dmax < 2^ex
-    return max(0, ex - 15);
-}
-
-// 8 int8 quants (two dwords) times the f16 scale d: q8 ^ 0x80 under the exponent byte 0x64
-// is 1024 + q8 + 128 exactly; subtracting 1152 gives q8; the product is rounded once.
-__device__ __forceinline__ void q8x4_to_f16(uint32_t v, h2 d2, uint32_t &o0, uint32_t &o1) {
-    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const uint32_t u = v ^ 0x80808080u;
-    o0 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04010400u) + off) * d2);
-    o1 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04030402u) + off) * d2);
-}
 
 // Q8_1 MMQ rows [N][K/128] x 144 B -> f16 rows d8*q8*2^-e, unscale[row] = 2^e.
 __global__ void __launch_bounds__(kStageThreads) stage_q8_1_kernel(const uint8_t *__restrict__ A, int K, int N,
@@ -542,9 +592,10 @@ static int device_cus_gemm() {
     return cus;
 }
 
-template <int MODE>
+template <int MODE, bool Q8>
 static void launch_mode(int type, bool atomic, dim3 grid, const GemmArgs &g, hipStream_t stream) {
-#define MNEMO_GEMM_LAUNCH(T_, A_) hipLaunchKernelGGL((gemm_q8_1_kernel<T_, MODE, A_>), grid, dim3(kThreads), 0, stream, g)
+#define MNEMO_GEMM_LAUNCH(T_, A_) \
+    hipLaunchKernelGGL((gemm_q8_1_kernel<T_, MODE, A_, Q8>), grid, dim3(kThreads), 0, stream, g)
     if (type == kTypeQ4K) {
         if (atomic) MNEMO_GEMM_LAUNCH(kTypeQ4K, true);
         else MNEMO_GEMM_LAUNCH(kTypeQ4K, false);
@@ -569,37 +620,24 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
     int splits = 1;
     while (2 * tm * tn * splits < device_cus_gemm() && nks / (splits * 2) >= 16) splits *= 2;
     if (((long)M * N) % 4 != 0) splits = 1;  // the fill kernel clears float4s
-    // stage the activations (stream-ordered scratch: N*K f16 + N unscale factors)
-    const size_t a16_bytes = ((size_t)N * K * 2 + 255) & ~(size_t)255;
-    void *stage = nullptr;
-    if (hipMallocAsync(&stage, a16_bytes + (size_t)N * 4, stream) != hipSuccess || !stage) {
-        (void)hipGetLastError();
-        return set_error(kErrLaunch, "gemm: cannot allocate %zu bytes of staging memory", a16_bytes + (size_t)N * 4);
-    }
-    _Float16 *a16 = (_Float16 *)stage;
-    float *unscale = (float *)((uint8_t *)stage + a16_bytes);
-    int rc = launch_stage_q8_1(act, K, N, a16, unscale, stream);
+    // activations are read as Q8_1 blocks and converted per tile: nothing is allocated, so
+    // the call may sit inside a graph capture
     GemmArgs g{};
     g.W = (const uint8_t *)w;
-    g.A = a16;
-    g.a_unscale = unscale;
+    g.A = act;
     g.out = out;
     g.M = M;
     g.K = K;
     g.N = N;
     g.splits = splits;
     g.out_ld = M;
-    if (!rc && splits > 1) {
+    if (splits > 1) {
         const long n = (long)M * N;
         hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<long>((n / 4 + 255) / 256, 4096)), dim3(256), 0,
                            stream, (float4 *)out, n / 4);
     }
-    if (!rc) {
-        launch_mode<kModePlain>(type, splits > 1, dim3(tm, tn, splits), g, stream);
-        rc = check_launch("gemm_q8_1");
-    }
-    (void)hipFreeAsync(stage, stream);
-    return rc;
+    launch_mode<kModePlain, true>(type, splits > 1, dim3(tm, tn, splits), g, stream);
+    return check_launch("gemm_q8_1");
 }
 
 // Grouped launches used by the MoE prefill path (moe.hip): tiles[] and the routing arrays
@@ -625,8 +663,8 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
     g.offsets = offsets;
     g.perm = perm;
     g.tiles = tiles;
-    if (swiglu) launch_mode<kModeSwiGLU>(type, false, dim3((M + kBM / 2 - 1) / (kBM / 2), max_tiles, 1), g, stream);
-    else launch_mode<kModeGrouped>(type, false, dim3((M + kBM - 1) / kBM, max_tiles, 1), g, stream);
+    if (swiglu) launch_mode<kModeSwiGLU, false>(type, false, dim3((M + kBM / 2 - 1) / (kBM / 2), max_tiles, 1), g, stream);
+    else launch_mode<kModeGrouped, false>(type, false, dim3((M + kBM - 1) / kBM, max_tiles, 1), g, stream);
     return check_launch("gemm_grouped");
 }
 

@@ -215,19 +215,6 @@ __device__ __forceinline__ void load_q6k(const uint8_t *__restrict__ blk, int hf
     r.dd = dd;
 }
 
-// Mixed-type launches issue one instruction sequence for both types (offsets chosen with
-// selects), so that no branch separates the loads of one pass from those of the next.
-__device__ __forceinline__ void load_any(const uint8_t *__restrict__ blk, int hf, bool q4, RawH &r) {
-    r.h = ld16(blk + (q4 ? 0 : 192));
-#pragma unroll
-    for (int i = 0; i < 4; i++) r.q[i] = ld16(blk + (q4 ? 16 + 64 * hf : 64 * hf) + 16 * i);
-    r.qh[0] = ld16(blk + (q4 ? 0 : 128 + 32 * hf));
-    r.qh[1] = ld16(blk + (q4 ? 0 : 144 + 32 * hf));
-    uint16_t dd;
-    __builtin_memcpy(&dd, blk + (q4 ? 0 : 208), 2);
-    r.dd = dd;
-}
-
 __device__ __forceinline__ int dot16(const uint32_t (&q)[4], const int4 &d, int acc) {
     acc = sdot4((int)q[0], d.x, acc);
     acc = sdot4((int)q[1], d.y, acc);
@@ -317,74 +304,6 @@ __device__ __forceinline__ float q6k_dot(const RawH &r, int hf, int c, const XLd
     return h2f(r.dd) * acc;
 }
 
-// Mixed-type launches (Q4_K and Q6_K matrices in one grid): one code path for both types
-// so that the LDS digit reads are not duplicated per type (which would keep both sets of
-// reads live and halve occupancy).  Per 16-value group k of the half super-block:
-//   sum = A_k * u * i_k - B_k * s16_k,  i_k = 254 * <q, d1> + <q, d2>
-// Q4_K: A = d*sc, B = dmin*m (both 16-groups of a sub-block share them);
-// Q6_K: A = d*sc_k, B = 32*d*sc_k (the -32 offset of the 6-bit quants).
-__device__ __forceinline__ float mixed_dot(const RawH &r, int hf, int c, const XLds &X, bool q4) {
-    uint32_t q[4][8];
-    float A[8], B[8];
-    if (q4) {
-        const uint32_t S0 = r.h.y, S1 = r.h.z, S2 = r.h.w;
-        const uint32_t sc = hf ? ((S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u)) : (S0 & 0x3F3F3F3Fu);
-        const uint32_t mm = hf ? (((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) : (S1 & 0x3F3F3F3Fu);
-        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            A[2 * t] = A[2 * t + 1] = d * (float)((sc >> (8 * t)) & 0xFF);
-            B[2 * t] = B[2 * t + 1] = dmin * (float)((mm >> (8 * t)) & 0xFF);
-            const int sh = 4 * (t & 1);
-            const uint4 qa = r.q[2 * (t >> 1)], qb = r.q[2 * (t >> 1) + 1];
-            const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-#pragma unroll
-            for (int k = 0; k < 8; k++) q[t][k] = (w[k] >> sh) & 0x0F0F0F0Fu;
-        }
-    } else {
-        const float d = h2f(r.dd);
-        const uint32_t H[8] = {r.qh[0].x, r.qh[0].y, r.qh[0].z, r.qh[0].w,
-                               r.qh[1].x, r.qh[1].y, r.qh[1].z, r.qh[1].w};
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint32_t sw = hf ? (g < 2 ? r.h.z : r.h.w) : (g < 2 ? r.h.x : r.h.y);
-            A[2 * g] = d * (float)(int)(int8_t)(sw >> (16 * (g & 1)));
-            A[2 * g + 1] = d * (float)(int)(int8_t)(sw >> (16 * (g & 1) + 8));
-            B[2 * g] = 32.0f * A[2 * g];
-            B[2 * g + 1] = 32.0f * A[2 * g + 1];
-            const uint4 la = r.q[2 * (g & 1)], lb = r.q[2 * (g & 1) + 1];
-            const uint32_t L[8] = {la.x, la.y, la.z, la.w, lb.x, lb.y, lb.z, lb.w};
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint32_t lo = (g >= 2 ? (L[k] >> 4) : L[k]) & 0x0F0F0F0Fu;
-                const uint32_t hi = (2 * g <= 4 ? (H[k] << (4 - 2 * g)) : (H[k] >> (2 * g - 4))) & 0x30303030u;
-                q[g][k] = lo | hi;
-            }
-        }
-    }
-    const float4 u = *(const float4 *)(X.u + (c >> 5));
-    const float4 s16a = *(const float4 *)(X.s16 + (c >> 4));
-    const float4 s16b = *(const float4 *)(X.s16 + (c >> 4) + 4);
-    const float uu[4] = {u.x, u.y, u.z, u.w};
-    const float ss[8] = {s16a.x, s16a.y, s16a.z, s16a.w, s16b.x, s16b.y, s16b.z, s16b.w};
-    float acc = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int oa = X.off(c + 32 * t), ob = X.off(c + 32 * t + 16);
-        const int4 d1a = *(const int4 *)(X.d1 + oa), d1b = *(const int4 *)(X.d1 + ob);
-        const int4 d2a = *(const int4 *)(X.d2 + oa), d2b = *(const int4 *)(X.d2 + ob);
-        const uint32_t qa[4] = {q[t][0], q[t][1], q[t][2], q[t][3]}, qb[4] = {q[t][4], q[t][5], q[t][6], q[t][7]};
-        const int i0 = 254 * dot16(qa, d1a, 0) + dot16(qa, d2a, 0);
-        const int i1 = 254 * dot16(qb, d1b, 0) + dot16(qb, d2b, 0);
-        acc = fmaf(A[2 * t], uu[t] * (float)i0, acc);
-        acc = fmaf(A[2 * t + 1], uu[t] * (float)i1, acc);
-        acc = fmaf(-B[2 * t], ss[2 * t], acc);
-        acc = fmaf(-B[2 * t + 1], ss[2 * t + 1], acc);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    return acc;
-}
-
 // ------------------------------------------------------------------ the kernel
 template <int LPR>
 __device__ __forceinline__ float reduce_rows(float v) {
@@ -412,7 +331,7 @@ __device__ __forceinline__ int pass_matrix(const GemvArgs &args, int base) {
     return (base >= args.off[1]) + (base >= args.off[2]);
 }
 
-// TM: types present in the launch -- 1 Q4_K only, 2 Q6_K only, 3 both.
+// TM: the type of this pass's matrix -- 1 Q4_K, 2 Q6_K.
 template <int LPR, int UPL, int TM>
 __device__ __forceinline__ void load_pass(const GemvArgs &args, int base, int bpr, Pass<UPL> &ps) {
     const int lane = lane_id();
@@ -424,16 +343,14 @@ __device__ __forceinline__ void load_pass(const GemvArgs &args, int base, int bp
     // branch-free: a row past the end of its matrix re-loads the last row, dropped later
     ps.valid = lrow < M.rows;
     ps.lrow = min(lrow, M.rows - 1);
-    const bool q4 = TM == 1 || (TM == 3 && M.type == kTypeQ4K);  // uniform
-    const int bb = q4 ? kQ4KBytes : kQ6KBytes;
+    const int bb = TM == 1 ? kQ4KBytes : kQ6KBytes;
     const uint8_t *wrow = (const uint8_t *)M.w + (size_t)ps.lrow * bpr * bb;
 #pragma unroll
     for (int j = 0; j < UPL; j++) {
         const int u = min(ul + j * LPR, uph - 1);
         const uint8_t *blk = wrow + (size_t)(u >> 1) * bb;
         if (TM == 1) load_q4k(blk, u & 1, ps.q[j]);
-        else if (TM == 2) load_q6k(blk, u & 1, ps.q[j]);
-        else load_any(blk, u & 1, q4, ps.q[j]);
+        else load_q6k(blk, u & 1, ps.q[j]);
     }
 }
 
@@ -444,7 +361,6 @@ __device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int 
     const int ul = lane % LPR;
     const int uph = bpr * 2;
     const GemvMat &M = args.m[pass_matrix(args, base)];
-    const bool q4 = TM == 1 || (TM == 3 && M.type == kTypeQ4K);  // uniform
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < UPL; j++) {
@@ -452,9 +368,9 @@ __device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int 
         const int uc = min(u, uph - 1);
         float v;
         if (TM == 1) v = q4k_dot(ps.q[j], uc & 1, uc * 128, X);
-        else if (TM == 2) v = q6k_dot(ps.q[j], uc & 1, uc * 128, X);
-        else v = mixed_dot(ps.q[j], uc & 1, uc * 128, X, q4);
+        else v = q6k_dot(ps.q[j], uc & 1, uc * 128, X);
         acc += u < uph ? v : 0.0f;
+        __builtin_amdgcn_sched_barrier(0);  // one unit's digit reads at a time
     }
     acc = reduce_rows<LPR>(acc);
     if (ul == LPR - 1 && ps.valid) {
@@ -464,57 +380,59 @@ __device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int 
     }
 }
 
-// R wave passes per wave, all loaded before the x image is built.  The grid covers the
-// row space exactly once (no loop), so the loads of every pass are issued back to back.
-template <int LPR, int UPL, int XPT, bool SWI, int TM, int R>
-#ifndef MNEMO_GEMV_MINW
-#define MNEMO_GEMV_MINW 1
-#endif
-__global__ void __launch_bounds__(kGemvThreads, MNEMO_GEMV_MINW) gemv_kernel(GemvArgs args) {
-    extern __shared__ __align__(16) uint8_t smem[];
+// One wave pass per wave, loaded before the x image is built.  The grid covers the row
+// space exactly once (no loop), so the loads of every wave are issued back to back.
+template <int LPR, int UPL, int XPT, bool SWI, int TM>
+__device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     const int kp = (args.n_cols + 255) & ~255;
     const int bpr = kp / 256;
     XLds X(smem, kp);
     constexpr int P = 64 / LPR;
     constexpr int wpb = kGemvThreads / 64;
     const int wave = blockIdx.x * wpb + (threadIdx.x >> 6);
-    const int nwaves = gridDim.x * wpb;
-    const int base0 = __builtin_amdgcn_readfirstlane(wave * P);  // wave-uniform
+    const int base = __builtin_amdgcn_readfirstlane(wave * P);  // wave-uniform
     const int last = args.total_rows - P;
 
     XRegs<XPT> xr, xr2;
     load_x<XPT, SWI>(args.x, args.x2, args.n_cols, xr, xr2);
-    // pass r of this wave starts at row base0 + r * nwaves * P; a start past the end is
-    // clamped to the last pass (loaded again, dropped) so every wave issues the same loads
-    Pass<UPL> ps[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) load_pass<LPR, UPL, TM>(args, min(base0 + r * nwaves * P, last), bpr, ps[r]);
+    // a wave past the end loads the last pass again (dropped) so every wave issues the
+    // same loads
+    Pass<UPL> ps;
+    load_pass<LPR, UPL, TM>(args, min(base, last), bpr, ps);
     finish_x<XPT, SWI>(xr, xr2, args.n_cols, kp, X);
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int base = base0 + r * nwaves * P;
-        if (base < args.total_rows) finish_pass<LPR, UPL, TM>(args, base, bpr, ps[r], X);
+    if (base < args.total_rows) finish_pass<LPR, UPL, TM>(args, base, bpr, ps, X);
+}
+
+// TM: types present in the launch -- 1 Q4_K only, 2 Q6_K only, 3 both.  With both, every
+// matrix starts at a multiple of the rows of one workgroup, so the type is uniform per
+// workgroup and each workgroup runs the single-type code (the barrier of the x image
+// sits in both branches; each wave reaches exactly one).
+template <int LPR, int UPL, int XPT, bool SWI, int TM>
+__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    if constexpr (TM == 3) {
+        constexpr int rows_per_block = (kGemvThreads / 64) * (64 / LPR);
+        const int mi = pass_matrix(args, (int)blockIdx.x * rows_per_block);
+        if (args.m[mi].type == kTypeQ4K) gemv_body<LPR, UPL, XPT, SWI, 1>(args, smem);
+        else gemv_body<LPR, UPL, XPT, SWI, 2>(args, smem);
+    } else {
+        gemv_body<LPR, UPL, XPT, SWI, TM>(args, smem);
     }
 }
 
 template <int LPR, int UPL, int XPT, int TM>
-static void launch_tm(const GemvArgs &a, int blocks, int R, size_t lds, hipStream_t stream) {
-#define MNEMO_GEMV_LAUNCH(SWI_, R_)                                                                          \
-    hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, SWI_, TM, R_>), dim3(blocks), dim3(kGemvThreads), lds, \
-                       stream, a)
-    (void)R;
-    if (a.xmode == 1) MNEMO_GEMV_LAUNCH(true, 1);
-    else MNEMO_GEMV_LAUNCH(false, 1);
-#undef MNEMO_GEMV_LAUNCH
+static void launch_tm(const GemvArgs &a, int blocks, size_t lds, hipStream_t stream) {
+    if (a.xmode == 1)
+        hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, true, TM>), dim3(blocks), dim3(kGemvThreads), lds, stream, a);
+    else
+        hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, false, TM>), dim3(blocks), dim3(kGemvThreads), lds, stream, a);
 }
 
 template <int LPR, int UPL, int XPT>
-static void launch(const GemvArgs &a, int blocks, int R, size_t lds, hipStream_t stream) {
-    int tm = 0;
-    for (int i = 0; i < a.nmat; i++) tm |= a.m[i].type == kTypeQ4K ? 1 : 2;
-    if (tm == 1) launch_tm<LPR, UPL, XPT, 1>(a, blocks, R, lds, stream);
-    else if (tm == 2) launch_tm<LPR, UPL, XPT, 2>(a, blocks, R, lds, stream);
-    else launch_tm<LPR, UPL, XPT, 3>(a, blocks, R, lds, stream);
+static void launch(const GemvArgs &a, int tm, int blocks, size_t lds, hipStream_t stream) {
+    if (tm == 1) launch_tm<LPR, UPL, XPT, 1>(a, blocks, lds, stream);
+    else if (tm == 2) launch_tm<LPR, UPL, XPT, 2>(a, blocks, lds, stream);
+    else launch_tm<LPR, UPL, XPT, 3>(a, blocks, lds, stream);
 }
 
 static int device_cus() {
@@ -537,35 +455,44 @@ int launch_gemv(GemvArgs a, hipStream_t stream) {
     const int uph = kp / 128;
     int lpr = 2;
     while (lpr < uph && lpr < 64) lpr <<= 1;
-    const int P = 64 / lpr;
     constexpr int wpb = kGemvThreads / 64;
-    // each matrix starts at a multiple of P rows so that no wave pass spans two matrices
-    int off = 0;
-    for (int i = 0; i < a.nmat; i++) {
-        a.off[i] = off;
-        off += (a.m[i].rows + P - 1) / P * P;
-    }
-    for (int i = a.nmat; i < 3; i++) a.off[i] = INT_MAX;
-    a.total_rows = off;
-    const int passes = a.total_rows / P;
-    // One pass per wave: the loads of a wave are issued back to back and the hardware queues
-    // the workgroups beyond what fits on the chip.  (Two passes per wave once the grid
-    // exceeds the chip measured slower at every size: fewer waves in flight.)
-    const int R = 1;
+    int tm = 0;
+    for (int i = 0; i < a.nmat; i++) tm |= a.m[i].type == kTypeQ4K ? 1 : 2;
+    // Row space: each matrix starts at a multiple of P rows so that no wave pass spans two
+    // matrices; with mixed types at a multiple of a workgroup's rows (the type is then
+    // uniform per workgroup).  One pass per wave: the loads of a wave are issued back to
+    // back and the hardware queues the workgroups beyond what fits on the chip.
+    auto layout = [&](int lanes_per_row) {
+        const int P = 64 / lanes_per_row;
+        const int align = tm == 3 ? wpb * P : P;
+        int off = 0;
+        for (int i = 0; i < a.nmat; i++) {
+            a.off[i] = off;
+            off += (a.m[i].rows + align - 1) / align * align;
+        }
+        for (int i = a.nmat; i < 3; i++) a.off[i] = INT_MAX;
+        a.total_rows = off;
+        return off / P;
+    };
+    const int passes = layout(lpr);
+    // More waves than fit on the chip at once (16 per CU) leave a second, mostly idle
+    // generation of workgroups; the alternatives measured slower: two row passes per wave,
+    // two half super-blocks per lane (register pressure halves the waves per CU) and
+    // 640..1024-thread workgroups.
     const int blocks = (passes + wpb - 1) / wpb;
     const size_t lds = xlds_bytes(kp);
     // XPT = float4 of x per thread = kp / (4 * kGemvThreads), rounded up
     constexpr int T4 = 4 * kGemvThreads;
     constexpr int X4K = (4096 + T4 - 1) / T4, X8K = (8192 + T4 - 1) / T4, X16K = (16384 + T4 - 1) / T4;
     switch (lpr) {
-    case 2: launch<2, 1, 1>(a, blocks, R, lds, stream); break;
-    case 4: launch<4, 1, 1>(a, blocks, R, lds, stream); break;
-    case 8: launch<8, 1, 1>(a, blocks, R, lds, stream); break;
-    case 16: launch<16, 1, 1>(a, blocks, R, lds, stream); break;
-    case 32: launch<32, 1, X4K>(a, blocks, R, lds, stream); break;
+    case 2: launch<2, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 4: launch<4, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 8: launch<8, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 16: launch<16, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 32: launch<32, 1, X4K>(a, tm, blocks, lds, stream); break;
     default:
-        if (kp <= 8192) launch<64, 1, X8K>(a, blocks, R, lds, stream);
-        else launch<64, 2, X16K>(a, blocks, R, lds, stream);
+        if (kp <= 8192) launch<64, 1, X8K>(a, tm, blocks, lds, stream);
+        else launch<64, 2, X16K>(a, tm, blocks, lds, stream);
     }
     return check_launch("gemv");
 }
