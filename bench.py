@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="end with a 256 MiB device copy (torch.neg) whose HBM counters scale rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE readings (mnemocuda_amd/profiling.py)")
     return ap.parse_args()
 
 
@@ -242,6 +245,13 @@ def main():
               "shards by weight rows / experts with no exchange, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
     r = gpu_bench(args)
+    if args.copy_calibration:
+        import torch
+        src = torch.ones(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
     value = BYTES_LAYER * LAYERS / r["step_s"] / 1e9
     ach = BYTES_QKV / r["d_qkv"] / 1e9
     prof = ROOT / "profiles" / "gemv_qkv_fused_traffic.json"
