@@ -148,6 +148,24 @@ int mnemo_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off
                       const float *topk_w, int n_tokens, int hidden, int eff, int n_experts, int k,
                       void *workspace, size_t workspace_bytes, float *out, hipStream_t stream);
 
+/* ---- Decode MoE block with device-side expert dispatch (no reference counterpart) --------
+ * Replaces the reference's decode MoE block (src/forward.c:814-1077: router matvec, top-k,
+ * a host synchronisation to read the expert ids, then expert_fwd per expert) for one token:
+ *   z = W_router x;  (idx, w) = top-k softmax of z;
+ *   out += sum_slot w[slot] * W_down[e] (silu(W_gate[e] x) * W_up[e] x),  e = idx[slot]
+ * The ids stay on the device; four launches, no synchronisation, capture-safe.  Expert e's
+ * matrices sit at experts + e*expert_stride + {gate,up,down}_off (gate/up Q4_K [eff][hidden],
+ * down Q4_K or Q6_K [hidden][eff]); router_w is fp32 [n_experts][hidden].  topk_idx /
+ * topk_w (may be NULL) receive the routing.  k <= 16, n_experts <= 1024, hidden and eff
+ * multiples of 256.  workspace: mnemo_moe_decode_workspace_bytes(...) bytes, 16-byte
+ * aligned, no initialisation needed; calls that share a workspace must not overlap. */
+size_t mnemo_moe_decode_workspace_bytes(int hidden, int eff, int n_experts, int k);
+int mnemo_moe_decode(const float *router_w, const void *experts, size_t expert_stride,
+                     size_t gate_off, size_t up_off, size_t down_off, int down_type,
+                     const float *x, int hidden, int eff, int n_experts, int k, void *workspace,
+                     size_t workspace_bytes, float *out, int *topk_idx, float *topk_w,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,10 @@ int launch_scaled_add(float *out, const float *x, float sc, int n, hipStream_t s
 int launch_quantize_q8_1(const float *src, void *dst, int K, int N, hipStream_t s);
 int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M, int K, int N, hipStream_t s);
 size_t moe_prefill_workspace_bytes(int T, int hidden, int eff, int E, int k);
+size_t moe_decode_workspace_bytes(int hidden, int eff, int E, int k);
+int launch_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
+                      size_t up_off, size_t down_off, int down_type, const float *x, int hidden, int eff, int E,
+                      int k, void *ws, size_t ws_bytes, float *out, int *idx_out, float *w_out, hipStream_t s);
 int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off, size_t up_off, size_t down_off,
                        int down_type, const float *x, const int *topk_idx, const float *topk_w, int T, int hidden,
                        int eff, int E, int k, void *ws, size_t ws_bytes, float *out, hipStream_t s);
@@ -219,6 +223,18 @@ int mnemo_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off
                       hipStream_t s) {
     return launch_moe_prefill(experts, expert_stride, gate_off, up_off, down_off, down_type, x, topk_idx, topk_w,
                               n_tokens, hidden, eff, n_experts, k, workspace, workspace_bytes, out, s);
+}
+
+size_t mnemo_moe_decode_workspace_bytes(int hidden, int eff, int n_experts, int k) {
+    return moe_decode_workspace_bytes(hidden, eff, n_experts, k);
+}
+
+int mnemo_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
+                     size_t up_off, size_t down_off, int down_type, const float *x, int hidden, int eff,
+                     int n_experts, int k, void *workspace, size_t workspace_bytes, float *out, int *topk_idx,
+                     float *topk_w, hipStream_t s) {
+    return launch_moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, hidden, eff,
+                             n_experts, k, workspace, workspace_bytes, out, topk_idx, topk_w, s);
 }
 
 }  // extern "C"

@@ -331,15 +331,45 @@ __device__ __forceinline__ int pass_matrix(const GemvArgs &args, int base) {
     return (base >= args.off[1]) + (base >= args.off[2]);
 }
 
+// The matrix of the pass starting at row `base` (wave-uniform) and its first row in the
+// row space.
+__device__ __forceinline__ GemvMat pass_mat(const GemvArgs &args, int base, int &row0) {
+    if (!args.experts) {
+        const int mi = pass_matrix(args, base);
+        row0 = args.off[mi];
+        return args.m[mi];
+    }
+    const GemvExperts &E = args.ex;
+    const int sm = base / E.rows;  // slot * nm + matrix
+    const int s = sm / E.nm, m = sm - s * E.nm;
+    row0 = sm * E.rows;
+    int e = E.idx[s];
+    const bool ok = e >= 0 && e < E.n_experts;  // a dropped slot computes expert 0 with weight 0
+    e = ok ? e : 0;
+    GemvMat M;
+    M.w = E.table + (size_t)e * E.stride + E.off[m];
+    M.rows = E.rows;
+    M.type = E.type;
+    M.res = nullptr;
+    if (E.nm == 2) {
+        M.y = E.y + (size_t)sm * E.rows;
+        M.mode = kEpiStore;
+        M.scale = 0.0f;
+    } else {
+        M.y = E.y + (size_t)s * E.rows;
+        M.mode = kEpiScaledStore;
+        M.scale = ok ? E.wt[s] : 0.0f;
+    }
+    return M;
+}
+
 // TM: the type of this pass's matrix -- 1 Q4_K, 2 Q6_K.
 template <int LPR, int UPL, int TM>
-__device__ __forceinline__ void load_pass(const GemvArgs &args, int base, int bpr, Pass<UPL> &ps) {
+__device__ __forceinline__ void load_pass(const GemvMat &M, int row0, int base, int bpr, Pass<UPL> &ps) {
     const int lane = lane_id();
     const int ul = lane % LPR;
     const int uph = bpr * 2;  // half super-blocks per row
-    const int mi = pass_matrix(args, base);
-    const GemvMat &M = args.m[mi];
-    const int lrow = base - args.off[mi] + lane / LPR;
+    const int lrow = base - row0 + lane / LPR;
     // branch-free: a row past the end of its matrix re-loads the last row, dropped later
     ps.valid = lrow < M.rows;
     ps.lrow = min(lrow, M.rows - 1);
@@ -355,12 +385,10 @@ __device__ __forceinline__ void load_pass(const GemvArgs &args, int base, int bp
 }
 
 template <int LPR, int UPL, int TM>
-__device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int bpr, const Pass<UPL> &ps,
-                                            const XLds &X) {
+__device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pass<UPL> &ps, const XLds &X) {
     const int lane = lane_id();
     const int ul = lane % LPR;
     const int uph = bpr * 2;
-    const GemvMat &M = args.m[pass_matrix(args, base)];
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < UPL; j++) {
@@ -376,7 +404,34 @@ __device__ __forceinline__ void finish_pass(const GemvArgs &args, int base, int 
     if (ul == LPR - 1 && ps.valid) {
         if (M.mode == kEpiStore) M.y[ps.lrow] = acc;
         else if (M.mode == kEpiResidual) M.y[ps.lrow] = acc + M.res[ps.lrow];
-        else M.y[ps.lrow] += M.scale * acc;
+        else if (M.mode == kEpiScaledAdd) M.y[ps.lrow] += M.scale * acc;
+        else M.y[ps.lrow] = M.scale * acc;
+    }
+}
+
+// Expert-mode down launch: after a workgroup has stored its rows' partials, the last of
+// the `slots` workgroups that cover the same row tile (one per slot) adds the slot sum,
+// in slot order, into out -- deterministic, and no separate combine launch.
+template <int RPB>
+__device__ __forceinline__ void experts_combine(const GemvExperts &E) {
+    __shared__ int is_last;
+    __syncthreads();  // every partial of this workgroup is stored
+    const int tile = (int)blockIdx.x % E.ntiles;
+    if (threadIdx.x == 0) {
+        __threadfence();  // publish them device-wide before counting in
+        const int old = atomicAdd(&E.tile_cnt[tile], 1);
+        is_last = old == E.slots - 1;
+        if (is_last) E.tile_cnt[tile] = 0;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    for (int r = threadIdx.x; r < RPB; r += kGemvThreads) {
+        const int row = tile * RPB + r;
+        float sum = 0.0f;
+        for (int s = 0; s < E.slots; s++)
+            sum += __hip_atomic_load(E.y + (size_t)s * E.rows + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        E.out[row] += sum;
     }
 }
 
@@ -389,18 +444,34 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     XLds X(smem, kp);
     constexpr int P = 64 / LPR;
     constexpr int wpb = kGemvThreads / 64;
+    constexpr int rows_per_block = wpb * P;
     const int wave = blockIdx.x * wpb + (threadIdx.x >> 6);
     const int base = __builtin_amdgcn_readfirstlane(wave * P);  // wave-uniform
     const int last = args.total_rows - P;
+    const bool down = args.experts && args.ex.nm == 1;  // uniform
+    const float *x0 = args.x, *x1 = args.x2;
+    if (down) {  // x of this workgroup's slot (rows is a multiple of the workgroup's rows)
+        const int s = (int)blockIdx.x * rows_per_block / args.ex.rows;
+        x0 = args.ex.xs + (size_t)(2 * s) * args.n_cols;
+        x1 = x0 + args.n_cols;
+    }
 
     XRegs<XPT> xr, xr2;
-    load_x<XPT, SWI>(args.x, args.x2, args.n_cols, xr, xr2);
+    load_x<XPT, SWI>(x0, x1, args.n_cols, xr, xr2);
     // a wave past the end loads the last pass again (dropped) so every wave issues the
     // same loads
+    int row0;
+    const int bc = min(base, last);
+    const GemvMat M = pass_mat(args, bc, row0);
     Pass<UPL> ps;
-    load_pass<LPR, UPL, TM>(args, min(base, last), bpr, ps);
+    load_pass<LPR, UPL, TM>(M, row0, bc, bpr, ps);
     finish_x<XPT, SWI>(xr, xr2, args.n_cols, kp, X);
-    if (base < args.total_rows) finish_pass<LPR, UPL, TM>(args, base, bpr, ps, X);
+    if (base < args.total_rows) finish_pass<LPR, UPL, TM>(M, bpr, ps, X);
+    if (args.experts && args.ex.nm == 2 && blockIdx.x == 0) {
+        // clear the tile counters of the down launch that follows on the stream
+        for (int t = threadIdx.x; t < args.ex.ntiles; t += kGemvThreads) args.ex.tile_cnt[t] = 0;
+    }
+    if (down) experts_combine<rows_per_block>(args.ex);
 }
 
 // TM: types present in the launch -- 1 Q4_K only, 2 Q6_K only, 3 both.  With both, every
@@ -495,6 +566,43 @@ int launch_gemv(GemvArgs a, hipStream_t stream) {
         else launch<64, 2, X16K>(a, tm, blocks, lds, stream);
     }
     return check_launch("gemv");
+}
+
+// Expert mode: lpr from n_cols as for the static launch; the rows of one matrix must be a
+// multiple of a workgroup's rows so that a workgroup never spans two slots (its x image
+// and its row tile belong to one slot).
+int launch_gemv_experts(GemvArgs a, hipStream_t stream) {
+    if (a.n_cols < 4 || a.n_cols > kMaxGemvCols) return kErrBadArg;
+    const int kp = (a.n_cols + 255) & ~255;
+    const int uph = kp / 128;
+    int lpr = 2;
+    while (lpr < uph && lpr < 64) lpr <<= 1;
+    const int P = 64 / lpr;
+    constexpr int wpb = kGemvThreads / 64;
+    const int rpb = wpb * P;
+    GemvExperts &E = a.ex;
+    if (E.rows % rpb != 0) return set_error(kErrBadArg, "expert GEMV: rows %d not a multiple of %d", E.rows, rpb);
+    a.experts = 1;
+    a.nmat = 0;
+    a.xmode = E.nm == 1 ? 1 : 0;
+    a.total_rows = E.slots * E.nm * E.rows;
+    if (E.nm == 1) E.ntiles = E.rows / rpb;
+    const int tm = E.type == kTypeQ4K ? 1 : 2;
+    const int blocks = a.total_rows / rpb;
+    const size_t lds = xlds_bytes(kp);
+    constexpr int T4 = 4 * kGemvThreads;
+    constexpr int X4K = (4096 + T4 - 1) / T4, X8K = (8192 + T4 - 1) / T4, X16K = (16384 + T4 - 1) / T4;
+    switch (lpr) {
+    case 2: launch<2, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 4: launch<4, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 8: launch<8, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 16: launch<16, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 32: launch<32, 1, X4K>(a, tm, blocks, lds, stream); break;
+    default:
+        if (kp <= 8192) launch<64, 1, X8K>(a, tm, blocks, lds, stream);
+        else launch<64, 2, X16K>(a, tm, blocks, lds, stream);
+    }
+    return check_launch("gemv_experts");
 }
 
 }  // namespace mnemo

@@ -16,7 +16,7 @@ constexpr int kMaxGemvCols = 16384;  // LDS image of x: 2.375 B per column
 constexpr int kMaxGemvColsPad = 16384;
 constexpr int kGemvMaxBlocks = 512;
 
-enum GemvEpilogue : int { kEpiStore = 0, kEpiResidual = 1, kEpiScaledAdd = 2 };
+enum GemvEpilogue : int { kEpiStore = 0, kEpiResidual = 1, kEpiScaledAdd = 2, kEpiScaledStore = 3 };
 
 struct GemvMat {
     const void *w;     // GGUF blocks, row-major, ceil(n_cols/256) blocks per row
@@ -28,6 +28,27 @@ struct GemvMat {
     int mode;  // GemvEpilogue
 };
 
+// Expert mode (GemvArgs::experts != 0): the matrices are chosen on the device from the
+// routed expert ids.  Slot s (0 <= s < slots) uses expert idx[s]; its matrix m (0 <= m < nm)
+// sits at table + idx[s] * stride + off[m].  The row space is [slot][matrix][rows].
+//  nm == 2 (gate + up of every slot, one x): y[(2s + m) * rows + r]; also clears tile_cnt.
+//  nm == 1 (down of every slot, x of slot s = silu(xs[2s]) * xs[2s + 1], n_cols each):
+//          partial[s * rows + r] = wt[s] * (W x); the last workgroup to finish a row tile
+//          adds sum_s partial (slot order) into out.
+struct GemvExperts {
+    const uint8_t *table;
+    size_t stride;
+    size_t off[2];
+    const int *idx;
+    const float *wt;
+    const float *xs;
+    float *y;
+    float *out;
+    int *tile_cnt;
+    int slots, nm, rows, type, n_experts;
+    int ntiles;  // nm == 2: counters to clear; nm == 1: row tiles per slot
+};
+
 struct GemvArgs {
     GemvMat m[3];
     int off[3];  // first concatenated row of each matrix (unused slots = INT32_MAX)
@@ -37,9 +58,12 @@ struct GemvArgs {
     int xmode;  // 0: x;  1: silu(x) * x2
     const float *x;
     const float *x2;
+    int experts;  // 0: the static matrices m[]; 1: expert mode (ex)
+    GemvExperts ex;
 };
 
 int launch_gemv(GemvArgs a, hipStream_t stream);
+int launch_gemv_experts(GemvArgs a, hipStream_t stream);
 
 // Records (and prints, as the reference's KERNEL_LAUNCH_CHECK does, kernels.cu:1062-1067)
 // the error of the last launch; returns a kErr code.

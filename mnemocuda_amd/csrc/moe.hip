@@ -22,6 +22,7 @@
 //   acts    T*k staged rows of Q8_1(act), actun: their 2^e_row
 //   down    T*k rows of hidden fp32
 #include <algorithm>
+#include <cstring>
 
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
@@ -33,6 +34,9 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
                         size_t w_off2, const _Float16 *act, const float *act_unscale, const int *counts,
                         const int *offsets, const int *perm, const int *tiles, int max_tiles, float *out,
                         int out_ld, int M, int K, hipStream_t stream);
+
+int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s);
+int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k, hipStream_t s);
 
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
@@ -227,6 +231,106 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)std::min<long>((n4 + 255) / 256, 8192)), dim3(256), 0, s,
                        down, inv, topk_w, out, T, hidden, k);
     return check_launch("moe_combine");
+}
+
+// ------------------------------------------------------------------ decode (one token)
+// The reference's decode MoE block (src/forward.c:814-1077): router matvec, top-k, then per
+// selected expert a host round trip to find its weights, gate+up, SwiGLU, down, scaled add.
+// Here the expert ids never leave the device: the two expert GEMVs read them from the
+// workspace (expert mode of the GEMV kernel), so the block is four stream-ordered launches
+// with no synchronisation, graph-capturable.
+//
+// Workspace: logits[E] | idx[k] | w[k] | gate/up rows [k][2][eff] | partial [k][hidden] |
+// tile counters [hidden], each 256-byte aligned.
+struct MoeDecodeLayout {
+    size_t logits, idx, w, gu, partial, cnt, total;
+};
+
+static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
+    MoeDecodeLayout L{};
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        size_t at = o;
+        o = align256(o + bytes);
+        return at;
+    };
+    L.logits = take((size_t)E * 4);
+    L.idx = take((size_t)k * 4);
+    L.w = take((size_t)k * 4);
+    L.gu = take((size_t)k * 2 * eff * 4);
+    L.partial = take((size_t)k * hidden * 4);
+    L.cnt = take((size_t)hidden * 4);
+    L.total = o;
+    return L;
+}
+
+size_t moe_decode_workspace_bytes(int hidden, int eff, int E, int k) {
+    if (hidden <= 0 || eff <= 0 || E <= 0 || k <= 0) return 0;
+    return moe_decode_layout(hidden, eff, E, k).total;
+}
+
+int launch_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
+                      size_t up_off, size_t down_off, int down_type, const float *x, int hidden, int eff, int E,
+                      int k, void *ws, size_t ws_bytes, float *out, int *idx_out, float *w_out, hipStream_t s) {
+    if (!router_w || !experts || !x || !ws || !out || hidden <= 0 || eff <= 0 || E <= 0 || k <= 0)
+        return set_error(kErrBadArg, "moe_decode: null pointer or non-positive size");
+    if (k > 16 || k > E || E > 1024) return set_error(kErrBadArg, "moe_decode: need k <= 16, k <= n_experts <= 1024");
+    if (down_type != kTypeQ4K && down_type != kTypeQ6K)
+        return set_error(kErrUnsupportedType, "moe_decode: unsupported down type %d", down_type);
+    if ((((uintptr_t)ws) & 15) != 0) return set_error(kErrBadArg, "moe_decode: workspace must be 16-byte aligned");
+    const MoeDecodeLayout L = moe_decode_layout(hidden, eff, E, k);
+    if (ws_bytes < L.total)
+        return set_error(kErrBadArg, "moe_decode: workspace of %zu bytes, need %zu", ws_bytes, L.total);
+    uint8_t *w8 = (uint8_t *)ws;
+    // the routing goes to the caller's arrays when given (the engine logs expert use),
+    // else to the workspace
+    float *logits = (float *)(w8 + L.logits), *wts = w_out ? w_out : (float *)(w8 + L.w);
+    int *idx = idx_out ? idx_out : (int *)(w8 + L.idx);
+    float *gu = (float *)(w8 + L.gu), *partial = (float *)(w8 + L.partial);
+    int *cnt = (int *)(w8 + L.cnt);
+
+    int rc = launch_matvec_f32(router_w, x, logits, E, hidden, s);
+    if (!rc) rc = launch_topk_softmax(logits, idx, wts, E, k, s);
+    if (rc) return rc;
+
+    GemvArgs a;
+    memset(&a, 0, sizeof a);
+    a.x = x;
+    a.n_cols = hidden;
+    a.ex.table = (const uint8_t *)experts;
+    a.ex.stride = expert_stride;
+    a.ex.off[0] = gate_off;
+    a.ex.off[1] = up_off;
+    a.ex.idx = idx;
+    a.ex.wt = wts;
+    a.ex.y = gu;
+    a.ex.tile_cnt = cnt;
+    a.ex.ntiles = hidden;
+    a.ex.slots = k;
+    a.ex.nm = 2;
+    a.ex.rows = eff;
+    a.ex.type = kTypeQ4K;  // gate/up are Q4_K in Q4_K_M experts (src/forward.c:866-872)
+    a.ex.n_experts = E;
+    if ((rc = launch_gemv_experts(a, s))) return rc;
+
+    memset(&a, 0, sizeof a);
+    a.n_cols = eff;
+    a.ex.table = (const uint8_t *)experts;
+    a.ex.stride = expert_stride;
+    a.ex.off[0] = down_off;
+    a.ex.idx = idx;
+    a.ex.wt = wts;
+    a.ex.xs = gu;
+    a.ex.y = partial;
+    a.ex.out = out;
+    a.ex.tile_cnt = cnt;
+    a.ex.slots = k;
+    a.ex.nm = 1;
+    a.ex.rows = hidden;
+    a.ex.type = down_type;
+    a.ex.n_experts = E;
+    if ((rc = launch_gemv_experts(a, s))) return rc;
+    return kOk;
 }
 
 }  // namespace mnemo

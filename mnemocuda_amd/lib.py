@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
     "mnemo_moe_prefill_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
     "mnemo_moe_prefill": (i32, [vp, sz, sz, sz, sz, i32, fp, ip, fp, i32, i32, i32, i32, i32, vp, sz, fp,
                                 stream_t]),
+    "mnemo_moe_decode_workspace_bytes": (sz, [i32, i32, i32, i32]),
+    "mnemo_moe_decode": (i32, [fp, vp, sz, sz, sz, sz, i32, fp, i32, i32, i32, i32, vp, sz, fp, ip, fp, stream_t]),
     # host composition (mnemo_host.h)
     "mnemo_matvec": (i32, [vp, fp, fp, i32, i32, i32, stream_t]),
     "mnemo_down_type_id": (i32, [sz, i32, i32]),

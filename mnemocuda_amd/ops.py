@@ -221,3 +221,26 @@ def moe_prefill(experts, expert_stride, gate_off, up_off, down_off, down_type, x
                               _dev(workspace, "workspace"), workspace.numel() * workspace.element_size(),
                               _dev(out, "out", torch.float32), _stream())
     _check_rc(lib, e, "mnemo_moe_prefill")
+
+
+def moe_decode_workspace_bytes(hidden, eff, n_experts, k) -> int:
+    return int(load_library().mnemo_moe_decode_workspace_bytes(hidden, eff, n_experts, k))
+
+
+def moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, hidden, eff,
+               n_experts, k, workspace, out, topk_idx=None, topk_w=None):
+    """One token's MoE block with device-side dispatch: out += sum_slot w * expert(x)."""
+    lib = load_library()
+    need = expert_stride * (n_experts - 1) + down_off + row_bytes(down_type, eff) * hidden \
+        if down_type in BLOCK_BYTES else 0
+    if experts.numel() * experts.element_size() < need:
+        raise MnemoError("moe_decode: expert table too small")
+    if router_w.numel() < n_experts * hidden or x.numel() < hidden or out.numel() < hidden:
+        raise MnemoError("moe_decode: router, x or out too small")
+    e = lib.mnemo_moe_decode(_dev(router_w, "router_w", torch.float32), _dev(experts, "experts"), expert_stride,
+                             gate_off, up_off, down_off, down_type, _dev(x, "x", torch.float32), hidden, eff,
+                             n_experts, k, _dev(workspace, "workspace"),
+                             workspace.numel() * workspace.element_size(), _dev(out, "out", torch.float32),
+                             None if topk_idx is None else _dev(topk_idx, "topk_idx", torch.int32),
+                             None if topk_w is None else _dev(topk_w, "topk_w", torch.float32), _stream())
+    _check_rc(lib, e, "mnemo_moe_decode")

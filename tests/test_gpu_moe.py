@@ -132,3 +132,84 @@ def test_moe_prefill_baseline_shape(gpu):
     err = rel_l2(host(out).astype(np.float64) - host(out0), host(ref) - host(out0))
     print(f"rel_l2 vs composition={err:.2e}")
     assert err < TOL
+
+
+# ------------------------------------------------------------------ decode (one token)
+def _decode_ref(oracle, table, lay, DT, router, x, H, EFF, E, k):
+    """fp64 oracle chain: router -> top-k -> sum_slot w * down(silu(gate x) * up x)."""
+    stride, g_off, u_off, d_off = lay
+    logits = oracle.matvec_f32(router, x, E, H)
+    idx, w = oracle.topk_softmax(logits.astype(np.float32), k)
+    delta = np.zeros(H)
+    for e, wt in zip(idx, w):
+        base = int(e) * stride
+        g = oracle.gemv(12, table[base + g_off: base + u_off], x, EFF, H)
+        u = oracle.gemv(12, table[base + u_off: base + d_off], x, EFF, H)
+        act = oracle.swiglu(g.astype(np.float32), u.astype(np.float32))
+        delta += float(wt) * oracle.gemv(DT, table[base + d_off: base + stride], act, H, EFF)
+    return logits, idx, w, delta
+
+
+def _routable(rng, E, H, k):
+    """router weights and x whose top-k has a clear margin (so the id set is exact in fp32)"""
+    while True:
+        router = (rng.standard_normal((E, H)) / np.sqrt(H)).astype(np.float32)
+        x = rng.standard_normal(H).astype(np.float32)
+        z = np.sort(router.astype(np.float64) @ x)[::-1]
+        if k == E or z[k - 1] - z[k] > 1e-3:
+            return router, x
+
+
+@pytest.mark.parametrize("H,EFF,E,k,DT", [(512, 256, 16, 4, 14), (1024, 512, 8, 8, 12), (4096, 1536, 24, 8, 14)])
+def test_moe_decode_vs_oracle(gpu, oracle, H, EFF, E, k, DT):
+    rng = np.random.default_rng(H + E * k)
+    table = synth.expert_table(rng, E, H, EFF, DT)
+    lay = synth.expert_layout(H, EFF, DT)
+    router, x = _routable(rng, E, H, k)
+    out0 = rng.standard_normal(H).astype(np.float32)
+    ws = torch.empty(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    out = dev(out0)
+    idx = torch.full((k,), -1, dtype=torch.int32, device="cuda")
+    w = torch.zeros(k, device="cuda")
+    case(f"moe_decode H={H} EFF={EFF} E={E} k={k} down={DT}")
+    gpu.ops.moe_decode(dev(router), dev(table), *lay, DT, dev(x), H, EFF, E, k, ws, out, idx, w)
+    _, ridx, rw, delta = _decode_ref(oracle, table, lay, DT, router, x, H, EFF, E, k)
+    assert sorted(host(idx).tolist()) == sorted(ridx.tolist())
+    assert np.allclose(host(w)[np.argsort(host(idx))], rw[np.argsort(ridx)], rtol=1e-5, atol=1e-6)
+    err = rel_l2(host(out).astype(np.float64) - out0, delta)
+    print(f"rel_l2={err:.2e}")
+    assert err < TOL
+    # a second call on the same workspace (tile counters must have been reset) adds again
+    gpu.ops.moe_decode(dev(router), dev(table), *lay, DT, dev(x), H, EFF, E, k, ws, out, idx, w)
+    assert rel_l2(host(out).astype(np.float64) - out0, 2 * delta) < TOL
+
+
+def test_moe_decode_graph_replays(gpu):
+    """Captured once, replayed several times with eager work in between: every replay
+    matches the eager result bit for bit (deterministic combine, counters reset)."""
+    H, EFF, E, k, DT = 1024, 512, 16, 8, 14
+    rng = np.random.default_rng(3)
+    table = dev(synth.expert_table(rng, E, H, EFF, DT))
+    lay = synth.expert_layout(H, EFF, DT)
+    router = dev((rng.standard_normal((E, H)) / 32).astype(np.float32))
+    x = dev(rng.standard_normal(H).astype(np.float32))
+    ws = torch.empty(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    out = torch.zeros(H, device="cuda")
+    case("moe_decode eager")
+    gpu.ops.moe_decode(router, table, *lay, DT, x, H, EFF, E, k, ws, out)
+    ref = host(out).copy()
+    case("moe_decode graph capture + replays")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            gpu.ops.moe_decode(router, table, *lay, DT, x, H, EFF, E, k, ws, out)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out), ref)
+        junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
