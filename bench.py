@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the full decode-step tok/s (147 GB of experts)")
+    ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with a 256 MiB device copy (torch.neg) whose HBM counters scale rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE readings (mnemocuda_amd/profiling.py)")
@@ -178,7 +180,70 @@ def gpu_bench(args):
         moe = None
         if not args.no_moe:
             moe = moe_prefill_bench(gen, s)
-    return dict(step_s=step_s, wall=wall, d_qkv=d_qkv, d_q=d_q, d_kv=d_kv, d_o=d_o, gemm=gemm, moe=moe)
+        decode = None
+        if not args.no_decode:
+            decode = decode_bench(gen, s, layers, args.decode_tokens)
+    return dict(step_s=step_s, wall=wall, d_qkv=d_qkv, d_q=d_q, d_kv=d_kv, d_o=d_o, gemm=gemm, moe=moe,
+                decode=decode)
+
+
+def decode_bench(gen, stream, layers, tokens):
+    """configs[2] in a full decode step: per token and layer, fused QKV, O (+ residual,
+    its input the Q output standing in for the attention core, which is out of scope),
+    then the MoE block with device-side dispatch (router 128 x 4096 fp32, top-8, gate+up
+    Q4_K 4096->1536 x 8, down Q6_K 1536->4096 x 8 + router-weighted combine); then the
+    lm_head Q6_K 151936 x 4096 GEMV.  All 128 experts of all 94 layers are resident
+    (147 GB).  Each token and layer gets a fresh random input vector, so routing varies
+    like real traffic (no expert reuse in the caches between tokens)."""
+    import torch
+    from mnemocuda_amd import ops, synth
+    E, k, EFF, VOCAB = 128, 8, 1536, 151936
+    stride, g_off, u_off, d_off = synth.expert_layout(H, EFF, Q6K)
+    tables = [synth.expert_table_torch(gen, E, H, EFF, Q6K, "cuda") for _ in range(LAYERS)]
+    routers = [torch.randn(E, H, device="cuda", generator=gen) / 64 for _ in range(LAYERS)]
+    lm_head = synth.weights_torch(gen, Q6K, VOCAB, H, "cuda")
+    X = torch.randn(tokens, LAYERS, H, device="cuda", generator=gen)
+    xbuf = torch.empty(LAYERS, H, device="cuda")
+    q, kk, v = torch.empty(QD, device="cuda"), torch.empty(KVD, device="cuda"), torch.empty(KVD, device="cuda")
+    hid = torch.empty(H, device="cuda")
+    logits = torch.empty(VOCAB, device="cuda")
+    ws = torch.zeros(ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+
+    def token():
+        for li, L in enumerate(layers):
+            ops.matvec_qkv(L["q"], Q4K, L["k"], Q4K, L["v"], Q6K, xbuf[li], q, kk, v, QD, KVD, H)
+            ops.matvec_q4k_add(L["o"], q, xbuf[li], hid, H, QD)
+            ops.moe_decode(routers[li], tables[li], stride, g_off, u_off, d_off, Q6K, hid, H, EFF, E, k, ws, hid)
+        ops.matvec_q6k(lm_head, hid, logits, VOCAB, H)
+
+    with torch.cuda.stream(stream):
+        xbuf.copy_(X[0])
+        token()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            token()
+        for t in range(2):
+            xbuf.copy_(X[t])
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for t in range(tokens):
+            xbuf.copy_(X[t])
+            g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / tokens
+    moe_bytes = (E * H * 4 + H * 4 + E * 4) + k * (2 * EFF * (H // 256) * 144 + H * (EFF // 256) * 210)
+    per_tok = BYTES_LAYER * LAYERS + moe_bytes * LAYERS + VOCAB * (H // 256) * 210
+    del tables, routers, lm_head
+    torch.cuda.empty_cache()
+    return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 3), "tokens": tokens,
+            "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
+            "frac_hbm_peak": round(per_tok / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "experts_resident_GB": round(E * LAYERS * stride / 1e9, 1),
+            "launches_per_token": LAYERS * 6 + 1}
 
 
 def moe_prefill_bench(gen, stream):
@@ -292,6 +357,7 @@ def main():
                               "q_proj_alone": round(r["d_q"] * 1e6, 2), "kv_dual_alone": round(r["d_kv"] * 1e6, 2)},
             "gemm_q4k_m512": r["gemm"],
             "moe_prefill_cfg4": r["moe"],
+            "decode_tok_s": r["decode"],
             "wall_s_timed": round(r["wall"], 3),
         },
     }

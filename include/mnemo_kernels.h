@@ -153,12 +153,13 @@ int mnemo_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off
  * a host synchronisation to read the expert ids, then expert_fwd per expert) for one token:
  *   z = W_router x;  (idx, w) = top-k softmax of z;
  *   out += sum_slot w[slot] * W_down[e] (silu(W_gate[e] x) * W_up[e] x),  e = idx[slot]
- * The ids stay on the device; four launches, no synchronisation, capture-safe.  Expert e's
+ * The ids stay on the device; three launches, no synchronisation, capture-safe.  Expert e's
  * matrices sit at experts + e*expert_stride + {gate,up,down}_off (gate/up Q4_K [eff][hidden],
  * down Q4_K or Q6_K [hidden][eff]); router_w is fp32 [n_experts][hidden].  topk_idx /
  * topk_w (may be NULL) receive the routing.  k <= 16, n_experts <= 1024, hidden and eff
  * multiples of 256.  workspace: mnemo_moe_decode_workspace_bytes(...) bytes, 16-byte
- * aligned, no initialisation needed; calls that share a workspace must not overlap. */
+ * aligned, zero-filled once after allocation (each call leaves it reusable); calls that
+ * share a workspace must not overlap. */
 size_t mnemo_moe_decode_workspace_bytes(int hidden, int eff, int n_experts, int k);
 int mnemo_moe_decode(const float *router_w, const void *experts, size_t expert_stride,
                      size_t gate_off, size_t up_off, size_t down_off, int down_type,

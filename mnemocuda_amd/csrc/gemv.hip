@@ -405,27 +405,33 @@ __device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pas
         if (M.mode == kEpiStore) M.y[ps.lrow] = acc;
         else if (M.mode == kEpiResidual) M.y[ps.lrow] = acc + M.res[ps.lrow];
         else if (M.mode == kEpiScaledAdd) M.y[ps.lrow] += M.scale * acc;
-        else M.y[ps.lrow] = M.scale * acc;
+        else  // expert partials: written through to the device coherence point (see experts_combine)
+            __hip_atomic_store(M.y + ps.lrow, M.scale * acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
 // Expert-mode down launch: after a workgroup has stored its rows' partials, the last of
 // the `slots` workgroups that cover the same row tile (one per slot) adds the slot sum,
 // in slot order, into out -- deterministic, and no separate combine launch.
+// Visibility across the XCDs' separate L2s without a device-scope fence (a fence writes
+// back and invalidates a whole L2 per workgroup; it cost ~48 us per MoE layer): the
+// partials are agent-scope atomic stores, which go through to the coherence point, every
+// thread waits for its stores to complete before the barrier, the counter is an
+// agent-scope atomic, and the last workgroup reads the partials with agent-scope atomic
+// loads.
 template <int RPB>
 __device__ __forceinline__ void experts_combine(const GemvExperts &E) {
     __shared__ int is_last;
-    __syncthreads();  // every partial of this workgroup is stored
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+    __syncthreads();
     const int tile = (int)blockIdx.x % E.ntiles;
     if (threadIdx.x == 0) {
-        __threadfence();  // publish them device-wide before counting in
-        const int old = atomicAdd(&E.tile_cnt[tile], 1);
+        const int old = __hip_atomic_fetch_add(&E.tile_cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         is_last = old == E.slots - 1;
-        if (is_last) E.tile_cnt[tile] = 0;
+        if (is_last) __hip_atomic_store(&E.tile_cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     for (int r = threadIdx.x; r < RPB; r += kGemvThreads) {
         const int row = tile * RPB + r;
         float sum = 0.0f;

@@ -37,6 +37,8 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
 
 int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s);
 int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k, hipStream_t s);
+int launch_router_topk(const float *w, const float *x, float *logits, int n, int n_cols, int k, int *cnt, int *idx,
+                       float *wts, hipStream_t stream);
 
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
@@ -237,13 +239,16 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
 // The reference's decode MoE block (src/forward.c:814-1077): router matvec, top-k, then per
 // selected expert a host round trip to find its weights, gate+up, SwiGLU, down, scaled add.
 // Here the expert ids never leave the device: the two expert GEMVs read them from the
-// workspace (expert mode of the GEMV kernel), so the block is four stream-ordered launches
-// with no synchronisation, graph-capturable.
+// workspace (expert mode of the GEMV kernel), so the block is three stream-ordered
+// launches (router + top-k, gate + up, down + combine) with no synchronisation,
+// graph-capturable.
 //
 // Workspace: logits[E] | idx[k] | w[k] | gate/up rows [k][2][eff] | partial [k][hidden] |
-// tile counters [hidden], each 256-byte aligned.
+// tile counters [hidden] | router arrival counter, each 256-byte aligned.  The router
+// counter must be zero before the first call (zero the workspace once when allocating it);
+// every call leaves it zero.
 struct MoeDecodeLayout {
-    size_t logits, idx, w, gu, partial, cnt, total;
+    size_t logits, idx, w, gu, partial, cnt, rcnt, total;
 };
 
 static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
@@ -260,6 +265,7 @@ static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
     L.gu = take((size_t)k * 2 * eff * 4);
     L.partial = take((size_t)k * hidden * 4);
     L.cnt = take((size_t)hidden * 4);
+    L.rcnt = take(4);
     L.total = o;
     return L;
 }
@@ -289,8 +295,7 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     float *gu = (float *)(w8 + L.gu), *partial = (float *)(w8 + L.partial);
     int *cnt = (int *)(w8 + L.cnt);
 
-    int rc = launch_matvec_f32(router_w, x, logits, E, hidden, s);
-    if (!rc) rc = launch_topk_softmax(logits, idx, wts, E, k, s);
+    int rc = launch_router_topk(router_w, x, logits, E, hidden, k, (int *)(w8 + L.rcnt), idx, wts, s);
     if (rc) return rc;
 
     GemvArgs a;

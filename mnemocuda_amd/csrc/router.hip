@@ -1,7 +1,7 @@
 // router.hip -- fp32 router matvec, top-k softmax, expert glue and the Q8_1 quantizer.
 //
-//  * matvec_f32      (MnemoCUDA kernels.cu:859-880): one wave per router row, 16-byte
-//                    loads, fp32 FMA, DPP row reduction.
+//  * matvec_f32      (MnemoCUDA kernels.cu:859-880): one workgroup per router row, all
+//                    16-byte loads issued up front, fp32 FMA, fixed-order reduction.
 //  * topk_softmax    (kernels.cu:993-1057): one wave; k rounds of a wave-wide arg-max
 //                    ordered by (value desc, index asc), then softmax over the winners.
 //                    Winners are written in that order (the reference's order is its
@@ -14,41 +14,68 @@
 
 namespace mnemo {
 
-__global__ void __launch_bounds__(256) matvec_f32_kernel(const float *__restrict__ w,
-                                                         const float *__restrict__ x,
-                                                         float *__restrict__ y, int n_rows,
-                                                         int n_cols, int vec4) {
-    const int lane = lane_id();
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+// One workgroup of kRowThreads per row: every thread's loads of W and x are issued before
+// any arithmetic (a loop over float4s with an FMA chain would wait for each load in turn;
+// one wave per row took 8.7 us for the 128 x 4096 router).
+constexpr int kRowThreads = 1024;
+constexpr int kRowMaxV4 = 4;  // float4 per thread: n_cols <= 16384 on the vector path
+
+__device__ __forceinline__ float row_dot(const float *__restrict__ wr, const float *__restrict__ x, int n_cols,
+                                         bool vec4) {
+    typedef float fv4 __attribute__((ext_vector_type(4)));
+    const int tid = threadIdx.x;
     float acc = 0.0f;
-    if (row < n_rows) {
-        const float *wr = w + (size_t)row * n_cols;
-        if (vec4) {
-            typedef float fv4 __attribute__((ext_vector_type(4)));
-            const fv4 *w4 = (const fv4 *)wr;
-            const fv4 *x4 = (const fv4 *)x;
-            for (int c = lane; c < n_cols / 4; c += 64) {
-                fv4 a = __builtin_nontemporal_load(w4 + c), b = x4[c];
-                acc = fmaf(a.x, b.x, acc);
-                acc = fmaf(a.y, b.y, acc);
-                acc = fmaf(a.z, b.z, acc);
-                acc = fmaf(a.w, b.w, acc);
-            }
-        } else {
-            for (int c = lane; c < n_cols; c += 64) acc = fmaf(wr[c], x[c], acc);
+    if (vec4) {
+        const fv4 *w4 = (const fv4 *)wr;
+        const fv4 *x4 = (const fv4 *)x;
+        const int n4 = n_cols / 4;
+        fv4 a[kRowMaxV4], b[kRowMaxV4];
+#pragma unroll
+        for (int i = 0; i < kRowMaxV4; i++) {
+            const int c = min(tid + i * kRowThreads, n4 - 1);  // clamped: branch-free loads
+            a[i] = __builtin_nontemporal_load(w4 + c);
+            b[i] = x4[c];
         }
+#pragma unroll
+        for (int i = 0; i < kRowMaxV4; i++) {
+            float t = fmaf(a[i].x, b[i].x, acc);
+            t = fmaf(a[i].y, b[i].y, t);
+            t = fmaf(a[i].z, b[i].z, t);
+            t = fmaf(a[i].w, b[i].w, t);
+            acc = tid + i * kRowThreads < n4 ? t : acc;
+        }
+    } else {
+        for (int c = tid; c < n_cols; c += kRowThreads) acc = fmaf(wr[c], x[c], acc);
     }
-    acc = sum64_lane63(acc);
-    if (lane == 63 && row < n_rows) y[row] = acc;
+    return acc;
+}
+
+// Workgroup sum in a fixed order (wave sums, then wave 0 .. 15): deterministic.
+__device__ __forceinline__ float block_sum(float v, float *part) {
+    v = sum64_lane63(v);
+    if (lane_id() == 63) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+    if (threadIdx.x == 0)
+        for (int i = 0; i < kRowThreads / 64; i++) s += part[i];
+    return s;
+}
+
+__global__ void __launch_bounds__(kRowThreads) matvec_f32_kernel(const float *__restrict__ w,
+                                                                 const float *__restrict__ x,
+                                                                 float *__restrict__ y, int n_cols, int vec4) {
+    __shared__ float part[kRowThreads / 64];
+    const int row = blockIdx.x;
+    const float s = block_sum(row_dot(w + (size_t)row * n_cols, x, n_cols, vec4), part);
+    if (threadIdx.x == 0) y[row] = s;
 }
 
 int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols,
                       hipStream_t stream) {
     if (!w || !x || !y || n_rows <= 0 || n_cols <= 0) return set_error(kErrBadArg, "matvec_f32: bad arguments");
-    const int vec4 = (n_cols % 4 == 0) && (((uintptr_t)w | (uintptr_t)x) % 16 == 0);
-    const int wpb = 4;
-    hipLaunchKernelGGL(matvec_f32_kernel, dim3((n_rows + wpb - 1) / wpb), dim3(64 * wpb), 0, stream,
-                       w, x, y, n_rows, n_cols, vec4);
+    const int vec4 = (n_cols % 4 == 0) && (n_cols <= 4 * kRowMaxV4 * kRowThreads) &&
+                     (((uintptr_t)w | (uintptr_t)x) % 16 == 0);
+    hipLaunchKernelGGL(matvec_f32_kernel, dim3(n_rows), dim3(kRowThreads), 0, stream, w, x, y, n_cols, vec4);
     return check_launch("matvec_f32");
 }
 
@@ -121,6 +148,90 @@ int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k,
                          64 * kTopkMaxPerLane);
     hipLaunchKernelGGL(topk_softmax_kernel, dim3(1), dim3(64), 0, stream, scores, idx, wts, n, k);
     return check_launch("topk_softmax");
+}
+
+// ---------------------------------------------------------------- router + top-k, one launch
+// The decode MoE block's router (kernels.cu:859-880) and top-k softmax (kernels.cu:993-1057)
+// in one launch: workgroup r computes logit r; the last workgroup to finish (an arrival
+// counter) selects the top k by rank -- logit i's rank is the number of logits ordered
+// before it by (value desc, index asc), so the k winners come out sorted and ties go to the
+// lower index, as topk_wave orders them -- and writes the softmax over the winners.
+// Logits <= -1e30 and NaN never win.  The counter must be zero before the first launch;
+// the last workgroup resets it.  Logits cross workgroups (and XCDs) as agent-scope atomic
+// stores/loads; each writer waits for its store before counting in.
+__global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *__restrict__ w,
+                                                                 const float *__restrict__ x,
+                                                                 float *__restrict__ logits, int n, int n_cols,
+                                                                 int k, int *__restrict__ cnt,
+                                                                 int *__restrict__ idx, float *__restrict__ wts,
+                                                                 int vec4) {
+    __shared__ float part[kRowThreads / 64];
+    __shared__ int is_last;
+    __shared__ float z[64 * kTopkMaxPerLane];
+    __shared__ float sel_v[kTopkMaxK];
+    __shared__ int sel_i[kTopkMaxK];
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x;
+    const float v = block_sum(row_dot(w + (size_t)row * n_cols, x, n_cols, vec4), part);
+    if (tid == 0) {
+        __hip_atomic_store(logits + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = old == n - 1;
+        if (is_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    for (int i = tid; i < n; i += kRowThreads) {
+        const float l = __hip_atomic_load(logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        z[i] = l > -1e30f ? l : -1e30f;  // NaN and <= -1e30 never win
+    }
+    if (tid < k) sel_i[tid] = -1;
+    __syncthreads();
+    // G threads per candidate (a power of two, within a wave) count the candidates ordered
+    // before it over a strided share of j; the counts meet in G-lane shuffle sums
+    int G = 1;
+    while (G < 64 && G * 2 * n <= kRowThreads) G *= 2;
+    const int sub = tid & (G - 1);
+    for (int i = tid / G; i < n; i += kRowThreads / G) {
+        const float zi = z[i];
+        int rank = 0;
+        for (int j = sub; j < n; j += G) {
+            const float zj = z[j];
+            rank += (zj > -1e30f) && better(zj, j, zi, i);
+        }
+        for (int o = 1; o < G; o <<= 1) rank += __shfl_xor(rank, o);
+        if (sub == 0 && zi > -1e30f && rank < k) {
+            sel_v[rank] = zi;
+            sel_i[rank] = i;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const float mx = sel_v[0];
+        float e[kTopkMaxK], sum = 0.0f;
+        for (int r = 0; r < k; r++) {
+            e[r] = sel_i[r] >= 0 ? expf(sel_v[r] - mx) : 0.0f;
+            sum += e[r];
+        }
+        for (int r = 0; r < k; r++) {
+            idx[r] = sel_i[r];
+            wts[r] = sum > 0.0f ? e[r] / sum : 0.0f;
+        }
+    }
+}
+
+int launch_router_topk(const float *w, const float *x, float *logits, int n, int n_cols, int k, int *cnt, int *idx,
+                       float *wts, hipStream_t stream) {
+    if (!w || !x || !logits || !cnt || !idx || !wts || n <= 0 || n_cols <= 0 || k <= 0 || k > kTopkMaxK ||
+        k > n || n > 64 * kTopkMaxPerLane)
+        return set_error(kErrBadArg, "router_topk: need 0 < k <= min(%d, n_experts), n_experts <= %d", kTopkMaxK,
+                         64 * kTopkMaxPerLane);
+    const int vec4 = (n_cols % 4 == 0) && (n_cols <= 4 * kRowMaxV4 * kRowThreads) &&
+                     (((uintptr_t)w | (uintptr_t)x) % 16 == 0);
+    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, logits, n, n_cols, k, cnt,
+                       idx, wts, vec4);
+    return check_launch("router_topk");
 }
 
 // ---------------------------------------------------------------- elementwise glue

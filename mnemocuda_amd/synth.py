@@ -98,11 +98,11 @@ def expert_table_torch(gen, n_experts: int, hidden: int, eff: int, down_type: in
     import torch
     stride, _, up_off, down_off = expert_layout(hidden, eff, down_type)
     t = torch.zeros((n_experts, stride), dtype=torch.uint8, device=device)
-    for e in range(n_experts):
-        t[e, :up_off] = weights_torch(gen, 12, eff, hidden, device)
-        t[e, up_off:down_off] = weights_torch(gen, 12, eff, hidden, device)
-        dw = weights_torch(gen, down_type, hidden, eff, device)
-        t[e, down_off:down_off + dw.numel()] = dw
+    g = up_off
+    t[:, :up_off] = weights_torch(gen, 12, n_experts * eff, hidden, device).view(n_experts, g)
+    t[:, up_off:down_off] = weights_torch(gen, 12, n_experts * eff, hidden, device).view(n_experts, g)
+    dw = weights_torch(gen, down_type, n_experts * hidden, eff, device)
+    t[:, down_off:down_off + dw.numel() // n_experts] = dw.view(n_experts, -1)
     return t.reshape(-1)
 
 

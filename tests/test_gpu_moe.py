@@ -167,7 +167,7 @@ def test_moe_decode_vs_oracle(gpu, oracle, H, EFF, E, k, DT):
     lay = synth.expert_layout(H, EFF, DT)
     router, x = _routable(rng, E, H, k)
     out0 = rng.standard_normal(H).astype(np.float32)
-    ws = torch.empty(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
     out = dev(out0)
     idx = torch.full((k,), -1, dtype=torch.int32, device="cuda")
     w = torch.zeros(k, device="cuda")
@@ -193,7 +193,7 @@ def test_moe_decode_graph_replays(gpu):
     lay = synth.expert_layout(H, EFF, DT)
     router = dev((rng.standard_normal((E, H)) / 32).astype(np.float32))
     x = dev(rng.standard_normal(H).astype(np.float32))
-    ws = torch.empty(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
     out = torch.zeros(H, device="cuda")
     case("moe_decode eager")
     gpu.ops.moe_decode(router, table, *lay, DT, x, H, EFF, E, k, ws, out)
