@@ -45,65 +45,62 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
 }
 
 // ------------------------------------------------------------------ raw loads (step k)
-// Each thread owns one row (weights) / one token (activations) and one half (32 values)
-// of the 64-wide K step.
+// 512 loader threads: thread t owns row (weights) / token (activations) t/4 and quarter
+// q = t%4 (16 values) of the 64-wide K step.
 struct RawW {
-    uint4 a, b, c, d;  // Q4_K: a = header, b = 16 qs bytes;  Q6_K: a,b = 32 ql, c,d = 32 qh
-    uint32_t s, dd;    // Q6_K: two int8 scales, f16 d
+    uint4 a, b;       // Q4_K: a = header (d, dmin, 12 scale bytes), b = 16 qs bytes
+                      // Q6_K: a = 16 ql bytes, b = 16 qh bytes
+    uint32_t s, dd;   // Q6_K: the int8 scale of the 16 values, f16 d
 };
-// Activation chunk of one step half: staged f16 values, or a raw Q8_1 sub-block.
+// Activation quarter: staged f16 values, or 16 int8 of a raw Q8_1 sub-block.
 template <bool Q8>
 struct RawA {
-    uint4 a, b, c, d;  // 32 f16 values
+    uint4 a, b;  // 16 f16 values
 };
 template <>
 struct RawA<true> {
-    uint4 a, b;   // 32 int8
-    uint32_t ds;  // half2 (d, d*sum) of the 32
+    uint4 a;      // 16 int8
+    uint32_t ds;  // half2 (d, d*sum) of their 32-value sub-block
 };
 
-// Q4_K step ks = super-block ks/4, nibble group g = ks%4 (qs bytes 32g..32g+31); half h
-// takes bytes 32g+16h .. +15: 16 weights of sub-block 2g (low nibbles) and 16 of 2g+1.
-__device__ __forceinline__ void load_w_q4k(const uint8_t *__restrict__ wrow, int ks, int h, RawW &r) {
+// Q4_K step ks: super-block ks/4, nibble group g = ks%4 (qs bytes 32g..32g+31).  Quarter q:
+// qs bytes 32g + 16(q%2) .. +15, low nibbles (sub-block 2g) for q < 2, else high (2g+1).
+__device__ __forceinline__ void load_w_q4k(const uint8_t *__restrict__ wrow, int ks, int q, RawW &r) {
     const uint8_t *blk = wrow + (size_t)(ks >> 2) * kQ4KBytes;
     r.a = ld16(blk);
-    r.b = ld16(blk + 16 + 32 * (ks & 3) + 16 * h);
+    r.b = ld16(blk + 16 + 32 * (ks & 3) + 16 * (q & 1));
 }
 
-// Q6_K step ks covers values 64*(ks%4) .. +63 of super-block ks/4: half hh = (ks%4)/2,
-// groups 2(ks%2) and 2(ks%2)+1; half h takes group grp = 2(ks%2) + h, i.e. ql bytes
-// [64hh + 32h, +32) (low nibbles if grp < 2, else high) and qh bytes [32hh, +32) at 2grp.
-__device__ __forceinline__ void load_w_q6k(const uint8_t *__restrict__ wrow, int ks, int h, RawW &r) {
+// Q6_K step ks: values 64(ks%4) .. +63 of super-block ks/4, half hh = (ks%4)/2, groups
+// 2(ks%2) .. +1.  Quarter q: group grp = 2(ks%2) + q/2, values 16(q%2) .. +15 of it: ql bytes
+// 64hh + 32(q/2) + 16(q%2) (low nibbles if grp < 2, else high), qh bytes 32hh + 16(q%2) at
+// bit 2grp, scale byte 8hh + 2grp + q%2.
+__device__ __forceinline__ void load_w_q6k(const uint8_t *__restrict__ wrow, int ks, int q, RawW &r) {
     const uint8_t *blk = wrow + (size_t)(ks >> 2) * kQ6KBytes;
-    const int g = ks & 3, hh = g >> 1, grp = 2 * (g & 1) + h;
-    r.a = ld16(blk + 64 * hh + 32 * h);
-    r.b = ld16(blk + 64 * hh + 32 * h + 16);
-    r.c = ld16(blk + 128 + 32 * hh);
-    r.d = ld16(blk + 128 + 32 * hh + 16);
-    uint16_t s, dd;
-    __builtin_memcpy(&s, blk + 192 + 8 * hh + 2 * grp, 2);
+    const int g = ks & 3, hh = g >> 1, grp = 2 * (g & 1) + (q >> 1);
+    r.a = ld16(blk + 64 * hh + 32 * (q >> 1) + 16 * (q & 1));
+    r.b = ld16(blk + 128 + 32 * hh + 16 * (q & 1));
+    uint8_t sc;
+    uint16_t dd;
+    __builtin_memcpy(&sc, blk + 192 + 8 * hh + 2 * grp + (q & 1), 1);
     __builtin_memcpy(&dd, blk + 208, 2);
-    r.s = s;
+    r.s = sc;
     r.dd = dd;
 }
 
-// Activations of step ks, half h: values 64ks + 32h .. +31 = one Q8_1 sub-block.
-// Half h of step ks: activations ks*64 + 32h .. +31 of the row (staged f16 row, or the
-// row's Q8_1 MMQ blocks: block v/128, sub-block (v/32)%4).
-__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int h, RawA<false> &r) {
-    const _Float16 *p = (const _Float16 *)arow + ks * kKS + 32 * h;
+// Activations of step ks, quarter q: values 64ks + 16q .. +15 of the row (staged f16 row,
+// or the row's Q8_1 MMQ blocks: block v/128, sub-block (v/32)%4).
+__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int q, RawA<false> &r) {
+    const _Float16 *p = (const _Float16 *)arow + ks * kKS + 16 * q;
     r.a = ld16((const uint8_t *)(p));
     r.b = ld16((const uint8_t *)(p + 8));
-    r.c = ld16((const uint8_t *)(p + 16));
-    r.d = ld16((const uint8_t *)(p + 24));
 }
-__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int h, RawA<true> &r) {
-    const int v0 = ks * kKS + 32 * h;
+__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int q, RawA<true> &r) {
+    const int v0 = ks * kKS + 16 * q;
     const uint8_t *blk = (const uint8_t *)arow + (size_t)(v0 >> 7) * kQ81Bytes;
     const int sub = (v0 >> 5) & 3;
     __builtin_memcpy(&r.ds, blk + 4 * sub, 4);
-    r.a = ld16(blk + 16 + 32 * sub);
-    r.b = ld16(blk + 32 + 32 * sub);
+    r.a = ld16(blk + 16 + (v0 & 127));
 }
 
 // ------------------------------------------------------------------ LDS tiles
@@ -151,101 +148,96 @@ __device__ __forceinline__ void q8x4_to_f16(uint32_t v, h2 d2, uint32_t &o0, uin
     o1 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04030402u) + off) * d2);
 }
 
-// Q4_K: half h of step ks holds 16 weights of sub-block 2g (K columns 16h .. 16h+15 of the
-// step: chunks 2h, 2h+1) and 16 of sub-block 2g+1 (columns 32+16h ..: chunks 4+2h, 5+2h).
-__device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int h, _Float16 *tile, int row) {
-    const int g = ks & 3;
-    const uint32_t s0 = r.a.y, s1 = r.a.z, s2 = r.a.w;
-    uint32_t sc0, m0, sc1, m1;
-    if (g < 2) {  // uniform per step
-        const int sh = 16 * g;
-        sc0 = (s0 >> sh) & 63; m0 = (s1 >> sh) & 63;
-        sc1 = (s0 >> (sh + 8)) & 63; m1 = (s1 >> (sh + 8)) & 63;
-    } else {
-        const int sh = 16 * (g - 2);
-        sc0 = ((s2 >> sh) & 15) | (((s0 >> (sh + 6)) & 3) << 4);
-        m0 = ((s2 >> (sh + 4)) & 15) | (((s1 >> (sh + 6)) & 3) << 4);
-        sc1 = ((s2 >> (sh + 8)) & 15) | (((s0 >> (sh + 14)) & 3) << 4);
-        m1 = ((s2 >> (sh + 12)) & 15) | (((s1 >> (sh + 14)) & 3) << 4);
-    }
-    const float d = h2f(r.a.x & 0xFFFFu), dmin = h2f(r.a.x >> 16);
-    const _Float16 a0 = (_Float16)(d * (float)sc0), b0 = (_Float16)(-dmin * (float)m0);
-    const _Float16 a1 = (_Float16)(d * (float)sc1), b1 = (_Float16)(-dmin * (float)m1);
-    const h2 A0 = {a0, a0}, B0 = {b0, b0}, A1 = {a1, a1}, B1 = {b1, b1};
-    const uint32_t w[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-    uint32_t lo[8], hi[8];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint32_t ml = w[k] & 0x0F0F0F0Fu, mh = (w[k] >> 4) & 0x0F0F0F0Fu;
-        lo[2 * k] = dq_fma(ml, 0x04010400u, A0, B0);
-        lo[2 * k + 1] = dq_fma(ml, 0x04030402u, A0, B0);
-        hi[2 * k] = dq_fma(mh, 0x04010400u, A1, B1);
-        hi[2 * k + 1] = dq_fma(mh, 0x04030402u, A1, B1);
-    }
-    put16(tile, row, 2 * h, lo[0], lo[1], lo[2], lo[3]);
-    put16(tile, row, 2 * h + 1, lo[4], lo[5], lo[6], lo[7]);
-    put16(tile, row, 4 + 2 * h, hi[0], hi[1], hi[2], hi[3]);
-    put16(tile, row, 5 + 2 * h, hi[4], hi[5], hi[6], hi[7]);
+// byte i of the 12 packed scale bytes held in three dwords
+__device__ __forceinline__ uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xFFu;
 }
 
-// Q6_K: half h of step ks = group 2(ks%2) + h, K columns 32h .. 32h+31 (chunks 4h .. 4h+3).
-__device__ __forceinline__ void store_w_q6k(const RawW &r, int ks, int h, _Float16 *tile, int row) {
-    const int grp = 2 * (ks & 1) + h;
-    const float d = h2f(r.dd);
-    const _Float16 s0 = (_Float16)(d * (float)(int8_t)(r.s & 0xFF)), s1 = (_Float16)(d * (float)(int8_t)(r.s >> 8));
-    const h2 S0 = {s0, s0}, S1 = {s1, s1};
-    const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-    const uint32_t ql[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-    const uint32_t qh[8] = {r.c.x, r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w};
-    const int shl = grp >= 2 ? 4 : 0;
-    uint32_t o[16];
+// Q4_K quarter q of step ks: sub-block j = 2(ks%4) + q/2 (get_scale_min_k4, kernels.cu:45-53),
+// K columns 16q .. 16q+15 of the step (chunks 2q, 2q+1).
+__device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int q, _Float16 *tile, int row) {
+    const int j = 2 * (ks & 3) + (q >> 1);
+    const uint32_t s0 = r.a.y, s1 = r.a.z, s2 = r.a.w;
+    uint32_t sc, m;
+    if (j < 4) {
+        sc = sbyte(s0, s1, s2, j) & 63;
+        m = sbyte(s0, s1, s2, j + 4) & 63;
+    } else {
+        sc = (sbyte(s0, s1, s2, j + 4) & 15) | ((sbyte(s0, s1, s2, j - 4) >> 6) << 4);
+        m = (sbyte(s0, s1, s2, j + 4) >> 4) | ((sbyte(s0, s1, s2, j) >> 6) << 4);
+    }
+    const float d = h2f(r.a.x & 0xFFFFu), dmin = h2f(r.a.x >> 16);
+    const _Float16 a = (_Float16)(d * (float)sc), b = (_Float16)(-dmin * (float)m);
+    const h2 A = {a, a}, B = {b, b};
+    const int sh = 4 * (q >> 1);
+    const uint32_t w[4] = {(r.b.x >> sh) & 0x0F0F0F0Fu, (r.b.y >> sh) & 0x0F0F0F0Fu, (r.b.z >> sh) & 0x0F0F0F0Fu,
+                           (r.b.w >> sh) & 0x0F0F0F0Fu};
+    uint32_t o[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int k = 0; k < 4; k++) {
+        o[2 * k] = dq_fma(w[k], 0x04010400u, A, B);
+        o[2 * k + 1] = dq_fma(w[k], 0x04030402u, A, B);
+    }
+    put16(tile, row, 2 * q, o[0], o[1], o[2], o[3]);
+    put16(tile, row, 2 * q + 1, o[4], o[5], o[6], o[7]);
+}
+
+// Q6_K quarter q of step ks: group grp = 2(ks%2) + q/2, its values 16(q%2) .. +15; K columns
+// 16q .. 16q+15 of the step (chunks 2q, 2q+1).
+__device__ __forceinline__ void store_w_q6k(const RawW &r, int ks, int q, _Float16 *tile, int row) {
+    const int grp = 2 * (ks & 1) + (q >> 1);
+    const _Float16 sc = (_Float16)(h2f(r.dd) * (float)(int8_t)(r.s & 0xFF));
+    const h2 S = {sc, sc};
+    const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    const uint32_t ql[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+    const uint32_t qh[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    const int shl = grp >= 2 ? 4 : 0;
+    uint32_t o[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
         // 6-bit q in bits 0..5 of each byte
         const uint32_t lo = (ql[k] >> shl) & 0x0F0F0F0Fu;
         const uint32_t hi = (2 * grp <= 4 ? (qh[k] << (4 - 2 * grp)) : (qh[k] >> (2 * grp - 4))) & 0x30303030u;
-        const uint32_t q = lo | hi;
-        const h2 S = k < 4 ? S0 : S1;
-        o[2 * k] = __builtin_bit_cast(uint32_t, (magic_pair(q, 0x04010400u) + off) * S);
-        o[2 * k + 1] = __builtin_bit_cast(uint32_t, (magic_pair(q, 0x04030402u) + off) * S);
+        const uint32_t v = lo | hi;
+        o[2 * k] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04010400u) + off) * S);
+        o[2 * k + 1] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04030402u) + off) * S);
     }
-#pragma unroll
-    for (int k = 0; k < 4; k++) put16(tile, row, 4 * h + k, o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+    put16(tile, row, 2 * q, o[0], o[1], o[2], o[3]);
+    put16(tile, row, 2 * q + 1, o[4], o[5], o[6], o[7]);
 }
 
-// Half h: K columns 32h .. 32h+31 (chunks 4h .. 4h+3) of the activation row.
-__device__ __forceinline__ void store_a(const RawA<false> &r, int h, _Float16 *tile, int row, float) {
-    put16(tile, row, 4 * h, r.a.x, r.a.y, r.a.z, r.a.w);
-    put16(tile, row, 4 * h + 1, r.b.x, r.b.y, r.b.z, r.b.w);
-    put16(tile, row, 4 * h + 2, r.c.x, r.c.y, r.c.z, r.c.w);
-    put16(tile, row, 4 * h + 3, r.d.x, r.d.y, r.d.z, r.d.w);
+// Quarter q: K columns 16q .. 16q+15 (chunks 2q, 2q+1) of the activation row.
+__device__ __forceinline__ void store_a(const RawA<false> &r, int q, _Float16 *tile, int row, float) {
+    put16(tile, row, 2 * q, r.a.x, r.a.y, r.a.z, r.a.w);
+    put16(tile, row, 2 * q + 1, r.b.x, r.b.y, r.b.z, r.b.w);
 }
 // Raw Q8_1: d8 * 2^-e (exact) times q8, as the staging kernel computes it.
-__device__ __forceinline__ void store_a(const RawA<true> &r, int h, _Float16 *tile, int row, float as) {
+__device__ __forceinline__ void store_a(const RawA<true> &r, int q, _Float16 *tile, int row, float as) {
     const _Float16 d = (_Float16)(h2f(r.ds & 0xFFFF) * as);
     const h2 d2 = {d, d};
-    const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-    uint32_t o[16];
+    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+    uint32_t o[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) q8x4_to_f16(w[k], d2, o[2 * k], o[2 * k + 1]);
-#pragma unroll
-    for (int k = 0; k < 4; k++) put16(tile, row, 4 * h + k, o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+    for (int k = 0; k < 4; k++) q8x4_to_f16(w[k], d2, o[2 * k], o[2 * k + 1]);
+    put16(tile, row, 2 * q, o[0], o[1], o[2], o[3]);
+    put16(tile, row, 2 * q + 1, o[4], o[5], o[6], o[7]);
 }
 
 // ------------------------------------------------------------------ kernel
-// Workgroup of 4 waves computes a 128 x 128 tile (weights x tokens) over one K slice
-// (blockIdx.z of `splits`); wave w owns rows 64*(w%2) .. +63 and tokens 64*(w/2) .. +63
-// (4 x 4 MFMA tiles).  Raw blocks are prefetched kPF-1 steps ahead into a ring of
+// Workgroup of 8 waves computes a 128 x 128 tile (weights x tokens) over one K slice
+// (blockIdx.z of `splits`).  Wave w owns rows 64*(w%2) .. +63 and tokens 64*((w/2)%2) .. +63
+// (4 x 4 MFMA tiles) and K half w/4 of every 64-wide step; the two K halves are summed
+// through LDS at the end (fixed order).  Two waves per SIMD let one wave's conversion
+// overlap the other's MFMAs.  Raw blocks are prefetched kPF-1 steps ahead into a ring of
 // registers (the loop is unrolled by kPF so every ring index is static and the waits the
 // compiler inserts count exactly the outstanding steps).  With splits > 1 the partial
 // tiles are added into the (pre-zeroed) output with fp32 atomics, in an order that may
 // differ from run to run.
-#ifndef MNEMO_GEMM_SCHED
-#define MNEMO_GEMM_SCHED 0
-#endif
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kBM = 128, kBN = 128;
-constexpr int kPF = 4;
+constexpr int kPF = 6;      // raw ring slots: loads run kPF-2 steps ahead of their conversion
+constexpr int kUnroll = 6;  // lcm(kPF, 3 LDS buffers)
 
 template <int TYPE, bool Q8>
 __device__ __forceinline__ void load_step(const uint8_t *wrow, const void *arow, int ks, int h, RawW &rw,
@@ -263,24 +255,22 @@ __device__ __forceinline__ void store_step(const RawW &rw, const RawA<Q8> &ra, i
     store_a(ra, h, bt, row, as);
 }
 
-__device__ __forceinline__ void mfma_step(const _Float16 *as, const _Float16 *bs, int wi, int wj, int lane,
-                                          f4 (&acc)[4][4]) {
+// Fragments of one 32-wide K half (kh) of a step for 4 x 4 MFMA 16x16x32 tiles.
+__device__ __forceinline__ void read_frags(const _Float16 *as, const _Float16 *bs, int wi, int wj, int kh, int lane,
+                                           h8 (&af)[4], h8 (&bf)[4]) {
+    const int chunk = 4 * kh + (lane >> 4);
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-        h8 af[4], bf[4];
-        const int chunk = 4 * kk + (lane >> 4);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int ra = wi + 16 * t + (lane & 15), rb = wj + 16 * t + (lane & 15);
-            af[t] = *(const h8 *)(as + tile_off(ra, chunk));
-            bf[t] = *(const h8 *)(bs + tile_off(rb, chunk));
-        }
-#pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int b = 0; b < 4; b++)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
+    for (int t = 0; t < 4; t++) {
+        const int ra = wi + 16 * t + (lane & 15), rb = wj + 16 * t + (lane & 15);
+        af[t] = *(const h8 *)(as + tile_off(ra, chunk));
+        bf[t] = *(const h8 *)(bs + tile_off(rb, chunk));
     }
+}
+__device__ __forceinline__ void mfma_frags(const h8 (&af)[4], const h8 (&bf)[4], f4 (&acc)[4][4]) {
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
 }
 
 // Epilogue / operand-addressing modes of the kernel:
@@ -309,11 +299,11 @@ struct GemmArgs {
 
 template <int TYPE, int MODE, bool ATOMIC, bool Q8>
 __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
-    __shared__ __align__(16) _Float16 lds[2][2][kBM * kKS];  // [buffer][weights | tokens]
+    __shared__ __align__(16) _Float16 lds[3][2][kBM * kKS];  // [buffer][weights | tokens]
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int K = g.K;
-    const int wi = (wave & 1) * 64, wj = (wave >> 1) * 64;
+    const int wi = (wave & 1) * 64, wj = ((wave >> 1) & 1) * 64, kh = wave >> 2;
     const size_t wrow_bytes = (size_t)(K / 256) * (TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
     const int nks_all = K / kKS;
     const int ks0 = (int)((long)nks_all * blockIdx.z / g.splits);
@@ -340,8 +330,8 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
         Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
     }
 
-    // loader role: thread -> (LDS row lr, half lh); rows past the end re-read the last
-    const int lr = tid >> 1, lh = tid & 1;
+    // loader role: thread -> (LDS row lr, quarter lh); rows past the end re-read the last
+    const int lr = tid >> 2, lh = tid & 3;
     const uint8_t *wrow;
     if (MODE == kModeSwiGLU) {
         // LDS rows 64w .. 64w+31 = gate features i0 + 32w + (0..31), 64w+32 .. = up features
@@ -363,12 +353,13 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
         const uint8_t *ar = (const uint8_t *)g.A + (size_t)arow_idx * (K / 128) * kQ81Bytes;
         arow = ar;
         float dmax = 0.0f;
-        for (int b = lh; b < K / 128; b += 2) {
+        for (int b = lh; b < K / 128; b += 4) {
             const uint4 hd = ld16(ar + (size_t)b * kQ81Bytes);
             dmax = fmaxf(dmax, fmaxf(fmaxf(fabsf(h2f(hd.x & 0xFFFF)), fabsf(h2f(hd.y & 0xFFFF))),
                                      fmaxf(fabsf(h2f(hd.z & 0xFFFF)), fabsf(h2f(hd.w & 0xFFFF)))));
         }
         dmax = fmaxf(dmax, __shfl_xor(dmax, 1));
+        dmax = fmaxf(dmax, __shfl_xor(dmax, 2));
         const int e = row_exponent(dmax);
         a_scale = ldexpf(1.0f, -e);
         if (lh == 0) row_unscale[lr] = ldexpf(1.0f, e);
@@ -383,47 +374,58 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
 
+    // Pipeline: three LDS tile buffers.  In step ks a wave multiplies the fragments of step
+    // ks (read during step ks-1), reads the fragments of step ks+1 (its tile was completed
+    // before the previous barrier), converts step ks+2 into the third buffer, then meets
+    // the barrier.  Raw blocks sit in a ring of kPF register slots, loaded kPF-2 steps
+    // before their conversion.  The loop is unrolled by lcm(kPF, 3) so all indices are static.
     RawW rw[kPF];
     RawA<Q8> ra[kPF];
-    // prologue: steps ks0 .. ks0+kPF-2 in flight (clamped to the last step, unconditional)
 #pragma unroll
-    for (int p = 0; p < kPF - 1; p++) load_step<TYPE, Q8>(wrow, arow, min(ks0 + p, last), lh, rw[p], ra[p]);
+    for (int p = 0; p < kPF; p++) load_step<TYPE, Q8>(wrow, arow, min(ks0 + p, last), lh, rw[p], ra[p]);
     store_step<TYPE, Q8>(rw[0], ra[0], ks0, lh, lds[0][0], lds[0][1], lr, a_scale);
+    store_step<TYPE, Q8>(rw[1], ra[1], ks0 + 1, lh, lds[1][0], lds[1][1], lr, a_scale);
     __syncthreads();
+    h8 af[4], bf[4];
+    read_frags(lds[0][0], lds[0][1], wi, wj, kh, lane, af, bf);
 
-    for (int kb = ks0; kb < ks1; kb += kPF) {
+    for (int kb = ks0; kb < ks1; kb += kUnroll) {
 #pragma unroll
-        for (int p = 0; p < kPF; p++) {
+        for (int p = 0; p < kUnroll; p++) {
             const int ks = kb + p;
             if (ks < ks1) {  // uniform
-                load_step<TYPE, Q8>(wrow, arow, min(ks + kPF - 1, last), lh, rw[(p + kPF - 1) % kPF],
-                                ra[(p + kPF - 1) % kPF]);
-                const int cur = (ks - ks0) & 1;
-                mfma_step(lds[cur][0], lds[cur][1], wi, wj, lane, acc);
-                // after the last step this fills the idle buffer with data nobody reads
-                store_step<TYPE, Q8>(rw[(p + 1) % kPF], ra[(p + 1) % kPF], ks + 1, lh, lds[cur ^ 1][0],
-                                     lds[cur ^ 1][1], lr, a_scale);
-#if MNEMO_GEMM_SCHED
-                // interleave the conversion of the next step with this step's MFMAs
-                __builtin_amdgcn_sched_group_barrier(0x020, 6, 0);  // global loads
-                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // LDS reads (first half)
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, MNEMO_GEMM_SCHED, 0);
-                }
-                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // LDS reads (second half)
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x002, MNEMO_GEMM_SCHED, 0);
-                }
-                __builtin_amdgcn_sched_group_barrier(0x200, 8, 0);  // LDS writes
-#endif
+                // kb - ks0 is a multiple of kUnroll, so these are compile-time constants
+                const int r = p % kPF, b = p % 3;
+                load_step<TYPE, Q8>(wrow, arow, min(ks + kPF, last), lh, rw[r], ra[r]);
+                mfma_frags(af, bf, acc);
+                // (past the end these read and fill idle buffers with data nobody uses)
+                read_frags(lds[(b + 1) % 3][0], lds[(b + 1) % 3][1], wi, wj, kh, lane, af, bf);
+                store_step<TYPE, Q8>(rw[(r + 2) % kPF], ra[(r + 2) % kPF], ks + 2, lh, lds[(b + 2) % 3][0],
+                                     lds[(b + 2) % 3][1], lr, a_scale);
                 __syncthreads();
             }
         }
     }
+    // sum the two K halves: waves 4..7 hand their tiles to waves 0..3 through the (now idle)
+    // tile buffers, laid out lane-minor so the accesses are conflict-free
+    __syncthreads();
+    float *red = (float *)&lds[0][0][0] + (size_t)(wave & 3) * (64 * 64);
+    if (kh) {
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) red[((a * 4 + b) * 4 + e) * 64 + lane] = acc[a][b][e];
+    }
+    __syncthreads();
+    if (kh) return;
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[a][b][e] += red[((a * 4 + b) * 4 + e) * 64 + lane];
     // D layout (16x16 f32): lane l holds rows 4*(l/16)+e, column l%16.  Rows index
     // weights (A operand), columns activation rows (B operand).
     if (MODE == kModeSwiGLU) {
