@@ -207,6 +207,7 @@ def decode_bench(gen, stream, layers, tokens):
     q, kk, v = torch.empty(QD, device="cuda"), torch.empty(KVD, device="cuda"), torch.empty(KVD, device="cuda")
     hid = torch.empty(H, device="cuda")
     logits = torch.empty(VOCAB, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws = torch.zeros(ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
 
     def token():
@@ -215,6 +216,7 @@ def decode_bench(gen, stream, layers, tokens):
             ops.matvec_q4k_add(L["o"], q, xbuf[li], hid, H, QD)
             ops.moe_decode(routers[li], tables[li], stride, g_off, u_off, d_off, Q6K, hid, H, EFF, E, k, ws, hid)
         ops.matvec_q6k(lm_head, hid, logits, VOCAB, H)
+        ops.sample_token(logits, VOCAB, 0.7, 0.9, 12345, tok)
 
     with torch.cuda.stream(stream):
         xbuf.copy_(X[0])
@@ -243,7 +245,7 @@ def decode_bench(gen, stream, layers, tokens):
             "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
             "frac_hbm_peak": round(per_tok / ms / 1e6 / HBM_PEAK_GBS, 4),
             "experts_resident_GB": round(E * LAYERS * stride / 1e9, 1),
-            "launches_per_token": LAYERS * 6 + 1}
+            "launches_per_token": LAYERS * 5 + 2}
 
 
 def moe_prefill_bench(gen, stream):

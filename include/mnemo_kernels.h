@@ -129,6 +129,13 @@ void cuda_gemm_q4k(const void *weights, const void *act_q8, float *output, int M
 void mnemo_gemm_q6k(const void *weights, const void *act_q8, float *output, int M, int K, int N,
                     hipStream_t stream);
 
+/* ---- next token (kernels.cu:2208-2215, kernels.cu:2020-2174; forward.c:1703-1704) ------
+ * temperature <= 0: argmax of logits[vocab_size] (exact ties go to the lower index);
+ * else top-p sampling over the reference's 2048 candidates (8 per residue class mod 256),
+ * drawn with xoroshiro128+ seeded from rng_state.  Writes one int to d_result. */
+void cuda_sample_token(const float *logits, int vocab_size, float temperature, float top_p,
+                       unsigned long long rng_state, int *d_result, hipStream_t stream);
+
 /* ---- Grouped-expert prefill (no reference counterpart) ---------------------------------
  * The reference prefills MoE layers token by token through the decode chain
  * (src/forward.c:1783-1830; per expert src/forward.c:876-893).  This entry point computes

@@ -40,6 +40,8 @@ int launch_scaled_add(float *out, const float *x, float sc, int n, hipStream_t s
 int launch_quantize_q8_1(const float *src, void *dst, int K, int N, hipStream_t s);
 int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M, int K, int N, hipStream_t s);
 size_t moe_prefill_workspace_bytes(int T, int hidden, int eff, int E, int k);
+int launch_sample_token(const float *logits, int V, float temperature, float top_p, unsigned long long seed,
+                        int *out, hipStream_t stream);
 size_t moe_decode_workspace_bytes(int hidden, int eff, int E, int k);
 int launch_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
                       size_t up_off, size_t down_off, int down_type, const float *x, int hidden, int eff, int E,
@@ -211,6 +213,11 @@ void cuda_gemm_q4k(const void *w, const void *act, float *out, int M, int K, int
 
 void mnemo_gemm_q6k(const void *w, const void *act, float *out, int M, int K, int N, hipStream_t s) {
     launch_gemm_q8_1(kTypeQ6K, w, act, out, M, K, N, s);
+}
+
+void cuda_sample_token(const float *logits, int vocab_size, float temperature, float top_p,
+                       unsigned long long rng_state, int *d_result, hipStream_t s) {
+    launch_sample_token(logits, vocab_size, temperature, top_p, rng_state, d_result, s);
 }
 
 size_t mnemo_moe_prefill_workspace_bytes(int n_tokens, int hidden, int eff, int n_experts, int k) {

@@ -37,6 +37,7 @@ SIGNATURES: dict[str, tuple] = {
     "cuda_quantize_mmq_q8_1": (None, [fp, vp, i32, i32, stream_t]),
     "cuda_gemm_q4k": (None, [vp, vp, fp, i32, i32, i32, stream_t]),
     "mnemo_gemm_q6k": (None, [vp, vp, fp, i32, i32, i32, stream_t]),
+    "cuda_sample_token": (None, [fp, i32, f32, f32, C.c_ulonglong, ip, stream_t]),
     "mnemo_moe_prefill_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
     "mnemo_moe_prefill": (i32, [vp, sz, sz, sz, sz, i32, fp, ip, fp, i32, i32, i32, i32, i32, vp, sz, fp,
                                 stream_t]),

@@ -244,3 +244,13 @@ def moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, dow
                              None if topk_idx is None else _dev(topk_idx, "topk_idx", torch.int32),
                              None if topk_w is None else _dev(topk_w, "topk_w", torch.float32), _stream())
     _check_rc(lib, e, "mnemo_moe_decode")
+
+
+def sample_token(logits, vocab, temperature, top_p, seed, out):
+    """Next token from logits[vocab] (greedy for temperature <= 0, else top-p) into out[0]."""
+    lib = load_library()
+    if logits.numel() < vocab or out.numel() < 1:
+        raise MnemoError("sample_token: logits or out too small")
+    lib.cuda_sample_token(_dev(logits, "logits", torch.float32), vocab, float(temperature), float(top_p),
+                          int(seed) & 0xFFFFFFFFFFFFFFFF, _dev(out, "out", torch.int32), _stream())
+    check(lib, "cuda_sample_token")

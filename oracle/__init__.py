@@ -51,6 +51,10 @@ class Oracle:
         L.mo_dequant_q8_1_mmq.argtypes = [P, P, C.c_int, C.c_int]
         L.mo_gemm_q8_1.restype = C.c_int
         L.mo_gemm_q8_1.argtypes = [C.c_int, P, P, P, C.c_int, C.c_int, C.c_int]
+        L.mo_sample_token.restype = C.c_int
+        L.mo_sample_token.argtypes = [P, C.c_int, C.c_float, C.c_float, C.c_ulonglong, P, P]
+        L.mo_xoroshiro_next.restype = C.c_uint64
+        L.mo_xoroshiro_next.argtypes = [P, P]
         self.L = L
 
     @staticmethod
@@ -131,6 +135,19 @@ class Oracle:
         if self.L.mo_gemm_q8_1(type_id, self._p(w), self._p(a), self._p(out), M, K, N):
             raise ValueError(type_id)
         return out
+
+    def sample_token(self, logits: np.ndarray, temperature: float, top_p: float, seed: int):
+        z = np.ascontiguousarray(logits, np.float32)
+        u = C.c_float(0.0)
+        ns = C.c_float(0.0)
+        tok = self.L.mo_sample_token(self._p(z), z.size, C.c_float(temperature), C.c_float(top_p),
+                                     C.c_ulonglong(seed), C.byref(u), C.byref(ns))
+        return int(tok), float(u.value), float(ns.value)
+
+    def xoroshiro_next(self, s0: int, s1: int) -> tuple[int, int, int]:
+        a, b = C.c_uint64(s0), C.c_uint64(s1)
+        v = self.L.mo_xoroshiro_next(C.byref(a), C.byref(b))
+        return int(v), int(a.value), int(b.value)
 
     def moe_prefill(self, table: np.ndarray, stride: int, gate_off: int, up_off: int, down_off: int,
                     down_type: int, x: np.ndarray, idx: np.ndarray, w: np.ndarray, hidden: int, eff: int,

@@ -363,3 +363,78 @@ int mo_gemm_q8_1(int type_id, const void *w, const void *act, double *out, int M
     free(ad);
     return 0;
 }
+
+/* ---- next-token selection (kernels.cu:2020-2174) ---------------------------------------- */
+uint64_t mo_xoroshiro_next(uint64_t *s0, uint64_t *s1) {
+    /* kernels.cu:2134-2143: t = s0 ^ (s0 << 23); s0 = s1; s1 = t ^ s1 ^ (t >> 17) ^ (s1 >> 26) */
+    const uint64_t t = *s0 ^ (*s0 << 23);
+    *s0 = *s1;
+    *s1 = t ^ *s1 ^ (t >> 17) ^ (*s1 >> 26);
+    return *s0 + *s1;
+}
+
+int mo_sample_token(const float *logits, int V, float temperature, float top_p,
+                    unsigned long long seed, float *u_out, float *nsum_out) {
+    enum { BLOCK = 256, LK = 8, NC = BLOCK * LK };
+    float gmax = -1e30f;                        /* kernels.cu:2038-2047 */
+    for (int i = 0; i < V; i++) gmax = fmaxf(gmax, logits[i]);
+    if (temperature <= 0.0f) {                  /* argmax, ties to the lower index */
+        float bv = -1e30f;
+        int bi = 0;
+        for (int i = 0; i < V; i++)
+            if (logits[i] > bv) { bv = logits[i]; bi = i; }
+        return bi;
+    }
+    float csum[BLOCK];
+    static float cand_p[NC];
+    static int cand_id[NC];
+    for (int t = 0; t < BLOCK; t++) {           /* kernels.cu:2075-2104: per thread t */
+        float sum = 0.0f, hv[LK];
+        int hid[LK];
+        for (int k = 0; k < LK; k++) { hv[k] = -1.0f; hid[k] = -1; }
+        for (int i = t; i < V; i += BLOCK) {
+            const float p = expf((logits[i] - gmax) / temperature);
+            sum += p;
+            int mi = 0;
+            for (int k = 1; k < LK; k++)
+                if (hv[k] < hv[mi]) mi = k;
+            if (p > hv[mi]) { hv[mi] = p; hid[mi] = i; }
+        }
+        csum[t] = sum;
+        for (int k = 0; k < LK; k++) { cand_p[t * LK + k] = hv[k]; cand_id[t * LK + k] = hid[k]; }
+    }
+    for (int s = BLOCK / 2; s > 0; s >>= 1)     /* the tree of kernels.cu:2079-2083 */
+        for (int t = 0; t < s; t++) csum[t] += csum[t + s];
+    const float total = csum[0];
+    uint64_t s0 = seed, s1 = seed ^ 0xDEADBEEFCAFEBABEull;  /* kernels.cu:2127-2143 */
+    for (int w = 0; w < 3; w++) mo_xoroshiro_next(&s0, &s1);
+    const float r = (float)(mo_xoroshiro_next(&s0, &s1) >> 11) * (1.0f / 9007199254740992.0f);
+    const float mass = top_p * total;           /* kernels.cu:2145-2166: selection sort */
+    float cumul = 0.0f;
+    int n = 0;
+    for (int pick = 0; pick < NC; pick++) {
+        int best = pick;
+        for (int j = pick + 1; j < NC; j++)
+            if (cand_p[j] > cand_p[best]) best = j;
+        if (cand_p[best] <= 0.0f) break;
+        const float tp = cand_p[pick];
+        const int ti = cand_id[pick];
+        cand_p[pick] = cand_p[best]; cand_id[pick] = cand_id[best];
+        cand_p[best] = tp; cand_id[best] = ti;
+        cumul += cand_p[pick];
+        n = pick + 1;
+        if (cumul >= mass) break;
+    }
+    float nsum = 0.0f;                          /* kernels.cu:2168-2177 */
+    for (int i = 0; i < n; i++) nsum += cand_p[i];
+    const float target = r * nsum;
+    float acc = 0.0f;
+    int id = cand_id[0];
+    for (int i = 0; i < n; i++) {
+        acc += cand_p[i];
+        if (acc >= target) { id = cand_id[i]; break; }
+    }
+    if (u_out) *u_out = r;
+    if (nsum_out) *nsum_out = nsum;
+    return id;
+}

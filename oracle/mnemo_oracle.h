@@ -22,6 +22,11 @@
  *                        round-half-even ties) and an independent numpy restatement.
  *   mo_topk_softmax      numpy argsort (stable) + fp64 softmax.
  *   mo_gemm_*            numpy fp64 matmul of the dequantised operands.
+ *   mo_xoroshiro_next    an independent Python restatement of xoroshiro128+ (64-bit
+ *                        wrap-around arithmetic) over many seeds.
+ *   mo_sample_token      greedy = numpy argmax; top_p -> 0 draws the argmax for every
+ *                        seed; draw frequencies over many seeds match the renormalised
+ *                        nucleus distribution (chi-square); a numpy restatement.
  */
 #ifndef MNEMO_ORACLE_H
 #define MNEMO_ORACLE_H
@@ -71,6 +76,14 @@ void mo_dequant_q8_1_mmq(const void *src, float *out, int K, int N);
 
 /* out[j*M + i] = sum_k deq(W)[i][k] * deq(A)[j][k] in fp64 (column-major [N][M]). */
 int mo_gemm_q8_1(int type_id, const void *w, const void *act, double *out, int M, int K, int N);
+
+/* Next-token selection of kernels.cu:2020-2174: greedy argmax for temperature <= 0, else
+ * top-p over 2048 per-class candidates with the reference's fp32 summation orders and
+ * selection sort, xoroshiro128+ draw.  Returns the token; *u_out (may be NULL) gets the
+ * uniform draw, *nsum_out the renormalised nucleus mass. */
+int mo_sample_token(const float *logits, int V, float temperature, float top_p,
+                    unsigned long long seed, float *u_out, float *nsum_out);
+uint64_t mo_xoroshiro_next(uint64_t *s0, uint64_t *s1);
 
 #ifdef __cplusplus
 }

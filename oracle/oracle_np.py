@@ -143,3 +143,65 @@ def topk_softmax(scores: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
     v = scores[order].astype(np.float64)
     e = np.exp(v - v.max())
     return order.astype(np.int32), (e / e.sum()).astype(np.float32)
+
+
+# ------------------------------------------------------------------ next-token selection
+def xoroshiro_next(s0: int, s1: int) -> tuple[int, int, int]:
+    """xoroshiro128+ step as kernels.cu:2134-2143 writes it, in Python integers masked to 64 bits."""
+    M = (1 << 64) - 1
+    t = (s0 ^ (s0 << 23)) & M
+    s0n = s1
+    s1n = (t ^ s1 ^ (t >> 17) ^ (s1 >> 26)) & M
+    return (s0n + s1n) & M, s0n, s1n
+
+
+def sample_draw(seed: int) -> float:
+    """The uniform draw of kernels.cu:2127-2143 for one call."""
+    M = (1 << 64) - 1
+    s0, s1 = seed & M, (seed ^ 0xDEADBEEFCAFEBABE) & M
+    for _ in range(3):
+        _, s0, s1 = xoroshiro_next(s0, s1)
+    v, s0, s1 = xoroshiro_next(s0, s1)
+    return float(np.float32(np.float32(v >> 11) * np.float32(1.0 / 9007199254740992.0)))
+
+
+def sample_candidates(logits: np.ndarray, temperature: float):
+    """The 2048 candidates of kernels.cu:2085-2104 as a set: for every residue class
+    i mod 256, the 8 largest p with earlier indices winning ties (a scan that replaces its
+    minimum only by a strictly larger value keeps exactly those).  Returns (p, ids) sorted
+    by p descending, p in fp64."""
+    z = logits.astype(np.float64)
+    p = np.exp((z - z.max()) / temperature)
+    V = p.size
+    ids, ps = [], []
+    for c in range(256):
+        idx = np.arange(c, V, 256)
+        if idx.size == 0:
+            continue
+        order = np.lexsort((idx, -p[idx]))[:8]
+        ids.extend(idx[order].tolist())
+        ps.extend(p[idx[order]].tolist())
+    ids, ps = np.array(ids), np.array(ps)
+    o = np.argsort(-ps, kind="stable")
+    return ps[o], ids[o], p.sum()
+
+
+def sample_token(logits: np.ndarray, temperature: float, top_p: float, seed: int):
+    """Restatement of the top-p draw in fp64; returns (token, margin) where margin is the
+    distance of the draw from the nearest cumulative boundary, relative to the nucleus
+    mass (fp32 rounding in the reference can only move the choice when it is tiny)."""
+    if temperature <= 0:
+        return int(np.argmax(logits)), 1.0
+    ps, ids, total = sample_candidates(logits, temperature)
+    c = np.cumsum(ps)
+    n = int(np.searchsorted(c, top_p * total) + 1)
+    n = min(n, ps.size)
+    mass_margin = abs(c[n - 1] - top_p * total) / total if n - 1 < ps.size else 1.0
+    if n >= 2:
+        mass_margin = min(mass_margin, abs(c[n - 2] - top_p * total) / total)
+    nsum = c[n - 1]
+    target = sample_draw(seed) * nsum
+    k = int(np.searchsorted(c[:n], target))
+    k = min(k, n - 1)
+    margin = min(abs(c[k] - target), abs(target - (c[k - 1] if k else 0.0))) / nsum
+    return int(ids[k]), min(margin, mass_margin)

@@ -276,3 +276,67 @@ def test_gemm_vs_numpy(oracle, rng, type_id):
         out2 = oracle.gemm(12, w2.reshape(-1), act, M, K, N)
         ref2 = onp.dequant_q8_1_mmq(act, K).astype(np.float64) @ onp.dequant_matrix(w2.reshape(-1), 12, M, K).T
         assert rel_l2(out2, ref2) < 1e-12
+
+
+# ------------------------------------------------------------------ next-token selection
+def test_xoroshiro_matches_independent_restatement(oracle):
+    rng = np.random.default_rng(0)
+    for seed in [0, 1, 0xDEADBEEF, 2**63 + 12345] + rng.integers(0, 2**63, 20).tolist():
+        a, b = int(seed), int(seed) ^ 0xDEADBEEFCAFEBABE
+        x, y = a, b
+        for _ in range(6):
+            v1, a, b = oracle.xoroshiro_next(a, b)
+            v2, x, y = onp.xoroshiro_next(x, y)
+            assert (v1, a, b) == (v2, x, y)
+
+
+def test_sample_greedy_is_first_argmax(oracle):
+    rng = np.random.default_rng(1)
+    z = rng.standard_normal(5000).astype(np.float32)
+    z[[17, 4000]] = z.max() + 1.0  # an exact tie: the lower index wins
+    assert oracle.sample_token(z, 0.0, 0.9, 7)[0] == 17
+    assert oracle.sample_token(z, -1.0, 0.9, 7)[0] == 17
+
+
+def test_sample_tiny_top_p_is_argmax(oracle):
+    rng = np.random.default_rng(2)
+    z = rng.standard_normal(151936).astype(np.float32)
+    for seed in range(20):
+        assert oracle.sample_token(z, 0.8, 1e-9, seed)[0] == int(np.argmax(z))
+
+
+@pytest.mark.parametrize("top_p", [1.0, 0.6])
+def test_sample_frequencies_follow_nucleus(oracle, top_p):
+    """Draw frequencies over many seeds against the renormalised nucleus distribution
+    (V < 2048, so every token is a candidate): chi-square well inside its bound."""
+    rng = np.random.default_rng(3)
+    V, T, n = 40, 0.9, 6000
+    z = rng.standard_normal(V).astype(np.float32)
+    p = np.exp((z.astype(np.float64) - z.max()) / T)
+    o = np.argsort(-p)
+    c = np.cumsum(p[o])
+    keep = o[: int(np.searchsorted(c, top_p * p.sum()) + 1)]
+    q = np.zeros(V)
+    q[keep] = p[keep] / p[keep].sum()
+    # random 64-bit seeds (four xoroshiro steps from seed, seed ^ const do not decorrelate
+    # consecutive small seeds; the draw quality itself is the reference's)
+    seeds = rng.integers(0, 2**63, n).tolist()
+    counts = np.bincount([oracle.sample_token(z, T, top_p, s)[0] for s in seeds], minlength=V)
+    assert counts[q == 0].sum() == 0
+    exp = q[q > 0] * n
+    chi2 = ((counts[q > 0] - exp) ** 2 / exp).sum()
+    dof = (q > 0).sum() - 1
+    assert chi2 < dof + 6 * np.sqrt(2 * dof)
+
+
+def test_sample_matches_numpy_restatement(oracle):
+    rng = np.random.default_rng(4)
+    z = (rng.standard_normal(151936) * 3).astype(np.float32)
+    checked = 0
+    for seed in range(40):
+        tok, margin = onp.sample_token(z, 0.7, 0.9, seed)
+        if margin < 1e-5:
+            continue
+        assert oracle.sample_token(z, 0.7, 0.9, seed)[0] == tok
+        checked += 1
+    assert checked >= 30
