@@ -21,7 +21,7 @@ BUILD = ROOT / "_build"
 LIB = PKG / "libmnemo_hip.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
-HIP_SOURCES = ["abi.hip", "gemv.hip", "router.hip", "gemm.hip", "moe.hip", "sample.hip"]
+HIP_SOURCES = ["abi.hip", "gemv_launch.hip", "router.hip", "gemm.hip", "moe.hip", "sample.hip"]
 C_SOURCES = ["host/mnemo_host.c"]
 
 HIPCC_FLAGS = [
@@ -53,6 +53,12 @@ def build(jobs: int = 4) -> Path:
     for src in HIP_SOURCES:
         obj = BUILD / (Path(src).stem + ".hip.o")
         cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    # the GEMV kernels, once per workgroup size (gemv_launch.hip picks per launch)
+    for threads in (512, 256):
+        obj = BUILD / f"gemv{threads}.hip.o"
+        cmds.append([hipcc, *HIPCC_FLAGS, f"-DMNEMO_GEMV_THREADS={threads}", f"-DMNEMO_GEMV_NS=g{threads}", "-c",
+                     str(CSRC / "gemv.hip"), "-o", str(obj)])
         objs.append(obj)
     for src in C_SOURCES:
         obj = BUILD / (Path(src).stem + ".c.o")

@@ -30,12 +30,20 @@
 #include "mnemo_internal.hpp"
 
 namespace mnemo {
+// This file is compiled once per workgroup size (MNEMO_GEMV_THREADS) into the namespace
+// MNEMO_GEMV_NS; gemv_launch.hip picks the variant per launch.
+#ifndef MNEMO_GEMV_NS
+#define MNEMO_GEMV_NS g512
+#endif
+namespace MNEMO_GEMV_NS {
 
 #ifndef MNEMO_GEMV_THREADS
 #define MNEMO_GEMV_THREADS 512
 #endif
 constexpr int kGemvThreads = MNEMO_GEMV_THREADS;
-static_assert(kGemvThreads >= 512 && kGemvThreads <= 1024 && kGemvThreads % 64 == 0, "x image staging assumes 512..1024 threads");
+static_assert(kGemvThreads >= 256 && kGemvThreads <= 1024 && kGemvThreads % 64 == 0, "x image staging assumes 256..1024 threads");
+// float4 of x per thread for rows of up to kp_max columns
+constexpr int xpt_for(int kp_max) { return (kp_max + 4 * kGemvThreads - 1) / (4 * kGemvThreads); }
 
 // ------------------------------------------------------------------ x preparation
 // LDS image of x for a padded length kp (multiple of 256):
@@ -525,7 +533,7 @@ static int device_cus() {
     return cus;
 }
 
-int launch_gemv(GemvArgs a, hipStream_t stream) {
+int launch_gemv_impl(GemvArgs a, hipStream_t stream) {
     if (a.n_cols < 4 || a.n_cols > kMaxGemvCols) return kErrBadArg;
     const int kp = (a.n_cols + 255) & ~255;
     // half super-blocks per row -> lanes per row (pow2, <= 64) and rows per wave pass
@@ -562,10 +570,10 @@ int launch_gemv(GemvArgs a, hipStream_t stream) {
     constexpr int T4 = 4 * kGemvThreads;
     constexpr int X4K = (4096 + T4 - 1) / T4, X8K = (8192 + T4 - 1) / T4, X16K = (16384 + T4 - 1) / T4;
     switch (lpr) {
-    case 2: launch<2, 1, 1>(a, tm, blocks, lds, stream); break;
-    case 4: launch<4, 1, 1>(a, tm, blocks, lds, stream); break;
-    case 8: launch<8, 1, 1>(a, tm, blocks, lds, stream); break;
-    case 16: launch<16, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 2: launch<2, 1, xpt_for(256)>(a, tm, blocks, lds, stream); break;
+    case 4: launch<4, 1, xpt_for(512)>(a, tm, blocks, lds, stream); break;
+    case 8: launch<8, 1, xpt_for(1024)>(a, tm, blocks, lds, stream); break;
+    case 16: launch<16, 1, xpt_for(2048)>(a, tm, blocks, lds, stream); break;
     case 32: launch<32, 1, X4K>(a, tm, blocks, lds, stream); break;
     default:
         if (kp <= 8192) launch<64, 1, X8K>(a, tm, blocks, lds, stream);
@@ -577,7 +585,7 @@ int launch_gemv(GemvArgs a, hipStream_t stream) {
 // Expert mode: lpr from n_cols as for the static launch; the rows of one matrix must be a
 // multiple of a workgroup's rows so that a workgroup never spans two slots (its x image
 // and its row tile belong to one slot).
-int launch_gemv_experts(GemvArgs a, hipStream_t stream) {
+int launch_gemv_experts_impl(GemvArgs a, hipStream_t stream) {
     if (a.n_cols < 4 || a.n_cols > kMaxGemvCols) return kErrBadArg;
     const int kp = (a.n_cols + 255) & ~255;
     const int uph = kp / 128;
@@ -599,10 +607,10 @@ int launch_gemv_experts(GemvArgs a, hipStream_t stream) {
     constexpr int T4 = 4 * kGemvThreads;
     constexpr int X4K = (4096 + T4 - 1) / T4, X8K = (8192 + T4 - 1) / T4, X16K = (16384 + T4 - 1) / T4;
     switch (lpr) {
-    case 2: launch<2, 1, 1>(a, tm, blocks, lds, stream); break;
-    case 4: launch<4, 1, 1>(a, tm, blocks, lds, stream); break;
-    case 8: launch<8, 1, 1>(a, tm, blocks, lds, stream); break;
-    case 16: launch<16, 1, 1>(a, tm, blocks, lds, stream); break;
+    case 2: launch<2, 1, xpt_for(256)>(a, tm, blocks, lds, stream); break;
+    case 4: launch<4, 1, xpt_for(512)>(a, tm, blocks, lds, stream); break;
+    case 8: launch<8, 1, xpt_for(1024)>(a, tm, blocks, lds, stream); break;
+    case 16: launch<16, 1, xpt_for(2048)>(a, tm, blocks, lds, stream); break;
     case 32: launch<32, 1, X4K>(a, tm, blocks, lds, stream); break;
     default:
         if (kp <= 8192) launch<64, 1, X8K>(a, tm, blocks, lds, stream);
@@ -611,4 +619,5 @@ int launch_gemv_experts(GemvArgs a, hipStream_t stream) {
     return check_launch("gemv_experts");
 }
 
+}  // namespace MNEMO_GEMV_NS
 }  // namespace mnemo
