@@ -322,10 +322,11 @@ def main():
     value = BYTES_LAYER * LAYERS / r["step_s"] / 1e9
     ach = BYTES_QKV / r["d_qkv"] / 1e9
     prof = ROOT / "profiles" / "gemv_qkv_fused_traffic.json"
-    traffic = None
+    traffic, kname = None, "gemv_kernel<32, 1, *, false, 3>"
     if prof.exists():
         try:
-            traffic = json.loads(prof.read_text()).get("hbm_bytes_per_launch")
+            pj = json.loads(prof.read_text())
+            traffic, kname = pj.get("hbm_bytes_per_launch"), pj.get("kernel", kname)
         except Exception:
             traffic = None
     line = {
@@ -347,7 +348,7 @@ def main():
                    "global_batch": 1, "layers": LAYERS, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "gemv_kernel<32,1,2,false,3,1> (fused Q 8192 + K 512 Q4_K + V 512 Q6_K, 4096 cols)",
+                     "kernel": kname + " (fused Q 8192 + K 512 Q4_K + V 512 Q6_K, 4096 cols)",
                      "bytes_per_launch": BYTES_QKV, "avg_launch_us": round(r["d_qkv"] * 1e6, 3)},
         "extra": {
             "fraction_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),

@@ -2,10 +2,14 @@
 
     python -m mnemocuda_amd.profiling stats <trace_dir> <out.md> "<command>"
     python -m mnemocuda_amd.profiling traffic <fetch_dir> <write_dir> <out.json> <out.md> "<command>"
+    python -m mnemocuda_amd.profiling probe
+
+`probe` is the program the two `--pmc` passes profile: the fused QKV GEMV of bench.py's
+workload (one layer's weights, 4 launches), then the calibration copy.
 
 `stats` turns a `rocprofv3 --kernel-trace --stats --output-format csv` run into a table of
 kernel durations.  `traffic` reads two `--pmc` runs (FETCH_SIZE, then WRITE_SIZE) of
-`bench.py --copy-calibration`, which ends with a device copy of known size (torch.neg
+`probe`, which ends with a device copy of known size (torch.neg
 over 256 MiB of fp32: 256 MiB read, 256 MiB written): the copy's
 counter reading gives the bytes-per-count factor, and the fused QKV GEMV's readings times
 that factor give its HBM bytes per launch (bench.py reports them as roofline.traffic).
@@ -18,7 +22,13 @@ import sys
 from collections import defaultdict
 from pathlib import Path
 
-QKV_KERNEL = "gemv_kernel<32, 1, 2, false, 3>"
+# the fused QKV GEMV: a mixed-type launch (TM = 3) of the 32-lanes-per-row GEMV; the library
+# builds it for 512- and 256-thread workgroups and the QKV shape runs the 256-thread one
+QKV_KERNEL = "gemv_kernel<32, 1, *, false, 3>"
+
+
+def _is_qkv(name: str) -> bool:
+    return "gemv_kernel<32, 1, " in name and ", false, 3>" in name
 COPY_BYTES = 256 << 20  # bench.py --copy-calibration copies this many bytes
 
 
@@ -68,17 +78,17 @@ def traffic(fetch_dir: str, write_dir: str, out_json: str, out_md: str, command:
     res = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         per = _per_kernel(Path(d), counter)
-        qn, q = _pick(per, lambda n: QKV_KERNEL in n)
+        qn, q = _pick(per, _is_qkv)
         cn, c = _pick(per, lambda n: "neg_kernel" in n)
         factor = COPY_BYTES / c  # bytes per counter unit, from the copy of known size
         res[counter] = {"kernel": qn, "per_launch_counter": q, "copy_kernel": cn, "copy_counter": c,
                         "bytes_per_unit": factor, "bytes_per_launch": q * factor}
     total = res["FETCH_SIZE"]["bytes_per_launch"] + res["WRITE_SIZE"]["bytes_per_launch"]
-    out = {"kernel": QKV_KERNEL, "hbm_bytes_per_launch": round(total), "algorithmic_bytes_per_launch": 21827584,
+    out = {"kernel": res["FETCH_SIZE"]["kernel"], "hbm_bytes_per_launch": round(total), "algorithmic_bytes_per_launch": 21827584,
            "counters": res, "command": command}
     Path(out_json).write_text(json.dumps(out, indent=1) + "\n")
     lines = [f"command: `{command}`", "",
-             f"fused QKV GEMV (`{QKV_KERNEL}`), HBM bytes per launch from FETCH_SIZE + WRITE_SIZE, each scaled",
+             f"fused QKV GEMV (`{res['FETCH_SIZE']['kernel']}`), HBM bytes per launch from FETCH_SIZE + WRITE_SIZE, each scaled",
              f"by the same counter over a {COPY_BYTES >> 20} MiB device copy (read {COPY_BYTES >> 20} MiB, "
              f"write {COPY_BYTES >> 20} MiB):", "",
              "| counter | per launch (counter units) | copy reading | bytes per unit | bytes per launch |",
@@ -91,10 +101,34 @@ def traffic(fetch_dir: str, write_dir: str, out_json: str, out_md: str, command:
     return out
 
 
+def probe(launches: int = 4) -> None:
+    import torch
+    from mnemocuda_amd import ops, synth
+    Q4K, Q6K, H, QD, KVD = 12, 14, 4096, 8192, 512
+    torch.cuda.set_device(0)
+    ops.init()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+    wq, wk = synth.weights_torch(gen, Q4K, QD, H, "cuda"), synth.weights_torch(gen, Q4K, KVD, H, "cuda")
+    wv = synth.weights_torch(gen, Q6K, KVD, H, "cuda")
+    x = torch.randn(H, device="cuda", generator=gen)
+    q, k, v = torch.empty(QD, device="cuda"), torch.empty(KVD, device="cuda"), torch.empty(KVD, device="cuda")
+    for _ in range(launches):
+        ops.matvec_qkv(wq, Q4K, wk, Q4K, wv, Q6K, x, q, k, v, QD, KVD, H)
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("probe done", flush=True)
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         stats(sys.argv[2], sys.argv[3], sys.argv[4])
     elif sys.argv[1] == "traffic":
         traffic(sys.argv[2], sys.argv[3], sys.argv[4], sys.argv[5], sys.argv[6])
+    elif sys.argv[1] == "probe":
+        probe()
     else:
         raise SystemExit(__doc__)
