@@ -78,8 +78,8 @@ __device__ __forceinline__ void load_w_q4k(const uint8_t *__restrict__ wrow, int
 __device__ __forceinline__ void load_w_q6k(const uint8_t *__restrict__ wrow, int ks, int q, RawW &r) {
     const uint8_t *blk = wrow + (size_t)(ks >> 2) * kQ6KBytes;
     const int g = ks & 3, hh = g >> 1, grp = 2 * (g & 1) + (q >> 1);
-    r.a = ld16(blk + 64 * hh + 32 * (q >> 1) + 16 * (q & 1));
-    r.b = ld16(blk + 128 + 32 * hh + 16 * (q & 1));
+    r.a = ld16_a2(blk + 64 * hh + 32 * (q >> 1) + 16 * (q & 1));
+    r.b = ld16_a2(blk + 128 + 32 * hh + 16 * (q & 1));
     uint8_t sc;
     uint16_t dd;
     __builtin_memcpy(&sc, blk + 192 + 8 * hh + 2 * grp + (q & 1), 1);

@@ -213,11 +213,9 @@ __device__ __forceinline__ void load_q4k(const uint8_t *__restrict__ blk, int hf
 // 192 (the half uses 8hf .. 8hf+7), d at 208 (kernels.cu:427-491;
 // validate_dequant.py:253-319).
 __device__ __forceinline__ void load_q6k(const uint8_t *__restrict__ blk, int hf, RawH &r) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) r.q[i] = ld16(blk + 64 * hf + 16 * i);
-    r.qh[0] = ld16(blk + 128 + 32 * hf);
-    r.qh[1] = ld16(blk + 144 + 32 * hf);
-    r.h = ld16(blk + 192);
+    ld16_a2<4>(blk + 64 * hf, r.q);
+    ld16_a2<2>(blk + 128 + 32 * hf, r.qh);
+    r.h = ld16_a2(blk + 192);
     uint16_t dd;
     __builtin_memcpy(&dd, blk + 208, 2);
     r.dd = dd;
@@ -249,9 +247,12 @@ __device__ __forceinline__ float q4k_dot(const RawH &r, int hf, int c, const XLd
         const int a1 = dot16(nb, d1b, dot16(na, d1a, 0));
         const int a2 = dot16(nb, d2b, dot16(na, d2a, 0));
         I[t] = 254 * a1 + a2;
-        // keep the scheduler from hoisting every sub-block's digit reads at once (that
-        // costs ~64 VGPRs and halves occupancy); other waves hide the LDS latency
+        // one sub-block's digit reads at a time: hoisting all of them costs ~64 VGPRs and
+        // occupancy.  The sched_barrier alone does not hold: the compiler sinks the
+        // arithmetic below later reads; the empty asm with the sub-block's result as an
+        // operand and a memory clobber pins both (62 instead of 96 VGPRs).
         __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" : "+v"(I[t])::"memory");
     }
     // four 6-bit scales and mins per dword: the packed form of get_scale_min_k4
     // (kernels.cu:45-53), the same unpacking as gemm_q4k.cu:53-56
@@ -308,6 +309,7 @@ __device__ __forceinline__ float q6k_dot(const RawH &r, int hf, int c, const XLd
         acc = fmaf((float)sc0, fmaf(uu[g], (float)i0, -32.0f * ss[2 * g]), acc);
         acc = fmaf((float)sc1, fmaf(uu[g], (float)i1, -32.0f * ss[2 * g + 1]), acc);
         __builtin_amdgcn_sched_barrier(0);
+        asm volatile("" : "+v"(acc)::"memory");  // as in q4k_dot (76 instead of 112 VGPRs)
     }
     return h2f(r.dd) * acc;
 }

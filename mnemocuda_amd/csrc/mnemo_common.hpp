@@ -28,6 +28,34 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) {
     __builtin_memcpy(&v, p, 16);
     return v;
 }
+// N 16-byte words from a 2-byte aligned address p.  Q6_K blocks are 210 B, so every other
+// block starts at 2 mod 4, and on gfx950 a 16-byte load from an address that is not 4-byte
+// aligned streams at ~2/3 of the aligned rate.  The words are loaded from the 4-byte
+// aligned address at or below p, plus one dword, and shifted into place with v_alignbyte.
+// Reads stay inside [p - 2, p + 16N): with p 4-byte aligned the extra dword is the last
+// one of the range again (unused).
+template <int N>
+__device__ __forceinline__ void ld16_a2(const uint8_t *p, uint4 (&out)[N]) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 2u;
+    const uint32_t *a = (const uint32_t *)(p - sh);
+    uint32_t w[4 * N + 1];
+#pragma unroll
+    for (int i = 0; i < N; i++) __builtin_memcpy(&w[4 * i], a + 4 * i, 16);
+    w[4 * N] = a[4 * N - (sh ? 0 : 1)];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        out[i].x = __builtin_amdgcn_alignbyte(w[4 * i + 1], w[4 * i], sh);
+        out[i].y = __builtin_amdgcn_alignbyte(w[4 * i + 2], w[4 * i + 1], sh);
+        out[i].z = __builtin_amdgcn_alignbyte(w[4 * i + 3], w[4 * i + 2], sh);
+        out[i].w = __builtin_amdgcn_alignbyte(w[4 * i + 4], w[4 * i + 3], sh);
+    }
+}
+__device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
+    uint4 o[1];
+    ld16_a2<1>(p, o);
+    return o[0];
+}
+
 __device__ __forceinline__ uint4 ld16_nt(const uint8_t *p) {
     // streaming weights: read once per call, do not keep them in the caches
     uint4 v;
