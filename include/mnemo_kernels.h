@@ -174,6 +174,63 @@ int mnemo_moe_decode(const float *router_w, const void *experts, size_t expert_s
                      size_t workspace_bytes, float *out, int *topk_idx, float *topk_w,
                      hipStream_t stream);
 
+/* ---- Attention chain around the projections (forward.c:687-786, graph form 1290-1420) ----
+ * Reference entry points, same arguments and semantics: */
+/* kernels.cu:1187-1193 (rms_norm_kernel :692-722): out = in * rsqrt(mean(in^2) + eps) * w. */
+void cuda_rms_norm(const float *input, const float *weight, float *output, int n, float eps,
+                   hipStream_t stream);
+/* kernels.cu:1178-1185 (:725-749): the same plus residual_output = input. */
+void cuda_rms_norm_residual(const float *input, const float *weight, float *normed_output,
+                            float *residual_output, int n, float eps, hipStream_t stream);
+/* kernels.cu:1221-1227 (:754-781): every head of head_dim values with the shared weight
+ * [head_dim]; output may equal input. */
+void cuda_rms_norm_batched(const float *input, const float *weight, float *output, int head_dim,
+                           int n_heads, float eps, hipStream_t stream);
+/* kernels.cu:1229-1236 (:1196-1219): q heads with q_weight, k heads with k_weight, in place. */
+void cuda_rms_norm_qk(float *q, float *k, const float *q_weight, const float *k_weight,
+                      int head_dim, int n_q, int n_k, float eps, hipStream_t stream);
+/* kernels.cu:1238-1244 (:784-793): out = a + b. */
+void cuda_residual_add(const float *a, const float *b, float *out, int n, hipStream_t stream);
+/* kernels.cu:1256-1273 (:818-852): rotates the pairs (j, j + head_dim/2) of every q and k
+ * head by pos / theta^(2j/head_dim), in place.  sin/cos are accurate (the reference's
+ * __sincosf approximation loses accuracy as pos grows). */
+void cuda_rope(float *q, float *k, int head_dim, int pos, float theta, int n_heads_q,
+               int n_heads_k, hipStream_t stream);
+/* kernels.cu:1328-1335 (:1320-1326): oa = f16(a), ob = f16(b), round to nearest even. */
+void cuda_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n,
+                          hipStream_t stream);
+/* kernels.cu:1526-1534 (:1493-1524): per head absmax a, scale = a/127, q = rne(x*127/a)
+ * clamped to +-127; out_* and *_scales point at the current position's row and slots. */
+void cuda_f32_to_int8_kv_dual(const float *k, const float *v, void *out_k, void *out_v,
+                              float *k_scales, float *v_scales, int head_dim, int n_kv_heads,
+                              hipStream_t stream);
+/* kernels.cu:1662-1673 (:1550-1660) and :1536-1546 (:1382-1481): softmax(scale q.k) v over
+ * positions 0..seq_len-1 of the cache [pos][n_kv_heads][head_dim] for every query head
+ * (kv head = head / gqa_ratio).  head_dim 64, 128 or 256. */
+void cuda_attention_f16kv(const void *q, const void *kv_k, const void *kv_v, float *out,
+                          int n_heads_q, int head_dim, int n_kv_heads, int seq_len, int gqa_ratio,
+                          float scale, hipStream_t stream);
+void cuda_attention_int8kv(const float *q, const void *kv_k, const void *kv_v,
+                           const float *k_scales, const float *v_scales, float *out,
+                           int n_heads_q, int head_dim, int n_kv_heads, int seq_len,
+                           int gqa_ratio, float scale, hipStream_t stream);
+
+/* New: the per-token steps 3-5 of forward.c:755-770 (QK norm, RoPE, KV store) in one launch
+ * with the position read from device memory (*pos_dev), so a captured graph replays for
+ * every token without the kernel-node updates of forward.c:638-666.  q [n_heads][head_dim]
+ * and k [n_kv_heads][head_dim] are normalised (when both weights are given) and rotated in
+ * place; k and v are stored at cache row *pos_dev ([pos][n_kv_heads][head_dim]; kv_type 0
+ * f16, 1 int8 with scales [pos][n_kv_heads]).  head_dim even, <= 512. */
+int mnemo_attn_prep(float *q, float *k, const float *v, const float *q_norm_w,
+                    const float *k_norm_w, int head_dim, int n_heads, int n_kv_heads, float eps,
+                    float theta, const int *pos_dev, void *k_cache, void *v_cache,
+                    float *k_scales, float *v_scales, int kv_type, hipStream_t stream);
+/* New: cuda_attention_* over positions 0..*pos_dev (the length read from device memory). */
+int mnemo_attention(const float *q, const void *k_cache, const void *v_cache,
+                    const float *k_scales, const float *v_scales, int kv_type, float *out,
+                    int n_heads, int head_dim, int n_kv_heads, const int *pos_dev, float scale,
+                    hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

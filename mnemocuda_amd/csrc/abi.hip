@@ -220,6 +220,182 @@ void cuda_sample_token(const float *logits, int vocab_size, float temperature, f
     launch_sample_token(logits, vocab_size, temperature, top_p, rng_state, d_result, s);
 }
 
+// ---------------------------------------------------------------- attention chain
+void cuda_rms_norm(const float *input, const float *weight, float *output, int n, float eps, hipStream_t s) {
+    launch_rms_norm(input, weight, output, nullptr, n, eps, s);
+}
+
+void cuda_rms_norm_residual(const float *input, const float *weight, float *normed_output, float *residual_output,
+                            int n, float eps, hipStream_t s) {
+    if (!residual_output) {
+        set_error(kErrBadArg, "rms_norm_residual: residual_output is NULL");
+        return;
+    }
+    launch_rms_norm(input, weight, normed_output, residual_output, n, eps, s);
+}
+
+void cuda_rms_norm_batched(const float *input, const float *weight, float *output, int head_dim, int n_heads,
+                           float eps, hipStream_t s) {
+    HeadPassArgs a = {};
+    a.q = (float *)input;
+    a.qo = output;
+    a.qw = weight;
+    a.hd = head_dim;
+    a.nq = n_heads;
+    a.eps = eps;
+    a.flags = kHeadNorm;
+    if (!weight || !output) {
+        set_error(kErrBadArg, "rms_norm_batched: NULL weight or output");
+        return;
+    }
+    launch_head_pass(a, s);
+}
+
+void cuda_rms_norm_qk(float *q, float *k, const float *q_weight, const float *k_weight, int head_dim, int n_q,
+                      int n_k, float eps, hipStream_t s) {
+    HeadPassArgs a = {};
+    a.q = q;
+    a.k = k;
+    a.qw = q_weight;
+    a.kw = k_weight;
+    a.hd = head_dim;
+    a.nq = n_q;
+    a.nk = n_k;
+    a.eps = eps;
+    a.flags = kHeadNorm;
+    if (!q_weight || !k_weight) {
+        set_error(kErrBadArg, "rms_norm_qk: NULL weights");
+        return;
+    }
+    launch_head_pass(a, s);
+}
+
+void cuda_residual_add(const float *a, const float *b, float *out, int n, hipStream_t s) {
+    launch_residual_add(a, b, out, n, s);
+}
+
+void cuda_rope(float *q, float *k, int head_dim, int pos, float theta, int n_heads_q, int n_heads_k, hipStream_t s) {
+    HeadPassArgs a = {};
+    a.q = q;
+    a.k = k;
+    a.hd = head_dim;
+    a.nq = n_heads_q;
+    a.nk = n_heads_k;
+    a.theta = theta;
+    a.pos = pos;
+    a.flags = kHeadRope;
+    launch_head_pass(a, s);
+}
+
+void cuda_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n, hipStream_t s) {
+    launch_f32_to_f16_dual(a, b, oa, ob, n, s);
+}
+
+void cuda_f32_to_int8_kv_dual(const float *k, const float *v, void *out_k, void *out_v, float *k_scales,
+                              float *v_scales, int head_dim, int n_kv_heads, hipStream_t s) {
+    // the reference passes the cache rows and scale slots of the current position
+    HeadPassArgs a = {};
+    a.k = (float *)k;  // read only: a store-only pass writes nothing back
+    a.v = v;
+    a.hd = head_dim;
+    a.nk = n_kv_heads;
+    a.nv = n_kv_heads;
+    a.kc = out_k;
+    a.vc = out_v;
+    a.ksc = k_scales;
+    a.vsc = v_scales;
+    a.kv_type = kKvInt8;
+    a.flags = kHeadStore;
+    launch_head_pass(a, s);
+}
+
+void cuda_attention_f16kv(const void *q, const void *kv_k, const void *kv_v, float *out, int n_heads_q, int head_dim,
+                          int n_kv_heads, int seq_len, int gqa_ratio, float scale, hipStream_t s) {
+    AttnArgs a = {};
+    a.q = (const float *)q;
+    a.kc = kv_k;
+    a.vc = kv_v;
+    a.out = out;
+    a.nh = n_heads_q;
+    a.hd = head_dim;
+    a.nkv = n_kv_heads;
+    a.gqa = gqa_ratio;
+    a.seq = seq_len;
+    a.scale = scale;
+    launch_attention(a, kKvF16, s);
+}
+
+void cuda_attention_int8kv(const float *q, const void *kv_k, const void *kv_v, const float *k_scales,
+                           const float *v_scales, float *out, int n_heads_q, int head_dim, int n_kv_heads,
+                           int seq_len, int gqa_ratio, float scale, hipStream_t s) {
+    AttnArgs a = {};
+    a.q = q;
+    a.kc = kv_k;
+    a.vc = kv_v;
+    a.ksc = k_scales;
+    a.vsc = v_scales;
+    a.out = out;
+    a.nh = n_heads_q;
+    a.hd = head_dim;
+    a.nkv = n_kv_heads;
+    a.gqa = gqa_ratio;
+    a.seq = seq_len;
+    a.scale = scale;
+    launch_attention(a, kKvInt8, s);
+}
+
+int mnemo_attn_prep(float *q, float *k, const float *v, const float *q_norm_w, const float *k_norm_w, int head_dim,
+                    int n_heads, int n_kv_heads, float eps, float theta, const int *pos_dev, void *k_cache,
+                    void *v_cache, float *k_scales, float *v_scales, int kv_type, hipStream_t s) {
+    if (!pos_dev) return set_error(kErrBadArg, "attn_prep: pos_dev is NULL");
+    if (kv_type != kKvF16 && kv_type != kKvInt8) return set_error(kErrBadArg, "attn_prep: kv_type %d", kv_type);
+    if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+        return set_error(kErrBadArg, "attn_prep: give both QK-norm weights or neither");
+    HeadPassArgs a = {};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.qw = q_norm_w;
+    a.kw = k_norm_w;
+    a.hd = head_dim;
+    a.nq = n_heads;
+    a.nk = n_kv_heads;
+    a.nv = n_kv_heads;
+    a.eps = eps;
+    a.theta = theta;
+    a.pos_dev = pos_dev;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.ksc = k_scales;
+    a.vsc = v_scales;
+    a.kv_type = kv_type;
+    a.flags = (q_norm_w ? kHeadNorm : 0) | kHeadRope | kHeadStore;
+    return launch_head_pass(a, s);
+}
+
+int mnemo_attention(const float *q, const void *k_cache, const void *v_cache, const float *k_scales,
+                    const float *v_scales, int kv_type, float *out, int n_heads, int head_dim, int n_kv_heads,
+                    const int *pos_dev, float scale, hipStream_t s) {
+    if (!pos_dev) return set_error(kErrBadArg, "attention: pos_dev is NULL");
+    if (kv_type != kKvF16 && kv_type != kKvInt8) return set_error(kErrBadArg, "attention: kv_type %d", kv_type);
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads) return set_error(kErrBadArg, "attention: n_heads %% n_kv_heads");
+    AttnArgs a = {};
+    a.q = q;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.ksc = k_scales;
+    a.vsc = v_scales;
+    a.out = out;
+    a.nh = n_heads;
+    a.hd = head_dim;
+    a.nkv = n_kv_heads;
+    a.gqa = n_heads / n_kv_heads;
+    a.seq = 1;
+    a.seq_dev = pos_dev;
+    a.scale = scale;
+    return launch_attention(a, kv_type, s);
+}
+
 size_t mnemo_moe_prefill_workspace_bytes(int n_tokens, int hidden, int eff, int n_experts, int k) {
     return moe_prefill_workspace_bytes(n_tokens, hidden, eff, n_experts, k);
 }

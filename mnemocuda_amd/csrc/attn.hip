@@ -1,0 +1,335 @@
+// attn.hip -- the decode attention chain around the projections (MnemoCUDA forward.c:687-786,
+// graph form forward.c:1290-1420): RMS norms, the per-head pass (QK norm, RoPE, KV-cache
+// store) and attention over the cache.
+//
+//  * rms_norm_row     (kernels.cu:692-749): one workgroup of 1024 threads per vector, fixed-
+//                     order reduction; optional copy of the input (the residual save).
+//  * head pass        (kernels.cu:754-781, 1196-1219, 818-852, 1320-1377): one wave per head;
+//                     lane j holds the RoPE pairs (j + 64t, j + 64t + hd/2), so the norm is a
+//                     wave reduction and the rotation needs no exchange.  Q heads, K heads and
+//                     V heads of one token go through one launch: norm -> RoPE -> store to the
+//                     cache (f16, or int8 with a per-head absmax scale).  The position can come
+//                     from device memory, so a captured graph replays for every token without
+//                     the reference's per-token kernel-node parameter updates
+//                     (forward.c:638-666).
+//  * attention        (kernels.cu:1382-1481, 1550-1660): one workgroup per query head over
+//                     tiles of positions with an online softmax, as the reference's entry
+//                     points define it (no workspace); the GQA-batched split-position kernel
+//                     lives in attn_decode.hip.
+//
+// RoPE: frequencies are 1 / powf(theta, 2j / hd) rounded as the reference's host powf
+// (a double power rounded once to float), angles pos * freq in fp32 as the reference forms
+// them; sin/cos are the accurate sincosf (the reference uses the __sincosf approximation,
+// whose error grows with the angle).
+#include "mnemo_common.hpp"
+#include "mnemo_internal.hpp"
+
+namespace mnemo {
+
+constexpr int kNormThreads = 1024;
+
+__device__ __forceinline__ float wave_sum_all(float v) {
+    v = sum64_lane63(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_max_all(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// ------------------------------------------------------------------ RMS norm of one vector
+__global__ void __launch_bounds__(kNormThreads) rms_norm_row_kernel(const float *__restrict__ in,
+                                                                   const float *__restrict__ w, float *out,
+                                                                   float *__restrict__ res, int n, float eps) {
+    __shared__ float part[kNormThreads / 64];
+    const int tid = threadIdx.x;
+    float ss = 0.0f;
+    for (int i = tid; i < n; i += kNormThreads) {
+        const float v = in[i];
+        ss = fmaf(v, v, ss);
+        if (res) res[i] = v;
+    }
+    ss = sum64_lane63(ss);
+    if (lane_id() == 63) part[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; i++) tot += part[i];  // same order in every thread
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int i = tid; i < n; i += kNormThreads) out[i] = in[i] * scale * w[i];
+}
+
+int launch_rms_norm(const float *in, const float *w, float *out, float *res, int n, float eps, hipStream_t s) {
+    if (!in || !w || !out || n <= 0) return set_error(kErrBadArg, "rms_norm: bad arguments");
+    hipLaunchKernelGGL(rms_norm_row_kernel, dim3(1), dim3(kNormThreads), 0, s, in, w, out, res, n, eps);
+    return check_launch("rms_norm");
+}
+
+__global__ void residual_add_kernel(const float *__restrict__ a, const float *__restrict__ b, float *out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+int launch_residual_add(const float *a, const float *b, float *out, int n, hipStream_t s) {
+    if (!a || !b || !out || n <= 0) return set_error(kErrBadArg, "residual_add: bad arguments");
+    hipLaunchKernelGGL(residual_add_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a, b, out, n);
+    return check_launch("residual_add");
+}
+
+__global__ void f32_to_f16_dual_kernel(const float *__restrict__ a, const float *__restrict__ b,
+                                       _Float16 *__restrict__ oa, _Float16 *__restrict__ ob, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        oa[i] = (_Float16)a[i];  // round to nearest even, as __float2half
+        ob[i] = (_Float16)b[i];
+    }
+}
+
+int launch_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n, hipStream_t s) {
+    if (!a || !b || !oa || !ob || n <= 0) return set_error(kErrBadArg, "f32_to_f16_dual: bad arguments");
+    hipLaunchKernelGGL(f32_to_f16_dual_kernel, dim3((n + 255) / 256), dim3(256), 0, s, a, b, (_Float16 *)oa,
+                       (_Float16 *)ob, n);
+    return check_launch("f32_to_f16_dual");
+}
+
+// ------------------------------------------------------------------ per-head pass
+constexpr int kHeadPairs = 4;  // RoPE pairs per lane: head_dim <= 512
+
+__global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
+    const int head = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int lane = lane_id();
+    const int half = a.hd / 2;
+    const int nqk = a.nq + a.nk;
+    if (head >= nqk + a.nv) return;  // wave-uniform
+    const bool is_q = head < a.nq, is_k = !is_q && head < nqk;
+    const int h = is_q ? head : (is_k ? head - a.nq : head - nqk);
+    const float *src = is_q ? a.q + (size_t)h * a.hd : (is_k ? a.k + (size_t)h * a.hd : a.v + (size_t)h * a.hd);
+    // q / k heads are written back only when the pass changes them (a store-only pass reads k)
+    const bool writes = (a.flags & (kHeadNorm | kHeadRope)) != 0;
+    float *dst = !writes ? nullptr : (is_q ? a.qo + (size_t)h * a.hd : (is_k ? a.ko + (size_t)h * a.hd : nullptr));
+    float x0[kHeadPairs], x1[kHeadPairs];
+#pragma unroll
+    for (int t = 0; t < kHeadPairs; t++) {
+        const int j = lane + 64 * t;
+        const bool ok = j < half;
+        x0[t] = ok ? src[j] : 0.0f;
+        x1[t] = ok ? src[j + half] : 0.0f;
+    }
+    const float *nw = is_q ? a.qw : (is_k ? a.kw : nullptr);
+    if ((a.flags & kHeadNorm) && nw) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kHeadPairs; t++) ss = fmaf(x0[t], x0[t], fmaf(x1[t], x1[t], ss));
+        const float scale = 1.0f / sqrtf(wave_sum_all(ss) / (float)a.hd + a.eps);
+#pragma unroll
+        for (int t = 0; t < kHeadPairs; t++) {
+            const int j = lane + 64 * t;
+            if (j < half) {
+                x0[t] = x0[t] * scale * nw[j];
+                x1[t] = x1[t] * scale * nw[j + half];
+            }
+        }
+    }
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+    if ((a.flags & kHeadRope) && (is_q || is_k)) {
+#pragma unroll
+        for (int t = 0; t < kHeadPairs; t++) {
+            const int j = lane + 64 * t;
+            if (j < half) {
+                const float e = (float)(2 * j) / (float)a.hd;
+                const float p = (float)pow((double)a.theta, (double)e);  // powf, correctly rounded
+                const float freq = 1.0f / p;
+                const float ang = (float)pos * freq;
+                float sn, cs;
+                sincosf(ang, &sn, &cs);
+                const float v0 = x0[t], v1 = x1[t];
+                x0[t] = v0 * cs - v1 * sn;
+                x1[t] = v0 * sn + v1 * cs;
+            }
+        }
+    }
+    if (dst) {
+#pragma unroll
+        for (int t = 0; t < kHeadPairs; t++) {
+            const int j = lane + 64 * t;
+            if (j < half) {
+                dst[j] = x0[t];
+                dst[j + half] = x1[t];
+            }
+        }
+    }
+    if ((a.flags & kHeadStore) && !is_q) {
+        const size_t base = ((size_t)pos * a.nk + h) * a.hd;
+        void *cache = is_k ? a.kc : a.vc;
+        if (a.kv_type == kKvF16) {
+            _Float16 *c = (_Float16 *)cache + base;
+#pragma unroll
+            for (int t = 0; t < kHeadPairs; t++) {
+                const int j = lane + 64 * t;
+                if (j < half) {
+                    c[j] = (_Float16)x0[t];
+                    c[j + half] = (_Float16)x1[t];
+                }
+            }
+        } else {
+            float m = 0.0f;
+#pragma unroll
+            for (int t = 0; t < kHeadPairs; t++) m = fmaxf(m, fmaxf(fabsf(x0[t]), fabsf(x1[t])));
+            m = wave_max_all(m);
+            const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+            int8_t *c = (int8_t *)cache + base;
+#pragma unroll
+            for (int t = 0; t < kHeadPairs; t++) {
+                const int j = lane + 64 * t;
+                if (j < half) {
+                    c[j] = (int8_t)fminf(fmaxf(rintf(x0[t] * inv), -127.0f), 127.0f);
+                    c[j + half] = (int8_t)fminf(fmaxf(rintf(x1[t] * inv), -127.0f), 127.0f);
+                }
+            }
+            float *sc = is_k ? a.ksc : a.vsc;
+            if (lane == 0) sc[(size_t)pos * a.nk + h] = m > 0.0f ? m / 127.0f : 0.0f;
+        }
+    }
+}
+
+int launch_head_pass(HeadPassArgs a, hipStream_t s) {
+    const int heads = a.nq + a.nk + a.nv;
+    if (a.hd <= 0 || (a.hd & 1) || a.hd > 2 * 64 * kHeadPairs || heads <= 0 || a.nq < 0 || a.nk < 0 || a.nv < 0)
+        return set_error(kErrBadArg, "head pass: need an even head_dim <= %d and heads > 0", 2 * 64 * kHeadPairs);
+    if ((a.nq && !a.q) || (a.nk && !a.k) || (a.nv && !a.v))
+        return set_error(kErrBadArg, "head pass: missing q / k / v");
+    if (!a.qo) a.qo = a.q;
+    if (!a.ko) a.ko = a.k;
+    if ((a.flags & kHeadStore) && (((a.nk && !a.kc) || (a.nv && !a.vc)) ||
+                                   (a.kv_type == kKvInt8 && ((a.nk && !a.ksc) || (a.nv && !a.vsc)))))
+        return set_error(kErrBadArg, "head pass: missing cache pointers");
+    if ((a.flags & kHeadStore) && a.nv && a.nk && a.nv != a.nk)
+        return set_error(kErrBadArg, "head pass: K and V must have the same number of heads");
+    if ((a.flags & kHeadStore) && !a.nk) a.nk = a.nv;  // V-only store: the cache row has nv heads
+    hipLaunchKernelGGL(head_pass_kernel, dim3((heads + 3) / 4), dim3(256), 0, s, a);
+    return check_launch("head pass");
+}
+
+// ------------------------------------------------------------------ attention (entry-point form)
+constexpr int kAttnThreads = 256;
+constexpr int kAttnTile = 1024;
+
+template <int KV>
+__device__ __forceinline__ void load8(const void *cache, size_t off, const float *scales, size_t si, float (&k)[8]) {
+    if (KV == kKvF16) {
+        uint4 raw;
+        __builtin_memcpy(&raw, (const _Float16 *)cache + off, 16);
+        const _Float16 *hv = (const _Float16 *)&raw;
+#pragma unroll
+        for (int i = 0; i < 8; i++) k[i] = (float)hv[i];
+    } else {
+        uint2 raw;
+        __builtin_memcpy(&raw, (const int8_t *)cache + off, 8);
+        const int8_t *iv = (const int8_t *)&raw;
+        const float sc = scales[si];
+#pragma unroll
+        for (int i = 0; i < 8; i++) k[i] = (float)iv[i] * sc;
+    }
+}
+
+template <int KV>
+__device__ __forceinline__ float load1(const void *cache, size_t off, const float *scales, size_t si) {
+    if (KV == kKvF16) return (float)((const _Float16 *)cache)[off];
+    return (float)((const int8_t *)cache)[off] * scales[si];
+}
+
+__device__ __forceinline__ float block_reduce(float v, float *part, bool is_max) {
+    v = is_max ? wave_max_all(v) : wave_sum_all(v);
+    __syncthreads();  // part[] may still be read from the previous reduction
+    if (lane_id() == 0) part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = part[0];
+#pragma unroll
+    for (int i = 1; i < kAttnThreads / 64; i++) r = is_max ? fmaxf(r, part[i]) : r + part[i];
+    return r;
+}
+
+// One workgroup per query head.  Scores: hd/8 lanes per position, 8 dims each (16-byte f16
+// loads).  Softmax: online over tiles of kAttnTile positions.  P.V: kAttnThreads/hd threads
+// per dim, each over every tpd-th position of the tile; summed through LDS at the end.
+template <int KV>
+__global__ void __launch_bounds__(kAttnThreads) attention_kernel(AttnArgs a) {
+    __shared__ float qs[256];
+    __shared__ float sc[kAttnTile];
+    __shared__ float part[kAttnThreads / 64];
+    __shared__ float accs[kAttnThreads];
+    const int head = blockIdx.x, kvh = head / a.gqa, tid = threadIdx.x, lane = lane_id();
+    const int hd = a.hd;
+    const int seq = (a.seq_dev ? *a.seq_dev : 0) + a.seq;
+    const size_t stride = (size_t)a.nkv * hd;
+    for (int d = tid; d < hd; d += kAttnThreads) qs[d] = a.q[(size_t)head * hd + d];
+    __syncthreads();
+    const int G = hd / 8;                    // lanes per position
+    const int ppw = 64 / G;                  // positions per wave per step
+    const int pps = ppw * (kAttnThreads / 64);
+    const int gi = lane % G, gp = lane / G;  // lane's 8-dim group, position slot in the wave
+    const int tpd = kAttnThreads / hd;       // threads per output dim
+    const int d = tid % hd, dpart = tid / hd;
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    for (int t0 = 0; t0 < seq; t0 += kAttnTile) {
+        const int tl = min(kAttnTile, seq - t0);
+        for (int i0 = 0; i0 < tl; i0 += pps) {
+            const int i = i0 + (tid >> 6) * ppw + gp;
+            const int p = t0 + min(i, tl - 1);
+            float k[8];
+            load8<KV>(a.kc, (size_t)p * stride + (size_t)kvh * hd + 8 * gi, a.ksc, (size_t)p * a.nkv + kvh, k);
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) s = fmaf(qs[8 * gi + e], k[e], s);
+            for (int o = G / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
+            if (gi == 0 && i < tl) sc[i] = s * a.scale;
+        }
+        __syncthreads();
+        float tm = -INFINITY;
+        for (int i = tid; i < tl; i += kAttnThreads) tm = fmaxf(tm, sc[i]);
+        tm = block_reduce(tm, part, true);
+        const float mn = fmaxf(m, tm);
+        const float rescale = l > 0.0f ? expf(m - mn) : 0.0f;
+        float ts = 0.0f;
+        for (int i = tid; i < tl; i += kAttnThreads) {
+            const float e = expf(sc[i] - mn);
+            sc[i] = e;
+            ts += e;
+        }
+        ts = block_reduce(ts, part, false);  // its barriers also publish sc[]
+        float v = 0.0f;
+        for (int i = dpart; i < tl; i += tpd) {
+            const int p = t0 + i;
+            v = fmaf(sc[i], load1<KV>(a.vc, (size_t)p * stride + (size_t)kvh * hd + d, a.vsc, (size_t)p * a.nkv + kvh),
+                     v);
+        }
+        acc = acc * rescale + v;
+        l = l * rescale + ts;
+        m = mn;
+        __syncthreads();  // sc[] is rewritten by the next tile
+    }
+    accs[tid] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        float o = 0.0f;
+        for (int j = 0; j < tpd; j++) o += accs[tid + j * hd];
+        a.out[(size_t)head * hd + tid] = seq > 0 && l > 0.0f ? o / l : 0.0f;
+    }
+}
+
+int launch_attention(AttnArgs a, int kv_type, hipStream_t s) {
+    if (!a.q || !a.kc || !a.vc || !a.out || a.nh <= 0 || a.nkv <= 0 || a.gqa <= 0 || a.nh != a.nkv * a.gqa)
+        return set_error(kErrBadArg, "attention: bad pointers or head counts (n_heads must be n_kv_heads * gqa)");
+    if (!(a.hd == 64 || a.hd == 128 || a.hd == 256))
+        return set_error(kErrBadArg, "attention: head_dim %d not supported (64, 128, 256)", a.hd);
+    if (a.seq < 0) return set_error(kErrBadArg, "attention: seq_len < 0");
+    if (kv_type == kKvInt8 && (!a.ksc || !a.vsc)) return set_error(kErrBadArg, "attention: int8 cache needs scales");
+    if (kv_type == kKvF16)
+        hipLaunchKernelGGL(attention_kernel<kKvF16>, dim3(a.nh), dim3(kAttnThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL(attention_kernel<kKvInt8>, dim3(a.nh), dim3(kAttnThreads), 0, s, a);
+    return check_launch("attention");
+}
+
+}  // namespace mnemo

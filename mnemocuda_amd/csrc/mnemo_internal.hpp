@@ -65,6 +65,45 @@ struct GemvArgs {
 int launch_gemv(GemvArgs a, hipStream_t stream);
 int launch_gemv_experts(GemvArgs a, hipStream_t stream);
 
+// ---- attention chain (attn.hip, attn_decode.hip)
+constexpr int kKvF16 = 0;
+constexpr int kKvInt8 = 1;
+constexpr int kHeadNorm = 1;   // RMS-normalise q and k heads with qw / kw
+constexpr int kHeadRope = 2;   // rotate q and k heads
+constexpr int kHeadStore = 4;  // store k and v heads at the cache row of pos
+
+struct HeadPassArgs {
+    float *q, *k;          // nq / nk heads, read (and by default written back)
+    const float *v;        // nv heads, only stored
+    float *qo, *ko;        // outputs of the q / k heads (null: in place)
+    const float *qw, *kw;  // norm weights [hd]
+    int hd, nq, nk, nv;
+    float eps, theta;
+    int pos;               // cache row and RoPE position ...
+    const int *pos_dev;    // ... or read from device memory when not null
+    void *kc, *vc;         // caches [pos][nk][hd] (f16 or int8)
+    float *ksc, *vsc;      // int8 scales [pos][nk]
+    int kv_type;
+    int flags;
+};
+
+struct AttnArgs {
+    const float *q;
+    const void *kc, *vc;
+    const float *ksc, *vsc;
+    float *out;
+    int nh, hd, nkv, gqa;
+    int seq;             // sequence length = seq + (seq_dev ? *seq_dev : 0): with seq_dev the
+    const int *seq_dev;  // current position in device memory and seq = 1
+    float scale;
+};
+
+int launch_rms_norm(const float *in, const float *w, float *out, float *res, int n, float eps, hipStream_t s);
+int launch_residual_add(const float *a, const float *b, float *out, int n, hipStream_t s);
+int launch_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n, hipStream_t s);
+int launch_head_pass(HeadPassArgs a, hipStream_t s);
+int launch_attention(AttnArgs a, int kv_type, hipStream_t s);
+
 // Records (and prints, as the reference's KERNEL_LAUNCH_CHECK does, kernels.cu:1062-1067)
 // the error of the last launch; returns a kErr code.
 int check_launch(const char *what);

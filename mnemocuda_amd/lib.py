@@ -43,6 +43,19 @@ SIGNATURES: dict[str, tuple] = {
                                 stream_t]),
     "mnemo_moe_decode_workspace_bytes": (sz, [i32, i32, i32, i32]),
     "mnemo_moe_decode": (i32, [fp, vp, sz, sz, sz, sz, i32, fp, i32, i32, i32, i32, vp, sz, fp, ip, fp, stream_t]),
+    # attention chain
+    "cuda_rms_norm": (None, [fp, fp, fp, i32, f32, stream_t]),
+    "cuda_rms_norm_residual": (None, [fp, fp, fp, fp, i32, f32, stream_t]),
+    "cuda_rms_norm_batched": (None, [fp, fp, fp, i32, i32, f32, stream_t]),
+    "cuda_rms_norm_qk": (None, [fp, fp, fp, fp, i32, i32, i32, f32, stream_t]),
+    "cuda_residual_add": (None, [fp, fp, fp, i32, stream_t]),
+    "cuda_rope": (None, [fp, fp, i32, i32, f32, i32, i32, stream_t]),
+    "cuda_f32_to_f16_dual": (None, [fp, fp, vp, vp, i32, stream_t]),
+    "cuda_f32_to_int8_kv_dual": (None, [fp, fp, vp, vp, fp, fp, i32, i32, stream_t]),
+    "cuda_attention_f16kv": (None, [vp, vp, vp, fp, i32, i32, i32, i32, i32, f32, stream_t]),
+    "cuda_attention_int8kv": (None, [fp, vp, vp, fp, fp, fp, i32, i32, i32, i32, i32, f32, stream_t]),
+    "mnemo_attn_prep": (i32, [fp, fp, fp, fp, fp, i32, i32, i32, f32, f32, ip, vp, vp, fp, fp, i32, stream_t]),
+    "mnemo_attention": (i32, [fp, vp, vp, fp, fp, i32, fp, i32, i32, i32, ip, f32, stream_t]),
     # host composition (mnemo_host.h)
     "mnemo_matvec": (i32, [vp, fp, fp, i32, i32, i32, stream_t]),
     "mnemo_down_type_id": (i32, [sz, i32, i32]),

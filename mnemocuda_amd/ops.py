@@ -254,3 +254,107 @@ def sample_token(logits, vocab, temperature, top_p, seed, out):
     lib.cuda_sample_token(_dev(logits, "logits", torch.float32), vocab, float(temperature), float(top_p),
                           int(seed) & 0xFFFFFFFFFFFFFFFF, _dev(out, "out", torch.int32), _stream())
     check(lib, "cuda_sample_token")
+
+
+# ---------------------------------------------------------------- attention chain
+F32 = torch.float32
+
+
+def _opt(t, name, dtype=None) -> int | None:
+    return None if t is None else _dev(t, name, dtype)
+
+
+def rms_norm(x, w, out, eps: float, residual=None):
+    """out = x * rsqrt(mean(x^2) + eps) * w (cuda_rms_norm); with residual, also residual = x
+    (cuda_rms_norm_residual)."""
+    lib = load_library()
+    n = x.numel()
+    if w.numel() < n or out.numel() < n or (residual is not None and residual.numel() < n):
+        raise MnemoError("rms_norm: buffers too small")
+    if residual is None:
+        lib.cuda_rms_norm(_dev(x, "x", F32), _dev(w, "w", F32), _dev(out, "out", F32), n, float(eps), _stream())
+        check(lib, "cuda_rms_norm")
+    else:
+        lib.cuda_rms_norm_residual(_dev(x, "x", F32), _dev(w, "w", F32), _dev(out, "out", F32),
+                                   _dev(residual, "residual", F32), n, float(eps), _stream())
+        check(lib, "cuda_rms_norm_residual")
+
+
+def rms_norm_batched(x, w, out, head_dim: int, eps: float):
+    lib = load_library()
+    lib.cuda_rms_norm_batched(_dev(x, "x", F32), _dev(w, "w", F32), _dev(out, "out", F32), head_dim,
+                              x.numel() // head_dim, float(eps), _stream())
+    check(lib, "cuda_rms_norm_batched")
+
+
+def rms_norm_qk(q, k, qw, kw, head_dim: int, eps: float):
+    lib = load_library()
+    lib.cuda_rms_norm_qk(_dev(q, "q", F32), _dev(k, "k", F32), _dev(qw, "qw", F32), _dev(kw, "kw", F32), head_dim,
+                         q.numel() // head_dim, k.numel() // head_dim, float(eps), _stream())
+    check(lib, "cuda_rms_norm_qk")
+
+
+def residual_add(a, b, out):
+    lib = load_library()
+    lib.cuda_residual_add(_dev(a, "a", F32), _dev(b, "b", F32), _dev(out, "out", F32), a.numel(), _stream())
+    check(lib, "cuda_residual_add")
+
+
+def rope(q, k, head_dim: int, pos: int, theta: float):
+    lib = load_library()
+    lib.cuda_rope(_dev(q, "q", F32), _dev(k, "k", F32), head_dim, int(pos), float(theta), q.numel() // head_dim,
+                  k.numel() // head_dim, _stream())
+    check(lib, "cuda_rope")
+
+
+def f32_to_f16_dual(a, b, oa, ob):
+    lib = load_library()
+    lib.cuda_f32_to_f16_dual(_dev(a, "a", F32), _dev(b, "b", F32), _dev(oa, "oa", torch.float16),
+                             _dev(ob, "ob", torch.float16), a.numel(), _stream())
+    check(lib, "cuda_f32_to_f16_dual")
+
+
+def f32_to_int8_kv_dual(k, v, ok, ov, ks, vs, head_dim: int):
+    lib = load_library()
+    lib.cuda_f32_to_int8_kv_dual(_dev(k, "k", F32), _dev(v, "v", F32), _dev(ok, "ok", torch.int8),
+                                 _dev(ov, "ov", torch.int8), _dev(ks, "ks", F32), _dev(vs, "vs", F32), head_dim,
+                                 k.numel() // head_dim, _stream())
+    check(lib, "cuda_f32_to_int8_kv_dual")
+
+
+def attention(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: int, seq_len: int, scale: float,
+              ks=None, vs=None):
+    """cuda_attention_f16kv (kc/vc float16) or cuda_attention_int8kv (int8 with scales)."""
+    lib = load_library()
+    gqa = n_heads // n_kv_heads
+    if kc.dtype == torch.float16:
+        lib.cuda_attention_f16kv(_dev(q, "q", F32), _dev(kc, "kc"), _dev(vc, "vc"), _dev(out, "out", F32), n_heads,
+                                 head_dim, n_kv_heads, int(seq_len), gqa, float(scale), _stream())
+        check(lib, "cuda_attention_f16kv")
+    else:
+        lib.cuda_attention_int8kv(_dev(q, "q", F32), _dev(kc, "kc", torch.int8), _dev(vc, "vc", torch.int8),
+                                  _dev(ks, "ks", F32), _dev(vs, "vs", F32), _dev(out, "out", F32), n_heads, head_dim,
+                                  n_kv_heads, int(seq_len), gqa, float(scale), _stream())
+        check(lib, "cuda_attention_int8kv")
+
+
+def attn_prep(q, k, v, qw, kw, head_dim: int, eps: float, theta: float, pos_dev, kc, vc, ks=None, vs=None):
+    """QK norm (when qw/kw are given) + RoPE + KV store at cache row pos_dev[0], one launch."""
+    lib = load_library()
+    kv_type = 0 if kc.dtype == torch.float16 else 1
+    rc = lib.mnemo_attn_prep(_dev(q, "q", F32), _dev(k, "k", F32), _dev(v, "v", F32), _opt(qw, "qw", F32),
+                             _opt(kw, "kw", F32), head_dim, q.numel() // head_dim, k.numel() // head_dim, float(eps),
+                             float(theta), _dev(pos_dev, "pos_dev", torch.int32), _dev(kc, "kc"), _dev(vc, "vc"),
+                             _opt(ks, "ks", F32), _opt(vs, "vs", F32), kv_type, _stream())
+    _check_rc(lib, rc, "mnemo_attn_prep")
+
+
+def attention_dev(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: int, pos_dev, scale: float,
+                  ks=None, vs=None):
+    """attention over positions 0..pos_dev[0] (length read on the device)."""
+    lib = load_library()
+    kv_type = 0 if kc.dtype == torch.float16 else 1
+    rc = lib.mnemo_attention(_dev(q, "q", F32), _dev(kc, "kc"), _dev(vc, "vc"), _opt(ks, "ks", F32),
+                             _opt(vs, "vs", F32), kv_type, _dev(out, "out", F32), n_heads, head_dim, n_kv_heads,
+                             _dev(pos_dev, "pos_dev", torch.int32), float(scale), _stream())
+    _check_rc(lib, rc, "mnemo_attention")

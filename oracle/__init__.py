@@ -55,6 +55,17 @@ class Oracle:
         L.mo_sample_token.argtypes = [P, C.c_int, C.c_float, C.c_float, C.c_ulonglong, P, P]
         L.mo_xoroshiro_next.restype = C.c_uint64
         L.mo_xoroshiro_next.argtypes = [P, P]
+        F = C.c_float
+        L.mo_rms_norm.argtypes = [P, P, P, C.c_int, F]
+        L.mo_rms_norm_residual.argtypes = [P, P, P, P, C.c_int, F]
+        L.mo_rms_norm_heads.argtypes = [P, P, P, C.c_int, C.c_int, F]
+        L.mo_residual_add.argtypes = [P, P, P, C.c_int]
+        L.mo_rope_freq.restype = F
+        L.mo_rope_freq.argtypes = [C.c_int, C.c_int, F]
+        L.mo_rope.argtypes = [P, P, C.c_int, C.c_int, F, C.c_int, C.c_int]
+        L.mo_kv_quant_int8.argtypes = [P, P, P, C.c_int, C.c_int]
+        L.mo_attention.restype = C.c_int
+        L.mo_attention.argtypes = [P, P, P, P, P, C.c_int, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, F]
         self.L = L
 
     @staticmethod
@@ -174,6 +185,64 @@ class Oracle:
             act = self.swiglu(g, u).reshape(tok.size, eff)
             d = self.gemm(down_type, wd, self.quantize_q8_1(act), hidden, eff, tok.size)
             np.add.at(out, tok, w[tok, slot][:, None].astype(np.float64) * d)
+        return out
+
+    # ---------------------------------------------------------------- attention chain
+    @staticmethod
+    def _f32(a) -> np.ndarray:
+        return np.ascontiguousarray(a, np.float32)
+
+    def rms_norm(self, x, w, eps: float) -> np.ndarray:
+        x, w = self._f32(x), self._f32(w)
+        out = np.zeros_like(x)
+        self.L.mo_rms_norm(self._p(x), self._p(w), self._p(out), x.size, eps)
+        return out
+
+    def rms_norm_residual(self, x, w, eps: float):
+        x, w = self._f32(x), self._f32(w)
+        normed, res = np.zeros_like(x), np.zeros_like(x)
+        self.L.mo_rms_norm_residual(self._p(x), self._p(w), self._p(normed), self._p(res), x.size, eps)
+        return normed, res
+
+    def rms_norm_heads(self, x, w, head_dim: int, eps: float) -> np.ndarray:
+        x, w = self._f32(x), self._f32(w)
+        out = np.zeros_like(x)
+        self.L.mo_rms_norm_heads(self._p(x), self._p(w), self._p(out), head_dim, x.size // head_dim, eps)
+        return out
+
+    def residual_add(self, a, b) -> np.ndarray:
+        a, b = self._f32(a), self._f32(b)
+        out = np.zeros_like(a)
+        self.L.mo_residual_add(self._p(a), self._p(b), self._p(out), a.size)
+        return out
+
+    def rope_freq(self, j: int, head_dim: int, theta: float) -> float:
+        return self.L.mo_rope_freq(j, head_dim, theta)
+
+    def rope(self, q, k, head_dim: int, pos: int, theta: float):
+        q, k = self._f32(q).copy(), self._f32(k).copy()
+        self.L.mo_rope(self._p(q), self._p(k), head_dim, pos, theta, q.size // head_dim, k.size // head_dim)
+        return q, k
+
+    def kv_quant_int8(self, x, head_dim: int):
+        x = self._f32(x)
+        out = np.zeros(x.size, np.int8)
+        sc = np.zeros(x.size // head_dim, np.float32)
+        self.L.mo_kv_quant_int8(self._p(x), self._p(out), self._p(sc), head_dim, x.size // head_dim)
+        return out, sc
+
+    def attention(self, q, kv_k, kv_v, n_heads: int, head_dim: int, n_kv_heads: int, seq_len: int,
+                  scale: float, k_scales=None, v_scales=None) -> np.ndarray:
+        """kv_k / kv_v: uint16 f16 bits (kv_type 0) or int8 with [pos][kv head] scales."""
+        q = self._f32(q)
+        kt = 0 if kv_k.dtype == np.uint16 else 1
+        kk, vv = np.ascontiguousarray(kv_k), np.ascontiguousarray(kv_v)
+        ks = self._f32(k_scales) if k_scales is not None else np.zeros(1, np.float32)
+        vs = self._f32(v_scales) if v_scales is not None else np.zeros(1, np.float32)
+        out = np.zeros(n_heads * head_dim, np.float32)
+        if self.L.mo_attention(self._p(q), self._p(kk), self._p(vv), self._p(ks), self._p(vs), kt, self._p(out),
+                               n_heads, head_dim, n_kv_heads, seq_len, n_heads // n_kv_heads, scale):
+            raise ValueError("attention arguments")
         return out
 
 

@@ -27,6 +27,13 @@
  *   mo_sample_token      greedy = numpy argmax; top_p -> 0 draws the argmax for every
  *                        seed; draw frequencies over many seeds match the renormalised
  *                        nucleus distribution (chi-square); a numpy restatement.
+ *   mo_rms_norm*         closed form for constant vectors, scale invariance, numpy.
+ *   mo_rope              pos 0 is the identity, per-pair norms are preserved, two
+ *                        rotations compose, numpy restatement (mnemo_oracle_attn.c).
+ *   mo_kv_quant_int8     closed forms (the absmax element maps to +-127, zero heads),
+ *                        round-half-even ties, numpy restatement.
+ *   mo_attention         one position returns v exactly, q = 0 gives the mean of v, a
+ *                        dominant score picks its v, numpy softmax restatement.
  */
 #ifndef MNEMO_ORACLE_H
 #define MNEMO_ORACLE_H
@@ -84,6 +91,19 @@ int mo_gemm_q8_1(int type_id, const void *w, const void *act, double *out, int M
 int mo_sample_token(const float *logits, int V, float temperature, float top_p,
                     unsigned long long seed, float *u_out, float *nsum_out);
 uint64_t mo_xoroshiro_next(uint64_t *s0, uint64_t *s1);
+
+/* Decode attention chain (mnemo_oracle_attn.c). */
+void mo_rms_norm(const float *in, const float *w, float *out, int n, float eps);
+void mo_rms_norm_residual(const float *in, const float *w, float *normed, float *residual, int n, float eps);
+void mo_rms_norm_heads(const float *in, const float *w, float *out, int head_dim, int n_heads, float eps);
+void mo_residual_add(const float *a, const float *b, float *out, int n);
+float mo_rope_freq(int j, int head_dim, float theta);
+void mo_rope(float *q, float *k, int head_dim, int pos, float theta, int n_heads_q, int n_heads_k);
+void mo_kv_quant_int8(const float *in, int8_t *out, float *scales, int head_dim, int n_kv_heads);
+#define MO_ATTN_MAX_HD 1024
+int mo_attention(const float *q, const void *kv_k, const void *kv_v, const float *k_scales,
+                 const float *v_scales, int kv_type, float *out, int n_heads, int head_dim,
+                 int n_kv_heads, int seq_len, int gqa, float scale);
 
 #ifdef __cplusplus
 }

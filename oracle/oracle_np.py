@@ -205,3 +205,51 @@ def sample_token(logits: np.ndarray, temperature: float, top_p: float, seed: int
     k = min(k, n - 1)
     margin = min(abs(c[k] - target), abs(target - (c[k - 1] if k else 0.0))) / nsum
     return int(ids[k]), min(margin, mass_margin)
+
+
+# ---------------------------------------------------------------- attention chain
+# Written from the layout and formulas in the reference's kernels.cu (norms :692-781,
+# RoPE :818-852 / :1256-1266, int8 KV :1339-1377, attention :1382-1481 / :1550-1660),
+# independently of mnemo_oracle_attn.c, in float64 numpy.
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = x.astype(np.float64)
+    return (x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w).astype(np.float32)
+
+
+def rope(v: np.ndarray, head_dim: int, pos: int, theta: float) -> np.ndarray:
+    half = head_dim // 2
+    j = np.arange(half, dtype=np.float32)
+    e = ((2 * j) / np.float32(head_dim)).astype(np.float32)
+    # powf, correctly rounded: the float64 power rounded once to float32 (numpy's float32
+    # power is off by up to 2 ulp)
+    p = np.power(np.float64(np.float32(theta)), e.astype(np.float64)).astype(np.float32)
+    freq = (np.float32(1.0) / p).astype(np.float32)
+    ang = (np.float32(pos) * freq).astype(np.float64)
+    c, s = np.cos(ang), np.sin(ang)
+    x = v.reshape(-1, head_dim).astype(np.float64)
+    a, b = x[:, :half], x[:, half:]
+    return np.concatenate([a * c - b * s, a * s + b * c], axis=1).astype(np.float32).reshape(v.shape)
+
+
+def kv_quant_int8(x: np.ndarray, head_dim: int):
+    h = x.reshape(-1, head_dim).astype(np.float32)
+    a = np.abs(h).max(axis=1)
+    with np.errstate(divide="ignore"):
+        inv = np.where(a > 0, np.float32(127.0) / a, np.float32(0.0)).astype(np.float32)
+        sc = np.where(a > 0, a / np.float32(127.0), np.float32(0.0)).astype(np.float32)
+    q = np.clip(np.rint((h * inv[:, None]).astype(np.float32)), -127, 127).astype(np.int8)
+    return q.reshape(-1), sc
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_heads: int, head_dim: int, n_kv_heads: int,
+              scale: float) -> np.ndarray:
+    """k, v: float arrays [seq][n_kv_heads][head_dim] (already dequantised)."""
+    seq = k.shape[0]
+    qh = q.reshape(n_heads, head_dim).astype(np.float64)
+    kv = np.arange(n_heads) // (n_heads // n_kv_heads)
+    out = np.zeros((n_heads, head_dim))
+    for h in range(n_heads):
+        s = (k[:, kv[h], :].astype(np.float64) @ qh[h]) * scale
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ v[:, kv[h], :].astype(np.float64)
+    return out.astype(np.float32).reshape(-1)

@@ -1,0 +1,252 @@
+"""GPU parity of the attention chain (MnemoCUDA kernels.cu:692-852, 1196-1244, 1309-1673)
+against the C oracle (oracle/mnemo_oracle_attn.c).
+
+Bars: RMS norms and residual add within fp32 rounding (rtol 2e-6 / exact); RoPE within
+1e-5 of max|x| (same fp32 frequencies and angles, accurate sin/cos on both sides); f16
+stores bit-exact; int8 KV bytes and scales bit-exact on the entry points (same fp32
+arithmetic); attention rel-L2 <= 1e-5 against the fp64 softmax (the cache values are the
+same f16 / int8 numbers on both sides).  Shapes: Qwen3-235B attention (64 query heads,
+4 KV heads, head_dim 128), plus head_dim 64 and 256, one position, positions across the
+1024-position tile boundary, and pos up to 40959."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle_np as onp
+from tests.conftest import rel_l2
+from tests.gpu_util import case, dev, host
+
+pytestmark = pytest.mark.gpu
+
+NH, NKV, HD = 64, 4, 128
+
+
+def test_rms_norm_variants(gpu, oracle, rng):
+    x = rng.standard_normal(4096).astype(np.float32)
+    w = rng.standard_normal(4096).astype(np.float32)
+    case("rms_norm 4096")
+    out = torch.empty(4096, device="cuda")
+    gpu.ops.rms_norm(dev(x), dev(w), out, 1e-6)
+    np.testing.assert_allclose(host(out), oracle.rms_norm(x, w, 1e-6), rtol=2e-6, atol=1e-7)
+    res = torch.zeros(4096, device="cuda")
+    out2 = torch.empty(4096, device="cuda")
+    gpu.ops.rms_norm(dev(x), dev(w), out2, 1e-6, residual=res)
+    assert np.array_equal(host(res), x)
+    assert np.array_equal(host(out2), host(out))
+    # in place, n not a multiple of the block
+    y = rng.standard_normal(5000).astype(np.float32)
+    wy = rng.standard_normal(5000).astype(np.float32)
+    t = dev(y)
+    gpu.ops.rms_norm(t, dev(wy), t, 1e-5)
+    np.testing.assert_allclose(host(t), oracle.rms_norm(y, wy, 1e-5), rtol=2e-6, atol=1e-7)
+    a, b = dev(x), dev(w)
+    s = torch.empty(4096, device="cuda")
+    gpu.ops.residual_add(a, b, s)
+    assert np.array_equal(host(s), x + w)
+
+
+@pytest.mark.parametrize("hd", [64, 128, 256])
+def test_rms_norm_heads(gpu, oracle, rng, hd):
+    q = rng.standard_normal(NH * hd).astype(np.float32)
+    k = rng.standard_normal(NKV * hd).astype(np.float32)
+    qw = rng.standard_normal(hd).astype(np.float32)
+    kw = rng.standard_normal(hd).astype(np.float32)
+    case(f"rms_norm heads hd={hd}")
+    out = torch.empty(NH * hd, device="cuda")
+    gpu.ops.rms_norm_batched(dev(q), dev(qw), out, hd, 1e-6)
+    np.testing.assert_allclose(host(out), oracle.rms_norm_heads(q, qw, hd, 1e-6), rtol=2e-6, atol=1e-7)
+    tq, tk = dev(q), dev(k)
+    gpu.ops.rms_norm_qk(tq, tk, dev(qw), dev(kw), hd, 1e-6)
+    np.testing.assert_allclose(host(tq), oracle.rms_norm_heads(q, qw, hd, 1e-6), rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(host(tk), oracle.rms_norm_heads(k, kw, hd, 1e-6), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("pos,theta,hd", [(0, 1e6, 128), (1, 1e6, 128), (1000, 1e6, 128), (40959, 1e6, 128),
+                                          (777, 1e4, 64), (12345, 5e5, 256)])
+def test_rope(gpu, oracle, rng, pos, theta, hd):
+    q = rng.standard_normal(NH * hd).astype(np.float32)
+    k = rng.standard_normal(NKV * hd).astype(np.float32)
+    case(f"rope pos={pos} theta={theta} hd={hd}")
+    tq, tk = dev(q), dev(k)
+    gpu.ops.rope(tq, tk, hd, pos, theta)
+    wq, wk = oracle.rope(q, k, hd, pos, theta)
+    if pos == 0:
+        assert np.array_equal(host(tq), q) and np.array_equal(host(tk), k)
+    tol = 1e-5 * max(np.abs(q).max(), np.abs(k).max())
+    np.testing.assert_allclose(host(tq), wq, rtol=0, atol=tol)
+    np.testing.assert_allclose(host(tk), wk, rtol=0, atol=tol)
+
+
+def test_kv_stores(gpu, oracle, rng):
+    k = (rng.standard_normal(NKV * HD) * 3).astype(np.float32)
+    v = (rng.standard_normal(NKV * HD) * 3).astype(np.float32)
+    k[HD:2 * HD] = 0.0  # a zero head: scale 0, all-zero bytes
+    case("f32_to_f16_dual / f32_to_int8_kv_dual")
+    ok = torch.empty(NKV * HD, dtype=torch.float16, device="cuda")
+    ov = torch.empty_like(ok)
+    gpu.ops.f32_to_f16_dual(dev(k), dev(v), ok, ov)
+    assert np.array_equal(host(ok).view(np.uint16), k.astype(np.float16).view(np.uint16))
+    assert np.array_equal(host(ov).view(np.uint16), v.astype(np.float16).view(np.uint16))
+    qk = torch.empty(NKV * HD, dtype=torch.int8, device="cuda")
+    qv = torch.empty_like(qk)
+    ks = torch.full((NKV,), -1.0, device="cuda")
+    vs = torch.full((NKV,), -1.0, device="cuda")
+    tk = dev(k)
+    gpu.ops.f32_to_int8_kv_dual(tk, dev(v), qk, qv, ks, vs, HD)
+    wk, wks = oracle.kv_quant_int8(k, HD)
+    wv, wvs = oracle.kv_quant_int8(v, HD)
+    assert np.array_equal(host(qk), wk) and np.array_equal(host(ks), wks)
+    assert np.array_equal(host(qv), wv) and np.array_equal(host(vs), wvs)
+    assert np.array_equal(host(tk), k)  # the input is not written
+
+
+def _caches(rng, seq, nkv, hd, kind):
+    k = rng.standard_normal((seq, nkv, hd)).astype(np.float32)
+    v = rng.standard_normal((seq, nkv, hd)).astype(np.float32)
+    if kind == "f16":
+        return k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16), None, None
+    kq, ks = onp.kv_quant_int8(k.reshape(-1), hd)
+    vq, vs = onp.kv_quant_int8(v.reshape(-1), hd)
+    return kq, vq, ks, vs
+
+
+def _to_dev(a):
+    if a is None:
+        return None
+    if a.dtype == np.uint16:
+        return dev(a.view(np.float16))
+    return dev(a)
+
+
+@pytest.mark.parametrize("kind", ["f16", "int8"])
+@pytest.mark.parametrize("seq,hd,nh,nkv", [(1, 128, NH, NKV), (5, 128, NH, NKV), (1000, 128, NH, NKV),
+                                           (2500, 128, NH, NKV), (300, 64, 16, 2), (700, 256, 8, 8)])
+def test_attention(gpu, oracle, rng, kind, seq, hd, nh, nkv):
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kc, vc, ks, vs = _caches(rng, seq, nkv, hd, kind)
+    scale = 1.0 / np.sqrt(hd)
+    case(f"attention {kind} seq={seq} hd={hd} nh={nh} nkv={nkv}")
+    out = torch.full((nh * hd,), np.nan, device="cuda")
+    gpu.ops.attention(dev(q), _to_dev(kc), _to_dev(vc), out, nh, hd, nkv, seq, scale, _to_dev(ks), _to_dev(vs))
+    want = oracle.attention(q, kc, vc, nh, hd, nkv, seq, scale, ks, vs)
+    got = host(out)
+    assert rel_l2(got, want) < 1e-5
+    if seq == 1:
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("kind", ["f16", "int8"])
+def test_attn_prep_and_dev_attention(gpu, oracle, rng, kind):
+    """mnemo_attn_prep (QK norm + RoPE + store at *pos) then mnemo_attention over 0..*pos,
+    against the oracle chain; the cache rows below pos hold earlier tokens."""
+    ctx, pos, theta, eps = 64, 37, 1e6, 1e-6
+    q = rng.standard_normal(NH * HD).astype(np.float32)
+    k = rng.standard_normal(NKV * HD).astype(np.float32)
+    v = rng.standard_normal(NKV * HD).astype(np.float32)
+    qw = (1 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+    kw = (1 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+    kc, vc, ks, vs = _caches(rng, ctx, NKV, HD, kind)
+    tkc, tvc, tks, tvs = _to_dev(kc), _to_dev(vc), _to_dev(ks), _to_dev(vs)
+    tq, tk, tv = dev(q), dev(k), dev(v)
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    case(f"attn_prep {kind} pos={pos}")
+    gpu.ops.attn_prep(tq, tk, tv, dev(qw), dev(kw), HD, eps, theta, pos_dev, tkc, tvc, tks, tvs)
+    wq, wk = oracle.rope(oracle.rms_norm_heads(q, qw, HD, eps), oracle.rms_norm_heads(k, kw, HD, eps), HD, pos,
+                         theta)
+    tol = 1e-5 * max(np.abs(wq).max(), np.abs(wk).max())
+    gq, gk = host(tq), host(tk)
+    np.testing.assert_allclose(gq, wq, rtol=0, atol=tol)
+    np.testing.assert_allclose(gk, wk, rtol=0, atol=tol)
+    # cache rows: pos holds the stored k / v; other rows untouched
+    if kind == "f16":
+        ck, cv = host(tkc).view(np.uint16).reshape(ctx, -1), host(tvc).view(np.uint16).reshape(ctx, -1)
+        assert np.array_equal(ck[pos], gk.astype(np.float16).view(np.uint16))
+        assert np.array_equal(cv[pos], v.astype(np.float16).view(np.uint16))
+        rows = np.arange(ctx) != pos
+        assert np.array_equal(ck[rows], kc.reshape(ctx, -1)[rows]) and np.array_equal(cv[rows], vc.reshape(ctx, -1)[rows])
+    else:
+        ck, cv = host(tkc).reshape(ctx, -1), host(tvc).reshape(ctx, -1)
+        wkq, wks = oracle.kv_quant_int8(gk, HD)
+        wvq, wvs = oracle.kv_quant_int8(v, HD)
+        assert np.array_equal(ck[pos], wkq) and np.array_equal(host(tks).reshape(ctx, -1)[pos], wks)
+        assert np.array_equal(cv[pos], wvq) and np.array_equal(host(tvs).reshape(ctx, -1)[pos], wvs)
+    # attention over 0..pos with the length read on the device = the entry point with seq = pos + 1
+    out = torch.empty(NH * HD, device="cuda")
+    out2 = torch.empty(NH * HD, device="cuda")
+    gpu.ops.attention_dev(tq, tkc, tvc, out, NH, HD, NKV, pos_dev, 1 / np.sqrt(HD), tks, tvs)
+    gpu.ops.attention(tq, tkc, tvc, out2, NH, HD, NKV, pos + 1, 1 / np.sqrt(HD), tks, tvs)
+    assert torch.equal(out, out2)
+    if kind == "f16":
+        kk, vv = host(tkc).view(np.uint16), host(tvc).view(np.uint16)
+        want = oracle.attention(gq, kk, vv, NH, HD, NKV, pos + 1, 1 / np.sqrt(HD))
+    else:
+        want = oracle.attention(gq, host(tkc), host(tvc), NH, HD, NKV, pos + 1, 1 / np.sqrt(HD), host(tks),
+                                host(tvs))
+    assert rel_l2(host(out), want) < 1e-5
+
+
+def test_attn_chain_graph_replay(gpu, rng):
+    """prep + attention captured once, replayed for consecutive positions (pos in device
+    memory); every replay equals the eager chain at that position."""
+    ctx, theta, eps = 32, 1e6, 1e-6
+    qs = rng.standard_normal((4, NH * HD)).astype(np.float32)
+    ks_ = rng.standard_normal((4, NKV * HD)).astype(np.float32)
+    vs_ = rng.standard_normal((4, NKV * HD)).astype(np.float32)
+    qw = np.ones(HD, np.float32)
+    kw = np.ones(HD, np.float32)
+
+    def run(graph: bool):
+        kc = torch.zeros(ctx * NKV * HD, dtype=torch.float16, device="cuda")
+        vc = torch.zeros_like(kc)
+        q = torch.empty(NH * HD, device="cuda")
+        k = torch.empty(NKV * HD, device="cuda")
+        v = torch.empty(NKV * HD, device="cuda")
+        out = torch.empty(NH * HD, device="cuda")
+        pos_dev = torch.zeros(1, dtype=torch.int32, device="cuda")
+        tqw, tkw = dev(qw), dev(kw)
+        s = torch.cuda.Stream()
+        outs = []
+
+        def step():
+            gpu.ops.attn_prep(q, k, v, tqw, tkw, HD, eps, theta, pos_dev, kc, vc)
+            gpu.ops.attention_dev(q, kc, vc, out, NH, HD, NKV, pos_dev, 1 / np.sqrt(HD))
+
+        with torch.cuda.stream(s):
+            g = None
+            if graph:
+                q.copy_(dev(qs[0])); k.copy_(dev(ks_[0])); v.copy_(dev(vs_[0]))
+                step()  # eager once
+                torch.cuda.synchronize()
+                kc.zero_(); vc.zero_()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=s):
+                    step()
+            for t in range(4):
+                pos_dev.fill_(t)
+                q.copy_(dev(qs[t])); k.copy_(dev(ks_[t])); v.copy_(dev(vs_[t]))
+                if graph:
+                    g.replay()
+                else:
+                    step()
+                torch.cuda.synchronize()
+                outs.append(out.clone())
+        return outs
+
+    case("attention chain graph replay")
+    eager, replay = run(False), run(True)
+    for a, b in zip(eager, replay):
+        assert torch.equal(a, b)
+
+
+def test_bad_args(gpu):
+    case("attention bad args")
+    q = torch.zeros(NH * HD, device="cuda")
+    kc = torch.zeros(4 * NKV * HD, dtype=torch.float16, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    with pytest.raises(gpu.MnemoError):
+        gpu.ops.attention_dev(q, kc, kc, out, NH, 96, NKV, pos, 0.1)  # head_dim 96 unsupported
+    with pytest.raises(gpu.MnemoError):
+        gpu.ops.attention_dev(q, kc, kc, out, 63, HD, NKV, pos, 0.1)  # 63 % 4
+    with pytest.raises(gpu.MnemoError):
+        gpu.ops.attn_prep(q, q, q, q[:HD], None, HD, 1e-6, 1e6, pos, kc, kc)  # one norm weight
