@@ -231,6 +231,19 @@ int mnemo_attention(const float *q, const void *k_cache, const void *v_cache,
                     int n_heads, int head_dim, int n_kv_heads, const int *pos_dev, float scale,
                     hipStream_t stream);
 
+/* New: the same attention for head_dim 128 and gqa <= 16 on the matrix cores, split over
+ * 64-position chunks (each KV head is read once per chunk for all of its query heads; the
+ * reference's attention_kernel_f16kv streams it once per query head, kernels.cu:1550-1660),
+ * then merged per query head: two launches, capture-safe.  Positions 0..*pos_dev
+ * (< max_ctx).  workspace: mnemo_attention_decode_workspace_bytes(n_kv_heads, max_ctx)
+ * bytes, 16-byte aligned, no initialisation; calls sharing it must not overlap. */
+size_t mnemo_attention_decode_workspace_bytes(int n_kv_heads, int max_ctx);
+int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_cache,
+                           const float *k_scales, const float *v_scales, int kv_type, float *out,
+                           int n_heads, int head_dim, int n_kv_heads, int max_ctx,
+                           const int *pos_dev, float scale, void *workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

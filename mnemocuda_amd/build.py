@@ -21,7 +21,7 @@ BUILD = ROOT / "_build"
 LIB = PKG / "libmnemo_hip.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
-HIP_SOURCES = ["abi.hip", "gemv_launch.hip", "router.hip", "gemm.hip", "moe.hip", "sample.hip", "attn.hip"]
+HIP_SOURCES = ["abi.hip", "gemv_launch.hip", "router.hip", "gemm.hip", "moe.hip", "sample.hip", "attn.hip", "attn_decode.hip"]
 C_SOURCES = ["host/mnemo_host.c"]
 
 HIPCC_FLAGS = [

@@ -396,6 +396,36 @@ int mnemo_attention(const float *q, const void *k_cache, const void *v_cache, co
     return launch_attention(a, kv_type, s);
 }
 
+size_t mnemo_attention_decode_workspace_bytes(int n_kv_heads, int max_ctx) {
+    return n_kv_heads > 0 && max_ctx > 0 ? attn_decode_workspace_bytes(n_kv_heads, max_ctx) : 0;
+}
+
+int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_cache, const float *k_scales,
+                           const float *v_scales, int kv_type, float *out, int n_heads, int head_dim, int n_kv_heads,
+                           int max_ctx, const int *pos_dev, float scale, void *workspace, size_t workspace_bytes,
+                           hipStream_t s) {
+    if (kv_type != kKvF16 && kv_type != kKvInt8) return set_error(kErrBadArg, "attention_decode: kv_type %d", kv_type);
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads) return set_error(kErrBadArg, "attention_decode: n_heads %% n_kv_heads");
+    if ((uintptr_t)workspace % 16) return set_error(kErrBadArg, "attention_decode: workspace not 16-byte aligned");
+    AttnDecodeArgs a = {};
+    a.q = q;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.ksc = k_scales;
+    a.vsc = v_scales;
+    a.out = out;
+    a.ws = (float *)workspace;
+    a.ws_bytes = workspace_bytes;
+    a.nh = n_heads;
+    a.hd = head_dim;
+    a.nkv = n_kv_heads;
+    a.gqa = n_heads / n_kv_heads;
+    a.max_ctx = max_ctx;
+    a.pos_dev = pos_dev;
+    a.scale = scale;
+    return launch_attention_decode(a, kv_type, s);
+}
+
 size_t mnemo_moe_prefill_workspace_bytes(int n_tokens, int hidden, int eff, int n_experts, int k) {
     return moe_prefill_workspace_bytes(n_tokens, hidden, eff, n_experts, k);
 }

@@ -1,0 +1,249 @@
+// attn_decode.hip -- decode attention for grouped-query heads on the matrix cores.
+//
+// Same result as the reference's attention_kernel_f16kv / _int8kv (MnemoCUDA
+// kernels.cu:1550-1660, 1382-1481): out[h] = softmax_p(scale * q_h . k_p) v_p over the
+// positions 0..*pos_dev of the cache [pos][n_kv_heads][head_dim].  The reference runs one
+// block per query head, so each KV head is streamed gqa times and one block walks the
+// whole sequence.  Here:
+//  * one wave per (KV head, 64-position chunk): the gqa (<= 16) query heads that share the
+//    KV head are the 16 rows of v_mfma_f32_16x16x32_f16, so K and V are read once per
+//    chunk, and the chunks of a long sequence spread over the whole chip;
+//  * S = Q K^T: K fragments come straight from the cache (8 consecutive dims per lane);
+//    Q is split into f16 hi + lo parts (two MFMAs) so the product keeps ~fp32 precision;
+//  * softmax over the chunk in registers (16-lane row reductions), P split hi + lo;
+//  * O = P V: V goes through LDS so that each lane can gather 8 consecutive positions of
+//    one dim (the MFMA's K direction);
+//  * each chunk writes (max, sum, O) to the workspace; a second launch merges the chunks
+//    per query head (the flash-decoding combine).
+// int8 caches: K and V bytes convert exactly to f16; the per-position K scale multiplies
+// the score column, the V scale is folded into P.
+#include "mnemo_common.hpp"
+#include "mnemo_internal.hpp"
+
+namespace mnemo {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kChunk = 64;       // positions per wave
+constexpr int kHd = 128;         // head_dim of this kernel
+constexpr int kRows = 16;        // query heads per KV head handled (MFMA rows)
+constexpr int kPart = 2 * kRows + kRows * kHd;  // floats per (KV head, chunk) partial
+
+size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx) {
+    const size_t chunks = ((size_t)max_ctx + kChunk - 1) / kChunk;
+    return (size_t)n_kv_heads * chunks * kPart * sizeof(float);
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+template <int KV>
+__global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
+    __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
+    __shared__ __align__(16) _Float16 vt[kChunk][kHd + 8];    // V tile [pos][dim]
+    __shared__ __align__(16) _Float16 ps[2][kRows][kChunk + 8];
+    const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
+    const int seq = min(*a.pos_dev + 1, a.max_ctx);
+    const int p0 = chunk * kChunk;
+    if (p0 >= seq) return;  // the combine reads ceil(seq / 64) chunks only
+    const int G = a.gqa;
+    const size_t stride = (size_t)a.nkv * kHd;
+    const int r = lane & 15, kg = lane >> 4;
+
+    // ---- loads first: K fragments (4 tiles of 16 positions x 4 steps of 32 dims) and the V tile
+    constexpr int EB = KV == kKvF16 ? 2 : 1;  // bytes per cache element
+    const uint8_t *kc = (const uint8_t *)a.kc, *vc = (const uint8_t *)a.vc;
+    uint4 kr[16];  // f16: 8 halves; int8: 8 bytes in .x/.y
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int p = min(p0 + 16 * t + r, seq - 1);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const size_t off = ((size_t)p * stride + (size_t)kvh * kHd + 32 * s + 8 * kg) * EB;
+            if (KV == kKvF16) __builtin_memcpy(&kr[4 * t + s], kc + off, 16);
+            else __builtin_memcpy(&kr[4 * t + s], kc + off, 8);
+        }
+    }
+    uint4 vr[16];  // 16-element chunk c = lane + 64u of the tile: position c / 16, dims 8 (c % 16)
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+        const int c = lane + 64 * u;
+        const int p = min(p0 + (c >> 4), seq - 1);
+        const size_t off = ((size_t)p * stride + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
+        if (KV == kKvF16) __builtin_memcpy(&vr[u], vc + off, 16);
+        else __builtin_memcpy(&vr[u], vc + off, 8);
+    }
+    float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, vsc = 1.0f;
+    if (KV == kKvInt8) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) ksc[t] = a.ksc[(size_t)min(p0 + 16 * t + r, seq - 1) * a.nkv + kvh];
+    }
+
+    // ---- Q rows (heads kvh*G .. +G-1) as f16 hi + lo
+    for (int e = lane; e < kRows * kHd / 4; e += 64) {
+        const int h = e / (kHd / 4), d = 4 * (e % (kHd / 4));
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (h < G) v = *(const float4 *)(a.q + (size_t)(kvh * G + h) * kHd + d);
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const _Float16 hi = (_Float16)vv[j];
+            qs[0][h][d + j] = hi;
+            qs[1][h][d + j] = (_Float16)(vv[j] - (float)hi);
+        }
+    }
+    __syncthreads();
+
+    // ---- S = Q K^T for 4 tiles of 16 positions
+    f4 sc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        f4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            h8 b;
+            if (KV == kKvF16) {
+                __builtin_memcpy(&b, &kr[4 * t + s], 16);
+            } else {
+                const int8_t *kb = (const int8_t *)&kr[4 * t + s];
+#pragma unroll
+                for (int j = 0; j < 8; j++) b[j] = (_Float16)kb[j];
+            }
+            h8 ah, al;
+            __builtin_memcpy(&ah, &qs[0][r][32 * s + 8 * kg], 16);
+            __builtin_memcpy(&al, &qs[1][r][32 * s + 8 * kg], 16);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, c, 0, 0, 0);
+        }
+        sc[t] = c;
+    }
+    // lane holds heads 4kg + i, position p0 + 16t + r
+    float m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const bool ok = p0 + 16 * t + r < seq;
+            const float s = ok ? sc[t][i] * (a.scale * ksc[t]) : -INFINITY;
+            sc[t][i] = s;
+            mx = fmaxf(mx, s);
+        }
+        m[i] = row16_max(mx);  // every row has position p0 < seq, so m is finite
+        float sum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float e = expf(sc[t][i] - m[i]);  // exp(-inf) = 0 for masked positions
+            sc[t][i] = e;
+            sum += e;
+        }
+        l[i] = row16_sum(sum);
+    }
+    // ---- P (times the V scale for int8) to LDS as hi + lo, V tile to LDS
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        if (KV == kKvInt8) vsc = a.vsc[(size_t)min(p0 + 16 * t + r, seq - 1) * a.nkv + kvh];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float pv = sc[t][i] * vsc;
+            const _Float16 hi = (_Float16)pv;
+            ps[0][4 * kg + i][16 * t + r] = hi;
+            ps[1][4 * kg + i][16 * t + r] = (_Float16)(pv - (float)hi);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 16; u++) {
+        const int c = lane + 64 * u;
+        h8 v;
+        if (KV == kKvF16) {
+            __builtin_memcpy(&v, &vr[u], 16);
+        } else {
+            const int8_t *vb = (const int8_t *)&vr[u];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = (_Float16)vb[j];
+        }
+        __builtin_memcpy(&vt[c >> 4][8 * (c & 15)], &v, 16);
+    }
+    __syncthreads();
+
+    // ---- O = P V: 8 tiles of 16 dims, 2 steps of 32 positions
+    f4 o[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++) o[n] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+        h8 ah, al;
+        __builtin_memcpy(&ah, &ps[0][r][32 * kk + 8 * kg], 16);
+        __builtin_memcpy(&al, &ps[1][r][32 * kk + 8 * kg], 16);
+#pragma unroll
+        for (int n = 0; n < 8; n++) {
+            h8 b;
+#pragma unroll
+            for (int j = 0; j < 8; j++) b[j] = vt[32 * kk + 8 * kg + j][16 * n + r];
+            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, o[n], 0, 0, 0);
+            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, o[n], 0, 0, 0);
+        }
+    }
+    // ---- partial: m[16], l[16], o[16][128]
+    float *part = a.ws + ((size_t)kvh * a.max_chunks + chunk) * kPart;
+    if (r == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            part[4 * kg + i] = m[i];
+            part[kRows + 4 * kg + i] = l[i];
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < 8; n++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * n + r] = o[n][i];
+}
+
+// One workgroup of head_dim threads per query head: merges the chunks' (max, sum, O).
+__global__ void __launch_bounds__(kHd) attn_combine_kernel(AttnDecodeArgs a) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    const int kvh = h / a.gqa, hh = h % a.gqa;
+    const int seq = min(*a.pos_dev + 1, a.max_ctx);
+    const int nc = (seq + kChunk - 1) / kChunk;
+    const float *base = a.ws + (size_t)kvh * a.max_chunks * kPart;
+    float M = -INFINITY;
+    for (int c = 0; c < nc; c++) M = fmaxf(M, base[(size_t)c * kPart + hh]);
+    float L = 0.0f, O = 0.0f;
+    for (int c = 0; c < nc; c++) {
+        const float *p = base + (size_t)c * kPart;
+        const float w = expf(p[hh] - M);
+        L = fmaf(p[kRows + hh], w, L);
+        O = fmaf(p[2 * kRows + hh * kHd + d], w, O);
+    }
+    a.out[(size_t)h * kHd + d] = O / L;
+}
+
+int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s) {
+    if (!a.q || !a.kc || !a.vc || !a.out || !a.pos_dev || !a.ws)
+        return set_error(kErrBadArg, "attention_decode: NULL pointer");
+    if (a.hd != kHd) return set_error(kErrBadArg, "attention_decode: head_dim %d (this kernel: %d)", a.hd, kHd);
+    if (a.nkv <= 0 || a.gqa <= 0 || a.gqa > kRows || a.nh != a.nkv * a.gqa)
+        return set_error(kErrBadArg, "attention_decode: n_heads = n_kv_heads * gqa with gqa <= %d", kRows);
+    if (a.max_ctx <= 0) return set_error(kErrBadArg, "attention_decode: max_ctx <= 0");
+    if (kv_type == kKvInt8 && (!a.ksc || !a.vsc)) return set_error(kErrBadArg, "attention_decode: int8 needs scales");
+    if (a.ws_bytes < attn_decode_workspace_bytes(a.nkv, a.max_ctx))
+        return set_error(kErrBadArg, "attention_decode: workspace %zu < %zu bytes", a.ws_bytes,
+                         attn_decode_workspace_bytes(a.nkv, a.max_ctx));
+    a.max_chunks = (a.max_ctx + kChunk - 1) / kChunk;
+    const dim3 grid(a.max_chunks, a.nkv);
+    if (kv_type == kKvF16) hipLaunchKernelGGL(attn_chunk_kernel<kKvF16>, grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(attn_chunk_kernel<kKvInt8>, grid, dim3(64), 0, s, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh), dim3(kHd), 0, s, a);
+    return check_launch("attention_decode");
+}
+
+}  // namespace mnemo

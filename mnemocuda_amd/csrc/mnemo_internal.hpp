@@ -98,6 +98,21 @@ struct AttnArgs {
     float scale;
 };
 
+struct AttnDecodeArgs {
+    const float *q;
+    const void *kc, *vc;
+    const float *ksc, *vsc;
+    float *out;
+    float *ws;
+    size_t ws_bytes;
+    int nh, hd, nkv, gqa;
+    int max_ctx, max_chunks;
+    const int *pos_dev;  // sequence length = min(*pos_dev + 1, max_ctx)
+    float scale;
+};
+size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx);
+int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s);
+
 int launch_rms_norm(const float *in, const float *w, float *out, float *res, int n, float eps, hipStream_t s);
 int launch_residual_add(const float *a, const float *b, float *out, int n, hipStream_t s);
 int launch_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n, hipStream_t s);

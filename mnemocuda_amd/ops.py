@@ -358,3 +358,19 @@ def attention_dev(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: int, 
                              _opt(vs, "vs", F32), kv_type, _dev(out, "out", F32), n_heads, head_dim, n_kv_heads,
                              _dev(pos_dev, "pos_dev", torch.int32), float(scale), _stream())
     _check_rc(lib, rc, "mnemo_attention")
+
+
+def attention_decode_workspace_bytes(n_kv_heads: int, max_ctx: int) -> int:
+    return int(load_library().mnemo_attention_decode_workspace_bytes(n_kv_heads, max_ctx))
+
+
+def attention_decode(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: int, max_ctx: int, pos_dev,
+                     scale: float, ws, ks=None, vs=None):
+    """GQA-batched split-position attention over positions 0..pos_dev[0] (matrix cores)."""
+    lib = load_library()
+    kv_type = 0 if kc.dtype == torch.float16 else 1
+    rc = lib.mnemo_attention_decode(_dev(q, "q", F32), _dev(kc, "kc"), _dev(vc, "vc"), _opt(ks, "ks", F32),
+                                    _opt(vs, "vs", F32), kv_type, _dev(out, "out", F32), n_heads, head_dim,
+                                    n_kv_heads, int(max_ctx), _dev(pos_dev, "pos_dev", torch.int32), float(scale),
+                                    _dev(ws, "ws"), ws.numel() * ws.element_size(), _stream())
+    _check_rc(lib, rc, "mnemo_attention_decode")

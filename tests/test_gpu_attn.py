@@ -250,3 +250,70 @@ def test_bad_args(gpu):
         gpu.ops.attention_dev(q, kc, kc, out, 63, HD, NKV, pos, 0.1)  # 63 % 4
     with pytest.raises(gpu.MnemoError):
         gpu.ops.attn_prep(q, q, q, q[:HD], None, HD, 1e-6, 1e6, pos, kc, kc)  # one norm weight
+
+
+# ------------------------------------------------------------------ GQA-batched decode attention
+@pytest.mark.parametrize("kind", ["f16", "int8"])
+@pytest.mark.parametrize("seq,nh,nkv", [(1, NH, NKV), (63, NH, NKV), (64, NH, NKV), (65, NH, NKV), (1000, NH, NKV),
+                                        (4097, NH, NKV), (300, 32, 4), (200, 8, 8)])
+def test_attention_decode(gpu, oracle, rng, kind, seq, nh, nkv):
+    max_ctx = 8192
+    q = rng.standard_normal(nh * HD).astype(np.float32)
+    kc, vc, ks, vs = _caches(rng, max_ctx, nkv, HD, kind)
+    pos_dev = torch.tensor([seq - 1], dtype=torch.int32, device="cuda")
+    ws = torch.empty(gpu.ops.attention_decode_workspace_bytes(nkv, max_ctx), dtype=torch.uint8, device="cuda")
+    out = torch.full((nh * HD,), np.nan, device="cuda")
+    scale = 1.0 / np.sqrt(HD)
+    case(f"attention_decode {kind} seq={seq} nh={nh} nkv={nkv}")
+    gpu.ops.attention_decode(dev(q), _to_dev(kc), _to_dev(vc), out, nh, HD, nkv, max_ctx, pos_dev, scale, ws,
+                             _to_dev(ks), _to_dev(vs))
+    if kind == "f16":
+        want = oracle.attention(q, kc[:seq], vc[:seq], nh, HD, nkv, seq, scale)
+    else:
+        want = oracle.attention(q, kc[:seq * nkv * HD], vc[:seq * nkv * HD], nh, HD, nkv, seq, scale,
+                                ks[:seq * nkv], vs[:seq * nkv])
+    assert rel_l2(host(out), want) < 1e-5
+
+
+def test_attention_decode_graph_replay(gpu, rng):
+    """captured once; replays at growing positions equal the eager calls."""
+    max_ctx = 1024
+    q = dev(rng.standard_normal(NH * HD).astype(np.float32))
+    kc, vc, _, _ = _caches(rng, max_ctx, NKV, HD, "f16")
+    tkc, tvc = _to_dev(kc), _to_dev(vc)
+    pos_dev = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(gpu.ops.attention_decode_workspace_bytes(NKV, max_ctx), dtype=torch.uint8, device="cuda")
+    out = torch.empty(NH * HD, device="cuda")
+    s = torch.cuda.Stream()
+    case("attention_decode graph replay")
+    positions = [0, 5, 63, 64, 500, 1023]
+    eager = []
+    with torch.cuda.stream(s):
+        for p in positions:
+            pos_dev.fill_(p)
+            gpu.ops.attention_decode(q, tkc, tvc, out, NH, HD, NKV, max_ctx, pos_dev, 0.088, ws)
+            torch.cuda.synchronize()
+            eager.append(out.clone())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            gpu.ops.attention_decode(q, tkc, tvc, out, NH, HD, NKV, max_ctx, pos_dev, 0.088, ws)
+        for p, e in zip(positions, eager):
+            pos_dev.fill_(p)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, e), p
+
+
+def test_attention_decode_bad_args(gpu):
+    case("attention_decode bad args")
+    q = torch.zeros(NH * HD, device="cuda")
+    kc = torch.zeros(64 * NKV * HD, dtype=torch.float16, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    ws = torch.empty(gpu.ops.attention_decode_workspace_bytes(NKV, 64), dtype=torch.uint8, device="cuda")
+    with pytest.raises(gpu.MnemoError):  # workspace too small for max_ctx
+        gpu.ops.attention_decode(q, kc, kc, out, NH, HD, NKV, 4096, pos, 0.1, ws)
+    with pytest.raises(gpu.MnemoError):  # gqa 32 > 16
+        gpu.ops.attention_decode(q, kc, kc, out, NH, HD, 2, 64, pos, 0.1, ws)
+    with pytest.raises(gpu.MnemoError):  # head_dim 64 not on this path
+        gpu.ops.attention_decode(q, kc, kc, out, NH, 64, NKV, 64, pos, 0.1, ws)
