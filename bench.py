@@ -57,6 +57,7 @@ def parse():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the full decode-step tok/s (147 GB of experts)")
     ap.add_argument("--decode-tokens", type=int, default=20)
+    ap.add_argument("--decode-pos", type=int, default=2048, help="KV-cache position of the first decoded token")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with a 256 MiB device copy (torch.neg) whose HBM counters scale rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE readings (mnemocuda_amd/profiling.py)")
@@ -180,72 +181,127 @@ def gpu_bench(args):
         moe = None
         if not args.no_moe:
             moe = moe_prefill_bench(gen, s)
-        decode = None
+        decode = attn = None
         if not args.no_decode:
-            decode = decode_bench(gen, s, layers, args.decode_tokens)
+            attn = attention_bench(s)
+            decode = decode_bench(gen, s, layers, args.decode_tokens, args.decode_pos)
     return dict(step_s=step_s, wall=wall, d_qkv=d_qkv, d_q=d_q, d_kv=d_kv, d_o=d_o, gemm=gemm, moe=moe,
-                decode=decode)
+                decode=decode, attn=attn)
 
 
-def decode_bench(gen, stream, layers, tokens):
-    """configs[2] in a full decode step: per token and layer, fused QKV, O (+ residual,
-    its input the Q output standing in for the attention core, which is out of scope),
-    then the MoE block with device-side dispatch (router 128 x 4096 fp32, top-8, gate+up
-    Q4_K 4096->1536 x 8, down Q6_K 1536->4096 x 8 + router-weighted combine); then the
-    lm_head Q6_K 151936 x 4096 GEMV.  All 128 experts of all 94 layers are resident
-    (147 GB).  Each token and layer gets a fresh random input vector, so routing varies
-    like real traffic (no expert reuse in the caches between tokens)."""
+def decode_bench(gen, stream, layers, tokens, ctx_pos):
+    """configs[2] inside a full decode step (forward.c:687-1077 per layer, then the lm_head
+    and sampling, forward.c:1601-1707), one token at cache position ctx_pos, ctx_pos+1, ...:
+    per layer  RMS norm (+ residual save) -> fused Q/K/V -> QK norm + RoPE + f16 KV store
+    (position in device memory) -> GQA decode attention over 0..pos -> O (+ residual) ->
+    RMS norm -> MoE block with device-side dispatch (router 128 x 4096 fp32, top-8, gate+up
+    Q4_K 4096->1536 x 8, down Q6_K 1536->4096 x 8, weighted sum added to the residual);
+    then the final norm, lm_head Q6_K 151936 x 4096 and top-p sampling.  All 128 experts of
+    all 94 layers are resident (147 GB); the KV cache rows below ctx_pos hold random
+    earlier tokens.  One hipGraph per token (the position advances on the device)."""
     import torch
     from mnemocuda_amd import ops, synth
     E, k, EFF, VOCAB = 128, 8, 1536, 151936
+    NH, NKV, HD, EPS, THETA = 64, 4, 128, 1e-6, 1e6
+    max_ctx = ctx_pos + tokens + 8
     stride, g_off, u_off, d_off = synth.expert_layout(H, EFF, Q6K)
     tables = [synth.expert_table_torch(gen, E, H, EFF, Q6K, "cuda") for _ in range(LAYERS)]
     routers = [torch.randn(E, H, device="cuda", generator=gen) / 64 for _ in range(LAYERS)]
+    norms = [dict(attn=1 + 0.05 * torch.randn(H, device="cuda", generator=gen),
+                  ffn=1 + 0.05 * torch.randn(H, device="cuda", generator=gen),
+                  q=1 + 0.05 * torch.randn(HD, device="cuda", generator=gen),
+                  k=1 + 0.05 * torch.randn(HD, device="cuda", generator=gen)) for _ in range(LAYERS)]
+    kcache = [(torch.randn(max_ctx * NKV * HD, device="cuda", generator=gen)).half() for _ in range(LAYERS)]
+    vn = ops.v_cache_bytes(NKV, HD, max_ctx, 0, 1) // 2  # V in the blocked layout of attention_decode
+    vcache = [(torch.randn(vn, device="cuda", generator=gen)).half() for _ in range(LAYERS)]
     lm_head = synth.weights_torch(gen, Q6K, VOCAB, H, "cuda")
-    X = torch.randn(tokens, LAYERS, H, device="cuda", generator=gen)
-    xbuf = torch.empty(LAYERS, H, device="cuda")
-    q, kk, v = torch.empty(QD, device="cuda"), torch.empty(KVD, device="cuda"), torch.empty(KVD, device="cuda")
+    final_norm = 1 + 0.05 * torch.randn(H, device="cuda", generator=gen)
+    X0 = torch.randn(H, device="cuda", generator=gen)
+    res = torch.empty(H, device="cuda")
     hid = torch.empty(H, device="cuda")
+    normed = torch.empty(H, device="cuda")
+    q, kk, v = torch.empty(QD, device="cuda"), torch.empty(KVD, device="cuda"), torch.empty(KVD, device="cuda")
+    attn = torch.empty(QD, device="cuda")
     logits = torch.empty(VOCAB, device="cuda")
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws = torch.zeros(ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    aws = torch.empty(ops.attention_decode_workspace_bytes(NKV, max_ctx), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / HD ** 0.5
 
     def token():
         for li, L in enumerate(layers):
-            ops.matvec_qkv(L["q"], Q4K, L["k"], Q4K, L["v"], Q6K, xbuf[li], q, kk, v, QD, KVD, H)
-            ops.matvec_q4k_add(L["o"], q, xbuf[li], hid, H, QD)
-            ops.moe_decode(routers[li], tables[li], stride, g_off, u_off, d_off, Q6K, hid, H, EFF, E, k, ws, hid)
-        ops.matvec_q6k(lm_head, hid, logits, VOCAB, H)
+            n = norms[li]
+            ops.rms_norm(res, n["attn"], normed, EPS, residual=res)  # res = layer input
+            ops.matvec_qkv(L["q"], Q4K, L["k"], Q4K, L["v"], Q6K, normed, q, kk, v, QD, KVD, H)
+            ops.attn_prep(q, kk, v, n["q"], n["k"], HD, EPS, THETA, pos, kcache[li], vcache[li], v_layout=1)
+            ops.attention_decode(q, kcache[li], vcache[li], attn, NH, HD, NKV, max_ctx, pos, scale, aws, v_layout=1)
+            ops.matvec_q4k_add(L["o"], attn, res, hid, H, QD)
+            ops.rms_norm(hid, n["ffn"], normed, EPS, residual=res)  # res = hid
+            ops.moe_decode(routers[li], tables[li], stride, g_off, u_off, d_off, Q6K, normed, H, EFF, E, k, ws, res)
+        ops.rms_norm(res, final_norm, normed, EPS)
+        ops.matvec_q6k(lm_head, normed, logits, VOCAB, H)
         ops.sample_token(logits, VOCAB, 0.7, 0.9, 12345, tok)
+        pos.add_(1)
 
     with torch.cuda.stream(stream):
-        xbuf.copy_(X[0])
+        res.copy_(X0)
+        pos.fill_(ctx_pos)
         token()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
             token()
-        for t in range(2):
-            xbuf.copy_(X[t])
+        for _ in range(2):
+            res.copy_(X0)
             g.replay()
         torch.cuda.synchronize()
+        pos.fill_(ctx_pos)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
         for t in range(tokens):
-            xbuf.copy_(X[t])
+            res.copy_(X0)
             g.replay()
         b.record(stream)
         torch.cuda.synchronize()
     ms = a.elapsed_time(b) / tokens
     moe_bytes = (E * H * 4 + H * 4 + E * 4) + k * (2 * EFF * (H // 256) * 144 + H * (EFF // 256) * 210)
-    per_tok = BYTES_LAYER * LAYERS + moe_bytes * LAYERS + VOCAB * (H // 256) * 210
-    del tables, routers, lm_head
+    kv_bytes = 2 * NKV * HD * 2 * (ctx_pos + tokens // 2)  # K + V rows read per layer, mean position
+    per_tok = (BYTES_LAYER + moe_bytes + kv_bytes) * LAYERS + VOCAB * (H // 256) * 210
+    del tables, routers, lm_head, kcache, vcache
     torch.cuda.empty_cache()
     return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 3), "tokens": tokens,
-            "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
+            "context_position": ctx_pos, "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
             "frac_hbm_peak": round(per_tok / ms / 1e6 / HBM_PEAK_GBS, 4),
             "experts_resident_GB": round(E * LAYERS * stride / 1e9, 1),
-            "launches_per_token": LAYERS * 5 + 2}
+            "launches_per_token": LAYERS * 10 + 4}
+
+
+def attention_bench(stream, lengths=(1024, 4096, 16384, 32768)):
+    """Decode attention for one layer (64 query heads, 4 KV heads, head_dim 128, f16 cache)
+    at several sequence lengths: the GQA-batched split kernel with V in the blocked layout
+    (the decode path) and in the reference's row layout, and the reference-form entry point
+    (one workgroup per query head), graph-timed over 20 launches."""
+    import torch
+    from mnemocuda_amd import ops
+    NH, NKV, HD = 64, 4, 128
+    out = {}
+    for L in lengths:
+        kc = torch.randn(L * NKV * HD, device="cuda").half()
+        vc = torch.randn(L * NKV * HD, device="cuda").half()
+        q = torch.randn(NH * HD, device="cuda")
+        o = torch.empty(NH * HD, device="cuda")
+        pos = torch.tensor([L - 1], dtype=torch.int32, device="cuda")
+        ws = torch.empty(ops.attention_decode_workspace_bytes(NKV, L), dtype=torch.uint8, device="cuda")
+        fast = time_launches(lambda i: ops.attention_decode(q, kc, vc, o, NH, HD, NKV, L, pos, 0.088, ws, v_layout=1),
+                             20, stream)
+        rows = time_launches(lambda i: ops.attention_decode(q, kc, vc, o, NH, HD, NKV, L, pos, 0.088, ws), 20, stream)
+        ref = time_launches(lambda i: ops.attention(q, kc, vc, o, NH, HD, NKV, L, 0.088), 20, stream)
+        kv = 2 * L * NKV * HD * 2
+        out[str(L)] = {"gqa_split_us": round(fast * 1e6, 2), "gqa_split_rowsV_us": round(rows * 1e6, 2),
+                       "per_head_us": round(ref * 1e6, 2), "gqa_split_kv_GBps": round(kv / fast / 1e9, 1)}
+        del kc, vc
+    return out
 
 
 def moe_prefill_bench(gen, stream):
@@ -361,6 +417,7 @@ def main():
             "gemm_q4k_m512": r["gemm"],
             "moe_prefill_cfg4": r["moe"],
             "decode_tok_s": r["decode"],
+            "decode_attention_one_layer": r["attn"],
             "wall_s_timed": round(r["wall"], 3),
         },
     }

@@ -219,12 +219,17 @@ void cuda_attention_int8kv(const float *q, const void *kv_k, const void *kv_v,
  * with the position read from device memory (*pos_dev), so a captured graph replays for
  * every token without the kernel-node updates of forward.c:638-666.  q [n_heads][head_dim]
  * and k [n_kv_heads][head_dim] are normalised (when both weights are given) and rotated in
- * place; k and v are stored at cache row *pos_dev ([pos][n_kv_heads][head_dim]; kv_type 0
- * f16, 1 int8 with scales [pos][n_kv_heads]).  head_dim even, <= 512. */
+ * place; k is stored at cache row *pos_dev ([pos][n_kv_heads][head_dim]), v likewise
+ * (v_layout 0) or in the blocked layout of mnemo_attention_decode (v_layout 1:
+ * [pos/64][n_kv_heads][head_dim][pos%64]).  kv_type 0 f16, 1 int8 with scales
+ * [pos][n_kv_heads].  head_dim even, <= 512. */
 int mnemo_attn_prep(float *q, float *k, const float *v, const float *q_norm_w,
                     const float *k_norm_w, int head_dim, int n_heads, int n_kv_heads, float eps,
                     float theta, const int *pos_dev, void *k_cache, void *v_cache,
-                    float *k_scales, float *v_scales, int kv_type, hipStream_t stream);
+                    float *k_scales, float *v_scales, int kv_type, int v_layout,
+                    hipStream_t stream);
+/* Bytes of a V cache for max_ctx positions in the given layout (blocked: rounded up to 64). */
+size_t mnemo_v_cache_bytes(int n_kv_heads, int head_dim, int max_ctx, int kv_type, int v_layout);
 /* New: cuda_attention_* over positions 0..*pos_dev (the length read from device memory). */
 int mnemo_attention(const float *q, const void *k_cache, const void *v_cache,
                     const float *k_scales, const float *v_scales, int kv_type, float *out,
@@ -235,12 +240,15 @@ int mnemo_attention(const float *q, const void *k_cache, const void *v_cache,
  * 64-position chunks (each KV head is read once per chunk for all of its query heads; the
  * reference's attention_kernel_f16kv streams it once per query head, kernels.cu:1550-1660),
  * then merged per query head: two launches, capture-safe.  Positions 0..*pos_dev
- * (< max_ctx).  workspace: mnemo_attention_decode_workspace_bytes(n_kv_heads, max_ctx)
- * bytes, 16-byte aligned, no initialisation; calls sharing it must not overlap. */
+ * (< max_ctx <= 65536).  K cache [pos][n_kv_heads][head_dim]; V cache in v_layout 0 (the
+ * same rows) or 1 (blocked, mnemo_attn_prep's v_layout 1: the fast path; allocate
+ * mnemo_v_cache_bytes and zero-fill it once, the rows past the sequence in the last block
+ * are read with weight 0).  workspace: mnemo_attention_decode_workspace_bytes(n_kv_heads,
+ * max_ctx) bytes, 16-byte aligned, no initialisation; calls sharing it must not overlap. */
 size_t mnemo_attention_decode_workspace_bytes(int n_kv_heads, int max_ctx);
 int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_cache,
-                           const float *k_scales, const float *v_scales, int kv_type, float *out,
-                           int n_heads, int head_dim, int n_kv_heads, int max_ctx,
+                           const float *k_scales, const float *v_scales, int kv_type, int v_layout,
+                           float *out, int n_heads, int head_dim, int n_kv_heads, int max_ctx,
                            const int *pos_dev, float scale, void *workspace,
                            size_t workspace_bytes, hipStream_t stream);
 

@@ -346,8 +346,9 @@ void cuda_attention_int8kv(const float *q, const void *kv_k, const void *kv_v, c
 
 int mnemo_attn_prep(float *q, float *k, const float *v, const float *q_norm_w, const float *k_norm_w, int head_dim,
                     int n_heads, int n_kv_heads, float eps, float theta, const int *pos_dev, void *k_cache,
-                    void *v_cache, float *k_scales, float *v_scales, int kv_type, hipStream_t s) {
+                    void *v_cache, float *k_scales, float *v_scales, int kv_type, int v_layout, hipStream_t s) {
     if (!pos_dev) return set_error(kErrBadArg, "attn_prep: pos_dev is NULL");
+    if (v_layout != 0 && v_layout != 1) return set_error(kErrBadArg, "attn_prep: v_layout %d", v_layout);
     if (kv_type != kKvF16 && kv_type != kKvInt8) return set_error(kErrBadArg, "attn_prep: kv_type %d", kv_type);
     if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
         return set_error(kErrBadArg, "attn_prep: give both QK-norm weights or neither");
@@ -369,6 +370,7 @@ int mnemo_attn_prep(float *q, float *k, const float *v, const float *q_norm_w, c
     a.ksc = k_scales;
     a.vsc = v_scales;
     a.kv_type = kv_type;
+    a.v_layout = v_layout;
     a.flags = (q_norm_w ? kHeadNorm : 0) | kHeadRope | kHeadStore;
     return launch_head_pass(a, s);
 }
@@ -400,10 +402,16 @@ size_t mnemo_attention_decode_workspace_bytes(int n_kv_heads, int max_ctx) {
     return n_kv_heads > 0 && max_ctx > 0 ? attn_decode_workspace_bytes(n_kv_heads, max_ctx) : 0;
 }
 
+size_t mnemo_v_cache_bytes(int n_kv_heads, int head_dim, int max_ctx, int kv_type, int v_layout) {
+    if (n_kv_heads <= 0 || head_dim <= 0 || max_ctx <= 0) return 0;
+    const size_t rows = v_layout == 1 ? ((size_t)max_ctx + 63) / 64 * 64 : (size_t)max_ctx;
+    return rows * n_kv_heads * head_dim * (kv_type == kKvInt8 ? 1 : 2);
+}
+
 int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_cache, const float *k_scales,
-                           const float *v_scales, int kv_type, float *out, int n_heads, int head_dim, int n_kv_heads,
-                           int max_ctx, const int *pos_dev, float scale, void *workspace, size_t workspace_bytes,
-                           hipStream_t s) {
+                           const float *v_scales, int kv_type, int v_layout, float *out, int n_heads, int head_dim,
+                           int n_kv_heads, int max_ctx, const int *pos_dev, float scale, void *workspace,
+                           size_t workspace_bytes, hipStream_t s) {
     if (kv_type != kKvF16 && kv_type != kKvInt8) return set_error(kErrBadArg, "attention_decode: kv_type %d", kv_type);
     if (n_kv_heads <= 0 || n_heads % n_kv_heads) return set_error(kErrBadArg, "attention_decode: n_heads %% n_kv_heads");
     if ((uintptr_t)workspace % 16) return set_error(kErrBadArg, "attention_decode: workspace not 16-byte aligned");
@@ -423,6 +431,7 @@ int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_ca
     a.max_ctx = max_ctx;
     a.pos_dev = pos_dev;
     a.scale = scale;
+    a.v_layout = v_layout;
     return launch_attention_decode(a, kv_type, s);
 }
 

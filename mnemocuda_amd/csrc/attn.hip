@@ -17,10 +17,13 @@
 //                     points define it (no workspace); the GQA-batched split-position kernel
 //                     lives in attn_decode.hip.
 //
-// RoPE: frequencies are 1 / powf(theta, 2j / hd) rounded as the reference's host powf
-// (a double power rounded once to float), angles pos * freq in fp32 as the reference forms
-// them; sin/cos are the accurate sincosf (the reference uses the __sincosf approximation,
-// whose error grows with the angle).
+// RoPE: frequencies 1.0f / powf(theta, (float)(2j) / (float)hd) are computed on the host
+// with the C library's powf, as the reference does (kernels.cu:1256-1266), and travel in the
+// kernel arguments; angles pos * freq in fp32 as the reference forms them; sin/cos are the
+// accurate sincosf (the reference uses the __sincosf approximation, whose error grows with
+// the angle).
+#include <math.h>
+
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
 
@@ -39,16 +42,42 @@ __device__ __forceinline__ float wave_max_all(float v) {
 }
 
 // ------------------------------------------------------------------ RMS norm of one vector
-__global__ void __launch_bounds__(kNormThreads) rms_norm_row_kernel(const float *__restrict__ in,
-                                                                   const float *__restrict__ w, float *out,
-                                                                   float *__restrict__ res, int n, float eps) {
+// out may alias in (each element is read and written by the same thread after the
+// reduction); res, when given, aliases neither.  Vector path (n % 4 == 0, n <= 16384,
+// 16-byte aligned): every thread's float4s are loaded once, up front, and kept in
+// registers; the general path reads in twice.
+constexpr int kNormV4 = 4;
+
+__global__ void __launch_bounds__(kNormThreads) rms_norm_row_kernel(const float *in, const float *__restrict__ w,
+                                                                   float *out, float *__restrict__ res, int n,
+                                                                   float eps, int vec4) {
     __shared__ float part[kNormThreads / 64];
     const int tid = threadIdx.x;
     float ss = 0.0f;
-    for (int i = tid; i < n; i += kNormThreads) {
-        const float v = in[i];
-        ss = fmaf(v, v, ss);
-        if (res) res[i] = v;
+    float4 xv[kNormV4];
+    const int n4 = n / 4;
+    if (vec4) {
+#pragma unroll
+        for (int u = 0; u < kNormV4; u++) {
+            const int i = min(tid + u * kNormThreads, n4 - 1);  // clamped: branch-free loads
+            xv[u] = ((const float4 *)in)[i];
+        }
+#pragma unroll
+        for (int u = 0; u < kNormV4; u++) {
+            if (tid + u * kNormThreads < n4) {
+                ss = fmaf(xv[u].x, xv[u].x, ss);
+                ss = fmaf(xv[u].y, xv[u].y, ss);
+                ss = fmaf(xv[u].z, xv[u].z, ss);
+                ss = fmaf(xv[u].w, xv[u].w, ss);
+                if (res) ((float4 *)res)[tid + u * kNormThreads] = xv[u];
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += kNormThreads) {
+            const float v = in[i];
+            ss = fmaf(v, v, ss);
+            if (res) res[i] = v;
+        }
     }
     ss = sum64_lane63(ss);
     if (lane_id() == 63) part[tid >> 6] = ss;
@@ -57,12 +86,32 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_row_kernel(const float 
 #pragma unroll
     for (int i = 0; i < kNormThreads / 64; i++) tot += part[i];  // same order in every thread
     const float scale = 1.0f / sqrtf(tot / (float)n + eps);
-    for (int i = tid; i < n; i += kNormThreads) out[i] = in[i] * scale * w[i];
+    if (vec4) {
+#pragma unroll
+        for (int u = 0; u < kNormV4; u++) {
+            const int i = tid + u * kNormThreads;
+            if (i < n4) {
+                const float4 wv = ((const float4 *)w)[i];
+                float4 o;
+                o.x = xv[u].x * scale * wv.x;
+                o.y = xv[u].y * scale * wv.y;
+                o.z = xv[u].z * scale * wv.z;
+                o.w = xv[u].w * scale * wv.w;
+                ((float4 *)out)[i] = o;
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += kNormThreads) out[i] = in[i] * scale * w[i];
+    }
 }
 
 int launch_rms_norm(const float *in, const float *w, float *out, float *res, int n, float eps, hipStream_t s) {
     if (!in || !w || !out || n <= 0) return set_error(kErrBadArg, "rms_norm: bad arguments");
-    hipLaunchKernelGGL(rms_norm_row_kernel, dim3(1), dim3(kNormThreads), 0, s, in, w, out, res, n, eps);
+    if (res == in) res = nullptr;  // saving the input onto itself: nothing to write
+    if (res && (res == out || res == w)) return set_error(kErrBadArg, "rms_norm: residual aliases out or weight");
+    const int vec4 = n % 4 == 0 && n <= 4 * kNormV4 * kNormThreads &&
+                     (((uintptr_t)in | (uintptr_t)w | (uintptr_t)out | (uintptr_t)res) % 16) == 0;
+    hipLaunchKernelGGL(rms_norm_row_kernel, dim3(1), dim3(kNormThreads), 0, s, in, w, out, res, n, eps, vec4);
     return check_launch("rms_norm");
 }
 
@@ -137,10 +186,7 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
         for (int t = 0; t < kHeadPairs; t++) {
             const int j = lane + 64 * t;
             if (j < half) {
-                const float e = (float)(2 * j) / (float)a.hd;
-                const float p = (float)pow((double)a.theta, (double)e);  // powf, correctly rounded
-                const float freq = 1.0f / p;
-                const float ang = (float)pos * freq;
+                const float ang = (float)pos * a.freq[j];
                 float sn, cs;
                 sincosf(ang, &sn, &cs);
                 const float v0 = x0[t], v1 = x1[t];
@@ -160,7 +206,12 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
         }
     }
     if ((a.flags & kHeadStore) && !is_q) {
-        const size_t base = ((size_t)pos * a.nk + h) * a.hd;
+        // K rows [pos][nk][hd]; V rows likewise, or blocked: element (pos, h, d) at
+        // ((pos/64 * nk + h) * hd + d) * 64 + pos % 64 (attention_decode reads it directly)
+        const bool blocked = !is_k && a.v_layout == 1;
+        const size_t base = blocked ? (((size_t)(pos / 64) * a.nk + h) * a.hd) * 64 + pos % 64
+                                    : ((size_t)pos * a.nk + h) * a.hd;
+        const int es = blocked ? 64 : 1;  // element stride along the head dim
         void *cache = is_k ? a.kc : a.vc;
         if (a.kv_type == kKvF16) {
             _Float16 *c = (_Float16 *)cache + base;
@@ -168,8 +219,8 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
             for (int t = 0; t < kHeadPairs; t++) {
                 const int j = lane + 64 * t;
                 if (j < half) {
-                    c[j] = (_Float16)x0[t];
-                    c[j + half] = (_Float16)x1[t];
+                    c[(size_t)j * es] = (_Float16)x0[t];
+                    c[(size_t)(j + half) * es] = (_Float16)x1[t];
                 }
             }
         } else {
@@ -183,8 +234,8 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
             for (int t = 0; t < kHeadPairs; t++) {
                 const int j = lane + 64 * t;
                 if (j < half) {
-                    c[j] = (int8_t)fminf(fmaxf(rintf(x0[t] * inv), -127.0f), 127.0f);
-                    c[j + half] = (int8_t)fminf(fmaxf(rintf(x1[t] * inv), -127.0f), 127.0f);
+                    c[(size_t)j * es] = (int8_t)fminf(fmaxf(rintf(x0[t] * inv), -127.0f), 127.0f);
+                    c[(size_t)(j + half) * es] = (int8_t)fminf(fmaxf(rintf(x1[t] * inv), -127.0f), 127.0f);
                 }
             }
             float *sc = is_k ? a.ksc : a.vsc;
@@ -195,6 +246,10 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
 
 int launch_head_pass(HeadPassArgs a, hipStream_t s) {
     const int heads = a.nq + a.nk + a.nv;
+    if (a.flags & kHeadRope) {
+        if (a.hd / 2 > kMaxRopeFreqs) return set_error(kErrBadArg, "rope: head_dim > %d", 2 * kMaxRopeFreqs);
+        for (int j = 0; j < a.hd / 2; j++) a.freq[j] = 1.0f / powf(a.theta, (float)(2 * j) / (float)a.hd);
+    }
     if (a.hd <= 0 || (a.hd & 1) || a.hd > 2 * 64 * kHeadPairs || heads <= 0 || a.nq < 0 || a.nk < 0 || a.nv < 0)
         return set_error(kErrBadArg, "head pass: need an even head_dim <= %d and heads > 0", 2 * 64 * kHeadPairs);
     if ((a.nq && !a.q) || (a.nk && !a.k) || (a.nv && !a.v))

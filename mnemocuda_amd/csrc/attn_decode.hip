@@ -35,21 +35,20 @@ size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx) {
     return (size_t)n_kv_heads * chunks * kPart * sizeof(float);
 }
 
-__device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-__device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
-    return v;
+// V cache layouts.  kVRows: the reference's [pos][n_kv][hd].  kVBlocked: blocks of 64
+// positions, [pos / 64][n_kv][hd][pos % 64], so that 8 consecutive positions of one dim
+// (an MFMA fragment of O = P V) are 16 contiguous bytes.
+constexpr int kVRows = 0;
+constexpr int kVBlocked = 1;
+
+size_t kv_blocked_offset(int pos, int kvh, int d, int nkv, int hd) {
+    return (((size_t)(pos / 64) * nkv + kvh) * hd + d) * 64 + pos % 64;
 }
 
-template <int KV>
+template <int KV, int VL>
 __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
-    __shared__ __align__(16) _Float16 vt[kChunk][kHd + 8];    // V tile [pos][dim]
+    __shared__ __align__(16) _Float16 vt[VL == kVRows ? kChunk : 1][kHd + 8];  // V tile [pos][dim]
     __shared__ __align__(16) _Float16 ps[2][kRows][kChunk + 8];
     const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
     const int seq = min(*a.pos_dev + 1, a.max_ctx);
@@ -73,12 +72,23 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
             else __builtin_memcpy(&kr[4 * t + s], kc + off, 8);
         }
     }
-    uint4 vr[16];  // 16-element chunk c = lane + 64u of the tile: position c / 16, dims 8 (c % 16)
+    // V: rows layout -- 16-element chunk c = lane + 64u of the tile (position c / 16, dims
+    // 8 (c % 16)); blocked layout -- the O = P V fragments themselves: u = 2n + kk holds dim
+    // 16n + r, positions 32kk + 8kg .. +7 of this chunk (rows past the sequence are read as
+    // stored and weighted by P = 0, so the cache must hold finite values there; the caller
+    // zero-fills the blocked cache once)
+    uint4 vr[16];
 #pragma unroll
     for (int u = 0; u < 16; u++) {
-        const int c = lane + 64 * u;
-        const int p = min(p0 + (c >> 4), seq - 1);
-        const size_t off = ((size_t)p * stride + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
+        size_t off;
+        if (VL == kVRows) {
+            const int c = lane + 64 * u;
+            const int p = min(p0 + (c >> 4), seq - 1);
+            off = ((size_t)p * stride + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
+        } else {
+            const int n = u >> 1, kk = u & 1;
+            off = ((((size_t)chunk * a.nkv + kvh) * kHd + 16 * n + r) * kChunk + 32 * kk + 8 * kg) * EB;
+        }
         if (KV == kKvF16) __builtin_memcpy(&vr[u], vc + off, 16);
         else __builtin_memcpy(&vr[u], vc + off, 8);
     }
@@ -94,12 +104,14 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (h < G) v = *(const float4 *)(a.q + (size_t)(kvh * G + h) * kHd + d);
         const float vv[4] = {v.x, v.y, v.z, v.w};
+        _Float16 hi[4], lo[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const _Float16 hi = (_Float16)vv[j];
-            qs[0][h][d + j] = hi;
-            qs[1][h][d + j] = (_Float16)(vv[j] - (float)hi);
+            hi[j] = (_Float16)vv[j];
+            lo[j] = (_Float16)(vv[j] - (float)hi[j]);
         }
+        __builtin_memcpy(&qs[0][h][d], hi, 8);
+        __builtin_memcpy(&qs[1][h][d], lo, 8);
     }
     __syncthreads();
 
@@ -138,7 +150,7 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
             sc[t][i] = s;
             mx = fmaxf(mx, s);
         }
-        m[i] = row16_max(mx);  // every row has position p0 < seq, so m is finite
+        m[i] = max16(mx);  // every row has position p0 < seq, so m is finite
         float sum = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -146,7 +158,7 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
             sc[t][i] = e;
             sum += e;
         }
-        l[i] = row16_sum(sum);
+        l[i] = sum16(sum);
     }
     // ---- P (times the V scale for int8) to LDS as hi + lo, V tile to LDS
 #pragma unroll
@@ -160,18 +172,20 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
             ps[1][4 * kg + i][16 * t + r] = (_Float16)(pv - (float)hi);
         }
     }
+    if (VL == kVRows) {
 #pragma unroll
-    for (int u = 0; u < 16; u++) {
-        const int c = lane + 64 * u;
-        h8 v;
-        if (KV == kKvF16) {
-            __builtin_memcpy(&v, &vr[u], 16);
-        } else {
-            const int8_t *vb = (const int8_t *)&vr[u];
+        for (int u = 0; u < 16; u++) {
+            const int c = lane + 64 * u;
+            h8 v;
+            if (KV == kKvF16) {
+                __builtin_memcpy(&v, &vr[u], 16);
+            } else {
+                const int8_t *vb = (const int8_t *)&vr[u];
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = (_Float16)vb[j];
+                for (int j = 0; j < 8; j++) v[j] = (_Float16)vb[j];
+            }
+            __builtin_memcpy(&vt[c >> 4][8 * (c & 15)], &v, 16);
         }
-        __builtin_memcpy(&vt[c >> 4][8 * (c & 15)], &v, 16);
     }
     __syncthreads();
 
@@ -187,8 +201,16 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
 #pragma unroll
         for (int n = 0; n < 8; n++) {
             h8 b;
+            if (VL == kVRows) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) b[j] = vt[32 * kk + 8 * kg + j][16 * n + r];
+                for (int j = 0; j < 8; j++) b[j] = vt[32 * kk + 8 * kg + j][16 * n + r];
+            } else if (KV == kKvF16) {
+                __builtin_memcpy(&b, &vr[2 * n + kk], 16);
+            } else {
+                const int8_t *vb = (const int8_t *)&vr[2 * n + kk];
+#pragma unroll
+                for (int j = 0; j < 8; j++) b[j] = (_Float16)vb[j];
+            }
             o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, o[n], 0, 0, 0);
             o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, o[n], 0, 0, 0);
         }
@@ -208,23 +230,70 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
         for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * n + r] = o[n][i];
 }
 
-// One workgroup of head_dim threads per query head: merges the chunks' (max, sum, O).
-__global__ void __launch_bounds__(kHd) attn_combine_kernel(AttnDecodeArgs a) {
-    const int h = blockIdx.x, d = threadIdx.x;
+// Merge of the chunks' (max, sum, O): grid (query head, quarter of head_dim).  Every
+// workgroup computes the chunk weights exp(m_c - M) in parallel into LDS; then thread
+// (dim d of 32, group g of 8) sums the chunks c = g mod 8 (four loads in flight), and the
+// 8 groups are added through LDS in a fixed order.
+constexpr int kCombThreads = 256;
+constexpr int kCombDims = kHd / 4;                    // dims per workgroup
+constexpr int kCombGroups = kCombThreads / kCombDims;  // 8
+constexpr int kMaxChunks = 1024;                      // max_ctx <= 65536
+
+__global__ void __launch_bounds__(kCombThreads) attn_combine_kernel(AttnDecodeArgs a) {
+    __shared__ float wc[kMaxChunks];
+    __shared__ float red[kCombThreads / 64];
+    __shared__ float part_o[kCombThreads];
+    const int h = blockIdx.x, tid = threadIdx.x;
     const int kvh = h / a.gqa, hh = h % a.gqa;
     const int seq = min(*a.pos_dev + 1, a.max_ctx);
     const int nc = (seq + kChunk - 1) / kChunk;
     const float *base = a.ws + (size_t)kvh * a.max_chunks * kPart;
-    float M = -INFINITY;
-    for (int c = 0; c < nc; c++) M = fmaxf(M, base[(size_t)c * kPart + hh]);
-    float L = 0.0f, O = 0.0f;
-    for (int c = 0; c < nc; c++) {
-        const float *p = base + (size_t)c * kPart;
-        const float w = expf(p[hh] - M);
-        L = fmaf(p[kRows + hh], w, L);
-        O = fmaf(p[2 * kRows + hh * kHd + d], w, O);
+    float mx = -INFINITY;
+    for (int c = tid; c < nc; c += kCombThreads) {
+        const float m = base[(size_t)c * kPart + hh];
+        wc[c] = m;
+        mx = fmaxf(mx, m);
     }
-    a.out[(size_t)h * kHd + d] = O / L;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int i = 1; i < kCombThreads / 64; i++) M = fmaxf(M, red[i]);
+    __syncthreads();  // red[] is reused below
+    float ls = 0.0f;
+    for (int c = tid; c < nc; c += kCombThreads) {
+        const float w = expf(wc[c] - M);
+        wc[c] = w;
+        ls = fmaf(base[(size_t)c * kPart + kRows + hh], w, ls);
+    }
+    ls = sum64_lane63(ls);
+    if ((tid & 63) == 63) red[tid >> 6] = ls;
+    __syncthreads();
+    float L = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCombThreads / 64; i++) L += red[i];
+    const int d = (int)blockIdx.y * kCombDims + tid % kCombDims, g = tid / kCombDims;
+    const float *ob = base + 2 * kRows + hh * kHd + d;
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    constexpr int G8 = kCombGroups;
+    int c = g;
+    for (; c + 3 * G8 < nc; c += 4 * G8) {
+        o0 = fmaf(ob[(size_t)c * kPart], wc[c], o0);
+        o1 = fmaf(ob[(size_t)(c + G8) * kPart], wc[c + G8], o1);
+        o2 = fmaf(ob[(size_t)(c + 2 * G8) * kPart], wc[c + 2 * G8], o2);
+        o3 = fmaf(ob[(size_t)(c + 3 * G8) * kPart], wc[c + 3 * G8], o3);
+    }
+    for (; c < nc; c += G8) o0 = fmaf(ob[(size_t)c * kPart], wc[c], o0);
+    part_o[tid] = (o0 + o1) + (o2 + o3);
+    __syncthreads();
+    if (tid < kCombDims) {
+        float o = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kCombGroups; j++) o += part_o[tid + j * kCombDims];
+        a.out[(size_t)h * kHd + d] = o / L;
+    }
 }
 
 int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s) {
@@ -233,16 +302,24 @@ int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s) {
     if (a.hd != kHd) return set_error(kErrBadArg, "attention_decode: head_dim %d (this kernel: %d)", a.hd, kHd);
     if (a.nkv <= 0 || a.gqa <= 0 || a.gqa > kRows || a.nh != a.nkv * a.gqa)
         return set_error(kErrBadArg, "attention_decode: n_heads = n_kv_heads * gqa with gqa <= %d", kRows);
-    if (a.max_ctx <= 0) return set_error(kErrBadArg, "attention_decode: max_ctx <= 0");
+    if (a.max_ctx <= 0 || a.max_ctx > kMaxChunks * kChunk)
+        return set_error(kErrBadArg, "attention_decode: max_ctx must be in 1..%d", kMaxChunks * kChunk);
     if (kv_type == kKvInt8 && (!a.ksc || !a.vsc)) return set_error(kErrBadArg, "attention_decode: int8 needs scales");
+    if (a.v_layout != kVRows && a.v_layout != kVBlocked)
+        return set_error(kErrBadArg, "attention_decode: v_layout %d", a.v_layout);
     if (a.ws_bytes < attn_decode_workspace_bytes(a.nkv, a.max_ctx))
         return set_error(kErrBadArg, "attention_decode: workspace %zu < %zu bytes", a.ws_bytes,
                          attn_decode_workspace_bytes(a.nkv, a.max_ctx));
     a.max_chunks = (a.max_ctx + kChunk - 1) / kChunk;
     const dim3 grid(a.max_chunks, a.nkv);
-    if (kv_type == kKvF16) hipLaunchKernelGGL(attn_chunk_kernel<kKvF16>, grid, dim3(64), 0, s, a);
-    else hipLaunchKernelGGL(attn_chunk_kernel<kKvInt8>, grid, dim3(64), 0, s, a);
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh), dim3(kHd), 0, s, a);
+    if (kv_type == kKvF16) {
+        if (a.v_layout == kVBlocked) hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVBlocked>), grid, dim3(64), 0, s, a);
+        else hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVRows>), grid, dim3(64), 0, s, a);
+    } else {
+        if (a.v_layout == kVBlocked) hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVBlocked>), grid, dim3(64), 0, s, a);
+        else hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVRows>), grid, dim3(64), 0, s, a);
+    }
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, kHd / kCombDims), dim3(kCombThreads), 0, s, a);
     return check_launch("attention_decode");
 }
 

@@ -128,6 +128,11 @@ __device__ __forceinline__ float max8(float v) {
     v = fmaxf(v, dpp_f<kDppRowHalfMirror>(v));
     return v;
 }
+// Max over aligned groups of 16 lanes (one DPP row); every lane gets the max.
+__device__ __forceinline__ float max16(float v) {
+    v = max8(v);
+    return fmaxf(v, dpp_f<kDppRowMirror>(v));
+}
 
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0)); }
 

@@ -72,6 +72,7 @@ constexpr int kHeadNorm = 1;   // RMS-normalise q and k heads with qw / kw
 constexpr int kHeadRope = 2;   // rotate q and k heads
 constexpr int kHeadStore = 4;  // store k and v heads at the cache row of pos
 
+constexpr int kMaxRopeFreqs = 256;  // head_dim <= 512
 struct HeadPassArgs {
     float *q, *k;          // nq / nk heads, read (and by default written back)
     const float *v;        // nv heads, only stored
@@ -85,6 +86,8 @@ struct HeadPassArgs {
     float *ksc, *vsc;      // int8 scales [pos][nk]
     int kv_type;
     int flags;
+    int v_layout;               // of the V cache store: 0 rows, 1 blocked (see AttnDecodeArgs)
+    float freq[kMaxRopeFreqs];  // RoPE frequencies, filled by launch_head_pass
 };
 
 struct AttnArgs {
@@ -109,6 +112,7 @@ struct AttnDecodeArgs {
     int max_ctx, max_chunks;
     const int *pos_dev;  // sequence length = min(*pos_dev + 1, max_ctx)
     float scale;
+    int v_layout;        // 0: V rows [pos][n_kv][hd]; 1: blocked [pos/64][n_kv][hd][pos%64]
 };
 size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx);
 int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s);

@@ -54,10 +54,12 @@ SIGNATURES: dict[str, tuple] = {
     "cuda_f32_to_int8_kv_dual": (None, [fp, fp, vp, vp, fp, fp, i32, i32, stream_t]),
     "cuda_attention_f16kv": (None, [vp, vp, vp, fp, i32, i32, i32, i32, i32, f32, stream_t]),
     "cuda_attention_int8kv": (None, [fp, vp, vp, fp, fp, fp, i32, i32, i32, i32, i32, f32, stream_t]),
-    "mnemo_attn_prep": (i32, [fp, fp, fp, fp, fp, i32, i32, i32, f32, f32, ip, vp, vp, fp, fp, i32, stream_t]),
+    "mnemo_attn_prep": (i32, [fp, fp, fp, fp, fp, i32, i32, i32, f32, f32, ip, vp, vp, fp, fp, i32, i32, stream_t]),
+    "mnemo_v_cache_bytes": (sz, [i32, i32, i32, i32, i32]),
     "mnemo_attention": (i32, [fp, vp, vp, fp, fp, i32, fp, i32, i32, i32, ip, f32, stream_t]),
     "mnemo_attention_decode_workspace_bytes": (sz, [i32, i32]),
-    "mnemo_attention_decode": (i32, [fp, vp, vp, fp, fp, i32, fp, i32, i32, i32, i32, ip, f32, vp, sz, stream_t]),
+    "mnemo_attention_decode": (i32, [fp, vp, vp, fp, fp, i32, i32, fp, i32, i32, i32, i32, ip, f32, vp, sz,
+                                     stream_t]),
     # host composition (mnemo_host.h)
     "mnemo_matvec": (i32, [vp, fp, fp, i32, i32, i32, stream_t]),
     "mnemo_down_type_id": (i32, [sz, i32, i32]),

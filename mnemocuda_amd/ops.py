@@ -338,14 +338,16 @@ def attention(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: int, seq_
         check(lib, "cuda_attention_int8kv")
 
 
-def attn_prep(q, k, v, qw, kw, head_dim: int, eps: float, theta: float, pos_dev, kc, vc, ks=None, vs=None):
-    """QK norm (when qw/kw are given) + RoPE + KV store at cache row pos_dev[0], one launch."""
+def attn_prep(q, k, v, qw, kw, head_dim: int, eps: float, theta: float, pos_dev, kc, vc, ks=None, vs=None,
+              v_layout: int = 0):
+    """QK norm (when qw/kw are given) + RoPE + KV store at cache row pos_dev[0], one launch
+    (v_layout 1: V in the blocked layout of attention_decode)."""
     lib = load_library()
     kv_type = 0 if kc.dtype == torch.float16 else 1
     rc = lib.mnemo_attn_prep(_dev(q, "q", F32), _dev(k, "k", F32), _dev(v, "v", F32), _opt(qw, "qw", F32),
                              _opt(kw, "kw", F32), head_dim, q.numel() // head_dim, k.numel() // head_dim, float(eps),
                              float(theta), _dev(pos_dev, "pos_dev", torch.int32), _dev(kc, "kc"), _dev(vc, "vc"),
-                             _opt(ks, "ks", F32), _opt(vs, "vs", F32), kv_type, _stream())
+                             _opt(ks, "ks", F32), _opt(vs, "vs", F32), kv_type, int(v_layout), _stream())
     _check_rc(lib, rc, "mnemo_attn_prep")
 
 
@@ -364,13 +366,18 @@ def attention_decode_workspace_bytes(n_kv_heads: int, max_ctx: int) -> int:
     return int(load_library().mnemo_attention_decode_workspace_bytes(n_kv_heads, max_ctx))
 
 
+def v_cache_bytes(n_kv_heads: int, head_dim: int, max_ctx: int, kv_type: int, v_layout: int) -> int:
+    return int(load_library().mnemo_v_cache_bytes(n_kv_heads, head_dim, max_ctx, kv_type, v_layout))
+
+
 def attention_decode(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: int, max_ctx: int, pos_dev,
-                     scale: float, ws, ks=None, vs=None):
+                     scale: float, ws, ks=None, vs=None, v_layout: int = 0):
     """GQA-batched split-position attention over positions 0..pos_dev[0] (matrix cores)."""
     lib = load_library()
     kv_type = 0 if kc.dtype == torch.float16 else 1
     rc = lib.mnemo_attention_decode(_dev(q, "q", F32), _dev(kc, "kc"), _dev(vc, "vc"), _opt(ks, "ks", F32),
-                                    _opt(vs, "vs", F32), kv_type, _dev(out, "out", F32), n_heads, head_dim,
+                                    _opt(vs, "vs", F32), kv_type, int(v_layout), _dev(out, "out", F32), n_heads,
+                                    head_dim,
                                     n_kv_heads, int(max_ctx), _dev(pos_dev, "pos_dev", torch.int32), float(scale),
                                     _dev(ws, "ws"), ws.numel() * ws.element_size(), _stream())
     _check_rc(lib, rc, "mnemo_attention_decode")

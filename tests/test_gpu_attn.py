@@ -253,26 +253,68 @@ def test_bad_args(gpu):
 
 
 # ------------------------------------------------------------------ GQA-batched decode attention
+def _blocked(v, max_ctx, nkv, hd):
+    """[pos][nkv][hd] -> the blocked V layout [pos/64][nkv][hd][pos%64], zero-padded."""
+    nb = (max_ctx + 63) // 64
+    x = np.zeros((nb * 64, nkv, hd), v.dtype)
+    x[:max_ctx] = v.reshape(max_ctx, nkv, hd)
+    return np.ascontiguousarray(x.reshape(nb, 64, nkv, hd).transpose(0, 2, 3, 1)).reshape(-1)
+
+
+@pytest.mark.parametrize("v_layout", [0, 1])
 @pytest.mark.parametrize("kind", ["f16", "int8"])
-@pytest.mark.parametrize("seq,nh,nkv", [(1, NH, NKV), (63, NH, NKV), (64, NH, NKV), (65, NH, NKV), (1000, NH, NKV),
-                                        (4097, NH, NKV), (300, 32, 4), (200, 8, 8)])
-def test_attention_decode(gpu, oracle, rng, kind, seq, nh, nkv):
-    max_ctx = 8192
+@pytest.mark.parametrize("seq,nh,nkv,max_ctx", [(1, NH, NKV, 8192), (63, NH, NKV, 8192), (64, NH, NKV, 8192),
+                                                (65, NH, NKV, 8192), (1000, NH, NKV, 8192), (4097, NH, NKV, 8192),
+                                                (300, 32, 4, 8192), (200, 8, 8, 8192), (1000, NH, NKV, 1000)])
+def test_attention_decode(gpu, oracle, rng, kind, seq, nh, nkv, max_ctx, v_layout):
     q = rng.standard_normal(nh * HD).astype(np.float32)
     kc, vc, ks, vs = _caches(rng, max_ctx, nkv, HD, kind)
     pos_dev = torch.tensor([seq - 1], dtype=torch.int32, device="cuda")
     ws = torch.empty(gpu.ops.attention_decode_workspace_bytes(nkv, max_ctx), dtype=torch.uint8, device="cuda")
     out = torch.full((nh * HD,), np.nan, device="cuda")
     scale = 1.0 / np.sqrt(HD)
-    case(f"attention_decode {kind} seq={seq} nh={nh} nkv={nkv}")
-    gpu.ops.attention_decode(dev(q), _to_dev(kc), _to_dev(vc), out, nh, HD, nkv, max_ctx, pos_dev, scale, ws,
-                             _to_dev(ks), _to_dev(vs))
+    case(f"attention_decode {kind} v_layout={v_layout} seq={seq} nh={nh} nkv={nkv} max_ctx={max_ctx}")
+    vdev = _to_dev(vc if v_layout == 0 else _blocked(vc, max_ctx, nkv, HD))
+    if v_layout == 1:
+        assert vdev.numel() * vdev.element_size() == gpu.ops.v_cache_bytes(nkv, HD, max_ctx, 0 if kind == "f16" else 1, 1)
+    gpu.ops.attention_decode(dev(q), _to_dev(kc), vdev, out, nh, HD, nkv, max_ctx, pos_dev, scale, ws,
+                             _to_dev(ks), _to_dev(vs), v_layout=v_layout)
     if kind == "f16":
         want = oracle.attention(q, kc[:seq], vc[:seq], nh, HD, nkv, seq, scale)
     else:
         want = oracle.attention(q, kc[:seq * nkv * HD], vc[:seq * nkv * HD], nh, HD, nkv, seq, scale,
                                 ks[:seq * nkv], vs[:seq * nkv])
     assert rel_l2(host(out), want) < 1e-5
+
+
+def test_attn_prep_blocked_v(gpu, rng):
+    """mnemo_attn_prep with v_layout 1 stores V at its blocked position; the K rows and
+    everything else in the caches are untouched."""
+    ctx, pos = 200, 131
+    q = dev(rng.standard_normal(NH * HD).astype(np.float32))
+    k = dev(rng.standard_normal(NKV * HD).astype(np.float32))
+    v = rng.standard_normal(NKV * HD).astype(np.float32)
+    for kind in ("f16", "int8"):
+        case(f"attn_prep blocked V {kind}")
+        dt = torch.float16 if kind == "f16" else torch.int8
+        kc = torch.zeros(ctx * NKV * HD, dtype=dt, device="cuda")
+        nb = gpu.ops.v_cache_bytes(NKV, HD, ctx, 0 if kind == "f16" else 1, 1) // kc.element_size()
+        vc = torch.zeros(nb, dtype=dt, device="cuda")
+        ks = torch.zeros(ctx * NKV, device="cuda")
+        vs = torch.zeros(ctx * NKV, device="cuda")
+        pos_dev = torch.tensor([pos], dtype=torch.int32, device="cuda")
+        gpu.ops.attn_prep(q.clone(), k.clone(), dev(v), None, None, HD, 1e-6, 1e6, pos_dev, kc, vc,
+                          ks if kind == "int8" else None, vs if kind == "int8" else None, v_layout=1)
+        got = host(vc)
+        if kind == "f16":
+            want_row = v.astype(np.float16)
+            got_rows = got.reshape(-1, NKV, HD, 64)[pos // 64, :, :, pos % 64].reshape(-1)
+            assert np.array_equal(got_rows.view(np.uint16), want_row.view(np.uint16))
+        else:
+            want_row, _ = onp.kv_quant_int8(v, HD)
+            got_rows = got.reshape(-1, NKV, HD, 64)[pos // 64, :, :, pos % 64].reshape(-1)
+            assert np.array_equal(got_rows, want_row)
+        assert np.count_nonzero(got) == np.count_nonzero(got_rows)
 
 
 def test_attention_decode_graph_replay(gpu, rng):
