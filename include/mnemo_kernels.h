@@ -39,6 +39,8 @@ extern "C" {
 #define MNEMO_ERR_BAD_ARG 1
 #define MNEMO_ERR_LAUNCH 2
 #define MNEMO_ERR_UNSUPPORTED_TYPE 3
+#define MNEMO_ERR_IO 4
+#define MNEMO_ERR_ALLOC 5
 
 /* Last error recorded by any entry point on this host thread (MNEMO_OK if none);
  * reading it clears it. */
@@ -214,6 +216,19 @@ void cuda_attention_int8kv(const float *q, const void *kv_k, const void *kv_v,
                            const float *k_scales, const float *v_scales, float *out,
                            int n_heads_q, int head_dim, int n_kv_heads, int seq_len,
                            int gqa_ratio, float scale, hipStream_t stream);
+
+/* ---- Token embedding (forward.c:1145-1280) ------------------------------------------
+ * kernels.cu:2192-2198: output[0..hidden_size) = dequantised row token_id of a Q4_K table
+ * with row_bytes per row.  Decodes the canonical GGUF layout (as the matvec kernels and the
+ * reference's CPU fallback forward.c:1189-1229 do; the reference GPU kernel, kernels.cu:
+ * 1901-1951, indexes the nibbles differently). */
+void cuda_embedding_lookup_q4k(const void *embd_table, float *output, int token_id,
+                               int hidden_size, int row_bytes, hipStream_t stream);
+/* New: the same for F32 (0), Q4_K (12) or Q6_K (14) tables of n_vocab rows, the token id
+ * read from device memory (e.g. cuda_sample_token's d_result) so a decode step's graph
+ * chains sampling into the next embedding; ids outside the table read the nearest row. */
+int mnemo_embedding_lookup(const void *table, int type_id, const int *token_dev, int n_vocab,
+                           float *output, int hidden_size, hipStream_t stream);
 
 /* New: the per-token steps 3-5 of forward.c:755-770 (QK norm, RoPE, KV store) in one launch
  * with the position read from device memory (*pos_dev), so a captured graph replays for

@@ -21,8 +21,8 @@ BUILD = ROOT / "_build"
 LIB = PKG / "libmnemo_hip.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
-HIP_SOURCES = ["abi.hip", "gemv_launch.hip", "router.hip", "gemm.hip", "moe.hip", "sample.hip", "attn.hip", "attn_decode.hip"]
-C_SOURCES = ["host/mnemo_host.c"]
+HIP_SOURCES = ["abi.hip", "gemv_launch.hip", "router.hip", "gemm.hip", "moe.hip", "sample.hip", "attn.hip", "attn_decode.hip", "embed.hip"]
+C_SOURCES = ["host/mnemo_host.c", "host/mnemo_model.c"]
 
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",

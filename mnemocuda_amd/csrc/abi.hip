@@ -98,6 +98,8 @@ int mnemo_last_error(void) {
 const char *mnemo_last_error_string(void) { return g_msg; }
 const char *mnemo_version(void) { return "mnemo-mi355x 0.1 gfx950"; }
 
+int mnemo_record_error(int code, const char *msg) { return set_error(code, "%s", msg ? msg : "error"); }
+
 void cuda_kernels_init(void) {
     int dev = 0;
     hipDeviceProp_t prop;
@@ -433,6 +435,27 @@ int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_ca
     a.scale = scale;
     a.v_layout = v_layout;
     return launch_attention_decode(a, kv_type, s);
+}
+
+// ---------------------------------------------------------------- embedding
+void cuda_embedding_lookup_q4k(const void *embd_table, float *output, int token_id, int hidden_size, int row_bytes,
+                               hipStream_t s) {
+    // the reference passes no vocabulary size; its row bound is the caller's
+    if (row_bytes <= 0 || (size_t)row_bytes < (size_t)((hidden_size + 255) / 256) * kQ4KBytes) {
+        set_error(kErrBadArg, "embedding_lookup_q4k: row_bytes %d too small for %d values", row_bytes, hidden_size);
+        return;
+    }
+    launch_embedding(embd_table, kTypeQ4K, nullptr, token_id, INT_MAX, output, hidden_size, (size_t)row_bytes, s);
+}
+
+int mnemo_embedding_lookup(const void *table, int type_id, const int *token_dev, int n_vocab, float *output,
+                           int hidden_size, hipStream_t s) {
+    size_t rb = 0;
+    if (type_id == kTypeF32) rb = (size_t)hidden_size * 4;
+    else if (type_id == kTypeQ4K) rb = (size_t)((hidden_size + 255) / 256) * kQ4KBytes;
+    else if (type_id == kTypeQ6K) rb = (size_t)((hidden_size + 255) / 256) * kQ6KBytes;
+    if (!token_dev) return set_error(kErrBadArg, "embedding_lookup: token_dev is NULL");
+    return launch_embedding(table, type_id, token_dev, 0, n_vocab, output, hidden_size, rb, s);
 }
 
 size_t mnemo_moe_prefill_workspace_bytes(int n_tokens, int hidden, int eff, int n_experts, int k) {

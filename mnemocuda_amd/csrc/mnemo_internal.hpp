@@ -117,6 +117,8 @@ struct AttnDecodeArgs {
 size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx);
 int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s);
 
+int launch_embedding(const void *table, int type, const int *tok_dev, int tok, int n_vocab, float *out, int hidden,
+                     size_t row_bytes, hipStream_t s);
 int launch_rms_norm(const float *in, const float *w, float *out, float *res, int n, float eps, hipStream_t s);
 int launch_residual_add(const float *a, const float *b, float *out, int n, hipStream_t s);
 int launch_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n, hipStream_t s);

@@ -60,6 +60,22 @@ SIGNATURES: dict[str, tuple] = {
     "mnemo_attention_decode_workspace_bytes": (sz, [i32, i32]),
     "mnemo_attention_decode": (i32, [fp, vp, vp, fp, fp, i32, i32, fp, i32, i32, i32, i32, ip, f32, vp, sz,
                                      stream_t]),
+    "cuda_embedding_lookup_q4k": (None, [vp, fp, i32, i32, i32, stream_t]),
+    "mnemo_embedding_lookup": (i32, [vp, i32, ip, i32, fp, i32, stream_t]),
+    # model directory (mnemo_model.h); structs travel as void*
+    "mnemo_parse_config": (i32, [C.c_char_p, vp]),
+    "mnemo_parse_resident_manifest": (i32, [C.c_char_p, vp, i32, vp]),
+    "mnemo_parse_expert_manifest": (i32, [C.c_char_p, i32, vp]),
+    "mnemo_row_bytes": (sz, [i32, i32]),
+    "mnemo_model_open": (i32, [C.c_char_p, vp]),
+    "mnemo_model_config_of": (vp, [vp]),
+    "mnemo_model_n_tensors": (i32, [vp]),
+    "mnemo_model_tensor_at": (i32, [vp, i32, vp]),
+    "mnemo_model_expert_layer": (i32, [vp, i32, vp]),
+    "mnemo_model_upload": (i32, [vp, i32]),
+    "mnemo_model_tensor": (i32, [vp, C.c_char_p, vp, vp]),
+    "mnemo_model_experts": (i32, [vp, i32, vp]),
+    "mnemo_model_close": (None, [vp]),
     # host composition (mnemo_host.h)
     "mnemo_matvec": (i32, [vp, fp, fp, i32, i32, i32, stream_t]),
     "mnemo_down_type_id": (i32, [sz, i32, i32]),

@@ -381,3 +381,22 @@ def attention_decode(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: in
                                     n_kv_heads, int(max_ctx), _dev(pos_dev, "pos_dev", torch.int32), float(scale),
                                     _dev(ws, "ws"), ws.numel() * ws.element_size(), _stream())
     _check_rc(lib, rc, "mnemo_attention_decode")
+
+
+# ---------------------------------------------------------------- embedding
+def embedding_lookup(table, type_id: int, token_dev, n_vocab: int, out, hidden: int):
+    """out[:hidden] = dequantised row token_dev[0] of table (F32 / Q4_K / Q6_K).  table is a
+    GPU tensor or a raw device pointer (int)."""
+    lib = load_library()
+    tp = table if isinstance(table, int) else _dev(table, "table")
+    rc = lib.mnemo_embedding_lookup(tp, int(type_id), _dev(token_dev, "token_dev", torch.int32), int(n_vocab),
+                                    _dev(out, "out", F32), int(hidden), _stream())
+    _check_rc(lib, rc, "mnemo_embedding_lookup")
+
+
+def embedding_lookup_q4k(table, out, token_id: int, hidden: int, row_bytes: int):
+    """cuda_embedding_lookup_q4k (reference signature)."""
+    lib = load_library()
+    tp = table if isinstance(table, int) else _dev(table, "table")
+    lib.cuda_embedding_lookup_q4k(tp, _dev(out, "out", F32), int(token_id), int(hidden), int(row_bytes), _stream())
+    check(lib, "cuda_embedding_lookup_q4k")

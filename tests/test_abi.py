@@ -11,7 +11,7 @@ import pytest
 from mnemocuda_amd import lib as mlib
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADERS = [ROOT / "include" / "mnemo_kernels.h", ROOT / "include" / "mnemo_host.h"]
+HEADERS = [ROOT / "include" / "mnemo_kernels.h", ROOT / "include" / "mnemo_host.h", ROOT / "include" / "mnemo_model.h"]
 
 
 def header_functions() -> set[str]:
