@@ -92,6 +92,13 @@ void mnemo_matvec_dual(const void *wa, int type_a, const void *wb, int type_b, c
 void mnemo_matvec_qkv(const void *wq, int tq, const void *wk, int tk, const void *wv, int tv,
                       const float *x, float *oq, float *ok, float *ov, int q_rows, int kv_rows,
                       int n_cols, hipStream_t stream);
+/* New: the same with the pre-attention RMS norm folded in (forward.c:695-699 runs
+ * cuda_rms_norm_residual first): the projections read x * rsqrt(mean(x^2) + eps) * norm_w,
+ * which every workgroup computes from the raw x it loads anyway.  n_cols % 4 == 0. */
+void mnemo_matvec_qkv_rmsnorm(const void *wq, int tq, const void *wk, int tk, const void *wv,
+                              int tv, const float *x, const float *norm_w, float eps, float *q,
+                              float *k, float *v, int q_rows, int kv_rows, int n_cols,
+                              hipStream_t stream);
 /* New: fused expert down projection of one expert:
  * y += scale * (W_down (silu(gate) * up)), W_down Q4_K or Q6_K [n_rows][n_cols].
  * Replaces cuda_swiglu + (cuda_matvec_q4k_scaled_add | cuda_matvec_q6k + cuda_scaled_add)
@@ -175,6 +182,14 @@ int mnemo_moe_decode(const float *router_w, const void *experts, size_t expert_s
                      const float *x, int hidden, int eff, int n_experts, int k, void *workspace,
                      size_t workspace_bytes, float *out, int *topk_idx, float *topk_w,
                      hipStream_t stream);
+/* New: mnemo_moe_decode with the pre-FFN RMS norm folded into the router and gate/up
+ * launches (x is the raw hidden state; both compute x * rsqrt(mean(x^2) + eps) * norm_w as
+ * forward.c:800-806's separate rms_norm launch would).  x may equal out. */
+int mnemo_moe_decode_rmsnorm(const float *router_w, const void *experts, size_t expert_stride,
+                             size_t gate_off, size_t up_off, size_t down_off, int down_type,
+                             const float *x, const float *norm_w, float eps, int hidden, int eff,
+                             int n_experts, int k, void *workspace, size_t workspace_bytes,
+                             float *out, int *topk_idx, float *topk_w, hipStream_t stream);
 
 /* ---- Attention chain around the projections (forward.c:687-786, graph form 1290-1420) ----
  * Reference entry points, same arguments and semantics: */

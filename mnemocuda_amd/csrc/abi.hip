@@ -44,8 +44,9 @@ int launch_sample_token(const float *logits, int V, float temperature, float top
                         int *out, hipStream_t stream);
 size_t moe_decode_workspace_bytes(int hidden, int eff, int E, int k);
 int launch_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
-                      size_t up_off, size_t down_off, int down_type, const float *x, int hidden, int eff, int E,
-                      int k, void *ws, size_t ws_bytes, float *out, int *idx_out, float *w_out, hipStream_t s);
+                      size_t up_off, size_t down_off, int down_type, const float *x, const float *norm_w, float eps,
+                      int hidden, int eff, int E, int k, void *ws, size_t ws_bytes, float *out, int *idx_out,
+                      float *w_out, hipStream_t s);
 int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off, size_t up_off, size_t down_off,
                        int down_type, const float *x, const int *topk_idx, const float *topk_w, int T, int hidden,
                        int eff, int E, int k, void *ws, size_t ws_bytes, float *out, hipStream_t s);
@@ -176,6 +177,23 @@ void mnemo_matvec_qkv(const void *wq, int tq, const void *wk, int tk, const void
     b.add(wk, tk, ok, kv_rows, kEpiStore);
     b.add(wv, tv, ov, kv_rows, kEpiStore);
     b.run("mnemo_matvec_qkv", s);
+}
+
+void mnemo_matvec_qkv_rmsnorm(const void *wq, int tq, const void *wk, int tk, const void *wv, int tv,
+                              const float *x, const float *norm_w, float eps, float *oq, float *ok, float *ov,
+                              int q_rows, int kv_rows, int n_cols, hipStream_t s) {
+    if (!norm_w) {
+        set_error(kErrBadArg, "mnemo_matvec_qkv_rmsnorm: norm_w == NULL");
+        return;
+    }
+    GemvBuilder b(x, n_cols);
+    b.a.x2 = norm_w;
+    b.a.xmode = 2;
+    b.a.eps = eps;
+    b.add(wq, tq, oq, q_rows, kEpiStore);
+    b.add(wk, tk, ok, kv_rows, kEpiStore);
+    b.add(wv, tv, ov, kv_rows, kEpiStore);
+    b.run("mnemo_matvec_qkv_rmsnorm", s);
 }
 
 void mnemo_matvec_swiglu_scaled_add(const void *w, int type, const float *gate, const float *up, float *y,
@@ -478,8 +496,17 @@ int mnemo_moe_decode(const float *router_w, const void *experts, size_t expert_s
                      size_t up_off, size_t down_off, int down_type, const float *x, int hidden, int eff,
                      int n_experts, int k, void *workspace, size_t workspace_bytes, float *out, int *topk_idx,
                      float *topk_w, hipStream_t s) {
-    return launch_moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, hidden, eff,
-                             n_experts, k, workspace, workspace_bytes, out, topk_idx, topk_w, s);
+    return launch_moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, nullptr, 0.0f,
+                             hidden, eff, n_experts, k, workspace, workspace_bytes, out, topk_idx, topk_w, s);
+}
+
+int mnemo_moe_decode_rmsnorm(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
+                             size_t up_off, size_t down_off, int down_type, const float *x, const float *norm_w,
+                             float eps, int hidden, int eff, int n_experts, int k, void *workspace,
+                             size_t workspace_bytes, float *out, int *topk_idx, float *topk_w, hipStream_t s) {
+    if (!norm_w) return set_error(kErrBadArg, "moe_decode_rmsnorm: norm_w is NULL");
+    return launch_moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, norm_w, eps,
+                             hidden, eff, n_experts, k, workspace, workspace_bytes, out, topk_idx, topk_w, s);
 }
 
 }  // extern "C"

@@ -83,7 +83,8 @@ struct XRegs {
 
 // One 16-byte load per 4 elements from e clamped to n-4 (x may be unaligned; the host
 // rejects n < 4), so the instruction sequence is fixed.
-template <int XPT, bool SWI>
+// XM: 0 x as given; 1 silu(x) * x2 (SwiGLU inputs); 2 rms_norm(x) * x2 (x2 = norm weight)
+template <int XPT, int XM>
 __device__ __forceinline__ void load_x(const float *__restrict__ x0, const float *__restrict__ x1, int n,
                                        XRegs<XPT> &R, XRegs<XPT> &R2) {
 #pragma unroll
@@ -91,7 +92,7 @@ __device__ __forceinline__ void load_x(const float *__restrict__ x0, const float
         const int e = 4 * (threadIdx.x + i * kGemvThreads);
         const int ec = min(e, n - 4);
         __builtin_memcpy(&R.v[i], x0 + ec, 16);
-        if (SWI) __builtin_memcpy(&R2.v[i], x1 + ec, 16);
+        if (XM != 0) __builtin_memcpy(&R2.v[i], x1 + ec, 16);
     }
 }
 
@@ -105,11 +106,36 @@ __device__ __forceinline__ uint32_t umax_dpp8(uint32_t v) {
 // Builds the LDS image; every thread of the block must call this (it ends in a barrier).
 // Elements at or past n (loaded from clamped addresses) are zeroed here, after the
 // weight loads have been issued, so that waiting for x does not wait for the weights.
-template <int XPT, bool SWI>
-__device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, XLds X) {
+template <int XPT, int XM>
+__device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, XLds X,
+                                         float eps) {
     const int lane = lane_id();
     constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23: adding it rounds to an integer (RNE)
-    const bool ragged = (n & 3) != 0;      // uniform
+    const bool ragged = (n & 3) != 0;      // uniform (the host rejects ragged n for XM == 2)
+    float nscale = 1.0f;
+    if (XM == 2) {
+        // the RMS norm of the whole x (every workgroup holds all of it): a fixed-order sum
+        // of the waves' sums, then scale = 1 / sqrt(mean(x^2) + eps) as the reference's
+        // rms_norm_kernel (kernels.cu:692-722)
+        __shared__ float part[kGemvThreads / 64];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            if (4 * (threadIdx.x + i * kGemvThreads) < n) {
+                ss = fmaf(R.v[i].x, R.v[i].x, ss);
+                ss = fmaf(R.v[i].y, R.v[i].y, ss);
+                ss = fmaf(R.v[i].z, R.v[i].z, ss);
+                ss = fmaf(R.v[i].w, R.v[i].w, ss);
+            }
+        }
+        ss = sum64_lane63(ss);
+        if (lane == 63) part[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGemvThreads / 64; w++) tot += part[w];
+        nscale = 1.0f / sqrtf(tot / (float)n + eps);
+    }
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
         // computed unconditionally (a load used only under a branch would be sunk into it,
@@ -118,10 +144,10 @@ __device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &
         const bool store = 4 * e4 < kp;  // uniform per 8-lane group: kp is a multiple of 256
         const int e = 4 * e4;
         float v[4] = {R.v[i].x, R.v[i].y, R.v[i].z, R.v[i].w};
-        if (SWI) {
+        if (XM != 0) {
             const float g[4] = {R2.v[i].x, R2.v[i].y, R2.v[i].z, R2.v[i].w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = silu_mul(v[j], g[j]);
+            for (int j = 0; j < 4; j++) v[j] = XM == 1 ? silu_mul(v[j], g[j]) : v[j] * nscale * g[j];
         }
         if (ragged) {
             // element e+j sits at v[j + sh], sh = e - min(e, n-4) (non-zero only in the last
@@ -453,7 +479,7 @@ __device__ __forceinline__ void experts_combine(const GemvExperts &E) {
 
 // One wave pass per wave, loaded before the x image is built.  The grid covers the row
 // space exactly once (no loop), so the loads of every wave are issued back to back.
-template <int LPR, int UPL, int XPT, bool SWI, int TM>
+template <int LPR, int UPL, int XPT, int XM, int TM>
 __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     const int kp = (args.n_cols + 255) & ~255;
     const int bpr = kp / 256;
@@ -473,7 +499,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     }
 
     XRegs<XPT> xr, xr2;
-    load_x<XPT, SWI>(x0, x1, args.n_cols, xr, xr2);
+    load_x<XPT, XM>(x0, x1, args.n_cols, xr, xr2);
     // a wave past the end loads the last pass again (dropped) so every wave issues the
     // same loads
     int row0;
@@ -481,7 +507,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     const GemvMat M = pass_mat(args, bc, row0);
     Pass<UPL> ps;
     load_pass<LPR, UPL, TM>(M, row0, bc, bpr, ps);
-    finish_x<XPT, SWI>(xr, xr2, args.n_cols, kp, X);
+    finish_x<XPT, XM>(xr, xr2, args.n_cols, kp, X, args.eps);
     if (base < args.total_rows) finish_pass<LPR, UPL, TM>(M, bpr, ps, X);
     if (args.experts && args.ex.nm == 2 && blockIdx.x == 0) {
         // clear the tile counters of the down launch that follows on the stream
@@ -494,25 +520,27 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
 // matrix starts at a multiple of the rows of one workgroup, so the type is uniform per
 // workgroup and each workgroup runs the single-type code (the barrier of the x image
 // sits in both branches; each wave reaches exactly one).
-template <int LPR, int UPL, int XPT, bool SWI, int TM>
+template <int LPR, int UPL, int XPT, int XM, int TM>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemvArgs args) {
     extern __shared__ __align__(16) uint8_t smem[];
     if constexpr (TM == 3) {
         constexpr int rows_per_block = (kGemvThreads / 64) * (64 / LPR);
         const int mi = pass_matrix(args, (int)blockIdx.x * rows_per_block);
-        if (args.m[mi].type == kTypeQ4K) gemv_body<LPR, UPL, XPT, SWI, 1>(args, smem);
-        else gemv_body<LPR, UPL, XPT, SWI, 2>(args, smem);
+        if (args.m[mi].type == kTypeQ4K) gemv_body<LPR, UPL, XPT, XM, 1>(args, smem);
+        else gemv_body<LPR, UPL, XPT, XM, 2>(args, smem);
     } else {
-        gemv_body<LPR, UPL, XPT, SWI, TM>(args, smem);
+        gemv_body<LPR, UPL, XPT, XM, TM>(args, smem);
     }
 }
 
 template <int LPR, int UPL, int XPT, int TM>
 static void launch_tm(const GemvArgs &a, int blocks, size_t lds, hipStream_t stream) {
     if (a.xmode == 1)
-        hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, true, TM>), dim3(blocks), dim3(kGemvThreads), lds, stream, a);
+        hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, 1, TM>), dim3(blocks), dim3(kGemvThreads), lds, stream, a);
+    else if (a.xmode == 2)
+        hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, 2, TM>), dim3(blocks), dim3(kGemvThreads), lds, stream, a);
     else
-        hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, false, TM>), dim3(blocks), dim3(kGemvThreads), lds, stream, a);
+        hipLaunchKernelGGL((gemv_kernel<LPR, UPL, XPT, 0, TM>), dim3(blocks), dim3(kGemvThreads), lds, stream, a);
 }
 
 template <int LPR, int UPL, int XPT>
@@ -537,6 +565,7 @@ static int device_cus() {
 
 int launch_gemv_impl(GemvArgs a, hipStream_t stream) {
     if (a.n_cols < 4 || a.n_cols > kMaxGemvCols) return kErrBadArg;
+    if (a.xmode == 2 && (a.n_cols % 4 || !a.x2)) return set_error(kErrBadArg, "gemv rms-norm input: n_cols %% 4 and a weight");
     const int kp = (a.n_cols + 255) & ~255;
     // half super-blocks per row -> lanes per row (pow2, <= 64) and rows per wave pass
     const int uph = kp / 128;
@@ -600,7 +629,8 @@ int launch_gemv_experts_impl(GemvArgs a, hipStream_t stream) {
     if (E.rows % rpb != 0) return set_error(kErrBadArg, "expert GEMV: rows %d not a multiple of %d", E.rows, rpb);
     a.experts = 1;
     a.nmat = 0;
-    a.xmode = E.nm == 1 ? 1 : 0;
+    a.xmode = E.nm == 1 ? 1 : (a.x2 ? 2 : 0);  // down: SwiGLU of the slot; gate/up: x, or its RMS norm
+    if (a.xmode == 2 && a.n_cols % 4) return set_error(kErrBadArg, "expert GEMV rms-norm input: n_cols %% 4");
     a.total_rows = E.slots * E.nm * E.rows;
     if (E.nm == 1) E.ntiles = E.rows / rpb;
     const int tm = E.type == kTypeQ4K ? 1 : 2;

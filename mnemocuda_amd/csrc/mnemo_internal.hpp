@@ -55,7 +55,8 @@ struct GemvArgs {
     int nmat;
     int total_rows;
     int n_cols;
-    int xmode;  // 0: x;  1: silu(x) * x2
+    int xmode;  // 0: x;  1: silu(x) * x2;  2: rms_norm(x, eps) * x2
+    float eps;
     const float *x;
     const float *x2;
     int experts;  // 0: the static matrices m[]; 1: expert mode (ex)

@@ -37,8 +37,8 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
 
 int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s);
 int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k, hipStream_t s);
-int launch_router_topk(const float *w, const float *x, float *logits, int n, int n_cols, int k, int *cnt, int *idx,
-                       float *wts, hipStream_t stream);
+int launch_router_topk(const float *w, const float *x, const float *nw, float eps, float *logits, int n, int n_cols,
+                       int k, int *cnt, int *idx, float *wts, hipStream_t stream);
 
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
@@ -276,8 +276,9 @@ size_t moe_decode_workspace_bytes(int hidden, int eff, int E, int k) {
 }
 
 int launch_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
-                      size_t up_off, size_t down_off, int down_type, const float *x, int hidden, int eff, int E,
-                      int k, void *ws, size_t ws_bytes, float *out, int *idx_out, float *w_out, hipStream_t s) {
+                      size_t up_off, size_t down_off, int down_type, const float *x, const float *norm_w, float eps,
+                      int hidden, int eff, int E, int k, void *ws, size_t ws_bytes, float *out, int *idx_out,
+                      float *w_out, hipStream_t s) {
     if (!router_w || !experts || !x || !ws || !out || hidden <= 0 || eff <= 0 || E <= 0 || k <= 0)
         return set_error(kErrBadArg, "moe_decode: null pointer or non-positive size");
     if (k > 16 || k > E || E > 1024) return set_error(kErrBadArg, "moe_decode: need k <= 16, k <= n_experts <= 1024");
@@ -295,12 +296,16 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     float *gu = (float *)(w8 + L.gu), *partial = (float *)(w8 + L.partial);
     int *cnt = (int *)(w8 + L.cnt);
 
-    int rc = launch_router_topk(router_w, x, logits, E, hidden, k, (int *)(w8 + L.rcnt), idx, wts, s);
+    // with norm_w, x is the raw hidden state and both the router and the gate/up launch apply
+    // the RMS norm themselves (the reference's separate rms_norm launch, forward.c:800-806)
+    int rc = launch_router_topk(router_w, x, norm_w, eps, logits, E, hidden, k, (int *)(w8 + L.rcnt), idx, wts, s);
     if (rc) return rc;
 
     GemvArgs a;
     memset(&a, 0, sizeof a);
     a.x = x;
+    a.x2 = norm_w;
+    a.eps = eps;
     a.n_cols = hidden;
     a.ex.table = (const uint8_t *)experts;
     a.ex.stride = expert_stride;

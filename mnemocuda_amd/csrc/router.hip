@@ -159,8 +159,49 @@ int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k,
 // Logits <= -1e30 and NaN never win.  The counter must be zero before the first launch;
 // the last workgroup resets it.  Logits cross workgroups (and XCDs) as agent-scope atomic
 // stores/loads; each writer waits for its store before counting in.
+// With nw, x is first RMS-normalised (x * rsqrt(mean(x^2) + eps) * nw, the reference's
+// rms_norm_kernel, kernels.cu:692-722) inside every workgroup: each holds all of x.
+__device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, const float *__restrict__ x,
+                                              const float *__restrict__ nw, int n_cols, float eps, float *part) {
+    typedef float fv4 __attribute__((ext_vector_type(4)));
+    const int tid = threadIdx.x;
+    const fv4 *w4 = (const fv4 *)wr, *x4 = (const fv4 *)x, *n4w = (const fv4 *)nw;
+    const int n4 = n_cols / 4;
+    fv4 a[kRowMaxV4], b[kRowMaxV4], c[kRowMaxV4];
+#pragma unroll
+    for (int i = 0; i < kRowMaxV4; i++) {
+        const int j = min(tid + i * kRowThreads, n4 - 1);
+        a[i] = __builtin_nontemporal_load(w4 + j);
+        b[i] = x4[j];
+        c[i] = n4w[j];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRowMaxV4; i++)
+        if (tid + i * kRowThreads < n4) ss += b[i].x * b[i].x + b[i].y * b[i].y + b[i].z * b[i].z + b[i].w * b[i].w;
+    ss = sum64_lane63(ss);
+    if (lane_id() == 63) part[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRowThreads / 64; i++) tot += part[i];
+    __syncthreads();  // part[] is reused by block_sum
+    const float scale = 1.0f / sqrtf(tot / (float)n_cols + eps);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRowMaxV4; i++) {
+        float t = fmaf(a[i].x, b[i].x * scale * c[i].x, acc);
+        t = fmaf(a[i].y, b[i].y * scale * c[i].y, t);
+        t = fmaf(a[i].z, b[i].z * scale * c[i].z, t);
+        t = fmaf(a[i].w, b[i].w * scale * c[i].w, t);
+        acc = tid + i * kRowThreads < n4 ? t : acc;
+    }
+    return acc;
+}
+
 __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *__restrict__ w,
                                                                  const float *__restrict__ x,
+                                                                 const float *__restrict__ nw, float eps,
                                                                  float *__restrict__ logits, int n, int n_cols,
                                                                  int k, int *__restrict__ cnt,
                                                                  int *__restrict__ idx, float *__restrict__ wts,
@@ -172,7 +213,9 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     __shared__ int sel_i[kTopkMaxK];
     const int tid = threadIdx.x;
     const int row = blockIdx.x;
-    const float v = block_sum(row_dot(w + (size_t)row * n_cols, x, n_cols, vec4), part);
+    const float v = block_sum(nw ? row_dot_norm(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
+                                 : row_dot(w + (size_t)row * n_cols, x, n_cols, vec4),
+                              part);
     if (tid == 0) {
         __hip_atomic_store(logits + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
@@ -221,16 +264,19 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     }
 }
 
-int launch_router_topk(const float *w, const float *x, float *logits, int n, int n_cols, int k, int *cnt, int *idx,
-                       float *wts, hipStream_t stream) {
+int launch_router_topk(const float *w, const float *x, const float *nw, float eps, float *logits, int n, int n_cols,
+                       int k, int *cnt, int *idx, float *wts, hipStream_t stream) {
     if (!w || !x || !logits || !cnt || !idx || !wts || n <= 0 || n_cols <= 0 || k <= 0 || k > kTopkMaxK ||
         k > n || n > 64 * kTopkMaxPerLane)
         return set_error(kErrBadArg, "router_topk: need 0 < k <= min(%d, n_experts), n_experts <= %d", kTopkMaxK,
                          64 * kTopkMaxPerLane);
     const int vec4 = (n_cols % 4 == 0) && (n_cols <= 4 * kRowMaxV4 * kRowThreads) &&
-                     (((uintptr_t)w | (uintptr_t)x) % 16 == 0);
-    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, logits, n, n_cols, k, cnt,
-                       idx, wts, vec4);
+                     (((uintptr_t)w | (uintptr_t)x | (uintptr_t)nw) % 16 == 0);
+    if (nw && !vec4)
+        return set_error(kErrBadArg, "router_topk: the fused RMS norm needs n_cols %% 4 == 0, <= %d and aligned vectors",
+                         4 * kRowMaxV4 * kRowThreads);
+    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, nw, eps, logits, n, n_cols, k,
+                       cnt, idx, wts, vec4);
     return check_launch("router_topk");
 }
 

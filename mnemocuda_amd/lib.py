@@ -29,6 +29,8 @@ SIGNATURES: dict[str, tuple] = {
     "mnemo_matvec_q6k_scaled_add": (None, [vp, fp, fp, i32, i32, f32, stream_t]),
     "mnemo_matvec_dual": (None, [vp, i32, vp, i32, fp, fp, fp, i32, i32, stream_t]),
     "mnemo_matvec_qkv": (None, [vp, i32, vp, i32, vp, i32, fp, fp, fp, fp, i32, i32, i32, stream_t]),
+    "mnemo_matvec_qkv_rmsnorm": (None, [vp, i32, vp, i32, vp, i32, fp, fp, f32, fp, fp, fp, i32, i32, i32,
+                                         stream_t]),
     "mnemo_matvec_swiglu_scaled_add": (None, [vp, i32, fp, fp, fp, i32, i32, f32, stream_t]),
     "cuda_matvec_f32": (None, [fp, fp, fp, i32, i32, stream_t]),
     "cuda_topk_softmax": (None, [fp, ip, fp, i32, i32, stream_t]),
@@ -43,6 +45,8 @@ SIGNATURES: dict[str, tuple] = {
                                 stream_t]),
     "mnemo_moe_decode_workspace_bytes": (sz, [i32, i32, i32, i32]),
     "mnemo_moe_decode": (i32, [fp, vp, sz, sz, sz, sz, i32, fp, i32, i32, i32, i32, vp, sz, fp, ip, fp, stream_t]),
+    "mnemo_moe_decode_rmsnorm": (i32, [fp, vp, sz, sz, sz, sz, i32, fp, fp, f32, i32, i32, i32, i32, vp, sz, fp,
+                                        ip, fp, stream_t]),
     # attention chain
     "cuda_rms_norm": (None, [fp, fp, fp, i32, f32, stream_t]),
     "cuda_rms_norm_residual": (None, [fp, fp, fp, fp, i32, f32, stream_t]),

@@ -123,6 +123,19 @@ def matvec_qkv(wq, tq, wk, tk, wv, tv, x, oq, ok, ov, q_rows, kv_rows, cols):
     check(lib, "mnemo_matvec_qkv")
 
 
+def matvec_qkv_rmsnorm(wq, tq, wk, tk, wv, tv, x, norm_w, eps, oq, ok, ov, q_rows, kv_rows, cols):
+    """matvec_qkv of rms_norm(x) * norm_w, the norm computed inside the projection launch."""
+    lib = load_library()
+    if x.numel() < cols or norm_w.numel() < cols:
+        raise MnemoError("matvec_qkv_rmsnorm: x or norm_w too small")
+    lib.mnemo_matvec_qkv_rmsnorm(_check_w(wq, tq, q_rows, cols, "wq"), tq, _check_w(wk, tk, kv_rows, cols, "wk"), tk,
+                                 _check_w(wv, tv, kv_rows, cols, "wv"), tv, _dev(x, "x", torch.float32),
+                                 _dev(norm_w, "norm_w", torch.float32), float(eps), _dev(oq, "oq", torch.float32),
+                                 _dev(ok, "ok", torch.float32), _dev(ov, "ov", torch.float32), q_rows, kv_rows, cols,
+                                 _stream())
+    check(lib, "mnemo_matvec_qkv_rmsnorm")
+
+
 def matvec_q4k_scaled_add(w, x, y, rows, cols, scale):
     lib = load_library()
     lib.cuda_matvec_q4k_scaled_add(_check_w(w, TYPE_Q4K, rows, cols), _dev(x, "x", torch.float32),
@@ -244,6 +257,27 @@ def moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, dow
                              None if topk_idx is None else _dev(topk_idx, "topk_idx", torch.int32),
                              None if topk_w is None else _dev(topk_w, "topk_w", torch.float32), _stream())
     _check_rc(lib, e, "mnemo_moe_decode")
+
+
+def moe_decode_rmsnorm(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, norm_w, eps,
+                       hidden, eff, n_experts, k, workspace, out, topk_idx=None, topk_w=None):
+    """moe_decode of rms_norm(x) * norm_w with the norm computed by the router and gate/up
+    launches; x is the raw hidden state and may be out itself."""
+    lib = load_library()
+    need = expert_stride * (n_experts - 1) + down_off + row_bytes(down_type, eff) * hidden \
+        if down_type in BLOCK_BYTES else 0
+    if experts.numel() * experts.element_size() < need:
+        raise MnemoError("moe_decode_rmsnorm: expert table too small")
+    if router_w.numel() < n_experts * hidden or x.numel() < hidden or out.numel() < hidden \
+            or norm_w.numel() < hidden:
+        raise MnemoError("moe_decode_rmsnorm: router, x, norm_w or out too small")
+    e = lib.mnemo_moe_decode_rmsnorm(
+        _dev(router_w, "router_w", torch.float32), _dev(experts, "experts"), expert_stride, gate_off, up_off,
+        down_off, down_type, _dev(x, "x", torch.float32), _dev(norm_w, "norm_w", torch.float32), float(eps), hidden,
+        eff, n_experts, k, _dev(workspace, "workspace"), workspace.numel() * workspace.element_size(),
+        _dev(out, "out", torch.float32), None if topk_idx is None else _dev(topk_idx, "topk_idx", torch.int32),
+        None if topk_w is None else _dev(topk_w, "topk_w", torch.float32), _stream())
+    _check_rc(lib, e, "mnemo_moe_decode_rmsnorm")
 
 
 def sample_token(logits, vocab, temperature, top_p, seed, out):

@@ -94,6 +94,30 @@ def test_qkv_mixed(gpu, oracle, types, q_rows, kv_rows, cols):
         assert rel_l2(host(o), oracle.gemv(t, w, x, r, cols)) < TOL
 
 
+@pytest.mark.parametrize("types,q_rows,kv_rows,cols", [((12, 12, 14), 8192, 512, 4096), ((14, 12, 14), 70, 9, 768),
+                                                       ((12, 14, 12), 33, 64, 1000), ((12, 12, 12), 256, 64, 12288)])
+def test_qkv_rmsnorm(gpu, oracle, types, q_rows, kv_rows, cols):
+    """The attention norm folded into the projection launch (forward.c:687-700 then :705-712):
+    each projection equals the oracle GEMV of rms_norm(x) * norm_w."""
+    rng = np.random.default_rng(q_rows * 5 + kv_rows)
+    rows = (q_rows, kv_rows, kv_rows)
+    ws = [_mk(rng, t, r, cols) for t, r in zip(types, rows)]
+    x = (4.0 * rng.standard_normal(cols)).astype(np.float32)
+    nw = (1.0 + 0.3 * rng.standard_normal(cols)).astype(np.float32)
+    eps = 1e-6
+    xn = oracle.rms_norm(x, nw, eps)
+    outs = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    case(f"qkv rmsnorm {types} {q_rows}/{kv_rows}x{cols}")
+    gpu.ops.matvec_qkv_rmsnorm(ws[0][1], types[0], ws[1][1], types[1], ws[2][1], types[2], dev(x), dev(nw), eps,
+                               *outs, q_rows, kv_rows, cols)
+    for (w, _), t, o, r in zip(ws, types, outs, rows):
+        assert rel_l2(host(o), oracle.gemv(t, w, xn, r, cols)) < TOL
+    case("qkv rmsnorm: n_cols % 4 != 0 rejected")
+    with pytest.raises(gpu.MnemoError):
+        gpu.ops.matvec_qkv_rmsnorm(ws[0][1], types[0], ws[1][1], types[1], ws[2][1], types[2], dev(x), dev(nw), eps,
+                                   *outs, q_rows, kv_rows, cols - 2)
+
+
 @pytest.mark.parametrize("ta,tb,rows,cols", [(12, 12, 1536, 4096), (12, 14, 512, 4096), (14, 12, 77, 768),
                                              (14, 14, 64, 1536)])
 def test_dual(gpu, oracle, ta, tb, rows, cols):

@@ -213,3 +213,53 @@ def test_moe_decode_graph_replays(gpu):
         junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between replays
         torch.cuda.synchronize()
         del junk
+
+
+@pytest.mark.parametrize("H,EFF,E,k,DT,alias", [(512, 256, 16, 4, 14, False), (4096, 1536, 24, 8, 14, True),
+                                                (1024, 512, 8, 8, 12, True)])
+def test_moe_decode_rmsnorm_vs_oracle(gpu, oracle, H, EFF, E, k, DT, alias):
+    """The norm folded into the router and gate/up launches: the same routing and delta as the
+    oracle chain on rms_norm(x) * norm_w (forward.c:800-806 then :808-895), also with x == out."""
+    rng = np.random.default_rng(7 * H + E + k)
+    table = synth.expert_table(rng, E, H, EFF, DT)
+    lay = synth.expert_layout(H, EFF, DT)
+    eps = 1e-6
+    while True:
+        router = (rng.standard_normal((E, H)) / np.sqrt(H)).astype(np.float32)
+        x = (3.0 * rng.standard_normal(H)).astype(np.float32)
+        nw = (1.0 + 0.25 * rng.standard_normal(H)).astype(np.float32)
+        xn = oracle.rms_norm(x, nw, eps)
+        z = np.sort(router.astype(np.float64) @ xn)[::-1]
+        if k == E or z[k - 1] - z[k] > 1e-3:
+            break
+    ws = torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    idx = torch.full((k,), -1, dtype=torch.int32, device="cuda")
+    w = torch.zeros(k, device="cuda")
+    _, ridx, rw, delta = _decode_ref(oracle, table, lay, DT, router, xn, H, EFF, E, k)
+    case(f"moe_decode_rmsnorm H={H} EFF={EFF} E={E} k={k} down={DT} alias={alias}")
+    if alias:  # the residual stream updated in place: out = x + moe(norm(x))
+        out = dev(x)
+        gpu.ops.moe_decode_rmsnorm(dev(router), dev(table), *lay, DT, out, dev(nw), eps, H, EFF, E, k, ws, out, idx, w)
+        base = x.astype(np.float64)
+    else:
+        out0 = rng.standard_normal(H).astype(np.float32)
+        out = dev(out0)
+        gpu.ops.moe_decode_rmsnorm(dev(router), dev(table), *lay, DT, dev(x), dev(nw), eps, H, EFF, E, k, ws, out,
+                                   idx, w)
+        base = out0.astype(np.float64)
+    assert sorted(host(idx).tolist()) == sorted(ridx.tolist())
+    assert np.allclose(host(w)[np.argsort(host(idx))], rw[np.argsort(ridx)], rtol=1e-5, atol=1e-6)
+    err = rel_l2(host(out).astype(np.float64) - base, delta)
+    print(f"rel_l2={err:.2e}")
+    assert err < TOL
+
+
+def test_moe_decode_rmsnorm_rejects_ragged_hidden(gpu):
+    H, EFF, E, k, DT = 514, 256, 4, 2, 14
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    table = torch.zeros(E * 4 << 20, dtype=torch.uint8, device="cuda")
+    case("moe_decode_rmsnorm hidden % 4 != 0 rejected")
+    with pytest.raises(gpu.MnemoError):
+        gpu.ops.moe_decode_rmsnorm(torch.zeros(E * H, device="cuda"), table, 1 << 20, 0, 1 << 18, 1 << 19, DT,
+                                   torch.zeros(H, device="cuda"), torch.ones(H, device="cuda"), 1e-6, H, EFF, E, k,
+                                   ws, torch.zeros(H, device="cuda"))
