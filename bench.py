@@ -192,8 +192,8 @@ def gpu_bench(args):
 def decode_bench(gen, stream, layers, tokens, ctx_pos):
     """configs[2] inside a full decode step (forward.c:687-1077 per layer, then the lm_head
     and sampling, forward.c:1601-1707), one token at cache position ctx_pos, ctx_pos+1, ...:
-    per layer  fused Q/K/V with the attention RMS norm -> QK norm + RoPE + f16 KV store
-    (position in device memory) -> GQA decode attention over 0..pos -> O (+ residual) ->
+    per layer  fused Q/K/V with the attention RMS norm -> GQA decode attention over 0..pos
+    with the QK norm, RoPE and f16 KV store in its launch (position in device memory) -> O (+ residual) ->
     MoE block with its RMS norm with device-side dispatch (router 128 x 4096 fp32, top-8, gate+up
     Q4_K 4096->1536 x 8, down Q6_K 1536->4096 x 8, weighted sum added to the residual);
     then the final norm, lm_head Q6_K 151936 x 4096 and top-p sampling.  All 128 experts of
@@ -235,8 +235,9 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos):
             n, src, dst = norms[li], bufs[li % 2], bufs[(li + 1) % 2]
             # attention norm inside the projection launch
             ops.matvec_qkv_rmsnorm(L["q"], Q4K, L["k"], Q4K, L["v"], Q6K, src, n["attn"], EPS, q, kk, v, QD, KVD, H)
-            ops.attn_prep(q, kk, v, n["q"], n["k"], HD, EPS, THETA, pos, kcache[li], vcache[li], v_layout=1)
-            ops.attention_decode(q, kcache[li], vcache[li], attn, NH, HD, NKV, max_ctx, pos, scale, aws, v_layout=1)
+            # QK norm + RoPE + KV store inside the attention launch
+            ops.attention_decode_prep(q, kk, v, n["q"], n["k"], EPS, THETA, kcache[li], vcache[li], attn, NH, HD, NKV,
+                                      max_ctx, pos, scale, aws, v_layout=1)
             ops.matvec_q4k_add(L["o"], attn, src, dst, H, QD)  # dst = src + W_o attn
             # dst += moe(rms_norm(dst) * ffn_norm): the norm inside the router and gate/up launches
             ops.moe_decode_rmsnorm(routers[li], tables[li], stride, g_off, u_off, d_off, Q6K, dst, n["ffn"], EPS, H,
@@ -276,7 +277,7 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos):
             "context_position": ctx_pos, "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
             "frac_hbm_peak": round(per_tok / ms / 1e6 / HBM_PEAK_GBS, 4),
             "experts_resident_GB": round(E * LAYERS * stride / 1e9, 1),
-            "launches_per_token": LAYERS * 8 + 4}
+            "launches_per_token": LAYERS * 7 + 4}
 
 
 def attention_bench(stream, lengths=(1024, 4096, 16384, 32768)):

@@ -281,6 +281,20 @@ int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_ca
                            float *out, int n_heads, int head_dim, int n_kv_heads, int max_ctx,
                            const int *pos_dev, float scale, void *workspace,
                            size_t workspace_bytes, hipStream_t stream);
+/* New: mnemo_attn_prep and mnemo_attention_decode in the same two launches, for the
+ * decode step's attention block (forward.c:720-775: QK norm, RoPE, cache store, attention).
+ * q [n_heads][128], k and v [n_kv_heads][128] are the projections' raw outputs and are not
+ * modified; every chunk normalises and rotates its query heads in registers, and the chunk
+ * holding *pos_dev writes the new K / V rows (K normalised and rotated; int8: with their
+ * scales) and uses them directly.  The caches and out are bit-identical to mnemo_attn_prep
+ * followed by mnemo_attention_decode.  Nothing is stored when *pos_dev >= max_ctx. */
+int mnemo_attention_decode_prep(const float *q, const float *k, const float *v,
+                                const float *q_norm_w, const float *k_norm_w, float eps,
+                                float theta, void *k_cache, void *v_cache, float *k_scales,
+                                float *v_scales, int kv_type, int v_layout, float *out,
+                                int n_heads, int head_dim, int n_kv_heads, int max_ctx,
+                                const int *pos_dev, float scale, void *workspace,
+                                size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

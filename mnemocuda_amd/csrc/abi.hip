@@ -455,6 +455,43 @@ int mnemo_attention_decode(const float *q, const void *k_cache, const void *v_ca
     return launch_attention_decode(a, kv_type, s);
 }
 
+int mnemo_attention_decode_prep(const float *q, const float *k, const float *v, const float *q_norm_w,
+                                const float *k_norm_w, float eps, float theta, void *k_cache, void *v_cache,
+                                float *k_scales, float *v_scales, int kv_type, int v_layout, float *out, int n_heads,
+                                int head_dim, int n_kv_heads, int max_ctx, const int *pos_dev, float scale,
+                                void *workspace, size_t workspace_bytes, hipStream_t s) {
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads)
+        return set_error(kErrBadArg, "attention_decode_prep: n_heads %% n_kv_heads");
+    if ((uintptr_t)workspace % 16) return set_error(kErrBadArg, "attention_decode_prep: workspace not 16-byte aligned");
+    AttnDecodeArgs a = {};
+    a.q = q;
+    a.kc = k_cache;
+    a.vc = v_cache;
+    a.ksc = k_scales;
+    a.vsc = v_scales;
+    a.out = out;
+    a.ws = (float *)workspace;
+    a.ws_bytes = workspace_bytes;
+    a.nh = n_heads;
+    a.hd = head_dim;
+    a.nkv = n_kv_heads;
+    a.gqa = n_heads / n_kv_heads;
+    a.max_ctx = max_ctx;
+    a.pos_dev = pos_dev;
+    a.scale = scale;
+    a.v_layout = v_layout;
+    a.kn = k;
+    a.vn = v;
+    a.qw = q_norm_w;
+    a.kw = k_norm_w;
+    a.eps = eps;
+    a.kcw = k_cache;
+    a.vcw = v_cache;
+    a.kscw = k_scales;
+    a.vscw = v_scales;
+    return launch_attention_decode_prep(a, kv_type, theta, s);
+}
+
 // ---------------------------------------------------------------- embedding
 void cuda_embedding_lookup_q4k(const void *embd_table, float *output, int token_id, int hidden_size, int row_bytes,
                                hipStream_t s) {

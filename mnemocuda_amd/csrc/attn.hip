@@ -31,15 +31,6 @@ namespace mnemo {
 
 constexpr int kNormThreads = 1024;
 
-__device__ __forceinline__ float wave_sum_all(float v) {
-    v = sum64_lane63(v);
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-__device__ __forceinline__ float wave_max_all(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
 
 // ------------------------------------------------------------------ RMS norm of one vector
 // out may alias in (each element is read and written by the same thread after the
@@ -190,8 +181,9 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
                 float sn, cs;
                 sincosf(ang, &sn, &cs);
                 const float v0 = x0[t], v1 = x1[t];
-                x0[t] = v0 * cs - v1 * sn;
-                x1[t] = v0 * sn + v1 * cs;
+                // explicit fmas: the fused decode attention repeats this rotation bit for bit
+                x0[t] = fmaf(v0, cs, -(v1 * sn));
+                x1[t] = fmaf(v0, sn, v1 * cs);
             }
         }
     }

@@ -17,6 +17,8 @@
 //    per query head (the flash-decoding combine).
 // int8 caches: K and V bytes convert exactly to f16; the per-position K scale multiplies
 // the score column, the V scale is folded into P.
+#include <math.h>
+
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
 
@@ -45,13 +47,64 @@ size_t kv_blocked_offset(int pos, int kvh, int d, int nkv, int hd) {
     return (((size_t)(pos / 64) * nkv + kvh) * hd + d) * 64 + pos % 64;
 }
 
-template <int KV, int VL>
+// The new token's preparation, the arithmetic of head_pass_kernel for one head of 128 in a
+// wave (lane holds dims lane and lane + 64): RMS norm with w (when given), then RoPE.
+__device__ __forceinline__ void prep_head(float &x0, float &x1, const float *w, float eps, float cs, float sn) {
+    const int lane = lane_id();
+    if (w) {
+        const float ss = fmaf(x0, x0, fmaf(x1, x1, 0.0f));
+        const float scale = 1.0f / sqrtf(wave_sum_all(ss) / (float)kHd + eps);
+        x0 = x0 * scale * w[lane];
+        x1 = x1 * scale * w[lane + kHd / 2];
+    }
+    const float v0 = x0, v1 = x1;
+    x0 = fmaf(v0, cs, -(v1 * sn));  // the same fmas as head_pass_kernel
+    x1 = fmaf(v0, sn, v1 * cs);
+}
+
+// One head row of the new position into the cache (K rows, V rows or V blocked) and into
+// an LDS copy in the cache's element type; returns the int8 scale (1 for f16).
+template <int KV>
+__device__ __forceinline__ float store_new_row(float x0, float x1, void *cache, float *scales, size_t base,
+                                               size_t es, size_t si, uint8_t *lds) {
+    const int lane = lane_id();
+    if (KV == kKvF16) {
+        const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+        _Float16 *c = (_Float16 *)cache + base;
+        c[(size_t)lane * es] = h0;
+        c[(size_t)(lane + kHd / 2) * es] = h1;
+        ((_Float16 *)lds)[lane] = h0;
+        ((_Float16 *)lds)[lane + kHd / 2] = h1;
+        return 1.0f;
+    } else {
+        const float m = wave_max_all(fmaxf(fabsf(x0), fabsf(x1)));
+        const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+        const int8_t q0 = (int8_t)fminf(fmaxf(rintf(x0 * inv), -127.0f), 127.0f);
+        const int8_t q1 = (int8_t)fminf(fmaxf(rintf(x1 * inv), -127.0f), 127.0f);
+        int8_t *c = (int8_t *)cache + base;
+        c[(size_t)lane * es] = q0;
+        c[(size_t)(lane + kHd / 2) * es] = q1;
+        ((int8_t *)lds)[lane] = q0;
+        ((int8_t *)lds)[lane + kHd / 2] = q1;
+        const float sc = m > 0.0f ? m / 127.0f : 0.0f;
+        if (lane == 0) scales[si] = sc;
+        return sc;
+    }
+}
+
+// PREP: the launch also prepares the new token (QK norm, RoPE, K/V store at *pos_dev) --
+// the same values head_pass_kernel would have written, formed in registers: every chunk
+// prepares its query heads itself, the chunk holding *pos_dev stores the new K / V rows
+// and uses them in place of what it loaded from the cache.
+template <int KV, int VL, bool PREP>
 __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
     __shared__ __align__(16) _Float16 vt[VL == kVRows ? kChunk : 1][kHd + 8];  // V tile [pos][dim]
     __shared__ __align__(16) _Float16 ps[2][kRows][kChunk + 8];
+    __shared__ __align__(16) uint8_t knew[PREP ? 2 : 1][PREP ? 2 * kHd : 1];  // new K, V rows as stored
     const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
-    const int seq = min(*a.pos_dev + 1, a.max_ctx);
+    const int pos = *a.pos_dev;
+    const int seq = min(pos + 1, a.max_ctx);
     const int p0 = chunk * kChunk;
     if (p0 >= seq) return;  // the combine reads ceil(seq / 64) chunks only
     const int G = a.gqa;
@@ -99,7 +152,43 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     }
 
     // ---- Q rows (heads kvh*G .. +G-1) as f16 hi + lo
-    for (int e = lane; e < kRows * kHd / 4; e += 64) {
+    const bool mine = PREP && pos < a.max_ctx && pos / kChunk == chunk;  // uniform
+    float new_ksc = 1.0f, new_vsc = 1.0f;
+    if (PREP) {
+        float qx0[kRows], qx1[kRows], k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+        for (int h = 0; h < kRows; h++) {
+            const float *qh = a.q + (size_t)(kvh * G + min(h, G - 1)) * kHd;
+            qx0[h] = qh[lane];
+            qx1[h] = qh[lane + kHd / 2];
+        }
+        if (mine) {
+            k0 = a.kn[(size_t)kvh * kHd + lane];
+            k1 = a.kn[(size_t)kvh * kHd + lane + kHd / 2];
+            v0 = a.vn[(size_t)kvh * kHd + lane];
+            v1 = a.vn[(size_t)kvh * kHd + lane + kHd / 2];
+        }
+        float sn, cs;
+        sincosf((float)pos * a.freq[lane], &sn, &cs);
+#pragma unroll
+        for (int h = 0; h < kRows; h++) {
+            float x0 = qx0[h], x1 = qx1[h];
+            prep_head(x0, x1, a.qw, a.eps, cs, sn);
+            if (h >= G) x0 = x1 = 0.0f;
+            const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+            qs[0][h][lane] = h0;
+            qs[0][h][lane + kHd / 2] = h1;
+            qs[1][h][lane] = (_Float16)(x0 - (float)h0);
+            qs[1][h][lane + kHd / 2] = (_Float16)(x1 - (float)h1);
+        }
+        if (mine) {
+            prep_head(k0, k1, a.kw, a.eps, cs, sn);
+            const size_t si = (size_t)pos * a.nkv + kvh;
+            new_ksc = store_new_row<KV>(k0, k1, a.kcw, a.kscw, si * kHd, 1, si, knew[0]);
+            const size_t vb = VL == kVBlocked ? (((size_t)(pos / 64) * a.nkv + kvh) * kHd) * 64 + pos % 64 : si * kHd;
+            new_vsc = store_new_row<KV>(v0, v1, a.vcw, a.vscw, vb, VL == kVBlocked ? 64 : 1, si, knew[1]);
+        }
+    } else for (int e = lane; e < kRows * kHd / 4; e += 64) {
         const int h = e / (kHd / 4), d = 4 * (e % (kHd / 4));
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (h < G) v = *(const float4 *)(a.q + (size_t)(kvh * G + h) * kHd + d);
@@ -114,6 +203,39 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
         __builtin_memcpy(&qs[1][h][d], lo, 8);
     }
     __syncthreads();
+    if (mine) {
+        // the loaded cache rows at pos are stale: take the new K / V rows from LDS (also
+        // where a position past pos was clamped to pos)
+        constexpr int EB = KV == kKvF16 ? 2 : 1;
+        const int o = pos - p0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if (16 * t + r >= o) {
+#pragma unroll
+                for (int s = 0; s < 4; s++) __builtin_memcpy(&kr[4 * t + s], &knew[0][(32 * s + 8 * kg) * EB], 8 * EB);
+                ksc[t] = new_ksc;
+            }
+        }
+        if (VL == kVRows) {
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (4 * u + (lane >> 4) >= o)  // position of the 16-element piece, clamped
+                    __builtin_memcpy(&vr[u], &knew[1][8 * (lane & 15) * EB], 8 * EB);
+        } else if (kg == ((o >> 3) & 3)) {
+            // vr[2n + kk] holds dim 16n + r at positions 32kk + 8kg .. +7
+#pragma unroll
+            for (int n = 0; n < 8; n++) {
+#pragma unroll
+                for (int kk = 0; kk < 2; kk++) {
+                    if (kk != (o >> 5)) continue;
+                    uint8_t *vb = (uint8_t *)&vr[2 * n + kk];
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        if (j == (o & 7)) __builtin_memcpy(vb + j * EB, &knew[1][(16 * n + r) * EB], EB);
+                }
+            }
+        }
+    }
 
     // ---- S = Q K^T for 4 tiles of 16 positions
     f4 sc[4];
@@ -163,7 +285,10 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     // ---- P (times the V scale for int8) to LDS as hi + lo, V tile to LDS
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        if (KV == kKvInt8) vsc = a.vsc[(size_t)min(p0 + 16 * t + r, seq - 1) * a.nkv + kvh];
+        if (KV == kKvInt8) {
+            const int p = min(p0 + 16 * t + r, seq - 1);
+            vsc = mine && p == pos ? new_vsc : a.vsc[(size_t)p * a.nkv + kvh];
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float pv = sc[t][i] * vsc;
@@ -296,7 +421,7 @@ __global__ void __launch_bounds__(kCombThreads) attn_combine_kernel(AttnDecodeAr
     }
 }
 
-int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s) {
+static int check_decode_args(AttnDecodeArgs &a, int kv_type) {
     if (!a.q || !a.kc || !a.vc || !a.out || !a.pos_dev || !a.ws)
         return set_error(kErrBadArg, "attention_decode: NULL pointer");
     if (a.hd != kHd) return set_error(kErrBadArg, "attention_decode: head_dim %d (this kernel: %d)", a.hd, kHd);
@@ -305,22 +430,48 @@ int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s) {
     if (a.max_ctx <= 0 || a.max_ctx > kMaxChunks * kChunk)
         return set_error(kErrBadArg, "attention_decode: max_ctx must be in 1..%d", kMaxChunks * kChunk);
     if (kv_type == kKvInt8 && (!a.ksc || !a.vsc)) return set_error(kErrBadArg, "attention_decode: int8 needs scales");
+    if (kv_type != kKvF16 && kv_type != kKvInt8) return set_error(kErrBadArg, "attention_decode: kv_type %d", kv_type);
     if (a.v_layout != kVRows && a.v_layout != kVBlocked)
         return set_error(kErrBadArg, "attention_decode: v_layout %d", a.v_layout);
     if (a.ws_bytes < attn_decode_workspace_bytes(a.nkv, a.max_ctx))
         return set_error(kErrBadArg, "attention_decode: workspace %zu < %zu bytes", a.ws_bytes,
                          attn_decode_workspace_bytes(a.nkv, a.max_ctx));
     a.max_chunks = (a.max_ctx + kChunk - 1) / kChunk;
+    return 0;
+}
+
+template <bool PREP>
+static int launch_decode(const AttnDecodeArgs &a, int kv_type, hipStream_t s) {
     const dim3 grid(a.max_chunks, a.nkv);
     if (kv_type == kKvF16) {
-        if (a.v_layout == kVBlocked) hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVBlocked>), grid, dim3(64), 0, s, a);
-        else hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVRows>), grid, dim3(64), 0, s, a);
+        if (a.v_layout == kVBlocked)
+            hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVBlocked, PREP>), grid, dim3(64), 0, s, a);
+        else hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVRows, PREP>), grid, dim3(64), 0, s, a);
     } else {
-        if (a.v_layout == kVBlocked) hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVBlocked>), grid, dim3(64), 0, s, a);
-        else hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVRows>), grid, dim3(64), 0, s, a);
+        if (a.v_layout == kVBlocked)
+            hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVBlocked, PREP>), grid, dim3(64), 0, s, a);
+        else hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVRows, PREP>), grid, dim3(64), 0, s, a);
     }
     hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, kHd / kCombDims), dim3(kCombThreads), 0, s, a);
     return check_launch("attention_decode");
+}
+
+int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s) {
+    if (int rc = check_decode_args(a, kv_type)) return rc;
+    return launch_decode<false>(a, kv_type, s);
+}
+
+// q raw; kn / vn the raw K / V heads of the new token; the caches are written at *pos_dev
+// (nothing is stored when *pos_dev >= max_ctx, and the attention covers 0..max_ctx-1).
+int launch_attention_decode_prep(AttnDecodeArgs a, int kv_type, float theta, hipStream_t s) {
+    if (int rc = check_decode_args(a, kv_type)) return rc;
+    if (!a.kn || !a.vn || !a.kcw || !a.vcw || (kv_type == kKvInt8 && (!a.kscw || !a.vscw)))
+        return set_error(kErrBadArg, "attention_decode_prep: NULL new K / V or cache pointer");
+    if ((a.qw == nullptr) != (a.kw == nullptr))
+        return set_error(kErrBadArg, "attention_decode_prep: give both QK-norm weights or neither");
+    // the frequencies of head_pass_kernel's RoPE, computed the same way
+    for (int j = 0; j < kHd / 2; j++) a.freq[j] = 1.0f / powf(theta, (float)(2 * j) / (float)kHd);
+    return launch_decode<true>(a, kv_type, s);
 }
 
 }  // namespace mnemo

@@ -106,18 +106,18 @@ __device__ __forceinline__ uint32_t umax_dpp8(uint32_t v) {
 // Builds the LDS image; every thread of the block must call this (it ends in a barrier).
 // Elements at or past n (loaded from clamped addresses) are zeroed here, after the
 // weight loads have been issued, so that waiting for x does not wait for the weights.
+// With XM == 2 the image holds the digits of x * g; the norm scale 1 / sqrt(mean(x^2) + eps)
+// is uniform over x, so it multiplies the finished dot products instead (returned here).
+// The waves' sums of squares go to LDS with the image and are summed after its barrier, in
+// a fixed order, so the norm costs no barrier of its own.
 template <int XPT, int XM>
-__device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, XLds X,
-                                         float eps) {
+__device__ __forceinline__ float finish_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, XLds X,
+                                          float eps) {
     const int lane = lane_id();
     constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23: adding it rounds to an integer (RNE)
     const bool ragged = (n & 3) != 0;      // uniform (the host rejects ragged n for XM == 2)
-    float nscale = 1.0f;
+    __shared__ float part[XM == 2 ? kGemvThreads / 64 : 1];
     if (XM == 2) {
-        // the RMS norm of the whole x (every workgroup holds all of it): a fixed-order sum
-        // of the waves' sums, then scale = 1 / sqrt(mean(x^2) + eps) as the reference's
-        // rms_norm_kernel (kernels.cu:692-722)
-        __shared__ float part[kGemvThreads / 64];
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
@@ -130,11 +130,6 @@ __device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &
         }
         ss = sum64_lane63(ss);
         if (lane == 63) part[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kGemvThreads / 64; w++) tot += part[w];
-        nscale = 1.0f / sqrtf(tot / (float)n + eps);
     }
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
@@ -147,7 +142,7 @@ __device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &
         if (XM != 0) {
             const float g[4] = {R2.v[i].x, R2.v[i].y, R2.v[i].z, R2.v[i].w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = XM == 1 ? silu_mul(v[j], g[j]) : v[j] * nscale * g[j];
+            for (int j = 0; j < 4; j++) v[j] = XM == 1 ? silu_mul(v[j], g[j]) : v[j] * g[j];
         }
         if (ragged) {
             // element e+j sits at v[j + sh], sh = e - min(e, n-4) (non-zero only in the last
@@ -214,6 +209,11 @@ __device__ __forceinline__ void finish_x(const XRegs<XPT> &R, const XRegs<XPT> &
         }
     }
     __syncthreads();
+    if (XM != 2) return 1.0f;
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kGemvThreads / 64; w++) tot += part[w];
+    return 1.0f / sqrtf(tot / (float)n + eps);
 }
 
 // ------------------------------------------------------------------ weight units
@@ -421,7 +421,8 @@ __device__ __forceinline__ void load_pass(const GemvMat &M, int row0, int base, 
 }
 
 template <int LPR, int UPL, int TM>
-__device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pass<UPL> &ps, const XLds &X) {
+__device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pass<UPL> &ps, const XLds &X,
+                                            float oscale) {
     const int lane = lane_id();
     const int ul = lane % LPR;
     const int uph = bpr * 2;
@@ -436,7 +437,7 @@ __device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pas
         acc += u < uph ? v : 0.0f;
         __builtin_amdgcn_sched_barrier(0);  // one unit's digit reads at a time
     }
-    acc = reduce_rows<LPR>(acc);
+    acc = reduce_rows<LPR>(acc) * oscale;
     if (ul == LPR - 1 && ps.valid) {
         if (M.mode == kEpiStore) M.y[ps.lrow] = acc;
         else if (M.mode == kEpiResidual) M.y[ps.lrow] = acc + M.res[ps.lrow];
@@ -507,8 +508,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     const GemvMat M = pass_mat(args, bc, row0);
     Pass<UPL> ps;
     load_pass<LPR, UPL, TM>(M, row0, bc, bpr, ps);
-    finish_x<XPT, XM>(xr, xr2, args.n_cols, kp, X, args.eps);
-    if (base < args.total_rows) finish_pass<LPR, UPL, TM>(M, bpr, ps, X);
+    const float oscale = finish_x<XPT, XM>(xr, xr2, args.n_cols, kp, X, args.eps);
+    if (base < args.total_rows) finish_pass<LPR, UPL, TM>(M, bpr, ps, X, oscale);
     if (args.experts && args.ex.nm == 2 && blockIdx.x == 0) {
         // clear the tile counters of the down launch that follows on the stream
         for (int t = threadIdx.x; t < args.ex.ntiles; t += kGemvThreads) args.ex.tile_cnt[t] = 0;

@@ -115,6 +115,18 @@ __device__ __forceinline__ float sum64_lane63(float v) {
     v += dpp_f<kDppRowBcast31, 0xC>(v);
     return v;
 }
+
+// the sum (max) of v over the wave, in every lane
+__device__ __forceinline__ float wave_sum_all(float v) {
+    v = sum64_lane63(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_max_all(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
 // Sum over aligned 32-lane halves; valid in lanes 31 and 63.
 __device__ __forceinline__ float sum32_lane31(float v) {
     v = sum16(v);

@@ -114,9 +114,18 @@ struct AttnDecodeArgs {
     const int *pos_dev;  // sequence length = min(*pos_dev + 1, max_ctx)
     float scale;
     int v_layout;        // 0: V rows [pos][n_kv][hd]; 1: blocked [pos/64][n_kv][hd][pos%64]
+    // the new token's preparation inside the launch (launch_attention_decode_prep): q is
+    // raw, kn / vn are the raw K / V heads [nkv][hd] of position *pos_dev
+    const float *kn, *vn;
+    const float *qw, *kw;  // QK-norm weights [hd], or both NULL
+    float eps;
+    void *kcw, *vcw;       // the caches again, written at *pos_dev
+    float *kscw, *vscw;
+    float freq[64];        // RoPE frequencies of the head_dim-128 kernel
 };
 size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx);
 int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s);
+int launch_attention_decode_prep(AttnDecodeArgs a, int kv_type, float theta, hipStream_t s);
 
 int launch_embedding(const void *table, int type, const int *tok_dev, int tok, int n_vocab, float *out, int hidden,
                      size_t row_bytes, hipStream_t s);

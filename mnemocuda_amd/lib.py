@@ -64,6 +64,8 @@ SIGNATURES: dict[str, tuple] = {
     "mnemo_attention_decode_workspace_bytes": (sz, [i32, i32]),
     "mnemo_attention_decode": (i32, [fp, vp, vp, fp, fp, i32, i32, fp, i32, i32, i32, i32, ip, f32, vp, sz,
                                      stream_t]),
+    "mnemo_attention_decode_prep": (i32, [fp, fp, fp, fp, fp, f32, f32, vp, vp, fp, fp, i32, i32, fp, i32, i32, i32,
+                                          i32, ip, f32, vp, sz, stream_t]),
     "cuda_embedding_lookup_q4k": (None, [vp, fp, i32, i32, i32, stream_t]),
     "mnemo_embedding_lookup": (i32, [vp, i32, ip, i32, fp, i32, stream_t]),
     # model directory (mnemo_model.h); structs travel as void*

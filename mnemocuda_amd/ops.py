@@ -417,6 +417,24 @@ def attention_decode(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: in
     _check_rc(lib, rc, "mnemo_attention_decode")
 
 
+def attention_decode_prep(q, k, v, qw, kw, eps: float, theta: float, kc, vc, out, n_heads: int, head_dim: int,
+                          n_kv_heads: int, max_ctx: int, pos_dev, scale: float, ws, ks=None, vs=None,
+                          v_layout: int = 0):
+    """attn_prep + attention_decode in the same two launches: q, k, v raw (left unchanged),
+    the new K / V rows stored at pos_dev[0], attention over 0..pos_dev[0]."""
+    lib = load_library()
+    kv_type = 0 if kc.dtype == torch.float16 else 1
+    if q.numel() < n_heads * head_dim or k.numel() < n_kv_heads * head_dim or v.numel() < n_kv_heads * head_dim:
+        raise MnemoError("attention_decode_prep: q, k or v too small")
+    rc = lib.mnemo_attention_decode_prep(
+        _dev(q, "q", F32), _dev(k, "k", F32), _dev(v, "v", F32), _opt(qw, "qw", F32), _opt(kw, "kw", F32),
+        float(eps), float(theta), _dev(kc, "kc"), _dev(vc, "vc"), _opt(ks, "ks", F32), _opt(vs, "vs", F32), kv_type,
+        int(v_layout), _dev(out, "out", F32), n_heads, head_dim, n_kv_heads, int(max_ctx),
+        _dev(pos_dev, "pos_dev", torch.int32), float(scale), _dev(ws, "ws"), ws.numel() * ws.element_size(),
+        _stream())
+    _check_rc(lib, rc, "mnemo_attention_decode_prep")
+
+
 # ---------------------------------------------------------------- embedding
 def embedding_lookup(table, type_id: int, token_dev, n_vocab: int, out, hidden: int):
     """out[:hidden] = dequantised row token_dev[0] of table (F32 / Q4_K / Q6_K).  table is a

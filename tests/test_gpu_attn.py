@@ -359,3 +359,118 @@ def test_attention_decode_bad_args(gpu):
         gpu.ops.attention_decode(q, kc, kc, out, NH, HD, 2, 64, pos, 0.1, ws)
     with pytest.raises(gpu.MnemoError):  # head_dim 64 not on this path
         gpu.ops.attention_decode(q, kc, kc, out, NH, 64, NKV, 64, pos, 0.1, ws)
+
+
+# ------------------------------------------------------------------ decode attention with the prep fused
+def _prep_inputs(rng, kind, max_ctx, nh, nkv, v_layout, pos):
+    kc, vc, ks, vs = _caches(rng, max_ctx, nkv, HD, kind)
+    if v_layout == 1:
+        vc = _blocked(vc, max_ctx, nkv, HD)
+    t = [_to_dev(a) for a in (kc, vc, ks, vs)]
+    # the row at pos holds garbage until this token stores it (the fused path must not read it)
+    if kind == "f16":
+        t[0].view(-1, nkv, HD)[pos] = float("nan")
+        if v_layout == 0:
+            t[1].view(-1, nkv, HD)[pos] = float("nan")
+        else:
+            t[1].view(-1, nkv, HD, 64)[pos // 64, :, :, pos % 64] = float("nan")
+    else:
+        t[2].view(-1, nkv)[pos] = float("nan")
+        t[3].view(-1, nkv)[pos] = float("nan")
+    return t
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("v_layout", [0, 1])
+@pytest.mark.parametrize("kind", ["f16", "int8"])
+@pytest.mark.parametrize("pos,nh,nkv,max_ctx", [(0, NH, NKV, 4096), (63, NH, NKV, 4096), (64, NH, NKV, 4096),
+                                                (1000, NH, NKV, 4096), (130, 32, 4, 512), (77, 8, 8, 200),
+                                                (199, 8, 8, 200)])
+def test_attention_decode_prep_matches_two_step(gpu, rng, kind, v_layout, norm, pos, nh, nkv, max_ctx):
+    """mnemo_attention_decode_prep == mnemo_attn_prep then mnemo_attention_decode, bit for bit:
+    the output, both caches (and int8 scales); q, k, v are left unchanged."""
+    q = dev(rng.standard_normal(nh * HD).astype(np.float32) * 2)
+    k = dev(rng.standard_normal(nkv * HD).astype(np.float32) * 2)
+    v = dev(rng.standard_normal(nkv * HD).astype(np.float32))
+    qw = dev(1 + 0.2 * rng.standard_normal(HD).astype(np.float32)) if norm else None
+    kw = dev(1 + 0.2 * rng.standard_normal(HD).astype(np.float32)) if norm else None
+    eps, theta, scale = 1e-6, 1e6, 1.0 / np.sqrt(HD)
+    st = rng.bit_generator.state
+    a = _prep_inputs(rng, kind, max_ctx, nh, nkv, v_layout, pos)
+    rng.bit_generator.state = st
+    b = _prep_inputs(rng, kind, max_ctx, nh, nkv, v_layout, pos)
+    pos_dev = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    ws = torch.empty(gpu.ops.attention_decode_workspace_bytes(nkv, max_ctx), dtype=torch.uint8, device="cuda")
+    out_a = torch.full((nh * HD,), np.nan, device="cuda")
+    out_b = torch.full((nh * HD,), np.nan, device="cuda")
+    case(f"attention_decode_prep {kind} v_layout={v_layout} norm={norm} pos={pos} nh={nh} nkv={nkv}")
+    qa, ka = q.clone(), k.clone()
+    gpu.ops.attn_prep(qa, ka, v, qw, kw, HD, eps, theta, pos_dev, a[0], a[1], a[2], a[3], v_layout=v_layout)
+    gpu.ops.attention_decode(qa, a[0], a[1], out_a, nh, HD, nkv, max_ctx, pos_dev, scale, ws, a[2], a[3],
+                             v_layout=v_layout)
+    q0, k0, v0 = q.clone(), k.clone(), v.clone()
+    gpu.ops.attention_decode_prep(q, k, v, qw, kw, eps, theta, b[0], b[1], out_b, nh, HD, nkv, max_ctx, pos_dev,
+                                  scale, ws, b[2], b[3], v_layout=v_layout)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q0) and torch.equal(k, k0) and torch.equal(v, v0)
+    assert not torch.isnan(out_b).any()
+    assert torch.equal(out_a, out_b)
+    for x, y in zip(a, b):
+        if x is not None:
+            assert torch.equal(x.view(torch.uint8) if x.dtype != torch.float32 else x,
+                               y.view(torch.uint8) if y.dtype != torch.float32 else y)
+
+
+def test_attention_decode_prep_token_sequence_graph(gpu, rng):
+    """a captured graph replayed token after token (position in device memory) reads back the
+    rows it stored at earlier replays and matches the eager two-step path at every token."""
+    max_ctx, nh, nkv = 300, NH, NKV
+    qw = dev(1 + 0.2 * rng.standard_normal(HD).astype(np.float32))
+    kw = dev(1 + 0.2 * rng.standard_normal(HD).astype(np.float32))
+    kc_a = torch.zeros(max_ctx * nkv * HD, dtype=torch.float16, device="cuda")
+    vc_a = torch.zeros(gpu.ops.v_cache_bytes(nkv, HD, max_ctx, 0, 1) // 2, dtype=torch.float16, device="cuda")
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    q, k, v = (torch.empty(n * HD, device="cuda") for n in (nh, nkv, nkv))
+    pos_a = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos_b = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws_a = torch.empty(gpu.ops.attention_decode_workspace_bytes(nkv, max_ctx), dtype=torch.uint8, device="cuda")
+    ws_b = torch.empty_like(ws_a)
+    out_a, out_b = torch.empty(nh * HD, device="cuda"), torch.empty(nh * HD, device="cuda")
+    s = torch.cuda.Stream()
+    case("attention_decode_prep graph over a token sequence")
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            gpu.ops.attention_decode_prep(q, k, v, qw, kw, 1e-6, 1e6, kc_b, vc_b, out_b, nh, HD, nkv, max_ctx,
+                                          pos_b, 0.088, ws_b, v_layout=1)
+        kc_b.zero_()
+        vc_b.zero_()
+        for t in range(70):
+            q.copy_(torch.randn(nh * HD, device="cuda"))
+            k.copy_(torch.randn(nkv * HD, device="cuda"))
+            v.copy_(torch.randn(nkv * HD, device="cuda"))
+            qa, ka = q.clone(), k.clone()
+            pos_a.fill_(t)
+            gpu.ops.attn_prep(qa, ka, v, qw, kw, HD, 1e-6, 1e6, pos_a, kc_a, vc_a, v_layout=1)
+            gpu.ops.attention_decode(qa, kc_a, vc_a, out_a, nh, HD, nkv, max_ctx, pos_a, 0.088, ws_a, v_layout=1)
+            pos_b.fill_(t)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out_a, out_b), t
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+
+
+def test_attention_decode_prep_bad_args(gpu):
+    case("attention_decode_prep bad args")
+    q = torch.zeros(NH * HD, device="cuda")
+    k = torch.zeros(NKV * HD, device="cuda")
+    kc = torch.zeros(64 * NKV * HD, dtype=torch.float16, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    ws = torch.empty(gpu.ops.attention_decode_workspace_bytes(NKV, 64), dtype=torch.uint8, device="cuda")
+    with pytest.raises(gpu.MnemoError):  # only one of the QK-norm weights
+        gpu.ops.attention_decode_prep(q, k, k, torch.ones(HD, device="cuda"), None, 1e-6, 1e6, kc, kc, out, NH, HD,
+                                      NKV, 64, pos, 0.1, ws)
+    with pytest.raises(gpu.MnemoError):  # int8 caches without scales
+        kc8 = torch.zeros(64 * NKV * HD, dtype=torch.int8, device="cuda")
+        gpu.ops.attention_decode_prep(q, k, k, None, None, 1e-6, 1e6, kc8, kc8, out, NH, HD, NKV, 64, pos, 0.1, ws)
