@@ -198,6 +198,9 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
         }
     }
     if ((a.flags & kHeadStore) && !is_q) {
+        // the cache takes the fp32 values rounded once more (no fma folded into the conversion)
+#pragma unroll
+        for (int t = 0; t < kHeadPairs; t++) asm volatile("" : "+v"(x0[t]), "+v"(x1[t]));
         // K rows [pos][nk][hd]; V rows likewise, or blocked: element (pos, h, d) at
         // ((pos/64 * nk + h) * hd + d) * 64 + pos % 64 (attention_decode reads it directly)
         const bool blocked = !is_k && a.v_layout == 1;

@@ -49,13 +49,13 @@ size_t kv_blocked_offset(int pos, int kvh, int d, int nkv, int hd) {
 
 // The new token's preparation, the arithmetic of head_pass_kernel for one head of 128 in a
 // wave (lane holds dims lane and lane + 64): RMS norm with w (when given), then RoPE.
-__device__ __forceinline__ void prep_head(float &x0, float &x1, const float *w, float eps, float cs, float sn) {
-    const int lane = lane_id();
-    if (w) {
+__device__ __forceinline__ void prep_head(float &x0, float &x1, bool norm, float w0, float w1, float eps, float cs,
+                                          float sn) {
+    if (norm) {
         const float ss = fmaf(x0, x0, fmaf(x1, x1, 0.0f));
         const float scale = 1.0f / sqrtf(wave_sum_all(ss) / (float)kHd + eps);
-        x0 = x0 * scale * w[lane];
-        x1 = x1 * scale * w[lane + kHd / 2];
+        x0 = x0 * scale * w0;
+        x1 = x1 * scale * w1;
     }
     const float v0 = x0, v1 = x1;
     x0 = fmaf(v0, cs, -(v1 * sn));  // the same fmas as head_pass_kernel
@@ -68,6 +68,9 @@ template <int KV>
 __device__ __forceinline__ float store_new_row(float x0, float x1, void *cache, float *scales, size_t base,
                                                size_t es, size_t si, uint8_t *lds) {
     const int lane = lane_id();
+    // x0, x1 are rounded to fp32 first (as a float row is, then converted): without the
+    // barrier the compiler folds the RoPE fma and the f16 conversion into one rounding
+    asm volatile("" : "+v"(x0), "+v"(x1));
     if (KV == kKvF16) {
         const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
         _Float16 *c = (_Float16 *)cache + base;
@@ -110,6 +113,33 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     const int G = a.gqa;
     const size_t stride = (size_t)a.nkv * kHd;
     const int r = lane & 15, kg = lane >> 4;
+    const bool mine = PREP && pos < a.max_ctx && pos / kChunk == chunk;  // uniform
+
+    // ---- PREP: the new token's raw rows, loaded before the cache so that waiting for them
+    // does not wait for the cache
+    float qx0[PREP ? kRows : 1], qx1[PREP ? kRows : 1];
+    float k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f, qw0 = 1.0f, qw1 = 1.0f, kw0 = 1.0f, kw1 = 1.0f, fr = 0.0f;
+    const bool norm = PREP && a.qw != nullptr;  // uniform
+    if (PREP) {
+#pragma unroll
+        for (int h = 0; h < kRows; h++) {
+            const float *qh = a.q + (size_t)(kvh * G + min(h, G - 1)) * kHd;
+            qx0[h] = qh[lane];
+            qx1[h] = qh[lane + kHd / 2];
+        }
+        if (norm) {
+            qw0 = a.qw[lane];
+            qw1 = a.qw[lane + kHd / 2];
+            kw0 = a.kw[lane];
+            kw1 = a.kw[lane + kHd / 2];
+        }
+        // (loaded by every chunk: a load under the branch would wait for the cache loads)
+        k0 = a.kn[(size_t)kvh * kHd + lane];
+        k1 = a.kn[(size_t)kvh * kHd + lane + kHd / 2];
+        v0 = a.vn[(size_t)kvh * kHd + lane];
+        v1 = a.vn[(size_t)kvh * kHd + lane + kHd / 2];
+        fr = a.freq[lane];
+    }
 
     // ---- loads first: K fragments (4 tiles of 16 positions x 4 steps of 32 dims) and the V tile
     constexpr int EB = KV == kKvF16 ? 2 : 1;  // bytes per cache element
@@ -152,28 +182,14 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     }
 
     // ---- Q rows (heads kvh*G .. +G-1) as f16 hi + lo
-    const bool mine = PREP && pos < a.max_ctx && pos / kChunk == chunk;  // uniform
     float new_ksc = 1.0f, new_vsc = 1.0f;
     if (PREP) {
-        float qx0[kRows], qx1[kRows], k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f;
-#pragma unroll
-        for (int h = 0; h < kRows; h++) {
-            const float *qh = a.q + (size_t)(kvh * G + min(h, G - 1)) * kHd;
-            qx0[h] = qh[lane];
-            qx1[h] = qh[lane + kHd / 2];
-        }
-        if (mine) {
-            k0 = a.kn[(size_t)kvh * kHd + lane];
-            k1 = a.kn[(size_t)kvh * kHd + lane + kHd / 2];
-            v0 = a.vn[(size_t)kvh * kHd + lane];
-            v1 = a.vn[(size_t)kvh * kHd + lane + kHd / 2];
-        }
         float sn, cs;
-        sincosf((float)pos * a.freq[lane], &sn, &cs);
+        sincosf((float)pos * fr, &sn, &cs);
 #pragma unroll
         for (int h = 0; h < kRows; h++) {
             float x0 = qx0[h], x1 = qx1[h];
-            prep_head(x0, x1, a.qw, a.eps, cs, sn);
+            prep_head(x0, x1, norm, qw0, qw1, a.eps, cs, sn);
             if (h >= G) x0 = x1 = 0.0f;
             const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
             qs[0][h][lane] = h0;
@@ -182,7 +198,7 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
             qs[1][h][lane + kHd / 2] = (_Float16)(x1 - (float)h1);
         }
         if (mine) {
-            prep_head(k0, k1, a.kw, a.eps, cs, sn);
+            prep_head(k0, k1, norm, kw0, kw1, a.eps, cs, sn);
             const size_t si = (size_t)pos * a.nkv + kvh;
             new_ksc = store_new_row<KV>(k0, k1, a.kcw, a.kscw, si * kHd, 1, si, knew[0]);
             const size_t vb = VL == kVBlocked ? (((size_t)(pos / 64) * a.nkv + kvh) * kHd) * 64 + pos % 64 : si * kHd;

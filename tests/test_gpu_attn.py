@@ -456,7 +456,18 @@ def test_attention_decode_prep_token_sequence_graph(gpu, rng):
             pos_b.fill_(t)
             g.replay()
             torch.cuda.synchronize()
-            assert torch.equal(out_a, out_b), t
+            if not torch.equal(out_a, out_b):
+                d = (out_a - out_b).abs()
+                bad = torch.nonzero(d).flatten()
+                msg = (f"token {t}: {bad.numel()} outputs differ, max {d.max().item():.3e}, first {bad[:8].tolist()}, "
+                       f"k rows equal {torch.equal(kc_a, kc_b)}, v equal {torch.equal(vc_a, vc_b)}")
+                ka3, kb3 = kc_a.view(max_ctx, nkv, HD).float(), kc_b.view(max_ctx, nkv, HD).float()
+                dk = torch.nonzero(ka3 != kb3)
+                msg += f"; k diffs (pos, head, dim) {dk[:12].tolist()} n={dk.shape[0]}"
+                if dk.shape[0]:
+                    p_, h_, d_ = dk[0].tolist()
+                    msg += f" a={ka3[p_, h_, d_].item()} b={kb3[p_, h_, d_].item()}"
+                raise AssertionError(msg)
     assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
 
 
