@@ -84,12 +84,13 @@ struct XRegs {
 // One 16-byte load per 4 elements from e clamped to n-4 (x may be unaligned; the host
 // rejects n < 4), so the instruction sequence is fixed.
 // XM: 0 x as given; 1 silu(x) * x2 (SwiGLU inputs); 2 rms_norm(x) * x2 (x2 = norm weight)
-template <int XPT, int XM>
+// NT threads share the image (the workgroup, or one wave); tid is the caller's index among them.
+template <int XPT, int XM, int NT = kGemvThreads>
 __device__ __forceinline__ void load_x(const float *__restrict__ x0, const float *__restrict__ x1, int n,
-                                       XRegs<XPT> &R, XRegs<XPT> &R2) {
+                                       XRegs<XPT> &R, XRegs<XPT> &R2, int tid = threadIdx.x) {
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
-        const int e = 4 * (threadIdx.x + i * kGemvThreads);
+        const int e = 4 * (tid + i * NT);
         const int ec = min(e, n - 4);
         __builtin_memcpy(&R.v[i], x0 + ec, 16);
         if (XM != 0) __builtin_memcpy(&R2.v[i], x1 + ec, 16);
@@ -103,39 +104,19 @@ __device__ __forceinline__ uint32_t umax_dpp8(uint32_t v) {
     return v;
 }
 
-// Builds the LDS image; every thread of the block must call this (it ends in a barrier).
-// Elements at or past n (loaded from clamped addresses) are zeroed here, after the
-// weight loads have been issued, so that waiting for x does not wait for the weights.
-// With XM == 2 the image holds the digits of x * g; the norm scale 1 / sqrt(mean(x^2) + eps)
-// is uniform over x, so it multiplies the finished dot products instead (returned here).
-// The waves' sums of squares go to LDS with the image and are summed after its barrier, in
-// a fixed order, so the norm costs no barrier of its own.
-template <int XPT, int XM>
-__device__ __forceinline__ float finish_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, XLds X,
-                                          float eps) {
+// The digit planes and sums of the elements held by tid (one of NT threads); no barrier.
+template <int XPT, int XM, int NT>
+__device__ __forceinline__ void build_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, const XLds &X,
+                                        int tid) {
     const int lane = lane_id();
     constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23: adding it rounds to an integer (RNE)
     const bool ragged = (n & 3) != 0;      // uniform (the host rejects ragged n for XM == 2)
-    __shared__ float part[XM == 2 ? kGemvThreads / 64 : 1];
-    if (XM == 2) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            if (4 * (threadIdx.x + i * kGemvThreads) < n) {
-                ss = fmaf(R.v[i].x, R.v[i].x, ss);
-                ss = fmaf(R.v[i].y, R.v[i].y, ss);
-                ss = fmaf(R.v[i].z, R.v[i].z, ss);
-                ss = fmaf(R.v[i].w, R.v[i].w, ss);
-            }
-        }
-        ss = sum64_lane63(ss);
-        if (lane == 63) part[threadIdx.x >> 6] = ss;
-    }
+
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
         // computed unconditionally (a load used only under a branch would be sunk into it,
         // behind the weight loads); only the stores are guarded
-        const int e4 = threadIdx.x + i * kGemvThreads;
+        const int e4 = tid + i * NT;
         const bool store = 4 * e4 < kp;  // uniform per 8-lane group: kp is a multiple of 256
         const int e = 4 * e4;
         float v[4] = {R.v[i].x, R.v[i].y, R.v[i].z, R.v[i].w};
@@ -208,6 +189,34 @@ __device__ __forceinline__ float finish_x(const XRegs<XPT> &R, const XRegs<XPT> 
             if ((lane & 3) == 0) X.s16[e >> 4] = s16;
         }
     }
+}
+
+// Builds the workgroup's LDS image; every thread of the block must call this (it ends in a
+// barrier).  Elements at or past n (loaded from clamped addresses) are zeroed, after the
+// weight loads have been issued, so that waiting for x does not wait for the weights.
+// With XM == 2 the image holds the digits of x * g; the norm scale 1 / sqrt(mean(x^2) + eps)
+// is uniform over x, so it multiplies the finished dot products instead (returned here).
+// The waves' sums of squares go to LDS with the image and are summed after its barrier, in
+// a fixed order, so the norm costs no barrier of its own.
+template <int XPT, int XM>
+__device__ __forceinline__ float finish_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, XLds X,
+                                          float eps) {
+    __shared__ float part[XM == 2 ? kGemvThreads / 64 : 1];
+    if (XM == 2) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            if (4 * (threadIdx.x + i * kGemvThreads) < n) {
+                ss = fmaf(R.v[i].x, R.v[i].x, ss);
+                ss = fmaf(R.v[i].y, R.v[i].y, ss);
+                ss = fmaf(R.v[i].z, R.v[i].z, ss);
+                ss = fmaf(R.v[i].w, R.v[i].w, ss);
+            }
+        }
+        ss = sum64_lane63(ss);
+        if (lane_id() == 63) part[threadIdx.x >> 6] = ss;
+    }
+    build_x<XPT, XM, kGemvThreads>(R, R2, n, kp, X, threadIdx.x);
     __syncthreads();
     if (XM != 2) return 1.0f;
     float tot = 0.0f;
@@ -376,7 +385,8 @@ __device__ __forceinline__ GemvMat pass_mat(const GemvArgs &args, int base, int 
         return args.m[mi];
     }
     const GemvExperts &E = args.ex;
-    const int sm = base / E.rows;  // slot * nm + matrix
+    const bool pair = E.act && E.nm == 2;  // row space [slot][row][gate, up]
+    const int sm = pair ? 2 * (base / (2 * E.rows)) : base / E.rows;  // slot * nm + matrix
     const int s = sm / E.nm, m = sm - s * E.nm;
     row0 = sm * E.rows;
     int e = E.idx[s];
@@ -387,7 +397,13 @@ __device__ __forceinline__ GemvMat pass_mat(const GemvArgs &args, int base, int 
     M.rows = E.rows;
     M.type = E.type;
     M.res = nullptr;
-    if (E.nm == 2) {
+    M.pair = pair;
+    M.mstride = (long long)E.off[1] - (long long)E.off[0];
+    if (pair) {
+        M.y = E.y + (size_t)s * E.rows;
+        M.mode = kEpiSwiGLU;
+        M.scale = 0.0f;
+    } else if (E.nm == 2) {
         M.y = E.y + (size_t)sm * E.rows;
         M.mode = kEpiStore;
         M.scale = 0.0f;
@@ -405,12 +421,13 @@ __device__ __forceinline__ void load_pass(const GemvMat &M, int row0, int base, 
     const int lane = lane_id();
     const int ul = lane % LPR;
     const int uph = bpr * 2;  // half super-blocks per row
-    const int lrow = base - row0 + lane / LPR;
+    const int i = lane / LPR;
+    const int lrow = M.pair ? ((base - row0) >> 1) + (i >> 1) : base - row0 + i;
     // branch-free: a row past the end of its matrix re-loads the last row, dropped later
     ps.valid = lrow < M.rows;
     ps.lrow = min(lrow, M.rows - 1);
     const int bb = TM == 1 ? kQ4KBytes : kQ6KBytes;
-    const uint8_t *wrow = (const uint8_t *)M.w + (size_t)ps.lrow * bpr * bb;
+    const uint8_t *wrow = (const uint8_t *)M.w + (M.pair ? (i & 1) * M.mstride : 0) + (size_t)ps.lrow * bpr * bb;
 #pragma unroll
     for (int j = 0; j < UPL; j++) {
         const int u = min(ul + j * LPR, uph - 1);
@@ -420,9 +437,9 @@ __device__ __forceinline__ void load_pass(const GemvMat &M, int row0, int base, 
     }
 }
 
+// The row sums of a pass, valid in lane LPR - 1 of each row's lanes.
 template <int LPR, int UPL, int TM>
-__device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pass<UPL> &ps, const XLds &X,
-                                            float oscale) {
+__device__ __forceinline__ float pass_dot(int bpr, const Pass<UPL> &ps, const XLds &X) {
     const int lane = lane_id();
     const int ul = lane % LPR;
     const int uph = bpr * 2;
@@ -437,8 +454,21 @@ __device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pas
         acc += u < uph ? v : 0.0f;
         __builtin_amdgcn_sched_barrier(0);  // one unit's digit reads at a time
     }
-    acc = reduce_rows<LPR>(acc) * oscale;
-    if (ul == LPR - 1 && ps.valid) {
+    return reduce_rows<LPR>(acc);
+}
+
+template <int LPR, int UPL, int TM>
+__device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pass<UPL> &ps, const XLds &X,
+                                            float oscale) {
+    const float acc = pass_dot<LPR, UPL, TM>(bpr, ps, X) * oscale;
+    if (M.mode == kEpiSwiGLU) {
+        // the gate row's sum sits LPR lanes below the up row's
+        const int lane = lane_id();
+        const float g = __shfl(acc, lane - LPR);
+        if (lane % LPR == LPR - 1 && ((lane / LPR) & 1) && ps.valid) M.y[ps.lrow] = silu_mul(g, acc);
+        return;
+    }
+    if (lane_id() % LPR == LPR - 1 && ps.valid) {
         if (M.mode == kEpiStore) M.y[ps.lrow] = acc;
         else if (M.mode == kEpiResidual) M.y[ps.lrow] = acc + M.res[ps.lrow];
         else if (M.mode == kEpiScaledAdd) M.y[ps.lrow] += M.scale * acc;
@@ -495,7 +525,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     const float *x0 = args.x, *x1 = args.x2;
     if (down) {  // x of this workgroup's slot (rows is a multiple of the workgroup's rows)
         const int s = (int)blockIdx.x * rows_per_block / args.ex.rows;
-        x0 = args.ex.xs + (size_t)(2 * s) * args.n_cols;
+        x0 = args.ex.xs + (size_t)(args.ex.act ? s : 2 * s) * args.n_cols;
         x1 = x0 + args.n_cols;
     }
 
@@ -516,6 +546,73 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     }
     if (down) experts_combine<rows_per_block>(args.ex);
 }
+
+#if MNEMO_GEMV_THREADS == 512
+// Expert-mode down projection with the slots side by side (slots <= 8, n_cols <= 2048): a
+// workgroup covers one tile of P = 64/LPR rows for every slot at once, wave w computing
+// slot w's expert with an x image of its own (the SwiGLU of the slot's gate and up rows,
+// built by the wave alone).  The slot results meet in LDS and are added in slot order into
+// out -- the arithmetic of the partial-buffer path (same digits, same products, same
+// order), without the partial stores, the arrival counter and the waits they need, and with
+// one workgroup per row tile (256 for 4096 rows at LPR 4: one round on the chip).
+constexpr int kSlotWaves = kGemvThreads / 64;
+template <int LPR, int UPL, int XPW, int XM, int TM>
+__global__ void __launch_bounds__(kGemvThreads) gemv_down_slots_kernel(GemvArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int P = 64 / LPR;
+    __shared__ float red[kSlotWaves][P];
+    const GemvExperts &E = args.ex;
+    const int n = args.n_cols;
+    const int kp = (n + 255) & ~255;
+    const int bpr = kp / 256;
+    const int w = threadIdx.x >> 6, lane = lane_id();
+    const int s = min(w, E.slots - 1);  // waves past the slots repeat the last one, weight 0
+    const float *x0 = E.xs + (size_t)(2 * s) * n, *x1 = x0 + n;
+    if (XM == 0) x0 = E.xs + (size_t)s * n;  // the SwiGLU output of the gate/up launch
+    XRegs<XPW> xr, xr2;
+    load_x<XPW, XM, 64>(x0, x1, n, xr, xr2, lane);
+    int e = E.idx[s];
+    const bool ok = e >= 0 && e < E.n_experts;  // a dropped slot computes expert 0 with weight 0
+    e = ok ? e : 0;
+    GemvMat M;
+    M.w = E.table + (size_t)e * E.stride + E.off[0];
+    M.rows = E.rows;
+    M.pair = 0;
+    M.mstride = 0;
+    const int base = (int)blockIdx.x * P;
+    Pass<UPL> ps;
+    load_pass<LPR, UPL, TM>(M, 0, base, bpr, ps);
+    const XLds X(smem + (size_t)w * xlds_bytes(kp), kp);
+    build_x<XPW, XM, 64>(xr, xr2, n, kp, X, lane);
+    __syncthreads();
+    const float wt = ok && w < E.slots ? E.wt[s] : 0.0f;
+    const float acc = pass_dot<LPR, UPL, TM>(bpr, ps, X);
+    if (lane % LPR == LPR - 1) red[w][lane / LPR] = wt * acc;
+    __syncthreads();
+    const int row = base + (int)threadIdx.x;
+    if (threadIdx.x < P && row < E.rows) {
+        float sum = 0.0f;
+        for (int k = 0; k < E.slots; k++) sum += red[k][threadIdx.x];
+        E.out[row] += sum;
+    }
+}
+
+template <int UPL, int XPW>
+static void launch_down_slots(const GemvArgs &a, int tm, hipStream_t stream) {
+    constexpr int LPR = 4, P = 64 / LPR;
+    const int kp = (a.n_cols + 255) & ~255;
+    const int blocks = (a.ex.rows + P - 1) / P;
+    const size_t lds = (size_t)kSlotWaves * xlds_bytes(kp);
+    const dim3 g(blocks), b(kGemvThreads);
+    if (a.ex.act) {
+        if (tm == 1) hipLaunchKernelGGL((gemv_down_slots_kernel<LPR, UPL, XPW, 0, 1>), g, b, lds, stream, a);
+        else hipLaunchKernelGGL((gemv_down_slots_kernel<LPR, UPL, XPW, 0, 2>), g, b, lds, stream, a);
+    } else {
+        if (tm == 1) hipLaunchKernelGGL((gemv_down_slots_kernel<LPR, UPL, XPW, 1, 1>), g, b, lds, stream, a);
+        else hipLaunchKernelGGL((gemv_down_slots_kernel<LPR, UPL, XPW, 1, 2>), g, b, lds, stream, a);
+    }
+}
+#endif
 
 // TM: types present in the launch -- 1 Q4_K only, 2 Q6_K only, 3 both.  With both, every
 // matrix starts at a multiple of the rows of one workgroup, so the type is uniform per
@@ -621,16 +718,38 @@ int launch_gemv_experts_impl(GemvArgs a, hipStream_t stream) {
     if (a.n_cols < 4 || a.n_cols > kMaxGemvCols) return kErrBadArg;
     const int kp = (a.n_cols + 255) & ~255;
     const int uph = kp / 128;
+#ifndef MNEMO_DOWN_SLOTS
+#define MNEMO_DOWN_SLOTS 1
+#endif
+#if MNEMO_GEMV_THREADS == 512
+    if (MNEMO_DOWN_SLOTS && a.ex.nm == 1 && a.ex.slots <= kSlotWaves && kp <= 2048 && a.ex.rows > 0) {
+        a.experts = 1;
+        a.nmat = 0;
+        a.xmode = a.ex.act ? 0 : 1;
+        a.total_rows = a.ex.rows;
+        const int tm = a.ex.type == kTypeQ4K ? 1 : 2;
+        // LPR 4: a row's uph half super-blocks over 4 lanes, UPL = uph / 4 each
+        if (uph <= 4) launch_down_slots<1, 2>(a, tm, stream);
+        else if (uph <= 8) launch_down_slots<2, 4>(a, tm, stream);
+        else if (uph <= 12) launch_down_slots<3, 6>(a, tm, stream);
+        else launch_down_slots<4, 8>(a, tm, stream);
+        return check_launch("gemv_experts down");
+    }
+#endif
     int lpr = 2;
     while (lpr < uph && lpr < 64) lpr <<= 1;
     const int P = 64 / lpr;
     constexpr int wpb = kGemvThreads / 64;
     const int rpb = wpb * P;
     GemvExperts &E = a.ex;
-    if (E.rows % rpb != 0) return set_error(kErrBadArg, "expert GEMV: rows %d not a multiple of %d", E.rows, rpb);
+    const bool pair = E.act && E.nm == 2;  // gate and up rows side by side in a pass
+    if (pair && P < 2) return set_error(kErrBadArg, "expert GEMV: paired gate/up needs n_cols <= 4096");
+    if ((pair ? 2 * E.rows : E.rows) % rpb != 0)
+        return set_error(kErrBadArg, "expert GEMV: rows %d not a multiple of %d", E.rows, pair ? rpb / 2 : rpb);
     a.experts = 1;
     a.nmat = 0;
-    a.xmode = E.nm == 1 ? 1 : (a.x2 ? 2 : 0);  // down: SwiGLU of the slot; gate/up: x, or its RMS norm
+    // down: SwiGLU of the slot (or its precomputed product); gate/up: x, or its RMS norm
+    a.xmode = E.nm == 1 ? (E.act ? 0 : 1) : (a.x2 ? 2 : 0);
     if (a.xmode == 2 && a.n_cols % 4) return set_error(kErrBadArg, "expert GEMV rms-norm input: n_cols %% 4");
     a.total_rows = E.slots * E.nm * E.rows;
     if (E.nm == 1) E.ntiles = E.rows / rpb;

@@ -116,6 +116,11 @@ __device__ __forceinline__ float sum64_lane63(float v) {
     return v;
 }
 
+// The top-k order of the router: value descending, ties to the lower index.
+__device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
+    return (v > v2) || (v == v2 && i < i2);
+}
+
 // the sum (max) of v over the wave, in every lane
 __device__ __forceinline__ float wave_sum_all(float v) {
     v = sum64_lane63(v);

@@ -16,7 +16,7 @@ constexpr int kMaxGemvCols = 16384;  // LDS image of x: 2.375 B per column
 constexpr int kMaxGemvColsPad = 16384;
 constexpr int kGemvMaxBlocks = 512;
 
-enum GemvEpilogue : int { kEpiStore = 0, kEpiResidual = 1, kEpiScaledAdd = 2, kEpiScaledStore = 3 };
+enum GemvEpilogue : int { kEpiStore = 0, kEpiResidual = 1, kEpiScaledAdd = 2, kEpiScaledStore = 3, kEpiSwiGLU = 4 };
 
 struct GemvMat {
     const void *w;     // GGUF blocks, row-major, ceil(n_cols/256) blocks per row
@@ -26,6 +26,10 @@ struct GemvMat {
     int rows;
     int type;  // 12 Q4_K | 14 Q6_K
     int mode;  // GemvEpilogue
+    // pair != 0: the rows of a pass alternate between this matrix and the one mstride bytes
+    // further (gate, up, gate, up, ...); lrow counts row pairs (kEpiSwiGLU)
+    int pair;
+    long long mstride;
 };
 
 // Expert mode (GemvArgs::experts != 0): the matrices are chosen on the device from the
@@ -35,6 +39,9 @@ struct GemvMat {
 //  nm == 1 (down of every slot, x of slot s = silu(xs[2s]) * xs[2s + 1], n_cols each):
 //          partial[s * rows + r] = wt[s] * (W x); the last workgroup to finish a row tile
 //          adds sum_s partial (slot order) into out.
+//  act != 0: gate row r and up row r sit side by side in one pass and the gate/up launch
+//          writes y[s * rows + r] = silu(gate) * up; the down launch reads x of slot s at
+//          xs[s * n_cols].
 struct GemvExperts {
     const uint8_t *table;
     size_t stride;
@@ -46,6 +53,7 @@ struct GemvExperts {
     float *out;
     int *tile_cnt;
     int slots, nm, rows, type, n_experts;
+    int act;
     int ntiles;  // nm == 2: counters to clear; nm == 1: row tiles per slot
 };
 

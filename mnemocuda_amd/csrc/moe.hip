@@ -319,6 +319,9 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     a.ex.slots = k;
     a.ex.nm = 2;
     a.ex.rows = eff;
+    // gate and up rows in one pass give silu(gate) * up directly (rows of up to 4096 values)
+    const int act = ((hidden + 255) & ~255) <= 4096;
+    a.ex.act = act;
     a.ex.type = kTypeQ4K;  // gate/up are Q4_K in Q4_K_M experts (src/forward.c:866-872)
     a.ex.n_experts = E;
     if ((rc = launch_gemv_experts(a, s))) return rc;
@@ -336,6 +339,7 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     a.ex.tile_cnt = cnt;
     a.ex.slots = k;
     a.ex.nm = 1;
+    a.ex.act = act;
     a.ex.rows = hidden;
     a.ex.type = down_type;
     a.ex.n_experts = E;

@@ -83,9 +83,6 @@ int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int 
 constexpr int kTopkMaxPerLane = 16;  // n_experts <= 1024
 constexpr int kTopkMaxK = 16;        // the reference's register budget (kernels.cu:1002)
 
-__device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
-    return (v > v2) || (v == v2 && i < i2);
-}
 
 __device__ void topk_wave(const float *scores, int n, int k, int *idx, float *wts, float *vals_out) {
     const int lane = lane_id();
@@ -275,8 +272,8 @@ int launch_router_topk(const float *w, const float *x, const float *nw, float ep
     if (nw && !vec4)
         return set_error(kErrBadArg, "router_topk: the fused RMS norm needs n_cols %% 4 == 0, <= %d and aligned vectors",
                          4 * kRowMaxV4 * kRowThreads);
-    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, nw, eps, logits, n, n_cols, k,
-                       cnt, idx, wts, vec4);
+    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, nw, eps, logits, n,
+                       n_cols, k, cnt, idx, wts, vec4);
     return check_launch("router_topk");
 }
 
