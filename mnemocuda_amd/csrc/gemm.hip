@@ -239,38 +239,45 @@ constexpr int kBM = 128, kBN = 128;
 constexpr int kPF = 6;      // raw ring slots: loads run kPF-2 steps ahead of their conversion
 constexpr int kUnroll = 6;  // lcm(kPF, 3 LDS buffers)
 
+// act: this thread's activation row is inside the tile's token count (rows past it are
+// neither loaded nor converted; their LDS rows only feed output columns that are dropped).
 template <int TYPE, bool Q8>
 __device__ __forceinline__ void load_step(const uint8_t *wrow, const void *arow, int ks, int h, RawW &rw,
-                                          RawA<Q8> &ra) {
+                                          RawA<Q8> &ra, bool act) {
     if (TYPE == kTypeQ4K) load_w_q4k(wrow, ks, h, rw);
     else load_w_q6k(wrow, ks, h, rw);
-    load_a(arow, ks, h, ra);
+    if (act) load_a(arow, ks, h, ra);
 }
 
 template <int TYPE, bool Q8>
 __device__ __forceinline__ void store_step(const RawW &rw, const RawA<Q8> &ra, int ks, int h, _Float16 *at,
-                                           _Float16 *bt, int row, float as) {
+                                           _Float16 *bt, int row, float as, bool act) {
     if (TYPE == kTypeQ4K) store_w_q4k(rw, ks, h, at, row);
     else store_w_q6k(rw, ks, h, at, row);
-    store_a(ra, h, bt, row, as);
+    if (act) store_a(ra, h, bt, row, as);
 }
 
 // Fragments of one 32-wide K half (kh) of a step for 4 x 4 MFMA 16x16x32 tiles.
+// nb (wave-uniform): token tiles of the wave that hold tokens; the others are skipped.
 __device__ __forceinline__ void read_frags(const _Float16 *as, const _Float16 *bs, int wi, int wj, int kh, int lane,
-                                           h8 (&af)[4], h8 (&bf)[4]) {
+                                           h8 (&af)[4], h8 (&bf)[4], int nb) {
     const int chunk = 4 * kh + (lane >> 4);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int ra = wi + 16 * t + (lane & 15), rb = wj + 16 * t + (lane & 15);
         af[t] = *(const h8 *)(as + tile_off(ra, chunk));
-        bf[t] = *(const h8 *)(bs + tile_off(rb, chunk));
+        if (t < nb) bf[t] = *(const h8 *)(bs + tile_off(rb, chunk));
     }
 }
-__device__ __forceinline__ void mfma_frags(const h8 (&af)[4], const h8 (&bf)[4], f4 (&acc)[4][4]) {
+__device__ __forceinline__ void mfma_frags(const h8 (&af)[4], const h8 (&bf)[4], f4 (&acc)[4][4], int nb) {
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int b = 0; b < 4; b++) {
+        if (b < nb) {
 #pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
+            for (int a = 0; a < 4; a++)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
+        }
+    }
 }
 
 // Epilogue / operand-addressing modes of the kernel:
@@ -341,6 +348,12 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     } else {
         wrow = Wm + (size_t)min(i0 + lr, g.M - 1) * wrow_bytes;
     }
+    // tokens of this tile: activation rows past them are skipped, and so are the MFMAs of a
+    // wave's 16-token tiles that hold none (the small experts of a grouped launch)
+    // (grouped launches only: a plain GEMM's tiles are full but for the last)
+    const int nvalid = min(kBN, n_rows - j0);
+    const bool act = MODE == kModePlain || lr < nvalid;
+    const int nb = MODE == kModePlain ? 4 : min(4, max(0, (nvalid - wj + 15) / 16));
     const int jr = min(j0 + lr, n_rows - 1);
     const int arow_idx = MODE == kModePlain ? jr : MODE == kModeSwiGLU ? g.perm[row_base + jr] : row_base + jr;
     __shared__ float row_unscale[kBN];
@@ -382,12 +395,12 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     RawW rw[kPF];
     RawA<Q8> ra[kPF];
 #pragma unroll
-    for (int p = 0; p < kPF; p++) load_step<TYPE, Q8>(wrow, arow, min(ks0 + p, last), lh, rw[p], ra[p]);
-    store_step<TYPE, Q8>(rw[0], ra[0], ks0, lh, lds[0][0], lds[0][1], lr, a_scale);
-    store_step<TYPE, Q8>(rw[1], ra[1], ks0 + 1, lh, lds[1][0], lds[1][1], lr, a_scale);
+    for (int p = 0; p < kPF; p++) load_step<TYPE, Q8>(wrow, arow, min(ks0 + p, last), lh, rw[p], ra[p], act);
+    store_step<TYPE, Q8>(rw[0], ra[0], ks0, lh, lds[0][0], lds[0][1], lr, a_scale, act);
+    store_step<TYPE, Q8>(rw[1], ra[1], ks0 + 1, lh, lds[1][0], lds[1][1], lr, a_scale, act);
     __syncthreads();
     h8 af[4], bf[4];
-    read_frags(lds[0][0], lds[0][1], wi, wj, kh, lane, af, bf);
+    read_frags(lds[0][0], lds[0][1], wi, wj, kh, lane, af, bf, nb);
 
     for (int kb = ks0; kb < ks1; kb += kUnroll) {
 #pragma unroll
@@ -396,12 +409,12 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
             if (ks < ks1) {  // uniform
                 // kb - ks0 is a multiple of kUnroll, so these are compile-time constants
                 const int r = p % kPF, b = p % 3;
-                load_step<TYPE, Q8>(wrow, arow, min(ks + kPF, last), lh, rw[r], ra[r]);
-                mfma_frags(af, bf, acc);
+                load_step<TYPE, Q8>(wrow, arow, min(ks + kPF, last), lh, rw[r], ra[r], act);
+                mfma_frags(af, bf, acc, nb);
                 // (past the end these read and fill idle buffers with data nobody uses)
-                read_frags(lds[(b + 1) % 3][0], lds[(b + 1) % 3][1], wi, wj, kh, lane, af, bf);
+                read_frags(lds[(b + 1) % 3][0], lds[(b + 1) % 3][1], wi, wj, kh, lane, af, bf, nb);
                 store_step<TYPE, Q8>(rw[(r + 2) % kPF], ra[(r + 2) % kPF], ks + 2, lh, lds[(b + 2) % 3][0],
-                                     lds[(b + 2) % 3][1], lr, a_scale);
+                                     lds[(b + 2) % 3][1], lr, a_scale, act);
                 __syncthreads();
             }
         }
