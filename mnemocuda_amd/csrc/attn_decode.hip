@@ -371,69 +371,72 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
         for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * n + r] = o[n][i];
 }
 
-// Merge of the chunks' (max, sum, O): grid (query head, quarter of head_dim).  Every
-// workgroup computes the chunk weights exp(m_c - M) in parallel into LDS; then thread
-// (dim d of 32, group g of 8) sums the chunks c = g mod 8 (four loads in flight), and the
-// 8 groups are added through LDS in a fixed order.
+// Merge of the chunks' (max, sum, O): grid (query head, quarter of head_dim), 256 threads =
+// 32 dims x 8 chunk groups.  Thread (d, g) takes chunks g, g + 8, ... in batches of 8 per
+// thread (64 chunks = 4096 positions per batch), every load of a batch issued before any
+// arithmetic: one round trip to the partials instead of three dependent ones.  Per batch:
+// the max over its chunks, then sum l and O with weights exp(m_c - M) (rescaled when a later
+// batch raises M); the 8 groups meet in LDS in a fixed order.
 constexpr int kCombThreads = 256;
 constexpr int kCombDims = kHd / 4;                    // dims per workgroup
 constexpr int kCombGroups = kCombThreads / kCombDims;  // 8
+constexpr int kCombPer = 8;                           // chunks per thread and batch
 constexpr int kMaxChunks = 1024;                      // max_ctx <= 65536
 
 __global__ void __launch_bounds__(kCombThreads) attn_combine_kernel(AttnDecodeArgs a) {
-    __shared__ float wc[kMaxChunks];
-    __shared__ float red[kCombThreads / 64];
+    __shared__ float red_m[kCombGroups], red_l[kCombGroups];
     __shared__ float part_o[kCombThreads];
     const int h = blockIdx.x, tid = threadIdx.x;
     const int kvh = h / a.gqa, hh = h % a.gqa;
     const int seq = min(*a.pos_dev + 1, a.max_ctx);
     const int nc = (seq + kChunk - 1) / kChunk;
     const float *base = a.ws + (size_t)kvh * a.max_chunks * kPart;
-    float mx = -INFINITY;
-    for (int c = tid; c < nc; c += kCombThreads) {
-        const float m = base[(size_t)c * kPart + hh];
-        wc[c] = m;
-        mx = fmaxf(mx, m);
-    }
+    const int dl = tid % kCombDims, g = tid / kCombDims;
+    const int d = (int)blockIdx.y * kCombDims + dl;
+    float M = -INFINITY, L = 0.0f, O = 0.0f;  // this thread's running state
+    for (int c0 = 0; c0 < nc; c0 += kCombGroups * kCombPer) {
+        float m[kCombPer], l[kCombPer], o[kCombPer];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
+        for (int i = 0; i < kCombPer; i++) {
+            const int c = min(c0 + g + kCombGroups * i, nc - 1);  // clamped: loaded, then masked
+            const float *pc = base + (size_t)c * kPart;
+            m[i] = pc[hh];
+            l[i] = pc[kRows + hh];
+            o[i] = pc[2 * kRows + hh * kHd + d];
+        }
+        float bm = M;
+#pragma unroll
+        for (int i = 0; i < kCombPer; i++)
+            if (c0 + g + kCombGroups * i < nc) bm = fmaxf(bm, m[i]);
+        const float r = M == bm ? 1.0f : expf(M - bm);  // 0 when M was -inf
+        L *= r;
+        O *= r;
+#pragma unroll
+        for (int i = 0; i < kCombPer; i++) {
+            const float w = c0 + g + kCombGroups * i < nc ? expf(m[i] - bm) : 0.0f;
+            L = fmaf(l[i], w, L);
+            O = fmaf(o[i], w, O);
+        }
+        M = bm;
+    }
+    // groups of the same dims: common max, then the sums in group order
+    if (dl == 0) red_m[g] = M;
     __syncthreads();
-    float M = red[0];
+    float gm = red_m[0];
 #pragma unroll
-    for (int i = 1; i < kCombThreads / 64; i++) M = fmaxf(M, red[i]);
-    __syncthreads();  // red[] is reused below
-    float ls = 0.0f;
-    for (int c = tid; c < nc; c += kCombThreads) {
-        const float w = expf(wc[c] - M);
-        wc[c] = w;
-        ls = fmaf(base[(size_t)c * kPart + kRows + hh], w, ls);
-    }
-    ls = sum64_lane63(ls);
-    if ((tid & 63) == 63) red[tid >> 6] = ls;
-    __syncthreads();
-    float L = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kCombThreads / 64; i++) L += red[i];
-    const int d = (int)blockIdx.y * kCombDims + tid % kCombDims, g = tid / kCombDims;
-    const float *ob = base + 2 * kRows + hh * kHd + d;
-    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
-    constexpr int G8 = kCombGroups;
-    int c = g;
-    for (; c + 3 * G8 < nc; c += 4 * G8) {
-        o0 = fmaf(ob[(size_t)c * kPart], wc[c], o0);
-        o1 = fmaf(ob[(size_t)(c + G8) * kPart], wc[c + G8], o1);
-        o2 = fmaf(ob[(size_t)(c + 2 * G8) * kPart], wc[c + 2 * G8], o2);
-        o3 = fmaf(ob[(size_t)(c + 3 * G8) * kPart], wc[c + 3 * G8], o3);
-    }
-    for (; c < nc; c += G8) o0 = fmaf(ob[(size_t)c * kPart], wc[c], o0);
-    part_o[tid] = (o0 + o1) + (o2 + o3);
+    for (int i = 1; i < kCombGroups; i++) gm = fmaxf(gm, red_m[i]);
+    const float r = M > -INFINITY ? expf(M - gm) : 0.0f;  // a group without chunks adds nothing
+    if (dl == 0) red_l[g] = L * r;
+    part_o[tid] = O * r;
     __syncthreads();
     if (tid < kCombDims) {
-        float o = 0.0f;
+        float Ls = 0.0f, o = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kCombGroups; j++) o += part_o[tid + j * kCombDims];
-        a.out[(size_t)h * kHd + d] = o / L;
+        for (int j = 0; j < kCombGroups; j++) {
+            Ls += red_l[j];
+            o += part_o[tid + j * kCombDims];
+        }
+        a.out[(size_t)h * kHd + d] = o / Ls;
     }
 }
 
