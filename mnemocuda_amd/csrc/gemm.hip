@@ -19,10 +19,11 @@
 //     the exponent byte 0x64 is the f16 1024 + q; subtracting 1024 (or 1056 for Q6_K's
 //     q - 32) is exact; then one fma with (f16(d*sc), f16(-dmin*m)) (Q4_K) or one multiply
 //     by f16(d*sc) (Q6_K).  Expected relative L2 error vs the fp64 product: ~4e-4.
-//   * Workgroup tile 128 weight rows x 128 tokens (4 waves of 64 x 64 = 4 x 4 MFMA tiles),
+//   * Workgroup tile 128 weight rows x 128 tokens (8 waves: quadrants of 64 x 64 = 4 x 4 MFMA
+//     tiles, each quadrant split over two waves by K half),
 //     K step 64 (one Q4_K nibble group, one Q6_K ql group).  Raw weight blocks and
-//     activation chunks are prefetched three steps ahead into registers; f16 tiles are
-//     double-buffered in LDS (XOR-swizzled, conflict-free); one barrier per step.
+//     activation chunks are loaded into registers ahead of their conversion; f16 tiles
+//     rotate through three LDS buffers (XOR-swizzled, conflict-free); one barrier per step.
 //   * When the tile grid covers less than half of the CUs, K is split across workgroups
 //     and the partial tiles are summed with fp32 atomics into the output, which a small
 //     fill kernel zeroes first.
@@ -160,7 +161,7 @@ __device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int q, _Float
     const int j = 2 * (ks & 3) + (q >> 1);
     const uint32_t s0 = r.a.y, s1 = r.a.z, s2 = r.a.w;
     uint32_t sc, m;
-    if (j < 4) {
+    if ((ks & 3) < 2) {  // j < 4, written in terms of the step alone: uniform over the wave
         sc = sbyte(s0, s1, s2, j) & 63;
         m = sbyte(s0, s1, s2, j + 4) & 63;
     } else {
@@ -229,15 +230,20 @@ __device__ __forceinline__ void store_a(const RawA<true> &r, int q, _Float16 *ti
 // (blockIdx.z of `splits`).  Wave w owns rows 64*(w%2) .. +63 and tokens 64*((w/2)%2) .. +63
 // (4 x 4 MFMA tiles) and K half w/4 of every 64-wide step; the two K halves are summed
 // through LDS at the end (fixed order).  Two waves per SIMD let one wave's conversion
-// overlap the other's MFMAs.  Raw blocks are prefetched kPF-1 steps ahead into a ring of
-// registers (the loop is unrolled by kPF so every ring index is static and the waits the
+// overlap the other's MFMAs.  Raw blocks are loaded into a ring of kPF register slots (the
+// loop is unrolled by lcm(kPF, 3) so every ring index is static and the waits the
 // compiler inserts count exactly the outstanding steps).  With splits > 1 the partial
 // tiles are added into the (pre-zeroed) output with fp32 atomics, in an order that may
 // differ from run to run.
 constexpr int kThreads = 512;
 constexpr int kBM = 128, kBN = 128;
-constexpr int kPF = 6;      // raw ring slots: loads run kPF-2 steps ahead of their conversion
-constexpr int kUnroll = 6;  // lcm(kPF, 3 LDS buffers)
+// raw ring slots: loads run kPF-2 steps ahead of their conversion.  3 (one step of
+// lookahead, the rest hidden by the three LDS buffers) measured faster than 4-6: the deeper
+// rings cost registers (Q6_K: 246-256 VGPRs with spills at 5-6 against 202 at 3) for
+// latency the other wave of the SIMD already hides (Q6_K 4096x1536x512: 34.1 -> 32.2 us,
+// Q4_K 8192x4096x512: 65.5 -> 63.3 us, grouped MoE prefill -4 %)
+constexpr int kPF = 3;
+constexpr int kUnroll = 3;  // lcm(kPF, 3 LDS buffers)
 
 // act: this thread's activation row is inside the tile's token count (rows past it are
 // neither loaded nor converted; their LDS rows only feed output columns that are dropped).
@@ -308,7 +314,8 @@ template <int TYPE, int MODE, bool ATOMIC, bool Q8>
 __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     __shared__ __align__(16) _Float16 lds[3][2][kBM * kKS];  // [buffer][weights | tokens]
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    // the wave index as a scalar, so that every per-wave decision below is a scalar branch
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = g.K;
     const int wi = (wave & 1) * 64, wj = ((wave >> 1) & 1) * 64, kh = wave >> 2;
     const size_t wrow_bytes = (size_t)(K / 256) * (TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
