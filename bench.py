@@ -227,6 +227,7 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos):
     pos = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws = torch.zeros(ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
     aws = torch.empty(ops.attention_decode_workspace_bytes(NKV, max_ctx), dtype=torch.uint8, device="cuda")
+    sws = torch.empty(ops.sample_workspace_bytes(), dtype=torch.uint8, device="cuda")
     scale = 1.0 / HD ** 0.5
 
     def token():
@@ -244,7 +245,7 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos):
                                    EFF, E, k, ws, dst)
         ops.rms_norm(bufs[len(layers) % 2], final_norm, normed, EPS)
         ops.matvec_q6k(lm_head, normed, logits, VOCAB, H)
-        ops.sample_token(logits, VOCAB, 0.7, 0.9, 12345, tok)
+        ops.sample_token_ws(logits, VOCAB, 0.7, 0.9, 12345, sws, tok)
         pos.add_(1)
 
     with torch.cuda.stream(stream):
@@ -277,7 +278,7 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos):
             "context_position": ctx_pos, "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
             "frac_hbm_peak": round(per_tok / ms / 1e6 / HBM_PEAK_GBS, 4),
             "experts_resident_GB": round(E * LAYERS * stride / 1e9, 1),
-            "launches_per_token": LAYERS * 7 + 4}
+            "launches_per_token": LAYERS * 7 + 5}
 
 
 def attention_bench(stream, lengths=(1024, 4096, 16384, 32768)):

@@ -144,6 +144,16 @@ void mnemo_gemm_q6k(const void *weights, const void *act_q8, float *output, int 
  * drawn with xoroshiro128+ seeded from rng_state.  Writes one int to d_result. */
 void cuda_sample_token(const float *logits, int vocab_size, float temperature, float top_p,
                        unsigned long long rng_state, int *d_result, hipStream_t stream);
+/* New: the same selection with the vocabulary scan spread over 64 workgroups (two
+ * launches, capture-safe): the class winners and partial sums go through a workspace of
+ * mnemo_sample_workspace_bytes() bytes (16-byte aligned, no initialisation; calls sharing it
+ * must not overlap).  vocab_size <= 262,144.  Same token as cuda_sample_token except when
+ * the draw lies within fp32 rounding of a nucleus boundary (the total is summed in another
+ * order).  Returns 0 or an MNEMO_ERR_* code. */
+size_t mnemo_sample_workspace_bytes(void);
+int mnemo_sample_token_ws(const float *logits, int vocab_size, float temperature, float top_p,
+                          unsigned long long rng_state, void *workspace, size_t workspace_bytes,
+                          int *d_result, hipStream_t stream);
 
 /* ---- Grouped-expert prefill (no reference counterpart) ---------------------------------
  * The reference prefills MoE layers token by token through the decode chain

@@ -42,6 +42,9 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
 size_t moe_prefill_workspace_bytes(int T, int hidden, int eff, int E, int k);
 int launch_sample_token(const float *logits, int V, float temperature, float top_p, unsigned long long seed,
                         int *out, hipStream_t stream);
+int launch_sample_token_ws(const float *logits, int V, float temperature, float top_p, unsigned long long seed,
+                           void *ws, size_t ws_bytes, int *out, hipStream_t stream);
+size_t sample_workspace_bytes();
 size_t moe_decode_workspace_bytes(int hidden, int eff, int E, int k);
 int launch_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
                       size_t up_off, size_t down_off, int down_type, const float *x, const float *norm_w, float eps,
@@ -238,6 +241,15 @@ void mnemo_gemm_q6k(const void *w, const void *act, float *out, int M, int K, in
 void cuda_sample_token(const float *logits, int vocab_size, float temperature, float top_p,
                        unsigned long long rng_state, int *d_result, hipStream_t s) {
     launch_sample_token(logits, vocab_size, temperature, top_p, rng_state, d_result, s);
+}
+
+size_t mnemo_sample_workspace_bytes(void) { return sample_workspace_bytes(); }
+
+int mnemo_sample_token_ws(const float *logits, int vocab_size, float temperature, float top_p,
+                          unsigned long long rng_state, void *workspace, size_t workspace_bytes, int *d_result,
+                          hipStream_t s) {
+    return launch_sample_token_ws(logits, vocab_size, temperature, top_p, rng_state, workspace, workspace_bytes,
+                                  d_result, s);
 }
 
 // ---------------------------------------------------------------- attention chain

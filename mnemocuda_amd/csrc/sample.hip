@@ -37,6 +37,73 @@ __device__ __forceinline__ bool before(float pa, int ia, float pb, int ib) {
     return pa > pb || (pa == pb && ia < ib);
 }
 
+// Top-p draw from the 2048 candidates (cp[] = p, ci[] = token id; p < 0 marks an empty slot)
+// with total = the sum of all p: bitonic sort by (p desc, id asc), running sums, nucleus,
+// draw.  All kSampleThreads threads call this; cs (2048 floats) and red (2 ints) are LDS
+// scratch.
+__device__ void select_candidates(float *cp, int *ci, float *cs, int *red_i, float total, float top_p,
+                                  unsigned long long seed, int *__restrict__ out) {
+    const int tid = threadIdx.x;
+    __syncthreads();
+    // bitonic sort of the candidates by (p desc, id asc)
+    for (int k = 2; k <= kCands; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int t = tid; t < kCands / 2; t += kSampleThreads) {
+                const int a = ((t & ~(j - 1)) << 1) | (t & (j - 1)), b = a + j;  // j is a power of two
+                const bool up = (a & k) == 0;
+                const float pa = cp[a], pb = cp[b];
+                const int ia = ci[a], ib = ci[b];
+                if (before(pa, ia, pb, ib) != up) {
+                    cp[a] = pb;
+                    cp[b] = pa;
+                    ci[a] = ib;
+                    ci[b] = ia;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // inclusive running sums of the positive p (Hillis-Steele, two elements per thread)
+    for (int t = tid; t < kCands; t += kSampleThreads) cs[t] = fmaxf(cp[t], 0.0f);
+    __syncthreads();
+    for (int off = 1; off < kCands; off <<= 1) {
+        float v[2];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int t = tid + q * kSampleThreads;
+            v[q] = cs[t] + (t >= off ? cs[t - off] : 0.0f);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 2; q++) cs[tid + q * kSampleThreads] = v[q];
+        __syncthreads();
+    }
+    // nucleus size n: 1 + the first position whose running sum reaches top_p * total, or
+    // the number of positive candidates
+    uint64_t s0 = seed, s1 = seed ^ 0xDEADBEEFCAFEBABEull;
+    for (int w = 0; w < 3; w++) xoro_next(s0, s1);
+    const float r = (float)(xoro_next(s0, s1) >> 11) * (1.0f / 9007199254740992.0f);
+    const float mass = top_p * total;
+    if (tid == 0) {
+        red_i[0] = kCands;
+        red_i[1] = 0x7FFFFFFF;
+    }
+    __syncthreads();
+    for (int t = tid; t < kCands; t += kSampleThreads)
+        if (cp[t] <= 0.0f || cs[t] >= mass) atomicMin(&red_i[0], cp[t] <= 0.0f ? t : t + 1);
+    __syncthreads();
+    const int n = red_i[0];
+    const float target = r * (n > 0 ? cs[n - 1] : 0.0f);
+    for (int t = tid; t < n; t += kSampleThreads)
+        if (cs[t] >= target) atomicMin(&red_i[1], t);
+    __syncthreads();
+    if (tid == 0) {
+        const int pick = red_i[1] == 0x7FFFFFFF ? 0 : red_i[1];
+        const int id = ci[pick];
+        *out = (id < 0 || id == 0x7FFFFFFF) ? 0 : id;
+    }
+}
+
 __global__ void __launch_bounds__(kSampleThreads) sample_token_kernel(const float *__restrict__ logits, int V,
                                                                       float temperature, float top_p,
                                                                       unsigned long long seed, int *__restrict__ out) {
@@ -162,64 +229,194 @@ __global__ void __launch_bounds__(kSampleThreads) sample_token_kernel(const floa
     }
     const float total = red_f[0];
 
-    // bitonic sort of the candidates by (p desc, id asc)
-    for (int k = 2; k <= kCands; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = tid; t < kCands / 2; t += kSampleThreads) {
-                const int a = ((t & ~(j - 1)) << 1) | (t & (j - 1)), b = a + j;  // j is a power of two
-                const bool up = (a & k) == 0;
-                const float pa = cp[a], pb = cp[b];
-                const int ia = ci[a], ib = ci[b];
-                if (before(pa, ia, pb, ib) != up) {
-                    cp[a] = pb;
-                    cp[b] = pa;
-                    ci[a] = ib;
-                    ci[b] = ia;
+    select_candidates(cp, ci, mp, red_i, total, top_p, seed, out);
+}
+
+// ------------------------------------------------------------------ workspace form
+// The same selection over two launches that spread the scan of the vocabulary:
+//  1. sample_classes_kernel, 64 workgroups: workgroup w takes the residue classes 4w .. 4w+3
+//     (i mod 256) over the whole vocabulary, each class on 64 threads; it writes its 32
+//     class winners -- the 8 largest logits of each class, equal logits by the lower index
+//     (the order of p = exp((z - max) / T), which is increasing in z) -- with their ids, its
+//     largest logit m_w and S_w = sum exp((z - m_w) / T) over its classes;
+//  2. sample_finish_kernel, one workgroup: M = max m_w, total = sum_w S_w exp((m_w - M) / T),
+//     p of the 2048 winners from their logits as the one-launch form computes them, then the
+//     same sort, nucleus and draw (temperature <= 0: the first winner in (z desc, id asc)
+//     order, the argmax).
+// Differences to the one-launch form: the total is summed per class group first (fp32 sums
+// in another order); a class's 8th and 9th largest p can only be exchanged when their
+// logits differ but round to the same p.
+constexpr int kClsGroups = 64;                 // workgroups of the first launch
+constexpr int kClsPerGroup = kClasses / kClsGroups;  // 4
+constexpr int kClsThreads = 256;               // 64 threads per class
+constexpr int kClsPerThread = 16;              // logits per thread: vocab <= 16 * 64 * 256 = 262144
+struct SampleWs {
+    float m[kClsGroups], s[kClsGroups];
+    float z[kCands];
+    int id[kCands];
+};
+
+size_t sample_workspace_bytes() { return sizeof(SampleWs); }
+
+__global__ void __launch_bounds__(kClsThreads) sample_classes_kernel(const float *__restrict__ logits, int V,
+                                                                     float temperature, SampleWs *__restrict__ ws) {
+    __shared__ float lz[kClsThreads * kPerClass];
+    __shared__ int li[kClsThreads * kPerClass];
+    __shared__ float red[kClsThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int cl = tid & (kClsPerGroup - 1);                   // class within the group
+    const int c = (int)blockIdx.x * kClsPerGroup + cl, j0 = tid / kClsPerGroup;  // 64 threads per class
+    float z[kClsPerThread];
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kClsPerThread; u++) {
+        const int i = c + kClasses * (j0 + 64 * u);
+        z[u] = i < V ? logits[i] : -INFINITY;
+        m = fmaxf(m, z[u]);
+    }
+    // the group's largest logit
+    m = wave_max_all(m);
+    if (lane == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // this thread's 8 largest (z desc, index asc: its indices increase with u) and its sum
+    float hv[kPerClass];
+    int hi[kPerClass];
+#pragma unroll
+    for (int k = 0; k < kPerClass; k++) {
+        hv[k] = -INFINITY;
+        hi[k] = 0x7FFFFFFF;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kClsPerThread; u++) {
+        const int i = c + kClasses * (j0 + 64 * u);
+        if (i < V) {
+            sum += expf((z[u] - m) / temperature);
+            // insert (z[u], i) keeping hv sorted descending; a later equal z goes after
+            float v = z[u];
+            int id = i;
+#pragma unroll
+            for (int k = 0; k < kPerClass; k++) {
+                const bool take = v > hv[k];
+                const float tv = hv[k];
+                const int ti = hi[k];
+                hv[k] = take ? v : hv[k];
+                hi[k] = take ? id : hi[k];
+                v = take ? tv : v;
+                id = take ? ti : id;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kPerClass; k++) {
+        lz[tid * kPerClass + k] = hv[k];
+        li[tid * kPerClass + k] = hi[k];
+    }
+    sum = sum64_lane63(sum);
+    __syncthreads();
+    if (lane == 63) red[tid >> 6] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        ws->m[blockIdx.x] = m;
+        ws->s[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+    }
+    // wave w merges class w's 64 lists (512 entries, 8 per lane) by 8 rounds of wave argmax
+    const int w = tid >> 6;
+    const int cw = (int)blockIdx.x * kClsPerGroup + w;
+    float bz[kPerClass];
+    int bi[kPerClass];
+#pragma unroll
+    for (int k = 0; k < kPerClass; k++) {
+        const int t = kClsPerGroup * lane + w;  // thread of class w in slot `lane`
+        bz[k] = lz[t * kPerClass + k];
+        bi[k] = li[t * kPerClass + k];
+    }
+    int head = 0;  // the lane's list is sorted: its best remaining entry is bz[head]
+    for (int r = 0; r < kPerClass; r++) {
+        float v = -INFINITY;
+        int id = 0x7FFFFFFF;
+#pragma unroll
+        for (int k = 0; k < kPerClass; k++)
+            if (k == head) {
+                v = bz[k];
+                id = bi[k];
+            }
+        float bv = v;
+        int bid = id;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bid, o);
+            if (ov > bv || (ov == bv && oi < bid)) {
+                bv = ov;
+                bid = oi;
+            }
+        }
+        if (id == bid && v == bv && bid != 0x7FFFFFFF) head++;  // the owner drops its head
+        if (lane == 0) {
+            ws->z[cw * kPerClass + r] = bv;
+            ws->id[cw * kPerClass + r] = bid;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kSampleThreads) sample_finish_kernel(const SampleWs *__restrict__ ws,
+                                                                       float temperature, float top_p,
+                                                                       unsigned long long seed, int *__restrict__ out) {
+    __shared__ float cp[kCands];
+    __shared__ int ci[kCands];
+    __shared__ float cs[kCands];
+    __shared__ int red_i[2];
+    __shared__ float tot;
+    const int tid = threadIdx.x;
+    float M = -INFINITY;
+    for (int g = 0; g < kClsGroups; g++) M = fmaxf(M, ws->m[g]);
+    if (temperature <= 0.0f) {  // argmax: the best class winner (ties to the lower id)
+        if (tid == 0) {
+            float bv = -INFINITY;
+            int bi = 0x7FFFFFFF;
+            for (int t = 0; t < kCands; t += kPerClass) {  // the first winner of each class
+                const float v = ws->z[t];
+                const int i = ws->id[t];
+                if (v > bv || (v == bv && i < bi)) {
+                    bv = v;
+                    bi = i;
                 }
             }
-            __syncthreads();
+            *out = bi == 0x7FFFFFFF ? 0 : bi;
         }
+        return;
     }
-    // inclusive running sums of the positive p (Hillis-Steele, two elements per thread)
-    float *cs = mp;
-    for (int t = tid; t < kCands; t += kSampleThreads) cs[t] = fmaxf(cp[t], 0.0f);
-    __syncthreads();
-    for (int off = 1; off < kCands; off <<= 1) {
-        float v[2];
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int t = tid + q * kSampleThreads;
-            v[q] = cs[t] + (t >= off ? cs[t - off] : 0.0f);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < 2; q++) cs[tid + q * kSampleThreads] = v[q];
-        __syncthreads();
-    }
-    // nucleus size n: 1 + the first position whose running sum reaches top_p * total, or
-    // the number of positive candidates
-    uint64_t s0 = seed, s1 = seed ^ 0xDEADBEEFCAFEBABEull;
-    for (int w = 0; w < 3; w++) xoro_next(s0, s1);
-    const float r = (float)(xoro_next(s0, s1) >> 11) * (1.0f / 9007199254740992.0f);
-    const float mass = top_p * total;
     if (tid == 0) {
-        red_i[0] = kCands;
-        red_i[1] = 0x7FFFFFFF;
+        float t = 0.0f;
+        for (int g = 0; g < kClsGroups; g++)
+            if (ws->m[g] > -INFINITY) t += ws->s[g] * expf((ws->m[g] - M) / temperature);
+        tot = t;
+    }
+    for (int t = tid; t < kCands; t += kSampleThreads) {
+        const int id = ws->id[t];
+        cp[t] = id == 0x7FFFFFFF ? -1.0f : expf((ws->z[t] - M) / temperature);
+        ci[t] = id;
     }
     __syncthreads();
-    for (int t = tid; t < kCands; t += kSampleThreads)
-        if (cp[t] <= 0.0f || cs[t] >= mass) atomicMin(&red_i[0], cp[t] <= 0.0f ? t : t + 1);
-    __syncthreads();
-    const int n = red_i[0];
-    const float target = r * (n > 0 ? cs[n - 1] : 0.0f);
-    for (int t = tid; t < n; t += kSampleThreads)
-        if (cs[t] >= target) atomicMin(&red_i[1], t);
-    __syncthreads();
-    if (tid == 0) {
-        const int pick = red_i[1] == 0x7FFFFFFF ? 0 : red_i[1];
-        const int id = ci[pick];
-        *out = (id < 0 || id == 0x7FFFFFFF) ? 0 : id;
-    }
+    select_candidates(cp, ci, cs, red_i, tot, top_p, seed, out);
+}
+
+int launch_sample_token_ws(const float *logits, int V, float temperature, float top_p, unsigned long long seed,
+                           void *ws, size_t ws_bytes, int *out, hipStream_t stream) {
+    if (!logits || !out || !ws || V <= 0) return set_error(kErrBadArg, "sample_token_ws: bad arguments");
+    if (V > kClasses * 64 * kClsPerThread)
+        return set_error(kErrBadArg, "sample_token_ws: vocabulary above %d", kClasses * 64 * kClsPerThread);
+    if (ws_bytes < sizeof(SampleWs) || ((uintptr_t)ws & 15))
+        return set_error(kErrBadArg, "sample_token_ws: workspace of %zu bytes (need %zu, 16-byte aligned)", ws_bytes,
+                         sizeof(SampleWs));
+    SampleWs *w = (SampleWs *)ws;
+    hipLaunchKernelGGL(sample_classes_kernel, dim3(kClsGroups), dim3(kClsThreads), 0, stream, logits, V,
+                       temperature > 0.0f ? temperature : 1.0f, w);
+    hipLaunchKernelGGL(sample_finish_kernel, dim3(1), dim3(kSampleThreads), 0, stream, w, temperature, top_p, seed,
+                       out);
+    return check_launch("sample_token_ws");
 }
 
 int launch_sample_token(const float *logits, int V, float temperature, float top_p, unsigned long long seed,

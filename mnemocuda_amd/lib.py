@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
     "cuda_gemm_q4k": (None, [vp, vp, fp, i32, i32, i32, stream_t]),
     "mnemo_gemm_q6k": (None, [vp, vp, fp, i32, i32, i32, stream_t]),
     "cuda_sample_token": (None, [fp, i32, f32, f32, C.c_ulonglong, ip, stream_t]),
+    "mnemo_sample_workspace_bytes": (sz, []),
+    "mnemo_sample_token_ws": (i32, [fp, i32, f32, f32, C.c_ulonglong, vp, sz, ip, stream_t]),
     "mnemo_moe_prefill_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
     "mnemo_moe_prefill": (i32, [vp, sz, sz, sz, sz, i32, fp, ip, fp, i32, i32, i32, i32, i32, vp, sz, fp,
                                 stream_t]),

@@ -290,6 +290,23 @@ def sample_token(logits, vocab, temperature, top_p, seed, out):
     check(lib, "cuda_sample_token")
 
 
+def sample_workspace_bytes() -> int:
+    return int(load_library().mnemo_sample_workspace_bytes())
+
+
+def sample_token_ws(logits, vocab, temperature, top_p, seed, workspace, out):
+    """sample_token with the vocabulary scan over 64 workgroups (workspace of
+    sample_workspace_bytes() bytes)."""
+    lib = load_library()
+    if logits.numel() < vocab or out.numel() < 1:
+        raise MnemoError("sample_token_ws: logits or out too small")
+    rc = lib.mnemo_sample_token_ws(_dev(logits, "logits", torch.float32), vocab, float(temperature), float(top_p),
+                                   int(seed) & 0xFFFFFFFFFFFFFFFF, _dev(workspace, "workspace"),
+                                   workspace.numel() * workspace.element_size(), _dev(out, "out", torch.int32),
+                                   _stream())
+    _check_rc(lib, rc, "mnemo_sample_token_ws")
+
+
 # ---------------------------------------------------------------- attention chain
 F32 = torch.float32
 

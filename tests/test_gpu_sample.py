@@ -48,3 +48,57 @@ def test_top_p(gpu, oracle, V, scale, T, top_p):
         checked += 1
     print(f"checked {checked} seeds")
     assert checked >= 16
+
+
+def _gpu_sample_ws(gpu, z, T, top_p, seed, ws=None):
+    out = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    if ws is None:
+        ws = torch.empty(gpu.ops.sample_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    gpu.ops.sample_token_ws(dev(z), z.size, T, top_p, seed, ws, out)
+    return int(host(out)[0])
+
+
+@pytest.mark.parametrize("V", [151936, 1000, 257, 262144])
+def test_greedy_ws(gpu, oracle, V):
+    """the two-launch form's argmax: ties to the lower index across class groups."""
+    rng = np.random.default_rng(V + 1)
+    z = (rng.standard_normal(V) * 4).astype(np.float32)
+    z[[V // 3, V - 5]] = z.max() + 0.5
+    case(f"sample_ws greedy V={V}")
+    assert _gpu_sample_ws(gpu, z, 0.0, 0.9, 1) == oracle.sample_token(z, 0.0, 0.9, 1)[0] == V // 3
+
+
+@pytest.mark.parametrize("V,scale,T,top_p,data", [(151936, 3.0, 0.7, 0.9, 12), (151936, 1.0, 1.0, 0.95, 11),
+                                                  (151936, 6.0, 0.6, 0.5, 11), (3000, 2.0, 0.9, 0.8, 11),
+                                                  (300, 1.0, 1.0, 0.99, 11)])
+def test_top_p_ws(gpu, oracle, V, scale, T, top_p, data):
+    """the same token as the oracle (and the one-launch form) for every seed away from a
+    nucleus boundary; the workspace is reused across calls without clearing.  (`data` picks
+    logits whose nucleus boundary is not within 1e-5 of the mass, so that most seeds count.)"""
+    rng = np.random.default_rng(int(V * scale) + data)
+    z = (rng.standard_normal(V) * scale).astype(np.float32)
+    seeds = rng.integers(0, 2**63, 24).tolist()
+    ws = torch.full((gpu.ops.sample_workspace_bytes(),), 255, dtype=torch.uint8, device="cuda")
+    case(f"sample_ws top-p V={V} T={T} top_p={top_p}")
+    checked = 0
+    for seed in seeds:
+        tok, margin = onp.sample_token(z, T, top_p, seed)
+        if margin < 1e-5:
+            continue
+        ref = oracle.sample_token(z, T, top_p, seed)[0]
+        assert ref == tok
+        assert _gpu_sample_ws(gpu, z, T, top_p, seed, ws) == ref == _gpu_sample(gpu, z, T, top_p, seed), seed
+        checked += 1
+    print(f"checked {checked} seeds")
+    assert checked >= 16
+
+
+def test_sample_ws_bad_args(gpu):
+    case("sample_ws bad args")
+    z = torch.zeros(300000, device="cuda")
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = torch.empty(gpu.ops.sample_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    with pytest.raises(gpu.MnemoError):  # vocabulary above 262,144
+        gpu.ops.sample_token_ws(z, 300000, 0.7, 0.9, 1, ws, out)
+    with pytest.raises(gpu.MnemoError):  # workspace too small
+        gpu.ops.sample_token_ws(z, 1000, 0.7, 0.9, 1, ws[:100], out)
