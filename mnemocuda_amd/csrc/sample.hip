@@ -369,30 +369,52 @@ __global__ void __launch_bounds__(kSampleThreads) sample_finish_kernel(const Sam
     __shared__ float cs[kCands];
     __shared__ int red_i[2];
     __shared__ float tot;
+    __shared__ float Ms;
     const int tid = threadIdx.x;
-    float M = -INFINITY;
-    for (int g = 0; g < kClsGroups; g++) M = fmaxf(M, ws->m[g]);
-    if (temperature <= 0.0f) {  // argmax: the best class winner (ties to the lower id)
+    if (tid < 64) {
+        // one group per lane: the common max and the rescaled total as wave reductions
+        // (one round trip to the workspace, a fixed summation order)
+        static_assert(kClsGroups == 64, "one class group per lane");
+        const float mg = ws->m[tid], sg = ws->s[tid];
+        const float M = wave_max_all(mg);
+        const float t = wave_sum_all(mg > -INFINITY ? sg * expf((mg - M) / temperature) : 0.0f);
         if (tid == 0) {
-            float bv = -INFINITY;
-            int bi = 0x7FFFFFFF;
-            for (int t = 0; t < kCands; t += kPerClass) {  // the first winner of each class
-                const float v = ws->z[t];
-                const int i = ws->id[t];
-                if (v > bv || (v == bv && i < bi)) {
-                    bv = v;
-                    bi = i;
+            Ms = M;
+            tot = t;
+        }
+    }
+    __syncthreads();
+    const float M = Ms;
+    if (temperature <= 0.0f) {  // argmax: the best class winner (ties to the lower id)
+        if (tid < kClasses) {  // thread c holds class c's first winner
+            float bv = ws->z[tid * kPerClass];
+            int bi = ws->id[tid * kPerClass];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const int oi = __shfl_xor(bi, o);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
                 }
             }
+            if ((tid & 63) == 0) {
+                cp[tid >> 6] = bv;
+                ci[tid >> 6] = bi;
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float bv = cp[0];
+            int bi = ci[0];
+            for (int w = 1; w < kClasses / 64; w++)
+                if (cp[w] > bv || (cp[w] == bv && ci[w] < bi)) {
+                    bv = cp[w];
+                    bi = ci[w];
+                }
             *out = bi == 0x7FFFFFFF ? 0 : bi;
         }
         return;
-    }
-    if (tid == 0) {
-        float t = 0.0f;
-        for (int g = 0; g < kClsGroups; g++)
-            if (ws->m[g] > -INFINITY) t += ws->s[g] * expf((ws->m[g] - M) / temperature);
-        tot = t;
     }
     for (int t = tid; t < kCands; t += kSampleThreads) {
         const int id = ws->id[t];
