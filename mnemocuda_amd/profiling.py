@@ -1,6 +1,6 @@
 """Summaries of rocprofv3 output for the kernels of this library (used to write profiles/).
 
-    python -m mnemocuda_amd.profiling stats <trace_dir> <out.md> "<command>"
+    python -m mnemocuda_amd.profiling stats <trace_dir> <out.md> "<command>" [<top> <name filter>]
     python -m mnemocuda_amd.profiling traffic <fetch_dir> <write_dir> <out.json> <out.md> "<command>"
     python -m mnemocuda_amd.profiling probe
 
@@ -24,11 +24,12 @@ from pathlib import Path
 
 # the fused QKV GEMV: a mixed-type launch (TM = 3) of the 32-lanes-per-row GEMV; the library
 # builds it for 512- and 256-thread workgroups and the QKV shape runs the 256-thread one
-QKV_KERNEL = "gemv_kernel<32, 1, *, false, 3>"
+QKV_KERNEL = "gemv_kernel<32, 1, *, 0, 3>"
 
 
 def _is_qkv(name: str) -> bool:
-    return "gemv_kernel<32, 1, " in name and ", false, 3>" in name
+    # template arguments <LPR 32, UPL 1, XPT, x mode 0 (plain x), types 3 (Q4_K and Q6_K)>
+    return "gemv_kernel<32, 1, " in name and (", 0, 3>" in name or ", false, 3>" in name)
 COPY_BYTES = 256 << 20  # bench.py --copy-calibration copies this many bytes
 
 
@@ -39,8 +40,11 @@ def _find(d: Path, suffix: str) -> Path:
     return hits[0]
 
 
-def stats(trace_dir: str, out_md: str, command: str, top: int = 16) -> None:
+def stats(trace_dir: str, out_md: str, command: str, top: int = 16, only: str | None = None) -> None:
+    """only: keep the kernels whose name contains this text (e.g. 'mnemo::')"""
     rows = list(csv.DictReader(open(_find(Path(trace_dir), "kernel_stats.csv"))))
+    if only:
+        rows = [r for r in rows if only in r["Name"]]
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
     lines = [f"command: `{command}`", "",
              "| kernel | calls | avg us | min us | max us | % time |", "|---|---|---|---|---|---|"]
@@ -125,7 +129,7 @@ def probe(launches: int = 4) -> None:
 
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
-        stats(sys.argv[2], sys.argv[3], sys.argv[4])
+        stats(sys.argv[2], sys.argv[3], sys.argv[4], *([int(sys.argv[5]), sys.argv[6]] if len(sys.argv) > 6 else []))
     elif sys.argv[1] == "traffic":
         traffic(sys.argv[2], sys.argv[3], sys.argv[4], sys.argv[5], sys.argv[6])
     elif sys.argv[1] == "probe":
