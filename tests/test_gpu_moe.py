@@ -264,3 +264,41 @@ def test_moe_decode_rmsnorm_rejects_ragged_hidden(gpu):
         gpu.ops.moe_decode_rmsnorm(torch.zeros(E * H, device="cuda"), table, 1 << 20, 0, 1 << 18, 1 << 19, DT,
                                    torch.zeros(H, device="cuda"), torch.ones(H, device="cuda"), 1e-6, H, EFF, E, k,
                                    ws, torch.zeros(H, device="cuda"))
+
+
+@pytest.mark.parametrize("k", [8, 12])
+def test_moe_decode_rmsnorm_in_place_graph(gpu, k):
+    """The residual stream updated in place (x == out) by a captured graph, replayed as a
+    token sequence: replay t reads the residual replay t-1 wrote.  Every replay equals the
+    eager call on the same state, bit for bit (k = 8: the slot-parallel down launch; k = 12:
+    the partial-buffer one with its counters)."""
+    H, EFF, E, DT = 2048, 768, 32, 14
+    rng = np.random.default_rng(k)
+    table = dev(synth.expert_table(rng, E, H, EFF, DT))
+    lay = synth.expert_layout(H, EFF, DT)
+    router = dev((rng.standard_normal((E, H)) / 32).astype(np.float32))
+    nw = dev((1 + 0.2 * rng.standard_normal(H)).astype(np.float32))
+    x0 = rng.standard_normal(H).astype(np.float32)
+    ws = torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    res = dev(x0)
+    case(f"moe_decode_rmsnorm in place, eager sequence k={k}")
+    eager = []
+    for _ in range(4):
+        gpu.ops.moe_decode_rmsnorm(router, table, *lay, DT, res, nw, 1e-6, H, EFF, E, k, ws, res)
+        eager.append(host(res).copy())
+    case(f"moe_decode_rmsnorm in place, graph replays k={k}")
+    res.copy_(dev(x0))
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            gpu.ops.moe_decode_rmsnorm(router, table, *lay, DT, res, nw, 1e-6, H, EFF, E, k, ws, res)
+    res.copy_(dev(x0))
+    torch.cuda.synchronize()
+    for t in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(res), eager[t]), t
+        junk = torch.randn(1 << 18, device="cuda").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
