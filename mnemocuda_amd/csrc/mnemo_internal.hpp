@@ -37,8 +37,10 @@ struct GemvMat {
 // sits at table + idx[s] * stride + off[m].  The row space is [slot][matrix][rows].
 //  nm == 2 (gate + up of every slot, one x): y[(2s + m) * rows + r]; also clears tile_cnt.
 //  nm == 1 (down of every slot, x of slot s = silu(xs[2s]) * xs[2s + 1], n_cols each):
-//          partial[s * rows + r] = wt[s] * (W x); the last workgroup to finish a row tile
-//          adds sum_s partial (slot order) into out.
+//          out += sum_s wt[s] * (W x) in slot order.  Up to 8 slots and 2048 columns: one
+//          workgroup covers a row tile for all slots (gemv_down_slots_kernel); otherwise
+//          partial[s * rows + r] = wt[s] * (W x) and the last workgroup to finish a row tile
+//          adds the partials (tile_cnt counts the arrivals).
 //  act != 0: gate row r and up row r sit side by side in one pass and the gate/up launch
 //          writes y[s * rows + r] = silu(gate) * up; the down launch reads x of slot s at
 //          xs[s * n_cols].
