@@ -58,6 +58,8 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the full decode-step tok/s (147 GB of experts)")
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--decode-pos", type=int, default=2048, help="KV-cache position of the first decoded token")
+    ap.add_argument("--decode-max-ctx", type=int, default=40960,
+                    help="KV-cache allocation in positions (the model's context length, as a server allocates it)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="end with a 256 MiB device copy (torch.neg) whose HBM counters scale rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE readings (mnemocuda_amd/profiling.py)")
@@ -184,12 +186,12 @@ def gpu_bench(args):
         decode = attn = None
         if not args.no_decode:
             attn = attention_bench(s)
-            decode = decode_bench(gen, s, layers, args.decode_tokens, args.decode_pos)
+            decode = decode_bench(gen, s, layers, args.decode_tokens, args.decode_pos, args.decode_max_ctx)
     return dict(step_s=step_s, wall=wall, d_qkv=d_qkv, d_q=d_q, d_kv=d_kv, d_o=d_o, gemm=gemm, moe=moe,
                 decode=decode, attn=attn)
 
 
-def decode_bench(gen, stream, layers, tokens, ctx_pos):
+def decode_bench(gen, stream, layers, tokens, ctx_pos, cache_ctx=40960):
     """configs[2] inside a full decode step (forward.c:687-1077 per layer, then the lm_head
     and sampling, forward.c:1601-1707), one token at cache position ctx_pos, ctx_pos+1, ...:
     per layer  fused Q/K/V with the attention RMS norm -> GQA decode attention over 0..pos
@@ -203,7 +205,7 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos):
     from mnemocuda_amd import ops, synth
     E, k, EFF, VOCAB = 128, 8, 1536, 151936
     NH, NKV, HD, EPS, THETA = 64, 4, 128, 1e-6, 1e6
-    max_ctx = ctx_pos + tokens + 8
+    max_ctx = max(cache_ctx, ctx_pos + tokens + 8)
     stride, g_off, u_off, d_off = synth.expert_layout(H, EFF, Q6K)
     tables = [synth.expert_table_torch(gen, E, H, EFF, Q6K, "cuda") for _ in range(LAYERS)]
     routers = [torch.randn(E, H, device="cuda", generator=gen) / 64 for _ in range(LAYERS)]
@@ -275,7 +277,7 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos):
     del tables, routers, lm_head, kcache, vcache
     torch.cuda.empty_cache()
     return {"tok_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 3), "tokens": tokens,
-            "context_position": ctx_pos, "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
+            "context_position": ctx_pos, "cache_positions": max_ctx, "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
             "frac_hbm_peak": round(per_tok / ms / 1e6 / HBM_PEAK_GBS, 4),
             "experts_resident_GB": round(E * LAYERS * stride / 1e9, 1),
             "launches_per_token": LAYERS * 7 + 5}
