@@ -1,0 +1,136 @@
+/*
+ * engine_calls.c -- a C caller of the library's C-ABI, written the way the reference engine
+ * calls its kernels (MnemoCUDA src/forward.c:160-173 matvec dispatch, :687-823 one decode
+ * layer): plain C, the HIP runtime's C API for device memory, the extern "C" entry points
+ * of include/mnemo_kernels.h with the reference's argument lists, one stream.
+ *
+ * It fills seeded GGUF blocks and activations, runs the decode-path entry points, and
+ * writes every input and output to one binary file that tests/test_gpu_c_caller.py checks
+ * against the oracle.  Exit status: 0 on success, 1 on a library or HIP error.
+ *
+ * File layout (little endian): int32 R, RK, C, E, K, then the bytes of Wq4 (R x C Q4_K),
+ * Wq6 (R x C Q6_K), Wk (RK x C Q4_K), Wv (RK x C Q6_K), fp32 x[C], res[R], router[E][C],
+ * then the outputs y4[R], y6[R], yadd[R], ya[R], yb[R], q[R], k[RK], v[RK], logits[E],
+ * int32 idx[K], fp32 w[K].
+ */
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/mnemo_kernels.h"
+
+#define R 512
+#define RK 128
+#define C 4096
+#define E 64
+#define K 8
+#define Q4_BYTES ((size_t)(C / 256) * 144)
+#define Q6_BYTES ((size_t)(C / 256) * 210)
+
+static uint64_t lcg = 0x9E3779B97F4A7C15ull;
+static uint32_t next32(void) {
+    lcg = lcg * 6364136223846793005ull + 1442695040888963407ull;
+    return (uint32_t)(lcg >> 32);
+}
+static float uniform(void) { return (float)(next32() >> 8) * (1.0f / 16777216.0f); }
+
+/* f16 bits of a small positive value (d, dmin, Q6_K d): exponent 2^-8..2^-7 range */
+static uint16_t small_f16(void) { return (uint16_t)(0x1C00 | (next32() & 0x3FF)); }
+
+static void fill_q4k(uint8_t *w, size_t rows) {
+    for (size_t b = 0; b < rows * (C / 256); b++) {
+        uint8_t *blk = w + b * 144;
+        uint16_t d = small_f16(), dmin = small_f16();
+        memcpy(blk, &d, 2);
+        memcpy(blk + 2, &dmin, 2);
+        for (int i = 4; i < 144; i++) blk[i] = (uint8_t)next32();
+    }
+}
+static void fill_q6k(uint8_t *w, size_t rows) {
+    for (size_t b = 0; b < rows * (C / 256); b++) {
+        uint8_t *blk = w + b * 210;
+        for (int i = 0; i < 192; i++) blk[i] = (uint8_t)next32();
+        for (int i = 192; i < 208; i++) blk[i] = (uint8_t)(int8_t)((int)(next32() % 61) - 30);
+        uint16_t d = small_f16();
+        memcpy(blk + 208, &d, 2);
+    }
+}
+
+static void *dev_copy(const void *h, size_t n) {
+    void *d = NULL;
+    if (hipMalloc(&d, n) != hipSuccess || hipMemcpy(d, h, n, hipMemcpyHostToDevice) != hipSuccess) return NULL;
+    return d;
+}
+
+int main(int argc, char **argv) {
+    if (argc != 2) {
+        fprintf(stderr, "usage: %s <out.bin>\n", argv[0]);
+        return 1;
+    }
+    cuda_kernels_init();
+    uint8_t *wq4 = malloc(R * Q4_BYTES), *wq6 = malloc(R * Q6_BYTES);
+    uint8_t *wk = malloc(RK * Q4_BYTES), *wv = malloc(RK * Q6_BYTES);
+    float *x = malloc(C * 4), *res = malloc(R * 4), *router = malloc((size_t)E * C * 4);
+    fill_q4k(wq4, R);
+    fill_q6k(wq6, R);
+    fill_q4k(wk, RK);
+    fill_q6k(wv, RK);
+    for (int i = 0; i < C; i++) x[i] = 2.0f * uniform() - 1.0f;
+    for (int i = 0; i < R; i++) res[i] = 2.0f * uniform() - 1.0f;
+    for (int i = 0; i < E * C; i++) router[i] = (2.0f * uniform() - 1.0f) * 0.03f;
+
+    void *d_wq4 = dev_copy(wq4, R * Q4_BYTES), *d_wq6 = dev_copy(wq6, R * Q6_BYTES);
+    void *d_wk = dev_copy(wk, RK * Q4_BYTES), *d_wv = dev_copy(wv, RK * Q6_BYTES);
+    float *d_x = dev_copy(x, C * 4), *d_res = dev_copy(res, R * 4), *d_router = dev_copy(router, (size_t)E * C * 4);
+    float *d_out = NULL;
+    int *d_idx = NULL;
+    const size_t n_out = 5 * R + R + 2 * RK + E + K;
+    if (!d_wq4 || !d_wq6 || !d_wk || !d_wv || !d_x || !d_res || !d_router ||
+        hipMalloc((void **)&d_out, n_out * 4) != hipSuccess || hipMalloc((void **)&d_idx, K * 4) != hipSuccess) {
+        fprintf(stderr, "hip allocation or copy failed\n");
+        return 1;
+    }
+    float *y4 = d_out, *y6 = y4 + R, *yadd = y6 + R, *ya = yadd + R, *yb = ya + R, *q = yb + R;
+    float *k = q + R, *v = k + RK, *logits = v + RK, *w = logits + E;
+    hipStream_t s;
+    if (hipStreamCreate(&s) != hipSuccess) return 1;
+
+    /* the engine's calls (reference argument lists) */
+    cuda_matvec_q4k(d_wq4, d_x, y4, R, C, s);
+    cuda_matvec_q6k(d_wq6, d_x, y6, R, C, s);
+    cuda_matvec_q4k_add(d_wq4, d_x, d_res, yadd, R, C, s);
+    cuda_matvec_q4k_dual(d_wq4, d_wq4, d_x, ya, yb, R, C, s);
+    mnemo_matvec_qkv(d_wq4, 12, d_wk, 12, d_wv, 14, d_x, q, k, v, R, RK, C, s);
+    cuda_matvec_f32(d_router, d_x, logits, E, C, s);
+    cuda_topk_softmax(logits, d_idx, w, E, K, s);
+    if (hipStreamSynchronize(s) != hipSuccess) return 1;
+    if (mnemo_last_error() != MNEMO_OK) {
+        fprintf(stderr, "library error: %s\n", mnemo_last_error_string());
+        return 1;
+    }
+
+    float *out = malloc(n_out * 4);
+    int idx[K];
+    if (hipMemcpy(out, d_out, n_out * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(idx, d_idx, K * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return 1;
+    FILE *f = fopen(argv[1], "wb");
+    if (!f) return 1;
+    const int32_t hdr[5] = {R, RK, C, E, K};
+    fwrite(hdr, 4, 5, f);
+    fwrite(wq4, 1, R * Q4_BYTES, f);
+    fwrite(wq6, 1, R * Q6_BYTES, f);
+    fwrite(wk, 1, RK * Q4_BYTES, f);
+    fwrite(wv, 1, RK * Q6_BYTES, f);
+    fwrite(x, 4, C, f);
+    fwrite(res, 4, R, f);
+    fwrite(router, 4, (size_t)E * C, f);
+    fwrite(out, 4, 5 * R + R + 2 * RK + E, f);
+    fwrite(idx, 4, K, f);
+    fwrite(out + 5 * R + R + 2 * RK + E, 4, K, f);
+    fclose(f);
+    printf("%s: ok\n", mnemo_version());
+    return 0;
+}
