@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(kNormThreads) rms_norm_row_kernel(const float 
     float tot = 0.0f;
 #pragma unroll
     for (int i = 0; i < kNormThreads / 64; i++) tot += part[i];  // same order in every thread
-    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+    const float scale = __builtin_amdgcn_rsqf(tot / (float)n + eps);  // rsqrtf, as the reference (kernels.cu:718)
     if (vec4) {
 #pragma unroll
         for (int u = 0; u < kNormV4; u++) {
@@ -161,7 +161,9 @@ __global__ void __launch_bounds__(256) head_pass_kernel(HeadPassArgs a) {
         float ss = 0.0f;
 #pragma unroll
         for (int t = 0; t < kHeadPairs; t++) ss = fmaf(x0[t], x0[t], fmaf(x1[t], x1[t], ss));
-        const float scale = 1.0f / sqrtf(wave_sum_all(ss) / (float)a.hd + a.eps);
+        // the hardware reciprocal square root, as the reference's rsqrtf (kernels.cu:777);
+        // the fused decode attention repeats this exact expression
+        const float scale = __builtin_amdgcn_rsqf(wave_sum_all(ss) / (float)a.hd + a.eps);
 #pragma unroll
         for (int t = 0; t < kHeadPairs; t++) {
             const int j = lane + 64 * t;

@@ -53,7 +53,7 @@ __device__ __forceinline__ void prep_head(float &x0, float &x1, bool norm, float
                                           float sn) {
     if (norm) {
         const float ss = fmaf(x0, x0, fmaf(x1, x1, 0.0f));
-        const float scale = 1.0f / sqrtf(wave_sum_all(ss) / (float)kHd + eps);
+        const float scale = __builtin_amdgcn_rsqf(wave_sum_all(ss) / (float)kHd + eps);  // as head_pass_kernel
         x0 = x0 * scale * w0;
         x1 = x1 * scale * w1;
     }

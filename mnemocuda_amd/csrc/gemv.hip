@@ -222,7 +222,7 @@ __device__ __forceinline__ float finish_x(const XRegs<XPT> &R, const XRegs<XPT> 
     float tot = 0.0f;
 #pragma unroll
     for (int w = 0; w < kGemvThreads / 64; w++) tot += part[w];
-    return 1.0f / sqrtf(tot / (float)n + eps);
+    return __builtin_amdgcn_rsqf(tot / (float)n + eps);  // rsqrtf, as the reference (kernels.cu:718)
 }
 
 // ------------------------------------------------------------------ weight units

@@ -183,7 +183,7 @@ __device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, cons
 #pragma unroll
     for (int i = 0; i < kRowThreads / 64; i++) tot += part[i];
     __syncthreads();  // part[] is reused by block_sum
-    const float scale = 1.0f / sqrtf(tot / (float)n_cols + eps);
+    const float scale = __builtin_amdgcn_rsqf(tot / (float)n_cols + eps);  // rsqrtf, as the reference (kernels.cu:718)
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < kRowMaxV4; i++) {
