@@ -146,12 +146,10 @@ __device__ __forceinline__ void build_x(const XRegs<XPT> &R, const XRegs<XPT> &R
 #pragma unroll
             for (int j = 0; j < 4; j++) v[j] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[j]) & keep);
         }
-        // |v| as unsigned bits orders like |v|; max over the 8 lanes of the sub-block
-        uint32_t ab = max(max(__builtin_bit_cast(uint32_t, v[0]) & 0x7FFFFFFFu,
-                              __builtin_bit_cast(uint32_t, v[1]) & 0x7FFFFFFFu),
-                          max(__builtin_bit_cast(uint32_t, v[2]) & 0x7FFFFFFFu,
-                              __builtin_bit_cast(uint32_t, v[3]) & 0x7FFFFFFFu));
-        const float amax = __builtin_bit_cast(float, umax_dpp8(ab));
+        // max |v| over the 8 lanes of the sub-block (|v| as float max3 with abs modifiers:
+        // two instructions; non-negative floats order like their bits for the DPP max)
+        const float a4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        const float amax = __builtin_bit_cast(float, umax_dpp8(__builtin_bit_cast(uint32_t, a4)));
         const float s = amax * (1.0f / 127.0f);
         const float u = s * (1.0f / 254.0f);
         const float inv1 = amax > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.0f;
