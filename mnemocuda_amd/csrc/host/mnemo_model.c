@@ -563,6 +563,10 @@ int mnemo_model_upload(mnemo_model *m, int with_experts) {
         for (int i = 0; !rc && i < m->n_tensors; i++)
             rc = upload_file(path, m->tensors[i].offset, m->tensors[i].size, (char *)m->d_resident + m->dev_off[i], stage,
                              stage_size);
+        if (rc && m->d_resident) {  // a partial copy is not kept: a later call starts over
+            (void)hipFree(m->d_resident);
+            m->d_resident = NULL;
+        }
     }
     for (int l = 0; !rc && with_experts && l < m->cfg.n_layers; l++) {
         if (!m->has_layer[l] || m->d_experts[l]) continue;
@@ -574,6 +578,10 @@ int mnemo_model_upload(mnemo_model *m, int with_experts) {
         }
         snprintf(path, sizeof path, "%s/experts/layer_%02d.bin", m->dir, l);
         rc = upload_file(path, 0, bytes, m->d_experts[l], stage, stage_size);
+        if (rc) {
+            (void)hipFree(m->d_experts[l]);
+            m->d_experts[l] = NULL;
+        }
     }
     hipHostFree(stage);
     return rc;
