@@ -24,9 +24,10 @@
 //     K step 64 (one Q4_K nibble group, one Q6_K ql group).  Raw weight blocks and
 //     activation chunks are loaded into registers ahead of their conversion; f16 tiles
 //     rotate through three LDS buffers (XOR-swizzled, conflict-free); one barrier per step.
-//   * When the tile grid covers less than half of the CUs, K is split across workgroups
+//   * When the tile grid covers at most half of the CUs, K is split across workgroups
 //     and the partial tiles are summed with fp32 atomics into the output, which a small
-//     fill kernel zeroes first.
+//     fill kernel zeroes first; the tiles pass through LDS so that each atomic instruction
+//     covers 64 consecutive outputs of one token.
 #include <algorithm>
 
 #include "mnemo_common.hpp"
@@ -479,9 +480,9 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
             for (int e = 0; e < 4; e++) acc[a][b][e] *= us;
             float *o = g.out + (size_t)(row_base + j) * g.out_ld + ib;
             if (ATOMIC) {
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (ib + e < g.M) __hip_atomic_fetch_add(o + e, acc[a][b][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // to the wave's own (idle) reduction buffer, token-major, 16-byte groups
+                // XOR-swizzled by token so that the row-wise reads below are conflict-free
+                *(f4 *)(red + (16 * b + (lane & 15)) * 64 + (((4 * a + (lane >> 4)) ^ (lane & 15)) << 2)) = acc[a][b];
             } else if (ib + 3 < g.M && ((g.out_ld & 3) == 0)) {
                 *(f4 *)o = acc[a][b];
             } else {
@@ -490,6 +491,20 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
                     if (ib + e < g.M) o[e] = acc[a][b][e];
             }
         }
+    if (ATOMIC) {
+        // one atomic instruction per token covers 64 consecutive outputs (two cache lines);
+        // the MFMA layout would spread each instruction over 16 token rows, which measured
+        // twice as slow in the L2 atomic units
+        const int ib = i0 + wi + lane;
+        for (int t = 0; t < 64; t++) {
+            const int j = j0 + wj + t;
+            if (j >= n_rows) break;
+            if (ib < g.M)
+                __hip_atomic_fetch_add(g.out + (size_t)(row_base + j) * g.out_ld + ib,
+                                       red[t * 64 + ((((lane >> 2) ^ (t & 15)) << 2) | (lane & 3))], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // ------------------------------------------------------------------ activation staging
@@ -636,11 +651,12 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
     if (((uintptr_t)out & 15) != 0) return set_error(kErrBadArg, "gemm: output must be 16-byte aligned");
     if (((uintptr_t)act & 3) != 0) return set_error(kErrBadArg, "gemm: activation blocks must be 4-byte aligned");
     const int tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
-    // split K only while the tile grid covers less than half of the CUs (the atomics cost
-    // more than idle CUs otherwise), keeping at least 16 steps of 64 per split
+    // split K while the split grid still fits the CUs once (one workgroup per CU at a time),
+    // keeping at least 8 steps of 64 per split: measured, M x 512 x K = 1536 x 4096 best at 4
+    // splits (31 us against 59 unsplit), 512 x 4096 at 8, 4096 x 8192 at 2 (75 against 100)
     const int nks = K / kKS;
     int splits = 1;
-    while (2 * tm * tn * splits < device_cus_gemm() && nks / (splits * 2) >= 16) splits *= 2;
+    while (2 * tm * tn * splits <= device_cus_gemm() && nks / (splits * 2) >= 8) splits *= 2;
     if (((long)M * N) % 4 != 0) splits = 1;  // the fill kernel clears float4s
     // activations are read as Q8_1 blocks and converted per tile: nothing is allocated, so
     // the call may sit inside a graph capture
