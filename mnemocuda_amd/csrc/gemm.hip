@@ -309,6 +309,8 @@ struct GemmArgs {
     const int *offsets;                  // [n_experts] first expert-sorted row
     const int *perm;                     // [rows] expert-sorted row -> token (SwiGLU gather)
     const int *tiles;                    // [max_tiles] (expert << 16) | n_tile; tiles[-1] = count
+    int skip_upto;                       // grouped: tiles of at most this many rows are left to
+                                         // the skinny kernel (0: none)
 };
 
 template <int TYPE, int MODE, bool ATOMIC, bool Q8>
@@ -340,6 +342,7 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
         n_rows = g.counts[e];
         row_base = g.offsets[e];
         j0 = nt * kBN;
+        if (min(kBN, n_rows - j0) <= g.skip_upto) return;  // uniform: a skinny tile
         i0 = blockIdx.x * (MODE == kModeSwiGLU ? kBM / 2 : kBM);
         Wm = g.W + (size_t)e * g.expert_stride + g.w_off;
         Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
@@ -678,6 +681,305 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
     return check_launch("gemm_q8_1");
 }
 
+// ------------------------------------------------------------------ skinny grouped kernel
+// Most token tiles of a grouped launch hold few rows (an expert of the MoE prefill receives
+// a few tens of tokens), and then the tiled kernel above spends its time converting 128
+// weight rows per step into LDS for a handful of MFMA columns.  This kernel serves the
+// tiles of at most kSkTok rows without staging weights at all: every lane loads the raw
+// bytes of its own A-operand values and converts them in registers, straight into the
+// 16x16x32 f16 MFMA.  The K order inside an MFMA is free as long as both operands follow
+// it, so each lane takes whole 16-byte chunks of a super-block (lane group q = lane/16,
+// MFMA t = 0..7 of a 256-value block):
+//   Q4_K: qs chunk m = q + 4(t/4): values 64(m/2) + 32h + 16(m%2) + 8s .. +7, with h = (t/2)%2
+//         the nibble (sub-block 2(m/2) + h) and s = t%2 the dword pair of the chunk;
+//   Q6_K: half H = t/4, ql chunk 64H + 16q, qh chunk 32H + 16(q%2), nibble n = (t/2)%2:
+//         group grp = q/2 + 2n, values 128H + 32grp + 16(q%2) + 8s .. +7, scale 8H + q + 4n.
+// The tile's activation rows (staged f16) are copied per block into LDS in that order, so
+// a B fragment is one 16-byte read.  Conversion arithmetic is the tiled kernel's (same f16
+// roundings), so the two kernels agree to the fp32 accumulation order.
+constexpr int kSkThreads = 512;  // 8 waves
+constexpr int kSkWaves = kSkThreads / 64;
+constexpr int kSkTok = 64;       // rows per tile served here: 4 column tiles of 16
+constexpr int kSkR = 2;          // 16-row MFMA tiles per wave (SwiGLU: 1 gate + 1 up)
+// weight blocks loaded ahead of their multiplication: 2 for Q4_K; 1 for Q6_K, whose raw
+// registers (and their 2-byte-aligned loads) would not fit two waves per SIMD otherwise
+template <int TYPE>
+constexpr int sk_ahead() { return TYPE == kTypeQ4K ? 2 : 1; }
+
+template <int TYPE>
+__device__ __forceinline__ int sk_k0(int t, int q) {
+    if (TYPE == kTypeQ4K) {
+        const int m = q + 4 * (t >> 2);
+        return 64 * (m >> 1) + 32 * ((t >> 1) & 1) + 16 * (m & 1) + 8 * (t & 1);
+    }
+    return 128 * (t >> 2) + 32 * ((q >> 1) + 2 * ((t >> 1) & 1)) + 16 * (q & 1) + 8 * (t & 1);
+}
+
+// raw bytes of one row tile's lane values for one 256-value block
+struct SkRaw {
+    uint4 c[2];   // Q4_K: qs chunks q, q+4;  Q6_K: ql chunks of halves 0, 1
+    uint4 h;      // Q4_K: the header (d, dmin, 12 scale bytes);  Q6_K: the lane's qh bits,
+                  // two dwords per half (below)
+    uint32_t sc;  // Q6_K: scale bytes q, q+4, q+8, q+12
+    uint32_t d;   // Q6_K: f16 d
+};
+
+template <int TYPE>
+__device__ __forceinline__ void sk_load(const uint8_t *__restrict__ blk, int q, SkRaw &r) {
+    if (TYPE == kTypeQ4K) {
+        r.h = ld16(blk);
+        r.c[0] = ld16(blk + 16 + 16 * q);
+        r.c[1] = ld16(blk + 80 + 16 * q);
+    } else {
+        r.c[0] = ld16_a2(blk + 16 * q);
+        r.c[1] = ld16_a2(blk + 64 + 16 * q);
+        const uint4 h0 = ld16_a2(blk + 128 + 16 * (q & 1)), h1 = ld16_a2(blk + 160 + 16 * (q & 1));
+        const uint4 sc = ld16_a2(blk + 192);
+        uint16_t dd;
+        __builtin_memcpy(&dd, blk + 208, 2);
+        r.d = dd;
+        // scale byte i of the lane is byte q of dword i
+        const uint32_t lo = __builtin_amdgcn_perm(sc.y, sc.x, 0x0C0C0400u + 0x00000101u * (uint32_t)q);
+        const uint32_t hi = __builtin_amdgcn_perm(sc.w, sc.z, 0x0C0C0400u + 0x00000101u * (uint32_t)q);
+        r.sc = (lo & 0xFFFFu) | (hi << 16);
+        // of each qh byte the lane needs groups q/2 (bits 2(q/2)..+1) and q/2 + 2 (bits
+        // 2(q/2)+4..+5); packed: byte i of dword 2H+s holds, for values i (dword 2s) and
+        // 4+i (dword 2s+1) of the chunk, bits 0-1 / 2-3 (low nibble group) and 4-5 / 6-7
+        const int sh = 2 * (q >> 1);
+        auto pk = [sh](uint32_t a, uint32_t b) {
+            return ((a >> sh) & 0x33333333u) | (((b >> sh) & 0x33333333u) << 2);
+        };
+        r.h = make_uint4(pk(h0.x, h0.y), pk(h0.z, h0.w), pk(h1.x, h1.y), pk(h1.z, h1.w));
+    }
+}
+
+__device__ __forceinline__ uint32_t dw(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// per-block scale pairs of a lane: Q4_K (d*sc, -dmin*m) of its 4 sub-blocks (index 2L + h);
+// Q6_K d*sc of its 4 scales (index 2H + n)
+template <int TYPE>
+__device__ __forceinline__ void sk_scales(const SkRaw &r, int q, h2 (&A)[4], h2 (&B)[4]) {
+    if (TYPE == kTypeQ4K) {
+        const uint32_t s0 = r.h.y, s1 = r.h.z, s2 = r.h.w;
+        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
+#pragma unroll
+        for (int L = 0; L < 2; L++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int j = 2 * ((q >> 1) + 2 * L) + h;  // get_scale_min_k4 (kernels.cu:45-53)
+                uint32_t sc, m;
+                if (L == 0) {
+                    sc = sbyte(s0, s1, s2, j) & 63;
+                    m = sbyte(s0, s1, s2, j + 4) & 63;
+                } else {
+                    sc = (sbyte(s0, s1, s2, j + 4) & 15) | ((sbyte(s0, s1, s2, j - 4) >> 6) << 4);
+                    m = (sbyte(s0, s1, s2, j + 4) >> 4) | ((sbyte(s0, s1, s2, j) >> 6) << 4);
+                }
+                const _Float16 a = (_Float16)(d * (float)sc), b = (_Float16)(-dmin * (float)m);
+                A[2 * L + h] = h2{a, a};
+                B[2 * L + h] = h2{b, b};
+            }
+    } else {
+        const float d = h2f(r.d);
+#pragma unroll
+        for (int H = 0; H < 2; H++)
+#pragma unroll
+            for (int n = 0; n < 2; n++) {  // scale 8H + q + 4n = lane byte 2H + n
+                const int8_t sc = (int8_t)((r.sc >> (8 * (2 * H + n))) & 0xFF);
+                const _Float16 a = (_Float16)(d * (float)sc);
+                A[2 * H + n] = h2{a, a};
+            }
+    }
+}
+
+// the 8 f16 A-operand values of MFMA t
+template <int TYPE>
+__device__ __forceinline__ h8 sk_operand(const SkRaw &r, int t, const h2 (&A)[4], const h2 (&B)[4]) {
+    const int L = t >> 2, h = (t >> 1) & 1, s = t & 1;
+    uint32_t o[4];
+    if (TYPE == kTypeQ4K) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t w = (dw(r.c[L], 2 * s + k) >> (4 * h)) & 0x0F0F0F0Fu;
+            o[2 * k] = dq_fma(w, 0x04010400u, A[2 * L + h], B[2 * L + h]);
+            o[2 * k + 1] = dq_fma(w, 0x04030402u, A[2 * L + h], B[2 * L + h]);
+        }
+    } else {
+        const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+        const uint32_t P = dw(r.h, 2 * L + s);
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t lo = (dw(r.c[L], 2 * s + k) >> (4 * h)) & 0x0F0F0F0Fu;
+            const int sh = 2 * k + 4 * h;  // the two bits of these values, moved to bits 4-5
+            const uint32_t hi = (sh <= 4 ? (P << (4 - sh)) : (P >> (sh - 4))) & 0x30303030u;
+            const uint32_t v = lo | hi;
+            o[2 * k] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04010400u) + off) * A[2 * L + h]);
+            o[2 * k + 1] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04030402u) + off) * A[2 * L + h]);
+        }
+    }
+    const uint4 u = make_uint4(o[0], o[1], o[2], o[3]);
+    return __builtin_bit_cast(h8, u);
+}
+
+// B slot u = 4t + q of token row r, 16-byte columns XOR-swizzled by the row so that the
+// 16 rows of a fragment read hit distinct banks
+__device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r & 31)) << 3); }
+
+// One 256-value block: multiply block k (raw weights in `cur`, activations in LDS buffer
+// k%2), load weight block k+sk_ahead into `dst` (the slot `cur` had before this block) and
+// the activations of block k+1 into registers, then into the other LDS buffer.
+template <int TYPE, int NB>
+__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int tid, const uint8_t *const (&wrow)[kSkR],
+                                         const _Float16 *const (&arow)[NB], _Float16 (*bs)[kSkTok * 256],
+                                         const SkRaw (&cur)[kSkR], SkRaw (&dst)[kSkR], f4 (&acc)[kSkR][NB]) {
+    const int su = tid & 31, sr0 = tid >> 5;
+    // past the end the last block is loaded again: unconditional loads keep every value in
+    // registers
+    const int kw = min(k + sk_ahead<TYPE>(), nkb - 1), ka = min(k + 1, nkb - 1);
+    h2 A[kSkR][4], B[kSkR][4];
+#pragma unroll
+    for (int a = 0; a < kSkR; a++) sk_scales<TYPE>(cur[a], q, A[a], B[a]);
+#pragma unroll
+    for (int a = 0; a < kSkR; a++) sk_load<TYPE>(wrow[a] + (size_t)kw * bbytes, q, dst[a]);
+    uint4 rb[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++) rb[i] = *(const uint4 *)(arow[i] + ka * 256);
+    const _Float16 *bb = bs[k & 1];
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        h8 bf[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) bf[b] = *(const h8 *)(bb + sk_slot(16 * b + c, 4 * t + q));
+#pragma unroll
+        for (int a = 0; a < kSkR; a++) {
+            const h8 af = sk_operand<TYPE>(cur[a], t, A[a], B[a]);
+#pragma unroll
+            for (int b = 0; b < NB; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[a][b], 0, 0, 0);
+        }
+    }
+    if (k + 1 < nkb) {
+#pragma unroll
+        for (int i = 0; i < NB; i++) *(uint4 *)(&bs[(k + 1) & 1][sk_slot(sr0 + 16 * i, su)]) = rb[i];
+    }
+    __syncthreads();
+}
+
+template <int TYPE, int MODE, int NB>
+__device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok * 256], int wave, int lane, int tid,
+                                        int e, int j0, int n_rows, int row_base) {
+    constexpr int H = kSkR / 2;  // SwiGLU: gate tiles 0 .. H-1, up tiles H .. 2H-1
+    const int q = lane >> 4, c = lane & 15;
+    const int K = g.K, nkb = K / 256;
+    const int bbytes = TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes;
+    const size_t wrow_bytes = (size_t)nkb * bbytes;
+    const uint8_t *Wm = g.W + (size_t)e * g.expert_stride + g.w_off;
+    const uint8_t *Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
+
+    // this lane's weight row of each row tile (rows past M re-read the last)
+    const uint8_t *wrow[kSkR];
+    int base;  // SwiGLU: first feature of the wave; grouped: first row
+    if (MODE == kModeSwiGLU) {
+        base = (blockIdx.x * kSkWaves + wave) * (16 * H);
+#pragma unroll
+        for (int a = 0; a < kSkR; a++) {
+            const int f = min(base + 16 * (a % H) + c, g.M - 1);
+            wrow[a] = (a < H ? Wm : Wm2) + (size_t)f * wrow_bytes;
+        }
+    } else {
+        base = (blockIdx.x * kSkWaves + wave) * (16 * kSkR);
+#pragma unroll
+        for (int a = 0; a < kSkR; a++) wrow[a] = Wm + (size_t)min(base + 16 * a + c, g.M - 1) * wrow_bytes;
+    }
+    // activation staging role: slot u = tid % 32 of rows tid/32 + 16i, i < NB
+    const int su = tid & 31, sr0 = tid >> 5;
+    const int sk = sk_k0<TYPE>(su >> 2, su & 3);
+    const _Float16 *arow[NB];
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int j = min(j0 + sr0 + 16 * i, n_rows - 1);
+        const int idx = MODE == kModeSwiGLU ? g.perm[row_base + j] : row_base + j;
+        arow[i] = (const _Float16 *)g.A + (size_t)idx * K + sk;
+    }
+    f4 acc[kSkR][NB];
+#pragma unroll
+    for (int a = 0; a < kSkR; a++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+    SkRaw r0[kSkR], r1[kSkR], r2[kSkR];
+#pragma unroll
+    for (int a = 0; a < kSkR; a++) {
+        sk_load<TYPE>(wrow[a], q, r0[a]);
+        if (sk_ahead<TYPE>() == 2) sk_load<TYPE>(wrow[a] + (size_t)min(1, nkb - 1) * bbytes, q, r1[a]);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; i++) *(uint4 *)(&bs[0][sk_slot(sr0 + 16 * i, su)]) = *(const uint4 *)arow[i];
+    __syncthreads();
+    // a ring of sk_ahead + 1 raw slots, unrolled by its size so that every slot is static
+    if (sk_ahead<TYPE>() == 2) {
+        for (int k = 0; k < nkb; k += 3) {
+            sk_block<TYPE, NB>(k, nkb, bbytes, q, c, tid, wrow, arow, bs, r0, r2, acc);
+            if (k + 1 >= nkb) break;
+            sk_block<TYPE, NB>(k + 1, nkb, bbytes, q, c, tid, wrow, arow, bs, r1, r0, acc);
+            if (k + 2 >= nkb) break;
+            sk_block<TYPE, NB>(k + 2, nkb, bbytes, q, c, tid, wrow, arow, bs, r2, r1, acc);
+        }
+    } else {
+        for (int k = 0; k < nkb; k += 2) {
+            sk_block<TYPE, NB>(k, nkb, bbytes, q, c, tid, wrow, arow, bs, r0, r1, acc);
+            if (k + 1 >= nkb) break;
+            sk_block<TYPE, NB>(k + 1, nkb, bbytes, q, c, tid, wrow, arow, bs, r1, r0, acc);
+        }
+    }
+
+    // D layout: lane holds weight rows 4q + e of each 16-row tile, token column c
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int j = j0 + 16 * b + c;
+        if (j >= n_rows) continue;
+        const int idx = MODE == kModeSwiGLU ? g.perm[row_base + j] : row_base + j;
+        const float us = g.a_unscale[idx];
+        float *orow = g.out + (size_t)(row_base + j) * g.out_ld;
+        if (MODE == kModeSwiGLU) {
+#pragma unroll
+            for (int a = 0; a < H; a++) {
+                const int f = base + 16 * a + 4 * q;
+#pragma unroll
+                for (int x = 0; x < 4; x++) {
+                    const float gt = acc[a][b][x] * us, up = acc[a + H][b][x] * us;
+                    if (f + x < g.M) orow[f + x] = gt / (1.0f + expf(-gt)) * up;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int a = 0; a < kSkR; a++) {
+                const int i = base + 16 * a + 4 * q;
+#pragma unroll
+                for (int x = 0; x < 4; x++)
+                    if (i + x < g.M) orow[i + x] = acc[a][b][x] * us;
+            }
+        }
+    }
+}
+
+template <int TYPE, int MODE>
+__global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmArgs g) {
+    __shared__ __align__(16) _Float16 bs[2][kSkTok * 256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if ((int)blockIdx.y >= g.tiles[-1]) return;
+    const int tl = g.tiles[blockIdx.y];
+    const int e = tl >> 16, nt = tl & 0xFFFF;
+    const int n_rows = g.counts[e], row_base = g.offsets[e], j0 = nt * kBN;
+    const int nvalid = min(kBN, n_rows - j0);
+    if (nvalid > kSkTok) return;  // uniform: the tiled kernel's tile
+    // one instantiation per count of 16-row column tiles, so every MFMA is unconditional
+    switch ((nvalid + 15) >> 4) {
+    case 1: sk_tile<TYPE, MODE, 1>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    case 2: sk_tile<TYPE, MODE, 2>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    case 3: sk_tile<TYPE, MODE, 3>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    default: sk_tile<TYPE, MODE, 4>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    }
+}
+
 // Grouped launches used by the MoE prefill path (moe.hip): tiles[] and the routing arrays
 // live in device memory, the grid covers max_tiles tile-list entries.
 int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert_stride, size_t w_off,
@@ -701,6 +1003,19 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
     g.offsets = offsets;
     g.perm = perm;
     g.tiles = tiles;
+    g.skip_upto = kSkTok;
+    // tiles of at most kSkTok rows: the skinny kernel; the rest: the tiled kernel
+    const int sk_rows = swiglu ? kSkR / 2 * 16 * kSkWaves : kSkR * 16 * kSkWaves;
+    const dim3 sk_grid((M + sk_rows - 1) / sk_rows, max_tiles, 1);
+#define MNEMO_SKINNY(T_, M_) hipLaunchKernelGGL((gemm_skinny_kernel<T_, M_>), sk_grid, dim3(kSkThreads), 0, stream, g)
+    if (swiglu) {
+        if (type == kTypeQ4K) MNEMO_SKINNY(kTypeQ4K, kModeSwiGLU);
+        else MNEMO_SKINNY(kTypeQ6K, kModeSwiGLU);
+    } else {
+        if (type == kTypeQ4K) MNEMO_SKINNY(kTypeQ4K, kModeGrouped);
+        else MNEMO_SKINNY(kTypeQ6K, kModeGrouped);
+    }
+#undef MNEMO_SKINNY
     if (swiglu) launch_mode<kModeSwiGLU, false>(type, false, dim3((M + kBM / 2 - 1) / (kBM / 2), max_tiles, 1), g, stream);
     else launch_mode<kModeGrouped, false>(type, false, dim3((M + kBM - 1) / kBM, max_tiles, 1), g, stream);
     return check_launch("gemm_grouped");
