@@ -701,11 +701,6 @@ constexpr int kSkThreads = 512;  // 8 waves
 constexpr int kSkWaves = kSkThreads / 64;
 constexpr int kSkTok = 64;       // rows per tile served here: 4 column tiles of 16
 constexpr int kSkR = 2;          // 16-row MFMA tiles per wave (SwiGLU: 1 gate + 1 up)
-// weight blocks loaded ahead of their multiplication: 2 for Q4_K; 1 for Q6_K, whose raw
-// registers (and their 2-byte-aligned loads) would not fit two waves per SIMD otherwise
-template <int TYPE>
-constexpr int sk_ahead() { return TYPE == kTypeQ4K ? 2 : 1; }
-
 template <int TYPE>
 __device__ __forceinline__ int sk_k0(int t, int q) {
     if (TYPE == kTypeQ4K) {
@@ -826,24 +821,30 @@ __device__ __forceinline__ h8 sk_operand(const SkRaw &r, int t, const h2 (&A)[4]
 __device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r & 31)) << 3); }
 
 // One 256-value block: multiply block k (raw weights in `cur`, activations in LDS buffer
-// k%2), load weight block k+sk_ahead into `dst` (the slot `cur` had before this block) and
-// the activations of block k+1 into registers, then into the other LDS buffer.
+// k%2) while the weights of block k+1 load into `nxt` and its activations into the other
+// LDS buffer (straight from memory, global_load_lds: lane l of a wave fills 16 bytes at
+// base + 16l).  The wait for those LDS writes before the barrier also covers the weight
+// loads issued after them (memory loads complete in issue order), so one block ahead is
+// what the pipeline can hold.
 template <int TYPE, int NB>
-__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int tid, const uint8_t *const (&wrow)[kSkR],
+__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int wave, const uint8_t *const (&wrow)[kSkR],
                                          const _Float16 *const (&arow)[NB], _Float16 (*bs)[kSkTok * 256],
-                                         const SkRaw (&cur)[kSkR], SkRaw (&dst)[kSkR], f4 (&acc)[kSkR][NB]) {
-    const int su = tid & 31, sr0 = tid >> 5;
-    // past the end the last block is loaded again: unconditional loads keep every value in
-    // registers
-    const int kw = min(k + sk_ahead<TYPE>(), nkb - 1), ka = min(k + 1, nkb - 1);
+                                         const SkRaw (&cur)[kSkR], SkRaw (&nxt)[kSkR], f4 (&acc)[kSkR][NB]) {
+    // past the end the last block is loaded again (into the idle buffer and registers)
+    const int kn = min(k + 1, nkb - 1);
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+        __builtin_amdgcn_global_load_lds((const void *)(arow[i] + kn * 256),
+                                         (__attribute__((address_space(3))) void *)&bs[(k + 1) & 1][(2 * wave + 16 * i) * 256],
+                                         16, 0, 0);
+#pragma unroll
+    for (int a = 0; a < kSkR; a++) sk_load<TYPE>(wrow[a] + (size_t)kn * bbytes, q, nxt[a]);
+    // keep the loads here, ahead of the multiplication (the scheduler would otherwise sink
+    // them past it to save registers, and nothing would be in flight during the MFMAs)
+    __builtin_amdgcn_sched_barrier(0);
     h2 A[kSkR][4], B[kSkR][4];
 #pragma unroll
     for (int a = 0; a < kSkR; a++) sk_scales<TYPE>(cur[a], q, A[a], B[a]);
-#pragma unroll
-    for (int a = 0; a < kSkR; a++) sk_load<TYPE>(wrow[a] + (size_t)kw * bbytes, q, dst[a]);
-    uint4 rb[NB];
-#pragma unroll
-    for (int i = 0; i < NB; i++) rb[i] = *(const uint4 *)(arow[i] + ka * 256);
     const _Float16 *bb = bs[k & 1];
 #pragma unroll
     for (int t = 0; t < 8; t++) {
@@ -856,10 +857,6 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int 
 #pragma unroll
             for (int b = 0; b < NB; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[a][b], 0, 0, 0);
         }
-    }
-    if (k + 1 < nkb) {
-#pragma unroll
-        for (int i = 0; i < NB; i++) *(uint4 *)(&bs[(k + 1) & 1][sk_slot(sr0 + 16 * i, su)]) = rb[i];
     }
     __syncthreads();
 }
@@ -890,45 +887,36 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
 #pragma unroll
         for (int a = 0; a < kSkR; a++) wrow[a] = Wm + (size_t)min(base + 16 * a + c, g.M - 1) * wrow_bytes;
     }
-    // activation staging role: slot u = tid % 32 of rows tid/32 + 16i, i < NB
-    const int su = tid & 31, sr0 = tid >> 5;
-    const int sk = sk_k0<TYPE>(su >> 2, su & 3);
+    // activation staging role: physical slot tid % 32 of rows r = tid/32 + 16i, i < NB, which
+    // holds the logical slot (tid % 32) ^ (r % 32)
+    const int sr0 = tid >> 5;
     const _Float16 *arow[NB];
 #pragma unroll
     for (int i = 0; i < NB; i++) {
-        const int j = min(j0 + sr0 + 16 * i, n_rows - 1);
+        const int r = sr0 + 16 * i, u = (tid & 31) ^ (r & 31);
+        const int j = min(j0 + r, n_rows - 1);
         const int idx = MODE == kModeSwiGLU ? g.perm[row_base + j] : row_base + j;
-        arow[i] = (const _Float16 *)g.A + (size_t)idx * K + sk;
+        arow[i] = (const _Float16 *)g.A + (size_t)idx * K + sk_k0<TYPE>(u >> 2, u & 3);
     }
     f4 acc[kSkR][NB];
 #pragma unroll
     for (int a = 0; a < kSkR; a++)
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-    SkRaw r0[kSkR], r1[kSkR], r2[kSkR];
+    SkRaw r0[kSkR], r1[kSkR];
 #pragma unroll
-    for (int a = 0; a < kSkR; a++) {
-        sk_load<TYPE>(wrow[a], q, r0[a]);
-        if (sk_ahead<TYPE>() == 2) sk_load<TYPE>(wrow[a] + (size_t)min(1, nkb - 1) * bbytes, q, r1[a]);
-    }
+    for (int i = 0; i < NB; i++)
+        __builtin_amdgcn_global_load_lds((const void *)arow[i],
+                                         (__attribute__((address_space(3))) void *)&bs[0][(2 * wave + 16 * i) * 256], 16,
+                                         0, 0);
 #pragma unroll
-    for (int i = 0; i < NB; i++) *(uint4 *)(&bs[0][sk_slot(sr0 + 16 * i, su)]) = *(const uint4 *)arow[i];
+    for (int a = 0; a < kSkR; a++) sk_load<TYPE>(wrow[a], q, r0[a]);
     __syncthreads();
-    // a ring of sk_ahead + 1 raw slots, unrolled by its size so that every slot is static
-    if (sk_ahead<TYPE>() == 2) {
-        for (int k = 0; k < nkb; k += 3) {
-            sk_block<TYPE, NB>(k, nkb, bbytes, q, c, tid, wrow, arow, bs, r0, r2, acc);
-            if (k + 1 >= nkb) break;
-            sk_block<TYPE, NB>(k + 1, nkb, bbytes, q, c, tid, wrow, arow, bs, r1, r0, acc);
-            if (k + 2 >= nkb) break;
-            sk_block<TYPE, NB>(k + 2, nkb, bbytes, q, c, tid, wrow, arow, bs, r2, r1, acc);
-        }
-    } else {
-        for (int k = 0; k < nkb; k += 2) {
-            sk_block<TYPE, NB>(k, nkb, bbytes, q, c, tid, wrow, arow, bs, r0, r1, acc);
-            if (k + 1 >= nkb) break;
-            sk_block<TYPE, NB>(k + 1, nkb, bbytes, q, c, tid, wrow, arow, bs, r1, r0, acc);
-        }
+    // two raw slots, the loop unrolled by two so that both are static
+    for (int k = 0; k < nkb; k += 2) {
+        sk_block<TYPE, NB>(k, nkb, bbytes, q, c, wave, wrow, arow, bs, r0, r1, acc);
+        if (k + 1 >= nkb) break;
+        sk_block<TYPE, NB>(k + 1, nkb, bbytes, q, c, wave, wrow, arow, bs, r1, r0, acc);
     }
 
     // D layout: lane holds weight rows 4q + e of each 16-row tile, token column c
