@@ -697,9 +697,12 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
 // The tile's activation rows (staged f16) are copied per block into LDS in that order, so
 // a B fragment is one 16-byte read.  Conversion arithmetic is the tiled kernel's (same f16
 // roundings), so the two kernels agree to the fp32 accumulation order.
+#ifndef MNEMO_SKTOK
+#define MNEMO_SKTOK 64
+#endif
 constexpr int kSkThreads = 512;  // 8 waves
 constexpr int kSkWaves = kSkThreads / 64;
-constexpr int kSkTok = 64;       // rows per tile served here: 4 column tiles of 16
+constexpr int kSkTok = MNEMO_SKTOK;       // rows per tile served here: 4 column tiles of 16
 constexpr int kSkR = 2;          // 16-row MFMA tiles per wave (SwiGLU: 1 gate + 1 up)
 template <int TYPE>
 __device__ __forceinline__ int sk_k0(int t, int q) {
@@ -964,7 +967,13 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmArgs g) {
     case 1: sk_tile<TYPE, MODE, 1>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
     case 2: sk_tile<TYPE, MODE, 2>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
     case 3: sk_tile<TYPE, MODE, 3>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-    default: sk_tile<TYPE, MODE, 4>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    case 4: sk_tile<TYPE, MODE, 4>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+#if MNEMO_SKTOK == 128
+    case 5: sk_tile<TYPE, MODE, 5>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    case 6: sk_tile<TYPE, MODE, 6>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    case 7: sk_tile<TYPE, MODE, 7>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+    default: sk_tile<TYPE, MODE, 8>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
+#endif
     }
 }
 

@@ -70,6 +70,9 @@ def _compose_plain(gpu, table, lay, DT, x, idx, w, T, H, EFF, out0):
     (300, 256, 512, 4, 2, 12, 3.0),    # expert 0 spans several tiles
     (1, 256, 256, 8, 8, 14, 1.1),      # one token, every expert once
     (37, 768, 256, 32, 3, 14, 0.0),    # most experts empty or single-row
+    # experts near the 64-row split between the skinny and the tiled grouped kernels
+    (130, 256, 256, 2, 1, 14, 0.0),
+    (200, 512, 256, 5, 2, 12, 0.5),
 ])
 def test_moe_prefill_vs_oracle(gpu, oracle, T, H, EFF, E, k, down_type, skew):
     rng = np.random.default_rng(T * 1000 + E)
