@@ -341,8 +341,8 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
         const int e = t >> 16, nt = t & 0xFFFF;
         n_rows = g.counts[e];
         row_base = g.offsets[e];
-        j0 = nt * kBN;
-        if (min(kBN, n_rows - j0) <= g.skip_upto) return;  // uniform: a skinny tile
+        j0 = nt * kGroupTile;
+        if (min(kGroupTile, n_rows - j0) <= g.skip_upto) return;  // uniform: a skinny tile
         i0 = blockIdx.x * (MODE == kModeSwiGLU ? kBM / 2 : kBM);
         Wm = g.W + (size_t)e * g.expert_stride + g.w_off;
         Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
@@ -959,8 +959,8 @@ __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmArgs g) {
     if ((int)blockIdx.y >= g.tiles[-1]) return;
     const int tl = g.tiles[blockIdx.y];
     const int e = tl >> 16, nt = tl & 0xFFFF;
-    const int n_rows = g.counts[e], row_base = g.offsets[e], j0 = nt * kBN;
-    const int nvalid = min(kBN, n_rows - j0);
+    const int n_rows = g.counts[e], row_base = g.offsets[e], j0 = nt * kGroupTile;
+    const int nvalid = min(kGroupTile, n_rows - j0);
     if (nvalid > kSkTok) return;  // uniform: the tiled kernel's tile
     // one instantiation per count of 16-row column tiles, so every MFMA is unconditional
     switch ((nvalid + 15) >> 4) {
@@ -1013,6 +1013,7 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
         else MNEMO_SKINNY(kTypeQ6K, kModeGrouped);
     }
 #undef MNEMO_SKINNY
+    if (kGroupTile <= kSkTok) return check_launch("gemm_grouped");  // no tile is left
     if (swiglu) launch_mode<kModeSwiGLU, false>(type, false, dim3((M + kBM / 2 - 1) / (kBM / 2), max_tiles, 1), g, stream);
     else launch_mode<kModeGrouped, false>(type, false, dim3((M + kBM - 1) / kBM, max_tiles, 1), g, stream);
     return check_launch("gemm_grouped");

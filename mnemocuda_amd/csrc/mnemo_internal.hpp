@@ -6,6 +6,16 @@
 
 namespace mnemo {
 
+// Token rows per tile of a grouped (MoE prefill) GEMM launch, the unit of the tile list the
+// routing writes.  64: every tile fits the skinny grouped kernel, and an expert with more
+// tokens is read once per 64 of them (measured 0.81 ms for the cfg5 prefill against 0.91 ms
+// with 128-row tiles, whose large tiles went to the tiled kernel).  Building with
+// -DMNEMO_MOE_TILE=128 restores that split.
+#ifndef MNEMO_MOE_TILE
+#define MNEMO_MOE_TILE 64
+#endif
+constexpr int kGroupTile = MNEMO_MOE_TILE;
+
 // Error codes reported through mnemo_last_error() (include/mnemo_kernels.h).
 constexpr int kOk = 0;
 constexpr int kErrBadArg = 1;

@@ -17,7 +17,7 @@
 //   rank    T*k ints   (rank of a pair within its expert; -1 for dropped slots)
 //   inv     T*k ints   (pair -> expert-sorted row, -1 for dropped slots)
 //   perm    T*k ints   (expert-sorted row -> token)
-//   tiles   1 + E + ceil(T*k/128) ints (count, then (expert << 16) | token tile)
+//   tiles   1 + E + ceil(T*k/kGroupTile) ints (count, then (expert << 16) | token tile)
 //   act     T*k rows of eff fp32 (SwiGLU output)
 //   acts    T*k staged rows of Q8_1(act), actun: their 2^e_row
 //   down    T*k rows of hidden fp32
@@ -43,7 +43,7 @@ int launch_router_topk(const float *w, const float *x, const float *nw, float ep
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
 constexpr int kMaxMoeExperts = 512;
-constexpr int kMoeTileRows = 128;  // token rows per GEMM tile (kBN of gemm.hip)
+constexpr int kMoeTileRows = kGroupTile;  // token rows per grouped GEMM tile
 
 struct MoeLayout {
     size_t xs, xun, counts, offsets, rank, inv, perm, tiles, act, acts, actun, down, total;
