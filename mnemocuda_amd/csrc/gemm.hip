@@ -703,7 +703,12 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
 constexpr int kSkThreads = 512;  // 8 waves
 constexpr int kSkWaves = kSkThreads / 64;
 constexpr int kSkTok = MNEMO_SKTOK;       // rows per tile served here: 4 column tiles of 16
-constexpr int kSkR = 2;          // 16-row MFMA tiles per wave (SwiGLU: 1 gate + 1 up)
+// weight rows per wave: SwiGLU one gate and one up tile of 16 (same features); grouped
+#ifndef MNEMO_SK_RPLAIN
+#define MNEMO_SK_RPLAIN 2
+#endif
+template <int MODE>
+constexpr int sk_rows_per_wave() { return MODE == kModeSwiGLU ? 32 : 16 * MNEMO_SK_RPLAIN; }
 template <int TYPE>
 __device__ __forceinline__ int sk_k0(int t, int q) {
     if (TYPE == kTypeQ4K) {
@@ -829,10 +834,10 @@ __device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r
 // base + 16l).  The wait for those LDS writes before the barrier also covers the weight
 // loads issued after them (memory loads complete in issue order), so one block ahead is
 // what the pipeline can hold.
-template <int TYPE, int NB>
-__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int wave, const uint8_t *const (&wrow)[kSkR],
+template <int TYPE, int NB, int R>
+__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int wave, const uint8_t *const (&wrow)[R],
                                          const _Float16 *const (&arow)[NB], _Float16 (*bs)[kSkTok * 256],
-                                         const SkRaw (&cur)[kSkR], SkRaw (&nxt)[kSkR], f4 (&acc)[kSkR][NB]) {
+                                         const SkRaw (&cur)[R], SkRaw (&nxt)[R], f4 (&acc)[R][NB]) {
     // past the end the last block is loaded again (into the idle buffer and registers)
     const int kn = min(k + 1, nkb - 1);
 #pragma unroll
@@ -841,13 +846,13 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int 
                                          (__attribute__((address_space(3))) void *)&bs[(k + 1) & 1][(2 * wave + 16 * i) * 256],
                                          16, 0, 0);
 #pragma unroll
-    for (int a = 0; a < kSkR; a++) sk_load<TYPE>(wrow[a] + (size_t)kn * bbytes, q, nxt[a]);
+    for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a] + (size_t)kn * bbytes, q, nxt[a]);
     // keep the loads here, ahead of the multiplication (the scheduler would otherwise sink
     // them past it to save registers, and nothing would be in flight during the MFMAs)
     __builtin_amdgcn_sched_barrier(0);
-    h2 A[kSkR][4], B[kSkR][4];
+    h2 A[R][4], B[R][4];
 #pragma unroll
-    for (int a = 0; a < kSkR; a++) sk_scales<TYPE>(cur[a], q, A[a], B[a]);
+    for (int a = 0; a < R; a++) sk_scales<TYPE>(cur[a], q, A[a], B[a]);
     const _Float16 *bb = bs[k & 1];
 #pragma unroll
     for (int t = 0; t < 8; t++) {
@@ -855,7 +860,7 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int 
 #pragma unroll
         for (int b = 0; b < NB; b++) bf[b] = *(const h8 *)(bb + sk_slot(16 * b + c, 4 * t + q));
 #pragma unroll
-        for (int a = 0; a < kSkR; a++) {
+        for (int a = 0; a < R; a++) {
             const h8 af = sk_operand<TYPE>(cur[a], t, A[a], B[a]);
 #pragma unroll
             for (int b = 0; b < NB; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[a][b], 0, 0, 0);
@@ -867,7 +872,8 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int 
 template <int TYPE, int MODE, int NB>
 __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok * 256], int wave, int lane, int tid,
                                         int e, int j0, int n_rows, int row_base) {
-    constexpr int H = kSkR / 2;  // SwiGLU: gate tiles 0 .. H-1, up tiles H .. 2H-1
+    constexpr int R = sk_rows_per_wave<MODE>() / 16;
+    constexpr int H = R / 2;  // SwiGLU: gate tiles 0 .. H-1, up tiles H .. 2H-1
     const int q = lane >> 4, c = lane & 15;
     const int K = g.K, nkb = K / 256;
     const int bbytes = TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes;
@@ -876,19 +882,19 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
     const uint8_t *Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
 
     // this lane's weight row of each row tile (rows past M re-read the last)
-    const uint8_t *wrow[kSkR];
+    const uint8_t *wrow[R];
     int base;  // SwiGLU: first feature of the wave; grouped: first row
     if (MODE == kModeSwiGLU) {
         base = (blockIdx.x * kSkWaves + wave) * (16 * H);
 #pragma unroll
-        for (int a = 0; a < kSkR; a++) {
+        for (int a = 0; a < R; a++) {
             const int f = min(base + 16 * (a % H) + c, g.M - 1);
             wrow[a] = (a < H ? Wm : Wm2) + (size_t)f * wrow_bytes;
         }
     } else {
-        base = (blockIdx.x * kSkWaves + wave) * (16 * kSkR);
+        base = (blockIdx.x * kSkWaves + wave) * (16 * R);
 #pragma unroll
-        for (int a = 0; a < kSkR; a++) wrow[a] = Wm + (size_t)min(base + 16 * a + c, g.M - 1) * wrow_bytes;
+        for (int a = 0; a < R; a++) wrow[a] = Wm + (size_t)min(base + 16 * a + c, g.M - 1) * wrow_bytes;
     }
     // activation staging role: physical slot tid % 32 of rows r = tid/32 + 16i, i < NB, which
     // holds the logical slot (tid % 32) ^ (r % 32)
@@ -901,25 +907,25 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
         const int idx = MODE == kModeSwiGLU ? g.perm[row_base + j] : row_base + j;
         arow[i] = (const _Float16 *)g.A + (size_t)idx * K + sk_k0<TYPE>(u >> 2, u & 3);
     }
-    f4 acc[kSkR][NB];
+    f4 acc[R][NB];
 #pragma unroll
-    for (int a = 0; a < kSkR; a++)
+    for (int a = 0; a < R; a++)
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-    SkRaw r0[kSkR], r1[kSkR];
+    SkRaw r0[R], r1[R];
 #pragma unroll
     for (int i = 0; i < NB; i++)
         __builtin_amdgcn_global_load_lds((const void *)arow[i],
                                          (__attribute__((address_space(3))) void *)&bs[0][(2 * wave + 16 * i) * 256], 16,
                                          0, 0);
 #pragma unroll
-    for (int a = 0; a < kSkR; a++) sk_load<TYPE>(wrow[a], q, r0[a]);
+    for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a], q, r0[a]);
     __syncthreads();
     // two raw slots, the loop unrolled by two so that both are static
     for (int k = 0; k < nkb; k += 2) {
-        sk_block<TYPE, NB>(k, nkb, bbytes, q, c, wave, wrow, arow, bs, r0, r1, acc);
+        sk_block<TYPE, NB, R>(k, nkb, bbytes, q, c, wave, wrow, arow, bs, r0, r1, acc);
         if (k + 1 >= nkb) break;
-        sk_block<TYPE, NB>(k + 1, nkb, bbytes, q, c, wave, wrow, arow, bs, r1, r0, acc);
+        sk_block<TYPE, NB, R>(k + 1, nkb, bbytes, q, c, wave, wrow, arow, bs, r1, r0, acc);
     }
 
     // D layout: lane holds weight rows 4q + e of each 16-row tile, token column c
@@ -942,7 +948,7 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
             }
         } else {
 #pragma unroll
-            for (int a = 0; a < kSkR; a++) {
+            for (int a = 0; a < R; a++) {
                 const int i = base + 16 * a + 4 * q;
 #pragma unroll
                 for (int x = 0; x < 4; x++)
@@ -1002,7 +1008,7 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
     g.tiles = tiles;
     g.skip_upto = kSkTok;
     // tiles of at most kSkTok rows: the skinny kernel; the rest: the tiled kernel
-    const int sk_rows = swiglu ? kSkR / 2 * 16 * kSkWaves : kSkR * 16 * kSkWaves;
+    const int sk_rows = swiglu ? sk_rows_per_wave<kModeSwiGLU>() / 2 * kSkWaves : sk_rows_per_wave<kModeGrouped>() * kSkWaves;
     const dim3 sk_grid((M + sk_rows - 1) / sk_rows, max_tiles, 1);
 #define MNEMO_SKINNY(T_, M_) hipLaunchKernelGGL((gemm_skinny_kernel<T_, M_>), sk_grid, dim3(kSkThreads), 0, stream, g)
     if (swiglu) {
