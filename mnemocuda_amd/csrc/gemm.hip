@@ -700,7 +700,11 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
 #ifndef MNEMO_SKTOK
 #define MNEMO_SKTOK 64
 #endif
-constexpr int kSkThreads = 512;  // 8 waves
+#ifndef MNEMO_SK_THREADS
+#define MNEMO_SK_THREADS 512
+#endif
+constexpr int kSkThreads = MNEMO_SK_THREADS;  // 8 waves
+constexpr int kSkStage = kSkThreads / 32;        // activation rows staged per pass
 constexpr int kSkWaves = kSkThreads / 64;
 constexpr int kSkTok = MNEMO_SKTOK;       // rows per tile served here: 4 column tiles of 16
 // weight rows per wave: SwiGLU one gate and one up tile of 16 (same features); grouped
@@ -836,14 +840,14 @@ __device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r
 // what the pipeline can hold.
 template <int TYPE, int NB, int R>
 __device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int wave, const uint8_t *const (&wrow)[R],
-                                         const _Float16 *const (&arow)[NB], _Float16 (*bs)[kSkTok * 256],
+                                         const _Float16 *const (&arow)[NB * 16 / kSkStage], _Float16 (*bs)[kSkTok * 256],
                                          const SkRaw (&cur)[R], SkRaw (&nxt)[R], f4 (&acc)[R][NB]) {
     // past the end the last block is loaded again (into the idle buffer and registers)
     const int kn = min(k + 1, nkb - 1);
 #pragma unroll
-    for (int i = 0; i < NB; i++)
+    for (int i = 0; i < NB * 16 / kSkStage; i++)
         __builtin_amdgcn_global_load_lds((const void *)(arow[i] + kn * 256),
-                                         (__attribute__((address_space(3))) void *)&bs[(k + 1) & 1][(2 * wave + 16 * i) * 256],
+                                         (__attribute__((address_space(3))) void *)&bs[(k + 1) & 1][(2 * wave + kSkStage * i) * 256],
                                          16, 0, 0);
 #pragma unroll
     for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a] + (size_t)kn * bbytes, q, nxt[a]);
@@ -896,13 +900,13 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
 #pragma unroll
         for (int a = 0; a < R; a++) wrow[a] = Wm + (size_t)min(base + 16 * a + c, g.M - 1) * wrow_bytes;
     }
-    // activation staging role: physical slot tid % 32 of rows r = tid/32 + 16i, i < NB, which
+    // activation staging role: physical slot tid % 32 of rows r = tid/32 + kSkStage i, which
     // holds the logical slot (tid % 32) ^ (r % 32)
     const int sr0 = tid >> 5;
-    const _Float16 *arow[NB];
+    const _Float16 *arow[NB * 16 / kSkStage];
 #pragma unroll
-    for (int i = 0; i < NB; i++) {
-        const int r = sr0 + 16 * i, u = (tid & 31) ^ (r & 31);
+    for (int i = 0; i < NB * 16 / kSkStage; i++) {
+        const int r = sr0 + kSkStage * i, u = (tid & 31) ^ (r & 31);
         const int j = min(j0 + r, n_rows - 1);
         const int idx = MODE == kModeSwiGLU ? g.perm[row_base + j] : row_base + j;
         arow[i] = (const _Float16 *)g.A + (size_t)idx * K + sk_k0<TYPE>(u >> 2, u & 3);
@@ -914,10 +918,10 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
         for (int b = 0; b < NB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
     SkRaw r0[R], r1[R];
 #pragma unroll
-    for (int i = 0; i < NB; i++)
+    for (int i = 0; i < NB * 16 / kSkStage; i++)
         __builtin_amdgcn_global_load_lds((const void *)arow[i],
-                                         (__attribute__((address_space(3))) void *)&bs[0][(2 * wave + 16 * i) * 256], 16,
-                                         0, 0);
+                                         (__attribute__((address_space(3))) void *)&bs[0][(2 * wave + kSkStage * i) * 256],
+                                         16, 0, 0);
 #pragma unroll
     for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a], q, r0[a]);
     __syncthreads();
