@@ -1,33 +1,40 @@
 // gemm.hip -- Q4_K / Q6_K x Q8_1 GEMM for prefill and batched experts (gfx950 MFMA).
 //
-// Semantics (MnemoCUDA gemm_q4k.cu:103-112, 164-166, 194):
-//   out[j*M + i] = sum_k deq(W)[i][k] * deq(A)[j][k]
-// with W GGUF blocks [M][K] and A the Q8_1 MMQ activations [N][K/128] x 144 B.
+// Semantics (MnemoCUDA gemm_q4k.cu:103-112, 164-166, 194), per 32-value sub-block s:
+//   Q4_K: out[j*M + i] = sum_s (d*sc_s)_i * d8_js * (sum_{k in s} q_ik * q8_jk) - (dmin*m_s)_i * ds_js
+//   Q6_K: out[j*M + i] = sum_s d_i * d8_js * (sum over the two 16-value groups g of s of
+//                                            sc_g * sum_{k in g} (q_ik - 32) * q8_jk)
+// with W GGUF blocks [M][K], the activations Q8_1 MMQ blocks [N][K/128] x 144 B
+// (half2 (d8, ds) per 32 values, ds = d8 * sum of the unquantized values), and the output
+// column-major [N][M].  The scales d*sc and dmin*m are exact in fp32 (the reference rounds
+// them to f16 in registers, gemm_q4k.cu:106-111; this build keeps the GEMV's fp32
+// dequantisation, kernels.cu:114-136).
 //
-// Design: both operands become f16 tiles in LDS multiplied with v_mfma_f32_16x16x32_f16
-// (fp32 accumulate).  The per-32 scales of both operands are folded into the values, so
-// the MFMA accumulates across the whole K without a per-sub-block fp32 rescale (an int8
-// MFMA would need one cvt + two FMAs per output per 32-K step, several times the MFMA
-// time in VALU work).
-//   * Activation values d8*q8 are held in f16 scaled per row by 2^-e_row, an exact power
-//     of two chosen so that they stay inside the f16 range (127*max d8*2^-e <= 2^15); the
-//     epilogue multiplies by 2^e.  The reference entry points (cuda_gemm_q4k,
-//     mnemo_gemm_q6k) convert Q8_1 blocks per tile and allocate nothing; the grouped
-//     expert path stages each activation row once in that f16 form (stage_* kernels, in
-//     the caller's workspace) and copies tiles.
-//   * Weights are dequantised on the fly in packed f16 arithmetic: a quant q placed under
-//     the exponent byte 0x64 is the f16 1024 + q; subtracting 1024 (or 1056 for Q6_K's
-//     q - 32) is exact; then one fma with (f16(d*sc), f16(-dmin*m)) (Q4_K) or one multiply
-//     by f16(d*sc) (Q6_K).  Expected relative L2 error vs the fp64 product: ~4e-4.
-//   * Workgroup tile 128 weight rows x 128 tokens (8 waves: quadrants of 64 x 64 = 4 x 4 MFMA
-//     tiles, each quadrant split over two waves by K half),
-//     K step 64 (one Q4_K nibble group, one Q6_K ql group).  Raw weight blocks and
-//     activation chunks are loaded into registers ahead of their conversion; f16 tiles
-//     rotate through three LDS buffers (XOR-swizzled, conflict-free); one barrier per step.
-//   * When the tile grid covers at most half of the CUs, K is split across workgroups
-//     and the partial tiles are summed with fp32 atomics into the output, which a small
-//     fill kernel zeroes first; the tiles pass through LDS so that each atomic instruction
-//     covers 64 consecutive outputs of one token.
+// Exact integer sub-block sums on f16 matrix cores.
+//   * Operands are integers that f16 holds exactly: A = sc * q (Q4_K, <= 63 * 15 = 945) and
+//     B = q8 (|q8| <= 127).  A 16x16x32 f16 MFMA over one sub-block sums 32 exact products
+//     below 2^22 in fp32, so its result t is the exact integer sub-block sum.  Q6_K's
+//     sc * (q - 32) reaches 4096 in magnitude, where f16 holds only even integers: it is
+//     split into two exact planes, (sc - b) * (q - 32) (even) and b * (q - 32) with
+//     b = sc & 1, and the two MFMAs chain into t (|t| < 2^24, still exact).
+//   * The fp32 rescale is a running scale: the accumulator holds the sum in units of the
+//     current (row scale d) x (token scale d8), and every sub-block does acc = acc * rho + t
+//     with rho = d8_prev / d8 of the token (one fma per output per sub-block); at a
+//     super-block boundary the rows' acc is multiplied by d_prev / d once.  The epilogue
+//     multiplies by the last d8 * d.  A zero scale leaves the running scale unchanged and
+//     zeroes its block's operand (its products are zero).
+//   * Q4_K's min term, sum_s -(dmin*m_s) * ds_js, is one more product over the sub-block
+//     index: -dmin*m (an f16 times a 6-bit integer, 17 significant bits) is split into an
+//     f16 hi + lo pair that is exact, ds is an f16 already, and two MFMAs per 32 sub-blocks
+//     add it to the finished absolute accumulator.
+//   Against the fp64 value the only roundings are the fp32 fma per output per sub-block
+//   and the rho quotients (measured ~1e-7 relative L2).
+//
+// An int8 MFMA does not fit this product on gfx950: v_mfma_i32_16x16x64_i8 sums 64 values,
+// two sub-blocks with different token scales, and the 32-deep v_mfma_i32_16x16x32_i8 runs
+// at the f16 MFMA's rate (16 cycles for 16x16x32, measured) while needing three VALU
+// operations per output per sub-block (int -> float, the product of the row and token
+// scales, the fma) where the exact f16 form needs one.
 #include <algorithm>
 
 #include "mnemo_common.hpp"
@@ -39,449 +46,530 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKS = 64;              // K per step
+// ------------------------------------------------------------------ operand conversions
+// Byte selectors placing bytes (0, 1) / (2, 3) of a dword under the f16 exponent byte 0x64:
+// the pair (1024 + b0, 1024 + b1) exactly.
+constexpr uint32_t kSelLo = 0x04010400u, kSelHi = 0x04030402u;
 
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
-    h2 v = {(_Float16)a, (_Float16)b};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-// ------------------------------------------------------------------ raw loads (step k)
-// 512 loader threads: thread t owns row (weights) / token (activations) t/4 and quarter
-// q = t%4 (16 values) of the 64-wide K step.
-struct RawW {
-    uint4 a, b;       // Q4_K: a = header (d, dmin, 12 scale bytes), b = 16 qs bytes
-                      // Q6_K: a = 16 ql bytes, b = 16 qh bytes
-    uint32_t s, dd;   // Q6_K: the int8 scale of the 16 values, f16 d
-};
-// Activation quarter: staged f16 values, or 16 int8 of a raw Q8_1 sub-block.
-template <bool Q8>
-struct RawA {
-    uint4 a, b;  // 16 f16 values
-};
-template <>
-struct RawA<true> {
-    uint4 a;      // 16 int8
-    uint32_t ds;  // half2 (d, d*sum) of their 32-value sub-block
-};
-
-// Q4_K step ks: super-block ks/4, nibble group g = ks%4 (qs bytes 32g..32g+31).  Quarter q:
-// qs bytes 32g + 16(q%2) .. +15, low nibbles (sub-block 2g) for q < 2, else high (2g+1).
-__device__ __forceinline__ void load_w_q4k(const uint8_t *__restrict__ wrow, int ks, int q, RawW &r) {
-    const uint8_t *blk = wrow + (size_t)(ks >> 2) * kQ4KBytes;
-    r.a = ld16(blk);
-    r.b = ld16(blk + 16 + 32 * (ks & 3) + 16 * (q & 1));
-}
-
-// Q6_K step ks: values 64(ks%4) .. +63 of super-block ks/4, half hh = (ks%4)/2, groups
-// 2(ks%2) .. +1.  Quarter q: group grp = 2(ks%2) + q/2, values 16(q%2) .. +15 of it: ql bytes
-// 64hh + 32(q/2) + 16(q%2) (low nibbles if grp < 2, else high), qh bytes 32hh + 16(q%2) at
-// bit 2grp, scale byte 8hh + 2grp + q%2.
-__device__ __forceinline__ void load_w_q6k(const uint8_t *__restrict__ wrow, int ks, int q, RawW &r) {
-    const uint8_t *blk = wrow + (size_t)(ks >> 2) * kQ6KBytes;
-    const int g = ks & 3, hh = g >> 1, grp = 2 * (g & 1) + (q >> 1);
-    r.a = ld16_a2(blk + 64 * hh + 32 * (q >> 1) + 16 * (q & 1));
-    r.b = ld16_a2(blk + 128 + 32 * hh + 16 * (q & 1));
-    uint8_t sc;
-    uint16_t dd;
-    __builtin_memcpy(&sc, blk + 192 + 8 * hh + 2 * grp + (q & 1), 1);
-    __builtin_memcpy(&dd, blk + 208, 2);
-    r.s = sc;
-    r.dd = dd;
-}
-
-// Activations of step ks, quarter q: values 64ks + 16q .. +15 of the row (staged f16 row,
-// or the row's Q8_1 MMQ blocks: block v/128, sub-block (v/32)%4).
-__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int q, RawA<false> &r) {
-    const _Float16 *p = (const _Float16 *)arow + ks * kKS + 16 * q;
-    r.a = ld16((const uint8_t *)(p));
-    r.b = ld16((const uint8_t *)(p + 8));
-}
-__device__ __forceinline__ void load_a(const void *__restrict__ arow, int ks, int q, RawA<true> &r) {
-    const int v0 = ks * kKS + 16 * q;
-    const uint8_t *blk = (const uint8_t *)arow + (size_t)(v0 >> 7) * kQ81Bytes;
-    const int sub = (v0 >> 5) & 3;
-    __builtin_memcpy(&r.ds, blk + 4 * sub, 4);
-    r.a = ld16(blk + 16 + (v0 & 127));
-}
-
-// ------------------------------------------------------------------ LDS tiles
-// f16 tiles of 64 K-columns per row = 8 chunks of 16 B, stored without padding with the
-// chunk index XOR-ed by (row % 8): the 8 rows read by one phase of an MFMA fragment load
-// then fall in 8 different chunks (no bank conflicts), and conversion stores spread too.
-__device__ __forceinline__ int tile_off(int row, int chunk) { return row * kKS + ((chunk ^ (row & 7)) << 3); }
-
-__device__ __forceinline__ void put16(_Float16 *tile, int row, int chunk, uint32_t a, uint32_t b, uint32_t c,
-                                      uint32_t d) {
-    *(uint4 *)(tile + tile_off(row, chunk)) = make_uint4(a, b, c, d);
-}
-
-// ------------------------------------------------------------------ conversion to LDS
-// Two byte-sized quants (bytes selected by `sel` from v) as the f16 pair 1024 + q.
 __device__ __forceinline__ h2 magic_pair(uint32_t v, uint32_t sel) {
     return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, sel));
 }
-// (q - 1024 + 1024) * a + b for two quants, in packed f16 (exact subtraction, one rounding)
-__device__ __forceinline__ uint32_t dq_fma(uint32_t v, uint32_t sel, h2 a, h2 b) {
-    const h2 off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    const h2 q = magic_pair(v, sel) + off;
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q, a, b));
+// q * sc for two 4-bit quants: (1024 + q) * sc - 1024 * sc in one fused f16 fma, whose
+// result q * sc <= 945 is an integer f16 holds exactly
+__device__ __forceinline__ uint32_t q4_scaled(uint32_t v, uint32_t sel, h2 sc, h2 nsc) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(magic_pair(v, sel), sc, nsc));
 }
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
-// Row exponent e >= 0 with 127 * dmax * 2^-e <= 2^15 (dmax = largest |d8| of the row).
-__device__ __forceinline__ int row_exponent(float dmax) {
-    int ex = 0;
-    frexpf(dmax * 127.0f, &ex);  // 127 * dmax < 2^ex
-    return max(0, ex - 15);
-}
-
-// 8 int8 quants (two dwords) times the f16 scale d: q8 ^ 0x80 under the exponent byte 0x64
-// is 1024 + q8 + 128 exactly; subtracting 1152 gives q8; the product is rounded once.
-__device__ __forceinline__ void q8x4_to_f16(uint32_t v, h2 d2, uint32_t &o0, uint32_t &o1) {
+// q8 as f16 integers: q8 ^ 0x80 under 0x64 is 1152 + q8 exactly
+__device__ __forceinline__ void q8x4_exact(uint32_t v, uint32_t &o0, uint32_t &o1) {
     const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     const uint32_t u = v ^ 0x80808080u;
-    o0 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04010400u) + off) * d2);
-    o1 = __builtin_bit_cast(uint32_t, (magic_pair(u, 0x04030402u) + off) * d2);
+    o0 = __builtin_bit_cast(uint32_t, magic_pair(u, kSelLo) + off);
+    o1 = __builtin_bit_cast(uint32_t, magic_pair(u, kSelHi) + off);
 }
+// Q6_K: two 6-bit quant bytes as the f16 pair (q - 32), exactly
+__device__ __forceinline__ h2 q6_centered(uint32_t v, uint32_t sel) {
+    const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    return magic_pair(v, sel) + off;
+}
+__device__ __forceinline__ uint32_t h2u(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 
 // byte i of the 12 packed scale bytes held in three dwords
 __device__ __forceinline__ uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
     const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
     return (w >> (8 * (i & 3))) & 0xFFu;
 }
-
-// Q4_K quarter q of step ks: sub-block j = 2(ks%4) + q/2 (get_scale_min_k4, kernels.cu:45-53),
-// K columns 16q .. 16q+15 of the step (chunks 2q, 2q+1).
-__device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int q, _Float16 *tile, int row) {
-    const int j = 2 * (ks & 3) + (q >> 1);
-    const uint32_t s0 = r.a.y, s1 = r.a.z, s2 = r.a.w;
-    uint32_t sc, m;
-    if ((ks & 3) < 2) {  // j < 4, written in terms of the step alone: uniform over the wave
+// (sc, m) of sub-block j (get_scale_min_k4, kernels.cu:45-53)
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, uint32_t &sc,
+                                              uint32_t &m) {
+    if (j < 4) {
         sc = sbyte(s0, s1, s2, j) & 63;
         m = sbyte(s0, s1, s2, j + 4) & 63;
     } else {
         sc = (sbyte(s0, s1, s2, j + 4) & 15) | ((sbyte(s0, s1, s2, j - 4) >> 6) << 4);
         m = (sbyte(s0, s1, s2, j + 4) >> 4) | ((sbyte(s0, s1, s2, j) >> 6) << 4);
     }
-    const float d = h2f(r.a.x & 0xFFFFu), dmin = h2f(r.a.x >> 16);
-    const _Float16 a = (_Float16)(d * (float)sc), b = (_Float16)(-dmin * (float)m);
-    const h2 A = {a, a}, B = {b, b};
-    const int sh = 4 * (q >> 1);
-    const uint32_t w[4] = {(r.b.x >> sh) & 0x0F0F0F0Fu, (r.b.y >> sh) & 0x0F0F0F0Fu, (r.b.z >> sh) & 0x0F0F0F0Fu,
-                           (r.b.w >> sh) & 0x0F0F0F0Fu};
-    uint32_t o[8];
+}
+
+// Q4_K min-term operand of one super-block: for its 8 sub-blocks, -dmin * m_s as an exact
+// f16 hi + lo pair (dmin is an f16, m a 6-bit integer: 17 significant bits).
+__device__ __forceinline__ void q4k_min_operand(const uint4 &hdr, h8 &hi, h8 &lo) {
+    const float dmin = h2f(hdr.x >> 16);
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        o[2 * k] = dq_fma(w[k], 0x04010400u, A, B);
-        o[2 * k + 1] = dq_fma(w[k], 0x04030402u, A, B);
+    for (int s = 0; s < 8; s++) {
+        uint32_t sc, m;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, s, sc, m);
+        const float v = -dmin * (float)m;  // exact in fp32
+        const _Float16 h = (_Float16)v;
+        hi[s] = h;
+        lo[s] = (_Float16)(v - (float)h);  // the remainder has at most 6 significant bits
     }
-    put16(tile, row, 2 * q, o[0], o[1], o[2], o[3]);
-    put16(tile, row, 2 * q + 1, o[4], o[5], o[6], o[7]);
+}
+// the ds halves of the 8 sub-blocks of a super-block: two Q8_1 block headers
+__device__ __forceinline__ h8 ds_operand(const uint4 &b0, const uint4 &b1) {
+    const uint32_t sel = 0x07060302u;  // the high halves of two dwords
+    const uint4 u = make_uint4(__builtin_amdgcn_perm(b0.y, b0.x, sel), __builtin_amdgcn_perm(b0.w, b0.z, sel),
+                               __builtin_amdgcn_perm(b1.y, b1.x, sel), __builtin_amdgcn_perm(b1.w, b1.z, sel));
+    return __builtin_bit_cast(h8, u);
 }
 
-// Q6_K quarter q of step ks: group grp = 2(ks%2) + q/2, its values 16(q%2) .. +15; K columns
-// 16q .. 16q+15 of the step (chunks 2q, 2q+1).
-__device__ __forceinline__ void store_w_q6k(const RawW &r, int ks, int q, _Float16 *tile, int row) {
-    const int grp = 2 * (ks & 1) + (q >> 1);
-    const _Float16 sc = (_Float16)(h2f(r.dd) * (float)(int8_t)(r.s & 0xFF));
-    const h2 S = {sc, sc};
-    const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-    const uint32_t ql[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
-    const uint32_t qh[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-    const int shl = grp >= 2 ? 4 : 0;
-    uint32_t o[8];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        // 6-bit q in bits 0..5 of each byte
-        const uint32_t lo = (ql[k] >> shl) & 0x0F0F0F0Fu;
-        const uint32_t hi = (2 * grp <= 4 ? (qh[k] << (4 - 2 * grp)) : (qh[k] >> (2 * grp - 4))) & 0x30303030u;
-        const uint32_t v = lo | hi;
-        o[2 * k] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04010400u) + off) * S);
-        o[2 * k + 1] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04030402u) + off) * S);
-    }
-    put16(tile, row, 2 * q, o[0], o[1], o[2], o[3]);
-    put16(tile, row, 2 * q + 1, o[4], o[5], o[6], o[7]);
+// Workgroup barrier for LDS hand-offs that leaves global loads in flight.  __syncthreads()
+// is a release/acquire fence plus s_barrier, and the release makes every wave wait for all
+// of its outstanding global loads (vmcnt(0)) -- the loads of the next steps included, which
+// drains the prefetch pipeline at every step.  Here only the wave's own LDS accesses
+// (lgkmcnt) are waited for; the asm's memory clobber keeps the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The same after LDS writes made by global_load_lds: those complete with the wave's vector
+// memory counter, so the wave waits until at most N vector memory operations (the ones it
+// issued after the LDS loads) are outstanding.
+template <int N>
+__device__ __forceinline__ void lds_dma_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+    lds_barrier();
 }
 
-// Quarter q: K columns 16q .. 16q+15 (chunks 2q, 2q+1) of the activation row.
-__device__ __forceinline__ void store_a(const RawA<false> &r, int q, _Float16 *tile, int row, float) {
-    put16(tile, row, 2 * q, r.a.x, r.a.y, r.a.z, r.a.w);
-    put16(tile, row, 2 * q + 1, r.b.x, r.b.y, r.b.z, r.b.w);
+__device__ __forceinline__ f4 mfma(const h8 &a, const h8 &b, const f4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-// Raw Q8_1: d8 * 2^-e (exact) times q8, as the staging kernel computes it.
-__device__ __forceinline__ void store_a(const RawA<true> &r, int q, _Float16 *tile, int row, float as) {
-    const _Float16 d = (_Float16)(h2f(r.ds & 0xFFFF) * as);
-    const h2 d2 = {d, d};
-    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
-    uint32_t o[8];
-#pragma unroll
-    for (int k = 0; k < 4; k++) q8x4_to_f16(w[k], d2, o[2 * k], o[2 * k + 1]);
-    put16(tile, row, 2 * q, o[0], o[1], o[2], o[3]);
-    put16(tile, row, 2 * q + 1, o[4], o[5], o[6], o[7]);
+__device__ __forceinline__ f4 mfma0(const h8 &a, const h8 &b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 }
 
-// ------------------------------------------------------------------ kernel
-// Workgroup of 8 waves computes a 128 x 128 tile (weights x tokens) over one K slice
-// (blockIdx.z of `splits`).  Wave w owns rows 64*(w%2) .. +63 and tokens 64*((w/2)%2) .. +63
-// (4 x 4 MFMA tiles) and K half w/4 of every 64-wide step; the two K halves are summed
-// through LDS at the end (fixed order).  Two waves per SIMD let one wave's conversion
-// overlap the other's MFMAs.  Raw blocks are loaded into a ring of kPF register slots (the
-// loop is unrolled by lcm(kPF, 3) so every ring index is static and the waits the
-// compiler inserts count exactly the outstanding steps).  With splits > 1 the partial
-// tiles are added into the (pre-zeroed) output with fp32 atomics, in an order that may
-// differ from run to run.
-constexpr int kThreads = 512;
+// ------------------------------------------------------------------ tiled kernel
+// A workgroup computes a 128 x 128 tile (weight rows x tokens) over one K slice (blockIdx.z
+// of `splits`, whole super-blocks).  Its waves form a 2 (rows: 64 each) x kWC (tokens) x 2
+// (sub-block parity) grid: wave (wi, wj, kh) multiplies rows wi .. wi+63 with tokens
+// wj .. wj+kWTok-1 over sub-block kh of every 64-wide K step (the step's sub-blocks 2ks and
+// 2ks + 1); the two parities are summed through LDS at the end.  All threads load and
+// convert the step's weights and activations once into LDS: thread t owns weight row /
+// token t / kParts and part t % kParts (kVP values) of the step.
+#ifndef MNEMO_GEMM_THREADS
+#define MNEMO_GEMM_THREADS 512
+#endif
+constexpr int kThreads = MNEMO_GEMM_THREADS;  // 512 or 1024
+constexpr int kWaves = kThreads / 64;
 constexpr int kBM = 128, kBN = 128;
-// raw ring slots: loads run kPF-2 steps ahead of their conversion.  3 (one step of
-// lookahead, the rest hidden by the three LDS buffers) measured faster than 4-6: the deeper
-// rings cost registers (Q6_K: 246-256 VGPRs with spills at 5-6 against 202 at 3) for
-// latency the other wave of the SIMD already hides (Q6_K 4096x1536x512: 34.1 -> 32.2 us,
-// Q4_K 8192x4096x512: 65.5 -> 63.3 us, grouped MoE prefill -4 %)
-constexpr int kPF = 3;
-constexpr int kUnroll = 3;  // lcm(kPF, 3 LDS buffers)
+constexpr int kKS = 64;                // K per step
+constexpr int kWC = kWaves / 4;        // token groups
+constexpr int kWTok = kBN / kWC;       // tokens per wave
+constexpr int kNB = kWTok / 16;        // 16-token MFMA columns per wave
+constexpr int kParts = kThreads / 128; // loader parts per row and step
+constexpr int kVP = kKS / kParts;      // values per part (16 or 8)
+static_assert(kVP == 8 || kVP == 16, "loader parts of 8 or 16 values");
+// raw ring slots: loads run kPF-2 steps ahead of their conversion
+#ifndef MNEMO_GEMM_PF
+#define MNEMO_GEMM_PF 3
+#endif
+constexpr int kPF = MNEMO_GEMM_PF;
+// lcm(kPF, 3 LDS stages, 4 steps per super-block): every ring slot, stage and super-block
+// boundary of the unrolled loop is a compile-time constant
+constexpr int kUnroll = 12;
+static_assert(kUnroll % kPF == 0, "ring size must divide the unroll");
 
-// act: this thread's activation row is inside the tile's token count (rows past it are
-// neither loaded nor converted; their LDS rows only feed output columns that are dropped).
-template <int TYPE, bool Q8>
-__device__ __forceinline__ void load_step(const uint8_t *wrow, const void *arow, int ks, int h, RawW &rw,
-                                          RawA<Q8> &ra, bool act) {
-    if (TYPE == kTypeQ4K) load_w_q4k(wrow, ks, h, rw);
-    else load_w_q6k(wrow, ks, h, rw);
-    if (act) load_a(arow, ks, h, ra);
+// kVP raw bytes as dwords
+struct PartBytes {
+    uint32_t w[kVP / 4];
+};
+__device__ __forceinline__ PartBytes ld_part(const uint8_t *p) {
+    PartBytes r;
+    if constexpr (kVP == 16) {
+        const uint4 v = ld16(p);
+        r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+    } else {
+        const uint2 v = ld8(p);
+        r.w[0] = v.x; r.w[1] = v.y;
+    }
+    return r;
+}
+__device__ __forceinline__ PartBytes ld_part_a2(const uint8_t *p) {
+    PartBytes r;
+    if constexpr (kVP == 16) {
+        const uint4 v = ld16_a2(p);
+        r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+    } else {
+        const uint2 v = ld8_a2(p);
+        r.w[0] = v.x; r.w[1] = v.y;
+    }
+    return r;
 }
 
-template <int TYPE, bool Q8>
-__device__ __forceinline__ void store_step(const RawW &rw, const RawA<Q8> &ra, int ks, int h, _Float16 *at,
-                                           _Float16 *bt, int row, float as, bool act) {
-    if (TYPE == kTypeQ4K) store_w_q4k(rw, ks, h, at, row);
-    else store_w_q6k(rw, ks, h, at, row);
-    if (act) store_a(ra, h, bt, row, as);
+struct RawW {
+    uint4 h;         // Q4_K: the super-block header (d, dmin, 12 scale bytes)
+    PartBytes a, b;  // Q4_K: a = qs bytes;  Q6_K: a = ql bytes, b = qh bytes
+    uint32_t s, dd;  // Q6_K: the int8 scale of the values, f16 d
+};
+struct RawA {
+    PartBytes q;  // int8 quants
+    uint32_t ds;  // half2 (d8, ds) of their 32-value sub-block
+};
+
+// Part p of step ks covers K columns kVP*p .. +kVP-1 of the step: sub-block 2(ks%4) + c/32 of
+// super-block ks/4, positions c%32 .. (c = kVP*p).
+// Q4_K: qs bytes 32(ks%4) + c%32 .., the low (c < 32) or high nibbles.
+__device__ __forceinline__ void load_w_q4k(const uint8_t *__restrict__ wrow, int ks, int p, RawW &r) {
+    const uint8_t *blk = wrow + (size_t)(ks >> 2) * kQ4KBytes;
+    r.h = ld16(blk);
+    r.a = ld_part(blk + 16 + 32 * (ks & 3) + ((kVP * p) & 31));
+}
+// Q6_K: values v0 = 64(ks%4) + c of the super-block: half hh = (ks%4)/2, group
+// grp = 2(ks%2) + c/32, positions l0 = c%32: ql bytes 64hh + 32(grp%2) + l0 (high nibbles if
+// grp >= 2), qh bytes 32hh + l0 at bit 2grp, scale byte 8hh + 2grp + l0/16.
+__device__ __forceinline__ void load_w_q6k(const uint8_t *__restrict__ wrow, int ks, int p, RawW &r) {
+    const uint8_t *blk = wrow + (size_t)(ks >> 2) * kQ6KBytes;
+    const int c = kVP * p, hh = (ks & 3) >> 1, grp = 2 * (ks & 1) + (c >> 5), l0 = c & 31;
+    r.a = ld_part_a2(blk + 64 * hh + 32 * (grp & 1) + l0);
+    r.b = ld_part_a2(blk + 128 + 32 * hh + l0);
+    uint8_t sc;
+    uint16_t dd;
+    __builtin_memcpy(&sc, blk + 192 + 8 * hh + 2 * grp + (l0 >> 4), 1);
+    __builtin_memcpy(&dd, blk + 208, 2);
+    r.s = sc;
+    r.dd = dd;
+}
+// Activations of step ks, part p: values 64ks + kVP*p .. of the token's Q8_1 MMQ row
+// (block v/128, sub-block (v/32)%4).
+__device__ __forceinline__ void load_a(const uint8_t *__restrict__ arow, int ks, int p, RawA &r) {
+    const int v0 = ks * kKS + kVP * p;
+    const uint8_t *blk = arow + (size_t)(v0 >> 7) * kQ81Bytes;
+    __builtin_memcpy(&r.ds, blk + 4 * ((v0 >> 5) & 3), 4);
+    r.q = ld_part(blk + 16 + (v0 & 127));
 }
 
-// Fragments of one 32-wide K half (kh) of a step for 4 x 4 MFMA 16x16x32 tiles.
-// nb (wave-uniform): token tiles of the wave that hold tokens; the others are skipped.
-__device__ __forceinline__ void read_frags(const _Float16 *as, const _Float16 *bs, int wi, int wj, int kh, int lane,
-                                           h8 (&af)[4], h8 (&bf)[4], int nb) {
+// f16 tiles of 64 K-columns per row = 8 chunks of 16 B (a row is 128 B, half of the 64 x 4 B
+// LDS banks), stored without padding with the chunk index XOR-ed by (row / 2) % 8: the 16
+// rows of an MFMA fragment read (one chunk each) cover the 64 banks once, and so do the
+// lanes of a conversion store.
+__device__ __forceinline__ int tile_off(int row, int chunk) { return row * kKS + ((chunk ^ ((row >> 1) & 7)) << 3); }
+// the part's converted values (kVP / 2 dwords of f16 pairs) into its chunks
+__device__ __forceinline__ void put_part(_Float16 *tile, int row, int p, const uint32_t (&o)[kVP / 2]) {
+#pragma unroll
+    for (int c = 0; c < kVP / 8; c++)
+        *(uint4 *)(tile + tile_off(row, (kVP / 8) * p + c)) = make_uint4(o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]);
+}
+
+// One LDS stage: the step's operand tiles and the running-scale factors.
+template <int TYPE>
+struct Stage {
+    static constexpr int kPlanes = TYPE == kTypeQ4K ? 1 : 2;
+    _Float16 a[kPlanes][kBM * kKS];  // weights: sc*q (Q4_K) or the two Q6_K planes
+    _Float16 b[kBN * kKS];           // q8
+    float rho[2][kBN];               // token scale ratio of sub-block 2ks + p
+    float sig[kBM];                  // row scale ratio (written at super-block starts)
+};
+
+// Running scales of a loader thread: the last nonzero d of its weight row (part 0 threads)
+// and the last nonzero d8 of its token for the sub-block parity of its part (the first part
+// of each sub-block).  Both start at 1.
+struct LoaderState {
+    float deff, d8eff;
+};
+
+__device__ __forceinline__ void row_scale_step(float d, int ks, int p, float *sig, int row, LoaderState &ls, bool live) {
+    if (p == 0 && (ks & 3) == 0 && live) {  // super-block start: the row scale changes
+        const float dn = d != 0.0f ? d : ls.deff;
+        sig[row] = ls.deff / dn;
+        ls.deff = dn;
+    }
+}
+
+__device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int p, Stage<kTypeQ4K> &st, int row,
+                                            LoaderState &ls, bool live) {
+    const int c = kVP * p;
+    const int j = 2 * (ks & 3) + (c >> 5);
+    uint32_t sc, m;
+    q4k_scale_min(r.h.y, r.h.z, r.h.w, j, sc, m);
+    const float d = h2f(r.h.x & 0xFFFFu);
+    if (d == 0.0f) sc = 0;  // the block's products are zero
+    const _Float16 s = (_Float16)(float)sc, ns = (_Float16)(-1024.0f * (float)sc);
+    const h2 S = {s, s}, N = {ns, ns};
+    const int sh = 4 * (c >> 5);
+    uint32_t o[kVP / 2];
+#pragma unroll
+    for (int k = 0; k < kVP / 4; k++) {
+        const uint32_t w = (r.a.w[k] >> sh) & 0x0F0F0F0Fu;
+        o[2 * k] = q4_scaled(w, kSelLo, S, N);
+        o[2 * k + 1] = q4_scaled(w, kSelHi, S, N);
+    }
+    put_part(st.a[0], row, p, o);
+    row_scale_step(d, ks, p, st.sig, row, ls, live);
+}
+
+// Q6_K planes (sc - b)(q - 32) and b(q - 32), b = sc & 1
+__device__ __forceinline__ void store_w_q6k(const RawW &r, int ks, int p, Stage<kTypeQ6K> &st, int row,
+                                            LoaderState &ls, bool live) {
+    const int c = kVP * p, grp = 2 * (ks & 1) + (c >> 5);
+    const float d = h2f(r.dd);
+    int sc = (int)(int8_t)(r.s & 0xFF);
+    if (d == 0.0f) sc = 0;
+    const int b1 = sc & 1;
+    const _Float16 e = (_Float16)(float)(sc - b1), bb = (_Float16)(float)b1;
+    const h2 E = {e, e}, B = {bb, bb};
+    const int shl = grp >= 2 ? 4 : 0;
+    uint32_t o1[kVP / 2], o2[kVP / 2];
+#pragma unroll
+    for (int k = 0; k < kVP / 4; k++) {
+        const uint32_t lo = (r.a.w[k] >> shl) & 0x0F0F0F0Fu;
+        const uint32_t qh = r.b.w[k];
+        const uint32_t hi = (2 * grp <= 4 ? (qh << (4 - 2 * grp)) : (qh >> (2 * grp - 4))) & 0x30303030u;
+        const uint32_t v = lo | hi;
+        const h2 c0 = q6_centered(v, kSelLo), c1 = q6_centered(v, kSelHi);
+        o1[2 * k] = h2u(c0 * E);
+        o1[2 * k + 1] = h2u(c1 * E);
+        o2[2 * k] = h2u(c0 * B);
+        o2[2 * k + 1] = h2u(c1 * B);
+    }
+    put_part(st.a[0], row, p, o1);
+    put_part(st.a[1], row, p, o2);
+    row_scale_step(d, ks, p, st.sig, row, ls, live);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void store_a(const RawA &r, int p, Stage<TYPE> &st, int row, LoaderState &ls, bool live) {
+    const float d8 = h2f(r.ds & 0xFFFFu);
+    const bool zero = d8 == 0.0f;  // x = 0 * q8 = 0 whatever the quants hold (a block whose d
+                                   // rounds to f16 zero keeps quants up to +-127)
+    uint32_t o[kVP / 2];
+#pragma unroll
+    for (int k = 0; k < kVP / 4; k++) q8x4_exact(zero ? 0u : r.q.w[k], o[2 * k], o[2 * k + 1]);
+    put_part(st.b, row, p, o);
+    const int c = kVP * p;
+    if ((c & 31) == 0 && live) {  // first part of a sub-block: its token scale ratio
+        const float dn = zero ? ls.d8eff : d8;
+        st.rho[c >> 5][row] = ls.d8eff / dn;
+        ls.d8eff = dn;
+    }
+}
+
+template <int TYPE>
+__device__ __forceinline__ void load_step(const uint8_t *wrow, const uint8_t *arow, int ks, int p, RawW &rw,
+                                          RawA &ra) {
+    if (TYPE == kTypeQ4K) load_w_q4k(wrow, ks, p, rw);
+    else load_w_q6k(wrow, ks, p, rw);
+    load_a(arow, ks, p, ra);
+}
+template <int TYPE>
+__device__ __forceinline__ void store_step(const RawW &rw, const RawA &ra, int ks, int p, Stage<TYPE> &st, int row,
+                                           LoaderState &ls, bool live) {
+    if constexpr (TYPE == kTypeQ4K) store_w_q4k(rw, ks, p, st, row, ls, live);
+    else store_w_q6k(rw, ks, p, st, row, ls, live);
+    store_a<TYPE>(ra, p, st, row, ls, live);
+}
+
+// A wave's operands of one step: fragments of its sub-block (kh) for 4 x kNB MFMA tiles, the
+// token scale ratios of its 16-token columns, and (at super-block starts) the row ratios of
+// the rows its accumulators hold.
+template <int TYPE>
+struct Frags {
+    h8 a[Stage<TYPE>::kPlanes][4];
+    h8 b[kNB];
+    float rho[kNB];
+};
+template <int TYPE>
+__device__ __forceinline__ void read_frags(const Stage<TYPE> &st, int wi, int wj, int kh, int lane, Frags<TYPE> &f) {
     const int chunk = 4 * kh + (lane >> 4);
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const int ra = wi + 16 * t + (lane & 15), rb = wj + 16 * t + (lane & 15);
-        af[t] = *(const h8 *)(as + tile_off(ra, chunk));
-        if (t < nb) bf[t] = *(const h8 *)(bs + tile_off(rb, chunk));
+        const int ra = wi + 16 * t + (lane & 15);
+#pragma unroll
+        for (int p = 0; p < Stage<TYPE>::kPlanes; p++) f.a[p][t] = *(const h8 *)(st.a[p] + tile_off(ra, chunk));
+    }
+#pragma unroll
+    for (int t = 0; t < kNB; t++) {
+        const int rb = wj + 16 * t + (lane & 15);
+        f.b[t] = *(const h8 *)(st.b + tile_off(rb, chunk));
+        f.rho[t] = st.rho[kh][rb];
     }
 }
-__device__ __forceinline__ void mfma_frags(const h8 (&af)[4], const h8 (&bf)[4], f4 (&acc)[4][4], int nb) {
+
+// acc = acc * rho + (the exact integer sub-block sums of the step): the MFMA adds its products
+// to the rescaled accumulator
+// (at a super-block start the row ratios come first, read from the step's own stage, which
+// no thread writes during the step)
+template <int TYPE>
+__device__ __forceinline__ void mfma_step(const Frags<TYPE> &f, const Stage<TYPE> &st, int wi, int lane,
+                                          f4 (&acc)[4][kNB], bool sb_start) {
+    if (sb_start) {
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (b < nb) {
+        for (int a = 0; a < 4; a++) {
+            const f4 sg = *(const f4 *)(st.sig + wi + 16 * a + 4 * (lane >> 4));
 #pragma unroll
-            for (int a = 0; a < 4; a++)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
+            for (int b = 0; b < kNB; b++) acc[a][b] *= sg;
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kNB; b++) {
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            acc[a][b] *= f.rho[b];
+            acc[a][b] = mfma(f.a[0][a], f.b[b], acc[a][b]);
+            if constexpr (TYPE == kTypeQ6K) acc[a][b] = mfma(f.a[1][a], f.b[b], acc[a][b]);
         }
     }
 }
 
-// Epilogue / operand-addressing modes of the kernel:
-//   kModePlain   : W [M][K], activations rows j = token, out[j*M + i] (column-major [N][M])
-//   kModeSwiGLU  : grouped experts; a tile covers 64 features with 64 gate rows and 64 up
-//                  rows interleaved; activation rows are tokens gathered through perm[];
-//                  out[q*ld + f] = silu(gate) * up for expert-sorted row q
-//   kModeGrouped : grouped experts; activation rows are the expert-sorted rows q themselves;
-//                  out[q*ld + i]
-enum GemmMode : int { kModePlain = 0, kModeSwiGLU = 1, kModeGrouped = 2 };
-
 struct GemmArgs {
-    const uint8_t *W;  // plain: weights; grouped: expert table base
-    const void *A;           // activation rows: staged f16 (K values) or Q8_1 MMQ blocks
-    const float *a_unscale;  // staged rows: 2^e per row
+    const uint8_t *W;   // weights [M][K] (plain); expert table base (grouped)
+    const void *A;      // Q8_1 MMQ rows (plain); staged q8 rows, f16 integers (grouped)
+    const float *a_rho;      // grouped: [rows][K/32] token scale ratios
+    const uint16_t *a_ds;    // grouped: [rows][K/32] f16 ds
+    const float *a_dlast;    // grouped: [rows] last nonzero d8 (1 if none)
     float *out;
     int M, K, N, splits;
     int out_ld;
-    // grouped modes
+    // grouped launches
     size_t expert_stride, w_off, w_off2;  // expert e's matrix at W + e*stride + w_off (up: w_off2)
     const int *counts;                   // [n_experts] rows per expert
     const int *offsets;                  // [n_experts] first expert-sorted row
     const int *perm;                     // [rows] expert-sorted row -> token (SwiGLU gather)
     const int *tiles;                    // [max_tiles] (expert << 16) | n_tile; tiles[-1] = count
-    int skip_upto;                       // grouped: tiles of at most this many rows are left to
-                                         // the skinny kernel (0: none)
 };
 
-template <int TYPE, int MODE, bool ATOMIC, bool Q8>
+template <int TYPE, bool ATOMIC>
 __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
-    __shared__ __align__(16) _Float16 lds[3][2][kBM * kKS];  // [buffer][weights | tokens]
+    __shared__ __align__(16) Stage<TYPE> lds[3];
+    __shared__ float dlast[kBM], d8last[2][kBN];
     const int tid = threadIdx.x;
     // the wave index as a scalar, so that every per-wave decision below is a scalar branch
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = g.K;
-    const int wi = (wave & 1) * 64, wj = ((wave >> 1) & 1) * 64, kh = wave >> 2;
-    const size_t wrow_bytes = (size_t)(K / 256) * (TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes);
-    const int nks_all = K / kKS;
-    const int ks0 = (int)((long)nks_all * blockIdx.z / g.splits);
-    const int ks1 = (int)((long)nks_all * (blockIdx.z + 1) / g.splits);
-    const int last = ks1 - 1;
+    const int wi = (wave & 1) * 64, wj = ((wave >> 1) % kWC) * kWTok, kh = wave / (2 * kWC);
+    const int bbytes = TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes;
+    const size_t wrow_bytes = (size_t)(K / 256) * bbytes;
+    // this split's super-blocks [sb0, sb1) = steps [ks0, ks1)
+    const int nsb = K / 256;
+    const int sb0 = (int)((long)nsb * blockIdx.z / g.splits), sb1 = (int)((long)nsb * (blockIdx.z + 1) / g.splits);
+    const int ks0 = 4 * sb0, ks1 = 4 * sb1, last = ks1 - 1;
+    const int i0 = blockIdx.x * kBM, j0 = blockIdx.y * kBN;
 
-    // tile coordinates: weights i0 (features for SwiGLU), activation rows j0 .. j0+127 of
-    // [row_base, row_base + n_rows)
-    int i0, j0, n_rows, row_base = 0;
-    const uint8_t *Wm = g.W, *Wm2 = g.W;
-    if (MODE == kModePlain) {
-        i0 = blockIdx.x * kBM;
-        j0 = blockIdx.y * kBN;
-        n_rows = g.N;
-    } else {
-        if ((int)blockIdx.y >= g.tiles[-1]) return;  // uniform: past the tile list
-        const int t = g.tiles[blockIdx.y];
-        const int e = t >> 16, nt = t & 0xFFFF;
-        n_rows = g.counts[e];
-        row_base = g.offsets[e];
-        j0 = nt * kGroupTile;
-        if (min(kGroupTile, n_rows - j0) <= g.skip_upto) return;  // uniform: a skinny tile
-        i0 = blockIdx.x * (MODE == kModeSwiGLU ? kBM / 2 : kBM);
-        Wm = g.W + (size_t)e * g.expert_stride + g.w_off;
-        Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
-    }
+    // loader role: thread -> (row / token lr, part lp); rows past the end re-read the last
+    const int lr = tid / kParts, lp = tid % kParts;
+    const uint8_t *wrow = g.W + (size_t)min(i0 + lr, g.M - 1) * wrow_bytes;
+    const uint8_t *arow = (const uint8_t *)g.A + (size_t)min(j0 + lr, g.N - 1) * (K / 128) * kQ81Bytes;
+    LoaderState ls{1.0f, 1.0f};
 
-    // loader role: thread -> (LDS row lr, quarter lh); rows past the end re-read the last
-    const int lr = tid >> 2, lh = tid & 3;
-    const uint8_t *wrow;
-    if (MODE == kModeSwiGLU) {
-        // LDS rows 64w .. 64w+31 = gate features i0 + 32w + (0..31), 64w+32 .. = up features
-        const int w = lr >> 6, rr = lr & 63;
-        const int f = min(i0 + 32 * w + (rr & 31), g.M - 1);
-        wrow = (rr < 32 ? Wm : Wm2) + (size_t)f * wrow_bytes;
-    } else {
-        wrow = Wm + (size_t)min(i0 + lr, g.M - 1) * wrow_bytes;
-    }
-    // tokens of this tile: activation rows past them are skipped, and so are the MFMAs of a
-    // wave's 16-token tiles that hold none (the small experts of a grouped launch)
-    // (grouped launches only: a plain GEMM's tiles are full but for the last)
-    const int nvalid = min(kBN, n_rows - j0);
-    const bool act = MODE == kModePlain || lr < nvalid;
-    const int nb = MODE == kModePlain ? 4 : min(4, max(0, (nvalid - wj + 15) / 16));
-    const int jr = min(j0 + lr, n_rows - 1);
-    const int arow_idx = MODE == kModePlain ? jr : MODE == kModeSwiGLU ? g.perm[row_base + jr] : row_base + jr;
-    __shared__ float row_unscale[kBN];
-    float a_scale = 1.0f;
-    const void *arow;
-    if constexpr (Q8) {
-        // f16 staging of d8*q8 overflows once |d8*q8| > 65504: scale the row by an exact
-        // power of two 2^-e from its largest d8 (127 * max d8 * 2^-e <= 2^15) and undo it
-        // in the epilogue (the staging kernels do the same for staged rows)
-        const uint8_t *ar = (const uint8_t *)g.A + (size_t)arow_idx * (K / 128) * kQ81Bytes;
-        arow = ar;
-        float dmax = 0.0f;
-        for (int b = lh; b < K / 128; b += 4) {
-            const uint4 hd = ld16(ar + (size_t)b * kQ81Bytes);
-            dmax = fmaxf(dmax, fmaxf(fmaxf(fabsf(h2f(hd.x & 0xFFFF)), fabsf(h2f(hd.y & 0xFFFF))),
-                                     fmaxf(fabsf(h2f(hd.z & 0xFFFF)), fabsf(h2f(hd.w & 0xFFFF)))));
-        }
-        dmax = fmaxf(dmax, __shfl_xor(dmax, 1));
-        dmax = fmaxf(dmax, __shfl_xor(dmax, 2));
-        const int e = row_exponent(dmax);
-        a_scale = ldexpf(1.0f, -e);
-        if (lh == 0) row_unscale[lr] = ldexpf(1.0f, e);
-    } else {
-        arow = (const _Float16 *)g.A + (size_t)arow_idx * K;
-        if (lh == 0) row_unscale[lr] = g.a_unscale[arow_idx];
-    }
-
-    f4 acc[4][4];
+    f4 acc[4][kNB];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < kNB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // Pipeline: three LDS tile buffers.  In step ks a wave multiplies the fragments of step
-    // ks (read during step ks-1), reads the fragments of step ks+1 (its tile was completed
-    // before the previous barrier), converts step ks+2 into the third buffer, then meets
-    // the barrier.  Raw blocks sit in a ring of kPF register slots, loaded kPF-2 steps
-    // before their conversion.  The loop is unrolled by lcm(kPF, 3) so all indices are static.
-    RawW rw[kPF];
-    RawA<Q8> ra[kPF];
+    // Q4_K min term, sum_s -(dmin*m_s)_i * ds_js, first: the accumulator starts as this
+    // absolute value (the running scales start at 1, their ratios telescope to
+    // 1 / (last d8 * last d), which the epilogue multiplies back).  Windows of 32 sub-blocks
+    // (4 super-blocks), wave parity kh taking windows kh, kh+2, ...; lane group q = lane/16
+    // holds super-block 4w + q of its row / token (K index 8q + s of the MFMA = sub-block s of
+    // that super-block).
+    if constexpr (TYPE == kTypeQ4K) {
+        const int q = lane >> 4;
+        const int nwin = (sb1 - sb0 + 3) / 4;
+        for (int w = kh; w < nwin; w += 2) {
+            const int sb = sb0 + 4 * w + q;
+            const bool valid = sb < sb1;
+            uint4 hdr[4], blk[kNB][2];
 #pragma unroll
-    for (int p = 0; p < kPF; p++) load_step<TYPE, Q8>(wrow, arow, min(ks0 + p, last), lh, rw[p], ra[p], act);
-    store_step<TYPE, Q8>(rw[0], ra[0], ks0, lh, lds[0][0], lds[0][1], lr, a_scale, act);
-    store_step<TYPE, Q8>(rw[1], ra[1], ks0 + 1, lh, lds[1][0], lds[1][1], lr, a_scale, act);
-    __syncthreads();
-    h8 af[4], bf[4];
-    read_frags(lds[0][0], lds[0][1], wi, wj, kh, lane, af, bf, nb);
+            for (int a = 0; a < 4; a++) {
+                const uint8_t *rp = g.W + (size_t)min(i0 + wi + 16 * a + (lane & 15), g.M - 1) * wrow_bytes;
+                hdr[a] = valid ? ld16(rp + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < kNB; b++) {
+                const uint8_t *ap = (const uint8_t *)g.A +
+                                    (size_t)min(j0 + wj + 16 * b + (lane & 15), g.N - 1) * (K / 128) * kQ81Bytes;
+                blk[b][0] = valid ? ld16(ap + (size_t)(2 * sb) * kQ81Bytes) : make_uint4(0, 0, 0, 0);
+                blk[b][1] = valid ? ld16(ap + (size_t)(2 * sb + 1) * kQ81Bytes) : make_uint4(0, 0, 0, 0);
+            }
+            h8 bd[kNB];
+#pragma unroll
+            for (int b = 0; b < kNB; b++) bd[b] = ds_operand(blk[b][0], blk[b][1]);
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                h8 hi, lo;
+                q4k_min_operand(hdr[a], hi, lo);
+#pragma unroll
+                for (int b = 0; b < kNB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
+            }
+        }
+    }
+
+    // Pipeline: three LDS stages.  In step ks a wave multiplies the fragments of step ks
+    // (read during step ks-1), reads the fragments of step ks+1 (its stage was completed
+    // before the previous barrier), converts step ks+2 into the third stage, then meets
+    // the barrier.  Raw blocks sit in a ring of kPF register slots, loaded kPF-2 steps
+    // before their conversion.  Conversions past the last step fill idle stages and leave
+    // the running scales alone.
+    RawW rw[kPF];
+    RawA ra[kPF];
+#pragma unroll
+    for (int p = 0; p < kPF; p++) load_step<TYPE>(wrow, arow, min(ks0 + p, last), lp, rw[p], ra[p]);
+    store_step<TYPE>(rw[0], ra[0], ks0, lp, lds[0], lr, ls, true);
+    store_step<TYPE>(rw[1], ra[1], ks0 + 1, lp, lds[1], lr, ls, ks0 + 1 < ks1);
+    lds_barrier();
+    Frags<TYPE> fr;
+    read_frags<TYPE>(lds[0], wi, wj, kh, lane, fr);
 
     for (int kb = ks0; kb < ks1; kb += kUnroll) {
 #pragma unroll
         for (int p = 0; p < kUnroll; p++) {
             const int ks = kb + p;
             if (ks < ks1) {  // uniform
-                // kb - ks0 is a multiple of kUnroll, so these are compile-time constants
+                // kb - ks0 is a multiple of kUnroll and ks0 of 4, so these are compile-time
+                // constants
                 const int r = p % kPF, b = p % 3;
-                load_step<TYPE, Q8>(wrow, arow, min(ks + kPF, last), lh, rw[r], ra[r], act);
-                mfma_frags(af, bf, acc, nb);
-                // (past the end these read and fill idle buffers with data nobody uses)
-                read_frags(lds[(b + 1) % 3][0], lds[(b + 1) % 3][1], wi, wj, kh, lane, af, bf, nb);
-                store_step<TYPE, Q8>(rw[(r + 2) % kPF], ra[(r + 2) % kPF], ks + 2, lh, lds[(b + 2) % 3][0],
-                                     lds[(b + 2) % 3][1], lr, a_scale, act);
-                __syncthreads();
+                load_step<TYPE>(wrow, arow, min(ks + kPF, last), lp, rw[r], ra[r]);
+                mfma_step<TYPE>(fr, lds[b], wi, lane, acc, p % 4 == 0);
+                read_frags<TYPE>(lds[(b + 1) % 3], wi, wj, kh, lane, fr);
+                store_step<TYPE>(rw[(r + 2) % kPF], ra[(r + 2) % kPF], ks + 2, lp, lds[(b + 2) % 3], lr, ls,
+                                 ks + 2 < ks1);
+                lds_barrier();
             }
         }
     }
-    // sum the two K halves: waves 4..7 hand their tiles to waves 0..3 through the (now idle)
-    // tile buffers, laid out lane-minor so the accesses are conflict-free
+    // absolute values: the last nonzero scales of each row and each token (per parity)
+    if (lp == 0) dlast[lr] = ls.deff;
+    if (((kVP * lp) & 31) == 0) d8last[(kVP * lp) >> 5][lr] = ls.d8eff;
     __syncthreads();
-    float *red = (float *)&lds[0][0][0] + (size_t)(wave & 3) * (64 * 64);
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const f4 dr = *(const f4 *)(dlast + wi + 16 * a + 4 * (lane >> 4));
+#pragma unroll
+        for (int b = 0; b < kNB; b++) {
+            const float dt = d8last[kh][wj + 16 * b + (lane & 15)];
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[a][b][e] *= dr[e] * dt;
+        }
+    }
+
+    // sum the two parities: the kh = 1 waves hand their tiles to their kh = 0 counterparts
+    // through the (now idle) stages, laid out lane-minor so the accesses are conflict-free
+    __syncthreads();
+    float *red = (float *)&lds[0] + (size_t)(wave % (kWaves / 2)) * (64 * kWTok);
     if (kh) {
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int b = 0; b < 4; b++)
+            for (int b = 0; b < kNB; b++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) red[((a * 4 + b) * 4 + e) * 64 + lane] = acc[a][b][e];
+                for (int e = 0; e < 4; e++) red[((a * kNB + b) * 4 + e) * 64 + lane] = acc[a][b][e];
     }
     __syncthreads();
     if (kh) return;
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++)
+        for (int b = 0; b < kNB; b++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[a][b][e] += red[((a * 4 + b) * 4 + e) * 64 + lane];
+            for (int e = 0; e < 4; e++) acc[a][b][e] += red[((a * kNB + b) * 4 + e) * 64 + lane];
     // D layout (16x16 f32): lane l holds rows 4*(l/16)+e, column l%16.  Rows index
-    // weights (A operand), columns activation rows (B operand).
-    if (MODE == kModeSwiGLU) {
-        // gate tile a pairs with up tile a+2: feature i0 + 32*(wave&1) + 16a + 4*(l/16) + e
-#pragma unroll
-        for (int a = 0; a < 2; a++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int j = j0 + wj + 16 * b + (lane & 15);
-                const int f = i0 + 32 * (wave & 1) + 16 * a + 4 * (lane >> 4);
-                if (j >= n_rows) continue;
-                const float us = row_unscale[wj + 16 * b + (lane & 15)];
-                float *o = g.out + (size_t)(row_base + j) * g.out_ld + f;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float gt = acc[a][b][e] * us, up = acc[a + 2][b][e] * us;
-                    if (f + e < g.M) o[e] = gt / (1.0f + expf(-gt)) * up;
-                }
-            }
-        return;
-    }
+    // weights (A operand), columns tokens (B operand).
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
+        for (int b = 0; b < kNB; b++) {
             const int j = j0 + wj + 16 * b + (lane & 15);
             const int ib = i0 + wi + 16 * a + 4 * (lane >> 4);
-            if (j >= n_rows) continue;
-            const float us = row_unscale[wj + 16 * b + (lane & 15)];
-#pragma unroll
-            for (int e = 0; e < 4; e++) acc[a][b][e] *= us;
-            float *o = g.out + (size_t)(row_base + j) * g.out_ld + ib;
+            if (j >= g.N) continue;
+            float *o = g.out + (size_t)j * g.out_ld + ib;
             if (ATOMIC) {
                 // to the wave's own (idle) reduction buffer, token-major, 16-byte groups
                 // XOR-swizzled by token so that the row-wise reads below are conflict-free
@@ -499,11 +587,11 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
         // the MFMA layout would spread each instruction over 16 token rows, which measured
         // twice as slow in the L2 atomic units
         const int ib = i0 + wi + lane;
-        for (int t = 0; t < 64; t++) {
+        for (int t = 0; t < kWTok; t++) {
             const int j = j0 + wj + t;
-            if (j >= n_rows) break;
+            if (j >= g.N) break;
             if (ib < g.M)
-                __hip_atomic_fetch_add(g.out + (size_t)(row_base + j) * g.out_ld + ib,
+                __hip_atomic_fetch_add(g.out + (size_t)j * g.out_ld + ib,
                                        red[t * 64 + ((((lane >> 2) ^ (t & 15)) << 2) | (lane & 3))], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -511,106 +599,83 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------ activation staging
-// One wave per activation row, 4 rows per 256-thread block.
+// fp32 rows [N][K] -> the grouped kernel's operand form of cuda_quantize_mmq_q8_1's output
+// (per 32 values d = amax/127, q = rint(x*127/amax) clamped to +-127, ds = f16(d * sum x);
+// gemm_q4k.cu:327-358): q8 as f16 integers [N][K], the f16 ds [N][K/32], the running-scale
+// ratio rho_s = d8eff_{s-1} / d8eff_s [N][K/32] (d8eff: the last nonzero f16 d8 at or before
+// s, 1 before the first) and the last d8eff of the row [N].  One wave per row.
 constexpr int kStageThreads = 256;
 
-// Q8_1 MMQ rows [N][K/128] x 144 B -> f16 rows d8*q8*2^-e, unscale[row] = 2^e.
-__global__ void __launch_bounds__(kStageThreads) stage_q8_1_kernel(const uint8_t *__restrict__ A, int K, int N,
-                                                                   _Float16 *__restrict__ out,
-                                                                   float *__restrict__ unscale) {
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (kStageThreads / 64) + (threadIdx.x >> 6);
-    if (row >= N) return;
-    const uint8_t *ar = A + (size_t)row * (K / 128) * kQ81Bytes;
-    float dmax = 0.0f;
-    for (int b = lane; b < K / 128; b += 64) {
-        const uint4 hd = ld16(ar + (size_t)b * kQ81Bytes);
-        dmax = fmaxf(dmax, fmaxf(fmaxf(fabsf(h2f(hd.x & 0xFFFF)), fabsf(h2f(hd.y & 0xFFFF))),
-                                 fmaxf(fabsf(h2f(hd.z & 0xFFFF)), fabsf(h2f(hd.w & 0xFFFF)))));
-    }
-    const int e = row_exponent(wave_max(dmax));
-    const float as = ldexpf(1.0f, -e);
-    if (lane == 0) unscale[row] = ldexpf(1.0f, e);
-    _Float16 *orow = out + (size_t)row * K;
-    for (int c = lane; c < K / 16; c += 64) {  // 16 values per chunk
-        const uint8_t *blk = ar + (size_t)(c >> 3) * kQ81Bytes;
-        uint16_t dbits;
-        __builtin_memcpy(&dbits, blk + 4 * ((c & 7) >> 1), 2);
-        const _Float16 d = (_Float16)(h2f(dbits) * as);  // exact: power-of-two scaling
-        const h2 d2 = {d, d};
-        const uint4 q = ld16(blk + 16 + 16 * (c & 7));
-        uint4 o0, o1;
-        q8x4_to_f16(q.x, d2, o0.x, o0.y);
-        q8x4_to_f16(q.y, d2, o0.z, o0.w);
-        q8x4_to_f16(q.z, d2, o1.x, o1.y);
-        q8x4_to_f16(q.w, d2, o1.z, o1.w);
-        *(uint4 *)(orow + 16 * c) = o0;
-        *(uint4 *)(orow + 16 * c + 8) = o1;
-    }
-}
-
-// fp32 rows [N][K] -> the same staged form as stage_q8_1_kernel applied to
-// cuda_quantize_mmq_q8_1's output: per 32 values d = f16(amax/127), q = rint(x*127/amax)
-// clamped to +-127 (gemm_q4k.cu:327-358), staged value f16(d*2^-e) * q.
 __global__ void __launch_bounds__(kStageThreads) stage_f32_kernel(const float *__restrict__ x, int K, int N,
-                                                                  _Float16 *__restrict__ out,
-                                                                  float *__restrict__ unscale) {
+                                                                  _Float16 *__restrict__ q8, float *__restrict__ rho,
+                                                                  uint16_t *__restrict__ dsv,
+                                                                  float *__restrict__ dlast) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (kStageThreads / 64) + (threadIdx.x >> 6);
     if (row >= N) return;
+    const int nsub = K / 32;
     const float4 *xr = (const float4 *)(x + (size_t)row * K);
-    float dmax = 0.0f;
-    for (int b = lane; b < K / 32; b += 64) {
-        float amax = 0.0f;
+    _Float16 *qrow = q8 + (size_t)row * K;
+    float carry = 1.0f;  // d8eff before this pass's first block
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    for (int b0 = 0; b0 < nsub; b0 += 64) {
+        const int b = b0 + lane;
+        float d8 = 0.0f;
+        if (b < nsub) {
+            // the arithmetic of quantize_q8_1_kernel (router.hip), so the values agree bit
+            // for bit with cuda_quantize_mmq_q8_1
+            float xv[32];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 v = xr[8 * b + i];
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            for (int i = 0; i < 8; i++) {
+                const float4 v = xr[8 * b + i];
+                xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(xv[i]));
+            const float d = amax / 127.0f;
+            const float id = (amax > 0.0f) ? 127.0f / amax : 0.0f;
+            float sum = 0.0f;
+            uint32_t o[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float r0 = rintf(xv[2 * i] * id), r1 = rintf(xv[2 * i + 1] * id);
+                r0 = fminf(fmaxf(r0, -127.0f), 127.0f);
+                r1 = fminf(fmaxf(r1, -127.0f), 127.0f);
+                sum += xv[2 * i];
+                sum += xv[2 * i + 1];
+                o[i] = h2u(h2{(_Float16)r0, (_Float16)r1});
+            }
+            float dsum = d * sum;
+            asm volatile("" : "+v"(dsum));  // fp32 product, then the f16 rounding
+            const uint16_t dh = f2h_bits(d);
+            d8 = h2f(dh);
+            dsv[(size_t)row * nsub + b] = f2h_bits(dsum);
+            // a block whose d rounds to f16 zero (amax < 2^-25 * 127) still has quants up to
+            // +-127; its values d8 * q8 are zero, and so are the staged operands (the running
+            // scale skips the block)
+            const uint32_t keep = d8 != 0.0f ? ~0u : 0u;
+            uint4 *dst = (uint4 *)(qrow + 32 * b);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                dst[i] = make_uint4(o[4 * i] & keep, o[4 * i + 1] & keep, o[4 * i + 2] & keep, o[4 * i + 3] & keep);
         }
-        float d = amax / 127.0f;
-        asm volatile("" : "+v"(d));  // round d to fp32 before the f16 conversion
-        dmax = fmaxf(dmax, (float)(_Float16)d);
+        // running scale: the last nonzero d8 before each block (the carry if none in this pass)
+        const uint64_t nz = __ballot(d8 != 0.0f);
+        const uint64_t m = nz & below;
+        const int src = m ? 63 - __builtin_clzll(m) : 0;
+        const float prev_in = __shfl(d8, src);
+        const float prev = m ? prev_in : carry;
+        const float cur = d8 != 0.0f ? d8 : prev;
+        if (b < nsub) rho[(size_t)row * nsub + b] = prev / cur;
+        carry = __shfl(cur, 63);
     }
-    const int e = row_exponent(wave_max(dmax));
-    const float as = ldexpf(1.0f, -e);
-    if (lane == 0) unscale[row] = ldexpf(1.0f, e);
-    _Float16 *orow = out + (size_t)row * K;
-    for (int b = lane; b < K / 32; b += 64) {
-        float xv[32];
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 v = xr[8 * b + i];
-            xv[4 * i] = v.x; xv[4 * i + 1] = v.y; xv[4 * i + 2] = v.z; xv[4 * i + 3] = v.w;
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
-        float d = amax / 127.0f;
-        asm volatile("" : "+v"(d));
-        const float id = amax > 0.0f ? 127.0f / amax : 0.0f;
-        const _Float16 ds = (_Float16)((float)(_Float16)d * as);
-        uint32_t o[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float r0 = fminf(fmaxf(rintf(xv[2 * i] * id), -127.0f), 127.0f);
-            const float r1 = fminf(fmaxf(rintf(xv[2 * i + 1] * id), -127.0f), 127.0f);
-            const h2 q = {(_Float16)r0, (_Float16)r1};
-            const h2 d2 = {ds, ds};
-            o[i] = __builtin_bit_cast(uint32_t, q * d2);
-        }
-        uint4 *dst = (uint4 *)(orow + 32 * b);
-#pragma unroll
-        for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-    }
+    if (lane == 0) dlast[row] = carry;
 }
 
-int launch_stage_q8_1(const void *act, int K, int N, _Float16 *out, float *unscale, hipStream_t s) {
-    hipLaunchKernelGGL(stage_q8_1_kernel, dim3((N + 3) / 4), dim3(kStageThreads), 0, s, (const uint8_t *)act, K, N,
-                       out, unscale);
-    return check_launch("stage_q8_1");
-}
-
-int launch_stage_f32(const float *x, int K, int N, _Float16 *out, float *unscale, hipStream_t s) {
-    hipLaunchKernelGGL(stage_f32_kernel, dim3((N + 3) / 4), dim3(kStageThreads), 0, s, x, K, N, out, unscale);
+int launch_stage_f32(const float *x, int K, int N, StagedAct sa, hipStream_t s) {
+    hipLaunchKernelGGL(stage_f32_kernel, dim3((N + 3) / 4), dim3(kStageThreads), 0, s, x, K, N, sa.q8, sa.rho, sa.ds,
+                       sa.dlast);
     return check_launch("stage_f32");
 }
 
@@ -632,20 +697,6 @@ static int device_cus_gemm() {
     return cus;
 }
 
-template <int MODE, bool Q8>
-static void launch_mode(int type, bool atomic, dim3 grid, const GemmArgs &g, hipStream_t stream) {
-#define MNEMO_GEMM_LAUNCH(T_, A_) \
-    hipLaunchKernelGGL((gemm_q8_1_kernel<T_, MODE, A_, Q8>), grid, dim3(kThreads), 0, stream, g)
-    if (type == kTypeQ4K) {
-        if (atomic) MNEMO_GEMM_LAUNCH(kTypeQ4K, true);
-        else MNEMO_GEMM_LAUNCH(kTypeQ4K, false);
-    } else {
-        if (atomic) MNEMO_GEMM_LAUNCH(kTypeQ6K, true);
-        else MNEMO_GEMM_LAUNCH(kTypeQ6K, false);
-    }
-#undef MNEMO_GEMM_LAUNCH
-}
-
 int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M, int K, int N,
                      hipStream_t stream) {
     if (!w || !act || !out || M <= 0 || N <= 0 || K <= 0 || K % 256 != 0)
@@ -654,12 +705,11 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
     if (((uintptr_t)out & 15) != 0) return set_error(kErrBadArg, "gemm: output must be 16-byte aligned");
     if (((uintptr_t)act & 3) != 0) return set_error(kErrBadArg, "gemm: activation blocks must be 4-byte aligned");
     const int tm = (M + kBM - 1) / kBM, tn = (N + kBN - 1) / kBN;
-    // split K while the split grid still fits the CUs once (one workgroup per CU at a time),
-    // keeping at least 8 steps of 64 per split: measured, M x 512 x K = 1536 x 4096 best at 4
-    // splits (31 us against 59 unsplit), 512 x 4096 at 8, 4096 x 8192 at 2 (75 against 100)
-    const int nks = K / kKS;
+    // split K (whole super-blocks) while the split grid still fits the CUs once, keeping
+    // at least 2 super-blocks per split
+    const int nsb = K / 256;
     int splits = 1;
-    while (2 * tm * tn * splits <= device_cus_gemm() && nks / (splits * 2) >= 8) splits *= 2;
+    while (2 * tm * tn * splits <= device_cus_gemm() && nsb / (splits * 2) >= 2) splits *= 2;
     if (((long)M * N) % 4 != 0) splits = 1;  // the fill kernel clears float4s
     // activations are read as Q8_1 blocks and converted per tile: nothing is allocated, so
     // the call may sit inside a graph capture
@@ -677,160 +727,129 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
         hipLaunchKernelGGL(zero_kernel, dim3((unsigned)std::min<long>((n / 4 + 255) / 256, 4096)), dim3(256), 0,
                            stream, (float4 *)out, n / 4);
     }
-    launch_mode<kModePlain, true>(type, splits > 1, dim3(tm, tn, splits), g, stream);
+    const dim3 grid(tm, tn, splits);
+#define MNEMO_GEMM_LAUNCH(T_, A_) hipLaunchKernelGGL((gemm_q8_1_kernel<T_, A_>), grid, dim3(kThreads), 0, stream, g)
+    if (type == kTypeQ4K) {
+        if (splits > 1) MNEMO_GEMM_LAUNCH(kTypeQ4K, true);
+        else MNEMO_GEMM_LAUNCH(kTypeQ4K, false);
+    } else {
+        if (splits > 1) MNEMO_GEMM_LAUNCH(kTypeQ6K, true);
+        else MNEMO_GEMM_LAUNCH(kTypeQ6K, false);
+    }
+#undef MNEMO_GEMM_LAUNCH
     return check_launch("gemm_q8_1");
 }
 
 // ------------------------------------------------------------------ skinny grouped kernel
-// Most token tiles of a grouped launch hold few rows (an expert of the MoE prefill receives
-// a few tens of tokens), and then the tiled kernel above spends its time converting 128
-// weight rows per step into LDS for a handful of MFMA columns.  This kernel serves the
-// tiles of at most kSkTok rows without staging weights at all: every lane loads the raw
-// bytes of its own A-operand values and converts them in registers, straight into the
-// 16x16x32 f16 MFMA.  The K order inside an MFMA is free as long as both operands follow
-// it, so each lane takes whole 16-byte chunks of a super-block (lane group q = lane/16,
-// MFMA t = 0..7 of a 256-value block):
-//   Q4_K: qs chunk m = q + 4(t/4): values 64(m/2) + 32h + 16(m%2) + 8s .. +7, with h = (t/2)%2
-//         the nibble (sub-block 2(m/2) + h) and s = t%2 the dword pair of the chunk;
-//   Q6_K: half H = t/4, ql chunk 64H + 16q, qh chunk 32H + 16(q%2), nibble n = (t/2)%2:
-//         group grp = q/2 + 2n, values 128H + 32grp + 16(q%2) + 8s .. +7, scale 8H + q + 4n.
-// The tile's activation rows (staged f16) are copied per block into LDS in that order, so
-// a B fragment is one 16-byte read.  Conversion arithmetic is the tiled kernel's (same f16
-// roundings), so the two kernels agree to the fp32 accumulation order.
-#ifndef MNEMO_SKTOK
-#define MNEMO_SKTOK 64
-#endif
-#ifndef MNEMO_SK_THREADS
-#define MNEMO_SK_THREADS 512
-#endif
-constexpr int kSkThreads = MNEMO_SK_THREADS;  // 8 waves
-constexpr int kSkStage = kSkThreads / 32;        // activation rows staged per pass
+// The grouped expert GEMMs of the MoE prefill: an expert receives a few tens of tokens, so a
+// tile is at most kGroupTile (64) token rows and the weights dominate the traffic.  Every
+// lane loads the raw bytes of its own A-operand values and converts them in registers;
+// nothing but the tile's activation rows is staged in LDS.  Each MFMA covers one sub-block
+// (the running scale needs the exact per-sub-block sums): lane group q = lane/16 holds
+// values 8q .. 8q+7 of the sub-block, i.e.
+//   Q4_K sub-block j = 2g + h: qs bytes 32g + 8q .. +7, nibble h;
+//   Q6_K sub-block j = 4H + grp: ql bytes 64H + 32(grp%2) + 8q .. +7 (nibble grp/2), qh bytes
+//        32H + 8q .. +7 (bits 2grp), scale 8H + 2grp + q/2;
+// and the activation fragment is the staged row's values 32j + 8q .. +7 (natural order).
+constexpr int kSkThreads = 512;  // 8 waves
 constexpr int kSkWaves = kSkThreads / 64;
-constexpr int kSkTok = MNEMO_SKTOK;       // rows per tile served here: 4 column tiles of 16
-// weight rows per wave: SwiGLU one gate and one up tile of 16 (same features); grouped
-#ifndef MNEMO_SK_RPLAIN
-#define MNEMO_SK_RPLAIN 2
-#endif
-template <int MODE>
-constexpr int sk_rows_per_wave() { return MODE == kModeSwiGLU ? 32 : 16 * MNEMO_SK_RPLAIN; }
-template <int TYPE>
-__device__ __forceinline__ int sk_k0(int t, int q) {
-    if (TYPE == kTypeQ4K) {
-        const int m = q + 4 * (t >> 2);
-        return 64 * (m >> 1) + 32 * ((t >> 1) & 1) + 16 * (m & 1) + 8 * (t & 1);
-    }
-    return 128 * (t >> 2) + 32 * ((q >> 1) + 2 * ((t >> 1) & 1)) + 16 * (q & 1) + 8 * (t & 1);
-}
+constexpr int kSkTok = kGroupTile;  // token rows per tile: up to 4 column tiles of 16
+constexpr int kSkStage = kSkThreads / 32;  // activation rows staged per pass (32 chunks each)
+// weight rows per wave: SwiGLU one gate and one up tile of 16 (same features); grouped two
+// tiles of 16 (Q4_K) or one (Q6_K, whose raw blocks take more registers)
+template <int TYPE, int MODE>
+constexpr int sk_rows_per_wave() { return MODE == 1 || TYPE == kTypeQ4K ? 32 : 16; }
 
 // raw bytes of one row tile's lane values for one 256-value block
 struct SkRaw {
-    uint4 c[2];   // Q4_K: qs chunks q, q+4;  Q6_K: ql chunks of halves 0, 1
-    uint4 h;      // Q4_K: the header (d, dmin, 12 scale bytes);  Q6_K: the lane's qh bits,
-                  // two dwords per half (below)
-    uint32_t sc;  // Q6_K: scale bytes q, q+4, q+8, q+12
+    uint4 h;      // Q4_K: header (d, dmin, 12 scale bytes);  Q6_K: h.x / h.y the lane's scale
+                  // bytes of halves 0 / 1 (byte grp: scale 8H + 2grp + q/2)
+    uint2 a[4];   // Q4_K: qs bytes 32g + 8q .. +7;  Q6_K: ql bytes 64H + 32p + 8q .. (index 2H + p)
+    uint2 b[2];   // Q6_K: qh bytes 32H + 8q .. +7
     uint32_t d;   // Q6_K: f16 d
 };
+
+// vector memory instructions sk_load issues per row tile: Q4_K one 16-byte header and four
+// 8-byte loads; Q6_K six 8-byte and one 16-byte unaligned loads (two instructions each:
+// ld8_a2, ld16_a2) and the 2-byte d
+template <int TYPE>
+constexpr int sk_loads_per_tile() { return TYPE == kTypeQ4K ? 5 : 15; }
 
 template <int TYPE>
 __device__ __forceinline__ void sk_load(const uint8_t *__restrict__ blk, int q, SkRaw &r) {
     if (TYPE == kTypeQ4K) {
         r.h = ld16(blk);
-        r.c[0] = ld16(blk + 16 + 16 * q);
-        r.c[1] = ld16(blk + 80 + 16 * q);
+#pragma unroll
+        for (int g = 0; g < 4; g++) r.a[g] = ld8(blk + 16 + 32 * g + 8 * q);
     } else {
-        r.c[0] = ld16_a2(blk + 16 * q);
-        r.c[1] = ld16_a2(blk + 64 + 16 * q);
-        const uint4 h0 = ld16_a2(blk + 128 + 16 * (q & 1)), h1 = ld16_a2(blk + 160 + 16 * (q & 1));
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.a[i] = ld8_a2(blk + 64 * (i >> 1) + 32 * (i & 1) + 8 * q);
+#pragma unroll
+        for (int H = 0; H < 2; H++) r.b[H] = ld8_a2(blk + 128 + 32 * H + 8 * q);
+        // of the 16 scale bytes the lane needs 8H + 2grp + q/2: bytes q/2, 2 + q/2, .. of each
+        // dword, packed into h.x (half 0) and h.y (half 1)
         const uint4 sc = ld16_a2(blk + 192);
+        const uint32_t sel = 0x06040200u + 0x01010101u * (uint32_t)(q >> 1);
+        r.h.x = __builtin_amdgcn_perm(sc.y, sc.x, sel);
+        r.h.y = __builtin_amdgcn_perm(sc.w, sc.z, sel);
         uint16_t dd;
         __builtin_memcpy(&dd, blk + 208, 2);
         r.d = dd;
-        // scale byte i of the lane is byte q of dword i
-        const uint32_t lo = __builtin_amdgcn_perm(sc.y, sc.x, 0x0C0C0400u + 0x00000101u * (uint32_t)q);
-        const uint32_t hi = __builtin_amdgcn_perm(sc.w, sc.z, 0x0C0C0400u + 0x00000101u * (uint32_t)q);
-        r.sc = (lo & 0xFFFFu) | (hi << 16);
-        // of each qh byte the lane needs groups q/2 (bits 2(q/2)..+1) and q/2 + 2 (bits
-        // 2(q/2)+4..+5); packed: byte i of dword 2H+s holds, for values i (dword 2s) and
-        // 4+i (dword 2s+1) of the chunk, bits 0-1 / 2-3 (low nibble group) and 4-5 / 6-7
-        const int sh = 2 * (q >> 1);
-        auto pk = [sh](uint32_t a, uint32_t b) {
-            return ((a >> sh) & 0x33333333u) | (((b >> sh) & 0x33333333u) << 2);
-        };
-        r.h = make_uint4(pk(h0.x, h0.y), pk(h0.z, h0.w), pk(h1.x, h1.y), pk(h1.z, h1.w));
     }
 }
 
-__device__ __forceinline__ uint32_t dw(const uint4 &v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
-
-// per-block scale pairs of a lane: Q4_K (d*sc, -dmin*m) of its 4 sub-blocks (index 2L + h);
-// Q6_K d*sc of its 4 scales (index 2H + n)
+// the block's d (0 when absent)
 template <int TYPE>
-__device__ __forceinline__ void sk_scales(const SkRaw &r, int q, h2 (&A)[4], h2 (&B)[4]) {
-    if (TYPE == kTypeQ4K) {
-        const uint32_t s0 = r.h.y, s1 = r.h.z, s2 = r.h.w;
-        const float d = h2f(r.h.x & 0xFFFFu), dmin = h2f(r.h.x >> 16);
-#pragma unroll
-        for (int L = 0; L < 2; L++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int j = 2 * ((q >> 1) + 2 * L) + h;  // get_scale_min_k4 (kernels.cu:45-53)
-                uint32_t sc, m;
-                if (L == 0) {
-                    sc = sbyte(s0, s1, s2, j) & 63;
-                    m = sbyte(s0, s1, s2, j + 4) & 63;
-                } else {
-                    sc = (sbyte(s0, s1, s2, j + 4) & 15) | ((sbyte(s0, s1, s2, j - 4) >> 6) << 4);
-                    m = (sbyte(s0, s1, s2, j + 4) >> 4) | ((sbyte(s0, s1, s2, j) >> 6) << 4);
-                }
-                const _Float16 a = (_Float16)(d * (float)sc), b = (_Float16)(-dmin * (float)m);
-                A[2 * L + h] = h2{a, a};
-                B[2 * L + h] = h2{b, b};
-            }
-    } else {
-        const float d = h2f(r.d);
-#pragma unroll
-        for (int H = 0; H < 2; H++)
-#pragma unroll
-            for (int n = 0; n < 2; n++) {  // scale 8H + q + 4n = lane byte 2H + n
-                const int8_t sc = (int8_t)((r.sc >> (8 * (2 * H + n))) & 0xFF);
-                const _Float16 a = (_Float16)(d * (float)sc);
-                A[2 * H + n] = h2{a, a};
-            }
-    }
+__device__ __forceinline__ float sk_d(const SkRaw &r) {
+    return TYPE == kTypeQ4K ? h2f(r.h.x & 0xFFFFu) : h2f(r.d);
 }
 
-// the 8 f16 A-operand values of MFMA t
+// A operand(s) of sub-block j: Q4_K sc*q; Q6_K the planes (sc - b)(q - 32), b(q - 32)
 template <int TYPE>
-__device__ __forceinline__ h8 sk_operand(const SkRaw &r, int t, const h2 (&A)[4], const h2 (&B)[4]) {
-    const int L = t >> 2, h = (t >> 1) & 1, s = t & 1;
-    uint32_t o[4];
+__device__ __forceinline__ void sk_operand(const SkRaw &r, int j, int q, bool dzero, h8 &a1, h8 &a2) {
+    uint32_t o1[4], o2[4];
     if (TYPE == kTypeQ4K) {
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const uint32_t w = (dw(r.c[L], 2 * s + k) >> (4 * h)) & 0x0F0F0F0Fu;
-            o[2 * k] = dq_fma(w, 0x04010400u, A[2 * L + h], B[2 * L + h]);
-            o[2 * k + 1] = dq_fma(w, 0x04030402u, A[2 * L + h], B[2 * L + h]);
-        }
+        uint32_t sc, m;
+        q4k_scale_min(r.h.y, r.h.z, r.h.w, j, sc, m);
+        if (dzero) sc = 0;
+        const _Float16 s = (_Float16)(float)sc, ns = (_Float16)(-1024.0f * (float)sc);
+        const h2 S = {s, s}, N = {ns, ns};
+        const uint2 c = r.a[j >> 1];
+        const int sh = 4 * (j & 1);
+        const uint32_t w0 = (c.x >> sh) & 0x0F0F0F0Fu, w1 = (c.y >> sh) & 0x0F0F0F0Fu;
+        o1[0] = q4_scaled(w0, kSelLo, S, N);
+        o1[1] = q4_scaled(w0, kSelHi, S, N);
+        o1[2] = q4_scaled(w1, kSelLo, S, N);
+        o1[3] = q4_scaled(w1, kSelHi, S, N);
+        a1 = __builtin_bit_cast(h8, make_uint4(o1[0], o1[1], o1[2], o1[3]));
     } else {
-        const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-        const uint32_t P = dw(r.h, 2 * L + s);
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const uint32_t lo = (dw(r.c[L], 2 * s + k) >> (4 * h)) & 0x0F0F0F0Fu;
-            const int sh = 2 * k + 4 * h;  // the two bits of these values, moved to bits 4-5
-            const uint32_t hi = (sh <= 4 ? (P << (4 - sh)) : (P >> (sh - 4))) & 0x30303030u;
-            const uint32_t v = lo | hi;
-            o[2 * k] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04010400u) + off) * A[2 * L + h]);
-            o[2 * k + 1] = __builtin_bit_cast(uint32_t, (magic_pair(v, 0x04030402u) + off) * A[2 * L + h]);
-        }
+        const int H = j >> 2, grp = j & 3;
+        int sc = (int)(int8_t)(((H ? r.h.y : r.h.x) >> (8 * grp)) & 0xFF);  // scale 8H + 2grp + q/2
+        if (dzero) sc = 0;
+        const int b1 = sc & 1;
+        const _Float16 e = (_Float16)(float)(sc - b1), bb = (_Float16)(float)b1;
+        const h2 E = {e, e}, B = {bb, bb};
+        const uint2 l = r.a[2 * H + (grp & 1)], hq = r.b[H];
+        const int shl = 4 * (grp >> 1), shh = 2 * grp;
+        const uint32_t v0 = ((l.x >> shl) & 0x0F0F0F0Fu) | (((hq.x >> shh) & 0x03030303u) << 4);
+        const uint32_t v1 = ((l.y >> shl) & 0x0F0F0F0Fu) | (((hq.y >> shh) & 0x03030303u) << 4);
+        const h2 c0 = q6_centered(v0, kSelLo), c1 = q6_centered(v0, kSelHi), c2 = q6_centered(v1, kSelLo),
+                 c3 = q6_centered(v1, kSelHi);
+        o1[0] = h2u(c0 * E); o1[1] = h2u(c1 * E); o1[2] = h2u(c2 * E); o1[3] = h2u(c3 * E);
+        o2[0] = h2u(c0 * B); o2[1] = h2u(c1 * B); o2[2] = h2u(c2 * B); o2[3] = h2u(c3 * B);
+        a1 = __builtin_bit_cast(h8, make_uint4(o1[0], o1[1], o1[2], o1[3]));
+        a2 = __builtin_bit_cast(h8, make_uint4(o2[0], o2[1], o2[2], o2[3]));
     }
-    const uint4 u = make_uint4(o[0], o[1], o[2], o[3]);
-    return __builtin_bit_cast(h8, u);
 }
 
-// B slot u = 4t + q of token row r, 16-byte columns XOR-swizzled by the row so that the
-// 16 rows of a fragment read hit distinct banks
+// staged activation chunk u (16 B = 8 values) of token row r, XOR-swizzled by the row so
+// that the 16 rows of a fragment read hit distinct banks
 __device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r & 31)) << 3); }
+
+struct SkLds {
+    _Float16 b[2][kSkTok * 256];  // staged q8 of one 256-value block, double-buffered
+    float rho[2][kSkTok * 8];     // the rows' scale ratios of that block's 8 sub-blocks
+};
 
 // One 256-value block: multiply block k (raw weights in `cur`, activations in LDS buffer
 // k%2) while the weights of block k+1 load into `nxt` and its activations into the other
@@ -839,44 +858,77 @@ __device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r
 // loads issued after them (memory loads complete in issue order), so one block ahead is
 // what the pipeline can hold.
 template <int TYPE, int NB, int R>
-__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int wave, const uint8_t *const (&wrow)[R],
-                                         const _Float16 *const (&arow)[NB * 16 / kSkStage], _Float16 (*bs)[kSkTok * 256],
-                                         const SkRaw (&cur)[R], SkRaw (&nxt)[R], f4 (&acc)[R][NB]) {
+__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int wave, int tid,
+                                         const uint8_t *const (&wrow)[R],
+                                         const _Float16 *const (&arow)[NB * 16 / kSkStage], const float *rrow,
+                                         SkLds &L, const SkRaw (&cur)[R], SkRaw (&nxt)[R], float (&deff)[R][4],
+                                         f4 (&acc)[R][NB]) {
     // past the end the last block is loaded again (into the idle buffer and registers)
     const int kn = min(k + 1, nkb - 1);
 #pragma unroll
     for (int i = 0; i < NB * 16 / kSkStage; i++)
         __builtin_amdgcn_global_load_lds((const void *)(arow[i] + kn * 256),
-                                         (__attribute__((address_space(3))) void *)&bs[(k + 1) & 1][(2 * wave + kSkStage * i) * 256],
+                                         (__attribute__((address_space(3))) void *)&L.b[(k + 1) & 1][(2 * wave + kSkStage * i) * 256],
                                          16, 0, 0);
+    if (tid < NB * 16 * 2)  // the ratios: two 16-byte chunks per row
+        __builtin_amdgcn_global_load_lds((const void *)(rrow + kn * 8),
+                                         (__attribute__((address_space(3))) void *)&L.rho[(k + 1) & 1][(tid & ~63) * 4], 16,
+                                         0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // the LDS loads go first (the barrier below counts on it)
 #pragma unroll
     for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a] + (size_t)kn * bbytes, q, nxt[a]);
     // keep the loads here, ahead of the multiplication (the scheduler would otherwise sink
     // them past it to save registers, and nothing would be in flight during the MFMAs)
     __builtin_amdgcn_sched_barrier(0);
-    h2 A[R][4], B[R][4];
+    // row scales: lane c owns A row c of each tile; the lane's outputs are rows 4q + e
+    bool dz[R];
 #pragma unroll
-    for (int a = 0; a < R; a++) sk_scales<TYPE>(cur[a], q, A[a], B[a]);
-    const _Float16 *bb = bs[k & 1];
+    for (int a = 0; a < R; a++) {
+        const float d = sk_d<TYPE>(cur[a]);
+        dz[a] = d == 0.0f;
+        const float dn = dz[a] ? 0.0f : d;
 #pragma unroll
-    for (int t = 0; t < 8; t++) {
-        h8 bf[NB];
+        for (int e = 0; e < 4; e++) {
+            const float dr = __shfl(dn, 4 * q + e);
+            const float nd = dr != 0.0f ? dr : deff[a][e];
+            const float sg = deff[a][e] / nd;
+            deff[a][e] = nd;
 #pragma unroll
-        for (int b = 0; b < NB; b++) bf[b] = *(const h8 *)(bb + sk_slot(16 * b + c, 4 * t + q));
-#pragma unroll
-        for (int a = 0; a < R; a++) {
-            const h8 af = sk_operand<TYPE>(cur[a], t, A[a], B[a]);
-#pragma unroll
-            for (int b = 0; b < NB; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[a][b], 0, 0, 0);
+            for (int b = 0; b < NB; b++) acc[a][b][e] *= sg;
         }
     }
-    __syncthreads();
+    const _Float16 *bb = L.b[k & 1];
+    const float *rb = L.rho[k & 1];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        h8 bf[NB];
+        float rho[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            bf[b] = *(const h8 *)(bb + sk_slot(16 * b + c, 4 * j + q));
+            rho[b] = rb[(16 * b + c) * 8 + j];
+        }
+#pragma unroll
+        for (int a = 0; a < R; a++) {
+            h8 a1, a2;
+            sk_operand<TYPE>(cur[a], j, q, dz[a], a1, a2);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                acc[a][b] *= rho[b];
+                acc[a][b] = mfma(a1, bf[b], acc[a][b]);
+                if constexpr (TYPE == kTypeQ6K) acc[a][b] = mfma(a2, bf[b], acc[a][b]);
+            }
+        }
+    }
+    // block k+1's activations are in LDS once at most the weight loads issued after them are
+    // outstanding; those stay in flight across the barrier
+    lds_dma_barrier<R * sk_loads_per_tile<TYPE>()>();
 }
 
 template <int TYPE, int MODE, int NB>
-__device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok * 256], int wave, int lane, int tid,
-                                        int e, int j0, int n_rows, int row_base) {
-    constexpr int R = sk_rows_per_wave<MODE>() / 16;
+__device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds &L, int wave, int lane, int tid, int e, int j0,
+                                        int n_rows, int row_base) {
+    constexpr int R = sk_rows_per_wave<TYPE, MODE>() / 16;
     constexpr int H = R / 2;  // SwiGLU: gate tiles 0 .. H-1, up tiles H .. 2H-1
     const int q = lane >> 4, c = lane & 15;
     const int K = g.K, nkb = K / 256;
@@ -888,7 +940,7 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
     // this lane's weight row of each row tile (rows past M re-read the last)
     const uint8_t *wrow[R];
     int base;  // SwiGLU: first feature of the wave; grouped: first row
-    if (MODE == kModeSwiGLU) {
+    if (MODE == 1) {
         base = (blockIdx.x * kSkWaves + wave) * (16 * H);
 #pragma unroll
         for (int a = 0; a < R; a++) {
@@ -901,52 +953,100 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
         for (int a = 0; a < R; a++) wrow[a] = Wm + (size_t)min(base + 16 * a + c, g.M - 1) * wrow_bytes;
     }
     // activation staging role: physical slot tid % 32 of rows r = tid/32 + kSkStage i, which
-    // holds the logical slot (tid % 32) ^ (r % 32)
+    // holds the logical slot (tid % 32) ^ (r % 32); ratio staging: threads below 2 NB 16 copy
+    // 16-byte chunk tid % 2 of row tid / 2
     const int sr0 = tid >> 5;
     const _Float16 *arow[NB * 16 / kSkStage];
+    auto stage_row = [&](int r) {
+        const int j = min(j0 + r, n_rows - 1);
+        return MODE == 1 ? g.perm[row_base + j] : row_base + j;
+    };
 #pragma unroll
     for (int i = 0; i < NB * 16 / kSkStage; i++) {
         const int r = sr0 + kSkStage * i, u = (tid & 31) ^ (r & 31);
-        const int j = min(j0 + r, n_rows - 1);
-        const int idx = MODE == kModeSwiGLU ? g.perm[row_base + j] : row_base + j;
-        arow[i] = (const _Float16 *)g.A + (size_t)idx * K + sk_k0<TYPE>(u >> 2, u & 3);
+        arow[i] = (const _Float16 *)g.A + (size_t)stage_row(r) * K + 8 * u;
     }
+    const float *rrow = g.a_rho + (size_t)stage_row(min(tid >> 1, NB * 16 - 1)) * (K / 32) + 4 * (tid & 1);
     f4 acc[R][NB];
+    float deff[R][4];
 #pragma unroll
-    for (int a = 0; a < R; a++)
+    for (int a = 0; a < R; a++) {
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int x = 0; x < 4; x++) deff[a][x] = 1.0f;
+    }
     SkRaw r0[R], r1[R];
 #pragma unroll
     for (int i = 0; i < NB * 16 / kSkStage; i++)
         __builtin_amdgcn_global_load_lds((const void *)arow[i],
-                                         (__attribute__((address_space(3))) void *)&bs[0][(2 * wave + kSkStage * i) * 256],
+                                         (__attribute__((address_space(3))) void *)&L.b[0][(2 * wave + kSkStage * i) * 256],
                                          16, 0, 0);
+    if (tid < NB * 16 * 2)
+        __builtin_amdgcn_global_load_lds((const void *)rrow,
+                                         (__attribute__((address_space(3))) void *)&L.rho[0][(tid & ~63) * 4], 16, 0,
+                                         0);
 #pragma unroll
     for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a], q, r0[a]);
     __syncthreads();
     // two raw slots, the loop unrolled by two so that both are static
     for (int k = 0; k < nkb; k += 2) {
-        sk_block<TYPE, NB, R>(k, nkb, bbytes, q, c, wave, wrow, arow, bs, r0, r1, acc);
+        sk_block<TYPE, NB, R>(k, nkb, bbytes, q, c, wave, tid, wrow, arow, rrow, L, r0, r1, deff, acc);
         if (k + 1 >= nkb) break;
-        sk_block<TYPE, NB, R>(k + 1, nkb, bbytes, q, c, wave, wrow, arow, bs, r1, r0, acc);
+        sk_block<TYPE, NB, R>(k + 1, nkb, bbytes, q, c, wave, tid, wrow, arow, rrow, L, r1, r0, deff, acc);
     }
 
-    // D layout: lane holds weight rows 4q + e of each 16-row tile, token column c
+    // absolute values, then Q4_K's min term over windows of 32 sub-blocks (lane group q:
+    // super-block 4w + q of its A row / token)
+    float dt[NB];
+    int tok[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int j = min(j0 + 16 * b + c, n_rows - 1);
+        tok[b] = MODE == 1 ? g.perm[row_base + j] : row_base + j;
+        dt[b] = g.a_dlast[tok[b]];
+    }
+#pragma unroll
+    for (int a = 0; a < R; a++)
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int x = 0; x < 4; x++) acc[a][b][x] *= deff[a][x] * dt[b];
+    if constexpr (TYPE == kTypeQ4K) {
+        for (int w = 0; w < (nkb + 3) / 4; w++) {
+            const int sb = 4 * w + q;
+            const bool valid = sb < nkb;
+            h8 bd[NB];
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const uint4 v = valid ? ld16((const uint8_t *)(g.a_ds + (size_t)tok[b] * (K / 32) + 8 * sb))
+                                      : make_uint4(0, 0, 0, 0);
+                bd[b] = __builtin_bit_cast(h8, v);
+            }
+#pragma unroll
+            for (int a = 0; a < R; a++) {
+                const uint4 hdr = valid ? ld16(wrow[a] + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
+                h8 hi, lo;
+                q4k_min_operand(hdr, hi, lo);
+#pragma unroll
+                for (int b = 0; b < NB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
+            }
+        }
+    }
+
+    // D layout: lane holds weight rows 4q + x of each 16-row tile, token column c
 #pragma unroll
     for (int b = 0; b < NB; b++) {
         const int j = j0 + 16 * b + c;
         if (j >= n_rows) continue;
-        const int idx = MODE == kModeSwiGLU ? g.perm[row_base + j] : row_base + j;
-        const float us = g.a_unscale[idx];
         float *orow = g.out + (size_t)(row_base + j) * g.out_ld;
-        if (MODE == kModeSwiGLU) {
+        if (MODE == 1) {
 #pragma unroll
             for (int a = 0; a < H; a++) {
                 const int f = base + 16 * a + 4 * q;
 #pragma unroll
                 for (int x = 0; x < 4; x++) {
-                    const float gt = acc[a][b][x] * us, up = acc[a + H][b][x] * us;
+                    const float gt = acc[a][b][x], up = acc[a + H][b][x];
                     if (f + x < g.M) orow[f + x] = gt / (1.0f + expf(-gt)) * up;
                 }
             }
@@ -956,47 +1056,43 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, _Float16 (*bs)[kSkTok
                 const int i = base + 16 * a + 4 * q;
 #pragma unroll
                 for (int x = 0; x < 4; x++)
-                    if (i + x < g.M) orow[i + x] = acc[a][b][x] * us;
+                    if (i + x < g.M) orow[i + x] = acc[a][b][x];
             }
         }
     }
 }
 
+// MODE 1: SwiGLU (gate and up rows of the same features, activation rows gathered through
+// perm[], out[q*ld + f] = silu(gate) * up); MODE 2: the expert-sorted rows themselves.
 template <int TYPE, int MODE>
 __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmArgs g) {
-    __shared__ __align__(16) _Float16 bs[2][kSkTok * 256];
+    __shared__ __align__(16) SkLds L;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if ((int)blockIdx.y >= g.tiles[-1]) return;
     const int tl = g.tiles[blockIdx.y];
     const int e = tl >> 16, nt = tl & 0xFFFF;
     const int n_rows = g.counts[e], row_base = g.offsets[e], j0 = nt * kGroupTile;
     const int nvalid = min(kGroupTile, n_rows - j0);
-    if (nvalid > kSkTok) return;  // uniform: the tiled kernel's tile
     // one instantiation per count of 16-row column tiles, so every MFMA is unconditional
     switch ((nvalid + 15) >> 4) {
-    case 1: sk_tile<TYPE, MODE, 1>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-    case 2: sk_tile<TYPE, MODE, 2>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-    case 3: sk_tile<TYPE, MODE, 3>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-    case 4: sk_tile<TYPE, MODE, 4>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-#if MNEMO_SKTOK == 128
-    case 5: sk_tile<TYPE, MODE, 5>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-    case 6: sk_tile<TYPE, MODE, 6>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-    case 7: sk_tile<TYPE, MODE, 7>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-    default: sk_tile<TYPE, MODE, 8>(g, bs, wave, lane, tid, e, j0, n_rows, row_base); break;
-#endif
+    case 1: sk_tile<TYPE, MODE, 1>(g, L, wave, lane, tid, e, j0, n_rows, row_base); break;
+    case 2: sk_tile<TYPE, MODE, 2>(g, L, wave, lane, tid, e, j0, n_rows, row_base); break;
+    case 3: sk_tile<TYPE, MODE, 3>(g, L, wave, lane, tid, e, j0, n_rows, row_base); break;
+    default: sk_tile<TYPE, MODE, 4>(g, L, wave, lane, tid, e, j0, n_rows, row_base); break;
     }
 }
 
 // Grouped launches used by the MoE prefill path (moe.hip): tiles[] and the routing arrays
 // live in device memory, the grid covers max_tiles tile-list entries.
 int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert_stride, size_t w_off,
-                        size_t w_off2, const _Float16 *act, const float *act_unscale, const int *counts, const int *offsets, const int *perm,
-                        const int *tiles, int max_tiles, float *out, int out_ld, int M, int K,
-                        hipStream_t stream) {
+                        size_t w_off2, StagedAct act, const int *counts, const int *offsets, const int *perm,
+                        const int *tiles, int max_tiles, float *out, int out_ld, int M, int K, hipStream_t stream) {
     GemmArgs g{};
     g.W = (const uint8_t *)experts;
-    g.A = act;
-    g.a_unscale = act_unscale;
+    g.A = act.q8;
+    g.a_rho = act.rho;
+    g.a_ds = act.ds;
+    g.a_dlast = act.dlast;
     g.out = out;
     g.M = M;
     g.K = K;
@@ -1010,22 +1106,18 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
     g.offsets = offsets;
     g.perm = perm;
     g.tiles = tiles;
-    g.skip_upto = kSkTok;
-    // tiles of at most kSkTok rows: the skinny kernel; the rest: the tiled kernel
-    const int sk_rows = swiglu ? sk_rows_per_wave<kModeSwiGLU>() / 2 * kSkWaves : sk_rows_per_wave<kModeGrouped>() * kSkWaves;
-    const dim3 sk_grid((M + sk_rows - 1) / sk_rows, max_tiles, 1);
-#define MNEMO_SKINNY(T_, M_) hipLaunchKernelGGL((gemm_skinny_kernel<T_, M_>), sk_grid, dim3(kSkThreads), 0, stream, g)
-    if (swiglu) {
-        if (type == kTypeQ4K) MNEMO_SKINNY(kTypeQ4K, kModeSwiGLU);
-        else MNEMO_SKINNY(kTypeQ6K, kModeSwiGLU);
-    } else {
-        if (type == kTypeQ4K) MNEMO_SKINNY(kTypeQ4K, kModeGrouped);
-        else MNEMO_SKINNY(kTypeQ6K, kModeGrouped);
-    }
+    if (swiglu && type != kTypeQ4K)
+        return set_error(kErrUnsupportedType, "grouped gate/up GEMM: Q4_K only (type %d)", type);
+#define MNEMO_SKINNY(T_, M_)                                                                                    \
+    do {                                                                                                        \
+        const int rows = sk_rows_per_wave<T_, M_>() / (M_ == 1 ? 2 : 1) * kSkWaves;                            \
+        hipLaunchKernelGGL((gemm_skinny_kernel<T_, M_>), dim3((M + rows - 1) / rows, max_tiles, 1), dim3(kSkThreads), \
+                           0, stream, g);                                                                       \
+    } while (0)
+    if (swiglu) MNEMO_SKINNY(kTypeQ4K, 1);
+    else if (type == kTypeQ4K) MNEMO_SKINNY(kTypeQ4K, 2);
+    else MNEMO_SKINNY(kTypeQ6K, 2);
 #undef MNEMO_SKINNY
-    if (kGroupTile <= kSkTok) return check_launch("gemm_grouped");  // no tile is left
-    if (swiglu) launch_mode<kModeSwiGLU, false>(type, false, dim3((M + kBM / 2 - 1) / (kBM / 2), max_tiles, 1), g, stream);
-    else launch_mode<kModeGrouped, false>(type, false, dim3((M + kBM - 1) / kBM, max_tiles, 1), g, stream);
     return check_launch("gemm_grouped");
 }
 

@@ -56,6 +56,22 @@ __device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
     return o[0];
 }
 
+__device__ __forceinline__ uint2 ld8(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+// 8 bytes from a 2-byte aligned address: three aligned dwords at or below p, shifted into
+// place (reads stay inside [p - 2, p + 10)).
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 2u;
+    const uint32_t *a = (const uint32_t *)(p - sh);
+    uint32_t w[3];
+    __builtin_memcpy(&w[0], a, 8);
+    w[2] = a[sh ? 2 : 1];
+    return make_uint2(__builtin_amdgcn_alignbyte(w[1], w[0], sh), __builtin_amdgcn_alignbyte(w[2], w[1], sh));
+}
+
 __device__ __forceinline__ uint4 ld16_nt(const uint8_t *p) {
     // streaming weights: read once per call, do not keep them in the caches
     uint4 v;

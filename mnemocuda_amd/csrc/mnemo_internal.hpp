@@ -7,14 +7,18 @@
 namespace mnemo {
 
 // Token rows per tile of a grouped (MoE prefill) GEMM launch, the unit of the tile list the
-// routing writes.  64: every tile fits the skinny grouped kernel, and an expert with more
-// tokens is read once per 64 of them (measured 0.81 ms for the cfg5 prefill against 0.91 ms
-// with 128-row tiles, whose large tiles went to the tiled kernel).  Building with
-// -DMNEMO_MOE_TILE=128 restores that split.
-#ifndef MNEMO_MOE_TILE
-#define MNEMO_MOE_TILE 64
-#endif
-constexpr int kGroupTile = MNEMO_MOE_TILE;
+// routing writes (up to four 16-token MFMA columns of the grouped kernel).
+constexpr int kGroupTile = 64;
+
+// Activation rows staged for the grouped GEMM (gemm.hip, stage_f32_kernel): the Q8_1 values
+// of each row as f16 integers [rows][K], the f16 ds of each 32-value sub-block [rows][K/32],
+// the running-scale ratio of each sub-block [rows][K/32] and the row's last nonzero d8 [rows].
+struct StagedAct {
+    _Float16 *q8;
+    float *rho;
+    uint16_t *ds;
+    float *dlast;
+};
 
 // Error codes reported through mnemo_last_error() (include/mnemo_kernels.h).
 constexpr int kOk = 0;

@@ -12,14 +12,15 @@
 // the quantized rows are staged directly in the GEMM's f16 operand form.
 //
 // Workspace layout (each part 256-byte aligned), sizes for T tokens, k slots, E experts:
-//   xs      T staged rows of x: f16 values of Q8_1(x) scaled by 2^-e_row; xun: 2^e_row
+//   xs      T staged rows of x (StagedAct: q8 [T][hidden] f16, rho and ds [T][hidden/32],
+//           dlast [T])
 //   counts  E ints, offsets E ints
 //   rank    T*k ints   (rank of a pair within its expert; -1 for dropped slots)
 //   inv     T*k ints   (pair -> expert-sorted row, -1 for dropped slots)
 //   perm    T*k ints   (expert-sorted row -> token)
 //   tiles   1 + E + ceil(T*k/kGroupTile) ints (count, then (expert << 16) | token tile)
 //   act     T*k rows of eff fp32 (SwiGLU output)
-//   acts    T*k staged rows of Q8_1(act), actun: their 2^e_row
+//   acts    T*k staged rows of Q8_1(act) (StagedAct)
 //   down    T*k rows of hidden fp32
 #include <algorithm>
 #include <cstring>
@@ -29,11 +30,10 @@
 
 namespace mnemo {
 
-int launch_stage_f32(const float *x, int K, int N, _Float16 *out, float *unscale, hipStream_t s);
+int launch_stage_f32(const float *x, int K, int N, StagedAct sa, hipStream_t s);
 int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert_stride, size_t w_off,
-                        size_t w_off2, const _Float16 *act, const float *act_unscale, const int *counts,
-                        const int *offsets, const int *perm, const int *tiles, int max_tiles, float *out,
-                        int out_ld, int M, int K, hipStream_t stream);
+                        size_t w_off2, StagedAct act, const int *counts, const int *offsets, const int *perm,
+                        const int *tiles, int max_tiles, float *out, int out_ld, int M, int K, hipStream_t stream);
 
 int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s);
 int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k, hipStream_t s);
@@ -46,7 +46,7 @@ constexpr int kMaxMoeExperts = 512;
 constexpr int kMoeTileRows = kGroupTile;  // token rows per grouped GEMM tile
 
 struct MoeLayout {
-    size_t xs, xun, counts, offsets, rank, inv, perm, tiles, act, acts, actun, down, total;
+    size_t xs, xr, xds, xdl, counts, offsets, rank, inv, perm, tiles, act, acts, actr, actds, actdl, down, total;
     int max_tiles;
 };
 
@@ -63,7 +63,9 @@ static MoeLayout moe_layout(int T, int hidden, int eff, int E, int k) {
         return at;
     };
     L.xs = take((size_t)T * hidden * 2);
-    L.xun = take((size_t)T * 4);
+    L.xr = take((size_t)T * (hidden / 32) * 4);
+    L.xds = take((size_t)T * (hidden / 32) * 2);
+    L.xdl = take((size_t)T * 4);
     L.counts = take((size_t)E * 4);
     L.offsets = take((size_t)E * 4);
     L.rank = take(pairs * 4);
@@ -72,7 +74,9 @@ static MoeLayout moe_layout(int T, int hidden, int eff, int E, int k) {
     L.tiles = take((size_t)(1 + L.max_tiles) * 4);
     L.act = take(pairs * eff * 4);
     L.acts = take(pairs * eff * 2);
-    L.actun = take(pairs * 4);
+    L.actr = take(pairs * (eff / 32) * 4);
+    L.actds = take(pairs * (eff / 32) * 2);
+    L.actdl = take(pairs * 4);
     L.down = take(pairs * hidden * 4);
     L.total = o;
     return L;
@@ -214,19 +218,21 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
     int bits = 1;
     while ((1 << bits) <= E) bits++;
 
-    _Float16 *xs = (_Float16 *)(w8 + L.xs), *acts = (_Float16 *)(w8 + L.acts);
-    float *xun = (float *)(w8 + L.xun), *actun = (float *)(w8 + L.actun);
-    int rc = launch_stage_f32(x, hidden, T, xs, xun, s);
+    const StagedAct xs{(_Float16 *)(w8 + L.xs), (float *)(w8 + L.xr), (uint16_t *)(w8 + L.xds),
+                       (float *)(w8 + L.xdl)};
+    const StagedAct acts{(_Float16 *)(w8 + L.acts), (float *)(w8 + L.actr), (uint16_t *)(w8 + L.actds),
+                         (float *)(w8 + L.actdl)};
+    int rc = launch_stage_f32(x, hidden, T, xs, s);
     if (rc) return rc;
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, s, topk_idx, pairs, E, bits, counts,
                        offsets, rank, inv, perm, tiles, k);
     if ((rc = check_launch("moe_route"))) return rc;
     // gate + up, SwiGLU fused: act[q][f]
-    rc = launch_gemm_grouped(kTypeQ4K, 1, experts, expert_stride, gate_off, up_off, xs, xun, counts, offsets, perm,
+    rc = launch_gemm_grouped(kTypeQ4K, 1, experts, expert_stride, gate_off, up_off, xs, counts, offsets, perm,
                              tiles + 1, L.max_tiles, act, eff, eff, hidden, s);
     if (rc) return rc;
-    if ((rc = launch_stage_f32(act, eff, pairs, acts, actun, s))) return rc;
-    rc = launch_gemm_grouped(down_type, 0, experts, expert_stride, down_off, down_off, acts, actun, counts, offsets,
+    if ((rc = launch_stage_f32(act, eff, pairs, acts, s))) return rc;
+    rc = launch_gemm_grouped(down_type, 0, experts, expert_stride, down_off, down_off, acts, counts, offsets,
                              nullptr, tiles + 1, L.max_tiles, down, hidden, hidden, eff, s);
     if (rc) return rc;
     const long n4 = (long)T * hidden / 4;

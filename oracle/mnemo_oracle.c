@@ -340,12 +340,49 @@ void mo_dequant_q8_1_mmq(const void *src, float *out, int K, int N) {
         }
 }
 
-/* out[j*M + i] = sum_k deq(W)[i][k] * deq(Q8_1)[j][k] in fp64: the product the
- * reference GEMM computes (gemm_q4k.cu:103-112, 164-166; output column-major [N][M]
- * as gemm_q4k.cu:194).  The min term is taken as dmin*m * sum_k deq(a)_k, i.e. the
- * exact dequantised activations, not the ds.y field. */
+/* The Q4_K x Q8_1 product of gemm_q4k.cu:103-112, 164-166 in fp64, per 32-value
+ * sub-block s of weight row i and token j:
+ *     (d*sc_s) * d8_js * sum_{k in s} q_ik * q8_jk  -  (dmin*m_s) * ds_js
+ * with ds_js the block's second half (d8 * sum of the unquantized values, the field
+ * gemm_q4k.cu:166 multiplies by dmA.y).  d*sc and dmin*m are taken exactly (the reference
+ * rounds them to f16, gemm_q4k.cu:106-111; the GEMV path keeps them in fp32,
+ * kernels.cu:114-136). */
+static void gemm_q4k_split(const uint8_t *w, const uint8_t *act, double *out, int M, int K, int N) {
+    const int nb = K / 256, na = K / 128;
+    for (int j = 0; j < N; j++)
+        for (int i = 0; i < M; i++) {
+            double acc = 0.0;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t *blk = w + ((size_t)i * nb + b) * MO_Q4K_BYTES;
+                const double d = mo_f16_to_f32(rd16(blk)), dmin = mo_f16_to_f32(rd16(blk + 2));
+                for (int s = 0; s < 8; s++) {
+                    uint8_t sc, m;
+                    mo_get_scale_min_k4(s, blk + 4, &sc, &m);
+                    const int sb = 2 * b + s / 4, sub = s % 4; /* Q8_1 block and sub-block */
+                    const uint8_t *ab = act + ((size_t)j * na + sb) * MO_Q8_1_MMQ_BYTES;
+                    const double d8 = mo_f16_to_f32(rd16(ab + 4 * sub));
+                    const double ds = mo_f16_to_f32(rd16(ab + 4 * sub + 2));
+                    long isum = 0;
+                    for (int l = 0; l < 32; l++) {
+                        const int q = (blk[16 + 32 * (s / 2) + l] >> (4 * (s % 2))) & 15;
+                        isum += (long)q * (int8_t)ab[16 + 32 * sub + l];
+                    }
+                    acc += d * sc * d8 * (double)isum - dmin * m * ds;
+                }
+            }
+            out[(size_t)j * M + i] = acc;
+        }
+}
+
+/* out[j*M + i] (column-major [N][M] as gemm_q4k.cu:194): Q4_K in the split form above;
+ * Q6_K (no min term) as the fp64 product of the dequantised operands,
+ * sum_k deq(W)[i][k] * d8_j * q8_jk. */
 int mo_gemm_q8_1(int type_id, const void *w, const void *act, double *out, int M, int K, int N) {
     if (K % 256) return -3;
+    if (type_id == MO_TYPE_Q4K) {
+        gemm_q4k_split((const uint8_t *)w, (const uint8_t *)act, out, M, K, N);
+        return 0;
+    }
     float *wd = (float *)malloc((size_t)M * K * sizeof(float));
     float *ad = (float *)malloc((size_t)N * K * sizeof(float));
     if (!wd || !ad) { free(wd); free(ad); return -2; }

@@ -21,7 +21,10 @@
  *   mo_quantize_q8_1     closed forms per block (zero block, +-amax maps to +-127,
  *                        round-half-even ties) and an independent numpy restatement.
  *   mo_topk_softmax      numpy argsort (stable) + fp64 softmax.
- *   mo_gemm_*            numpy fp64 matmul of the dequantised operands.
+ *   mo_gemm_*            an independent numpy restatement (main part from the decoded
+ *                        integers, min term from the ds field); d = 0 weights leave the min
+ *                        term alone; the identity split - full dequant product =
+ *                        sum_s dmin*m_s * (d8 * sum q8 - ds).
  *   mo_xoroshiro_next    an independent Python restatement of xoroshiro128+ (64-bit
  *                        wrap-around arithmetic) over many seeds.
  *   mo_sample_token      greedy = numpy argmax; top_p -> 0 draws the argmax for every

@@ -253,3 +253,37 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_heads: int, head_di
         p = np.exp(s - s.max())
         out[h] = (p / p.sum()) @ v[:, kv[h], :].astype(np.float64)
     return out.astype(np.float32).reshape(-1)
+
+
+def q8_1_ds(blocks: np.ndarray, k: int) -> np.ndarray:
+    """The second half of each (d8, ds) pair: (N, k // 32) float32."""
+    b = np.asarray(blocks, np.uint8).reshape(-1, k // 128, Q81_BYTES)
+    return f16_bits_to_f32(b[..., :16].copy().view("<u2")[..., 1::2]).reshape(b.shape[0], k // 32)
+
+
+def q4k_split(raw: np.ndarray, n_rows: int, n_cols: int):
+    """Q4_K rows -> (main, mins): main (n_rows, n_cols) = d * sc * q and mins
+    (n_rows, n_cols // 32) = dmin * m per 32-value sub-block, both exact in float64."""
+    b = np.asarray(raw, np.uint8).reshape(n_rows, n_cols // 256, Q4K_BYTES)
+    d = f16_bits_to_f32(b[..., 0:2].copy().view("<u2")[..., 0]).astype(np.float64)
+    dmin = f16_bits_to_f32(b[..., 2:4].copy().view("<u2")[..., 0]).astype(np.float64)
+    sc, m = scale_min_k4_all(b[..., 4:16].reshape(-1, 12))
+    sc = sc.reshape(n_rows, -1, 8).astype(np.float64)
+    m = m.reshape(n_rows, -1, 8).astype(np.float64)
+    qs = b[..., 16:].reshape(n_rows, -1, 4, 32)
+    q = np.empty(qs.shape[:2] + (8, 32), np.float64)
+    q[:, :, 0::2] = qs & 0x0F
+    q[:, :, 1::2] = qs >> 4
+    main = (d[..., None, None] * sc[..., None]) * q
+    mins = dmin[..., None] * m
+    return main.reshape(n_rows, n_cols), mins.reshape(n_rows, n_cols // 32)
+
+
+def gemm_q8_1(type_id: int, raw: np.ndarray, blocks: np.ndarray, M: int, K: int, N: int) -> np.ndarray:
+    """fp64 (N, M): Q4_K as main . deq(Q8_1)^T - ds . mins^T (gemm_q4k.cu:164-166, the min term
+    taken from the activation block's ds field); Q6_K as deq(W) . deq(Q8_1)^T."""
+    a = dequant_q8_1_mmq(blocks, K).astype(np.float64)
+    if type_id == 12:
+        main, mins = q4k_split(raw, M, K)
+        return a @ main.T - q8_1_ds(blocks, K).astype(np.float64) @ mins.T
+    return a @ dequant_matrix(raw, type_id, M, K).astype(np.float64).T

@@ -52,7 +52,7 @@ def main():
     fx["q8_1_src"], fx["q8_1_blocks"] = a, aq
     wg = synth.weights(rng, 12, 64, 512)
     fx["gemm_w"], fx["gemm_out"] = wg, o.gemm(12, wg, aq, 64, 512, 8)
-    ref = onp.dequant_q8_1_mmq(aq, 512).astype(np.float64) @ onp.dequant_matrix(wg, 12, 64, 512).T.astype(np.float64)
+    ref = onp.gemm_q8_1(12, wg, aq, 64, 512, 8)
     assert np.max(np.abs(fx["gemm_out"] - ref)) <= 1e-9 * np.max(np.abs(ref))
     # a 128-logit top-8 case (with a tie) and the router matvec
     logits = rng.standard_normal(128).astype(np.float32)

@@ -267,15 +267,32 @@ def test_gemm_vs_numpy(oracle, rng, type_id):
     w = synth.weights(rng, type_id, M, K)
     act = oracle.quantize_q8_1(rng.standard_normal((N, K)).astype(np.float32))
     out = oracle.gemm(type_id, w, act, M, K, N)
-    ref = onp.dequant_q8_1_mmq(act, K).astype(np.float64) @ onp.dequant_matrix(w, type_id, M, K).T.astype(np.float64)
-    assert rel_l2(out, ref) < 1e-12
-    # min term alone: d = 0 leaves -dmin * m * sum(deq(a)) (Q4_K)
-    if type_id == 12:
-        w2 = w.reshape(-1, 144).copy()
-        w2[:, 0:2] = 0
-        out2 = oracle.gemm(12, w2.reshape(-1), act, M, K, N)
-        ref2 = onp.dequant_q8_1_mmq(act, K).astype(np.float64) @ onp.dequant_matrix(w2.reshape(-1), 12, M, K).T
-        assert rel_l2(out2, ref2) < 1e-12
+    assert rel_l2(out, onp.gemm_q8_1(type_id, w, act, M, K, N)) < 1e-12
+    full = onp.dequant_q8_1_mmq(act, K).astype(np.float64) @ onp.dequant_matrix(w, type_id, M, K).T.astype(np.float64)
+    if type_id == 14:  # no min term: the product of the dequantised operands
+        assert rel_l2(out, full) < 1e-12
+        return
+    # Q4_K: the reference takes the min term from the block's ds field (gemm_q4k.cu:166), so
+    # out - (full dequantised product) = sum_s dmin*m_s * (d8 * sum_k q8_k - ds), computed
+    # here from the raw bytes alone
+    b = w.reshape(M, K // 256, 144)
+    dmin = b[..., 2:4].copy().view(np.float16)[..., 0].astype(np.float64)
+    _, m = onp.scale_min_k4_all(b[..., 4:16].reshape(-1, 12))
+    mins = (dmin[..., None] * m.reshape(M, -1, 8)).reshape(M, K // 32)
+    ab = act.reshape(N, K // 128, 144)
+    d8 = ab[..., :16].copy().view(np.float16)[..., 0::2].astype(np.float64).reshape(N, K // 32)
+    ds = ab[..., :16].copy().view(np.float16)[..., 1::2].astype(np.float64).reshape(N, K // 32)
+    qsum = ab[..., 16:].view(np.int8).reshape(N, K // 32, 32).sum(axis=2).astype(np.float64)
+    diff = (d8 * qsum - ds) @ mins.T
+    # (full holds the fp32-rounded dequantised weights: |error| <= 2^-24 sum_k |w_k a_k|)
+    bound = 2.0**-23 * (np.abs(onp.dequant_q8_1_mmq(act, K)).astype(np.float64)
+                        @ np.abs(onp.dequant_matrix(w, 12, M, K)).T.astype(np.float64))
+    assert np.all(np.abs(out - full - diff) <= bound + 1e-12)
+    # min term alone: d = 0 leaves -sum_s dmin * m_s * ds
+    w2 = w.reshape(-1, 144).copy()
+    w2[:, 0:2] = 0
+    out2 = oracle.gemm(12, w2.reshape(-1), act, M, K, N)
+    assert rel_l2(out2, -(ds @ mins.T)) < 1e-12
 
 
 # ------------------------------------------------------------------ next-token selection
