@@ -200,6 +200,21 @@ int mnemo_moe_decode_rmsnorm(const float *router_w, const void *experts, size_t 
                              const float *x, const float *norm_w, float eps, int hidden, int eff,
                              int n_experts, int k, void *workspace, size_t workspace_bytes,
                              float *out, int *topk_idx, float *topk_w, hipStream_t stream);
+/* New, no counterpart in the reference: mnemo_moe_decode_rmsnorm for callers that cannot
+ * allocate or hold a workspace (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  It allocates nothing: the workspace is a device array inside the
+ * library, one copy per GPU kept until the process ends, set up by cuda_kernels_init (or by
+ * the first call on a GPU).  Sizes must fit that array, 1,179,648 bytes of workspace
+ * (mnemo_moe_decode_workspace_bytes(hidden, eff, n_experts, k) <= that: hidden 8192,
+ * eff 4096, 1024 experts, k 16 fit); larger sizes are rejected with an error.  Every call on
+ * a GPU shares that GPU's array, so calls that overlap on one GPU (other streams or host
+ * threads) race. */
+int mnemo_moe_decode_rmsnorm_noalloc(const float *router_w, const void *experts,
+                                     size_t expert_stride, size_t gate_off, size_t up_off,
+                                     size_t down_off, int down_type, const float *x,
+                                     const float *norm_w, float eps, int hidden, int eff,
+                                     int n_experts, int k, float *out, int *topk_idx,
+                                     float *topk_w, hipStream_t stream);
 
 /* ---- Attention chain around the projections (forward.c:687-786, graph form 1290-1420) ----
  * Reference entry points, same arguments and semantics: */

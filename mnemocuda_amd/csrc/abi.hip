@@ -46,6 +46,11 @@ int launch_sample_token_ws(const float *logits, int V, float temperature, float 
                            void *ws, size_t ws_bytes, int *out, hipStream_t stream);
 size_t sample_workspace_bytes();
 size_t moe_decode_workspace_bytes(int hidden, int eff, int E, int k);
+int moe_decode_scratch_init();
+int launch_moe_decode_noalloc(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
+                              size_t up_off, size_t down_off, int down_type, const float *x, const float *norm_w,
+                              float eps, int hidden, int eff, int E, int k, float *out, int *idx_out, float *w_out,
+                              hipStream_t s);
 int launch_moe_decode(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
                       size_t up_off, size_t down_off, int down_type, const float *x, const float *norm_w, float eps,
                       int hidden, int eff, int E, int k, void *ws, size_t ws_bytes, float *out, int *idx_out,
@@ -111,8 +116,11 @@ void cuda_kernels_init(void) {
         set_error(kErrLaunch, "cuda_kernels_init: no HIP device");
         return;
     }
-    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
         set_error(kErrLaunch, "cuda_kernels_init: built for gfx950, device is %s", prop.gcnArchName);
+        return;
+    }
+    moe_decode_scratch_init();  // this device's copy of the no-allocation decode scratch
 }
 
 void cuda_matvec_q4k(const void *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s) {
@@ -556,6 +564,15 @@ int mnemo_moe_decode_rmsnorm(const float *router_w, const void *experts, size_t 
     if (!norm_w) return set_error(kErrBadArg, "moe_decode_rmsnorm: norm_w is NULL");
     return launch_moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, norm_w, eps,
                              hidden, eff, n_experts, k, workspace, workspace_bytes, out, topk_idx, topk_w, s);
+}
+
+int mnemo_moe_decode_rmsnorm_noalloc(const float *router_w, const void *experts, size_t expert_stride,
+                                     size_t gate_off, size_t up_off, size_t down_off, int down_type, const float *x,
+                                     const float *norm_w, float eps, int hidden, int eff, int n_experts, int k,
+                                     float *out, int *topk_idx, float *topk_w, hipStream_t s) {
+    if (!norm_w) return set_error(kErrBadArg, "moe_decode_rmsnorm_noalloc: norm_w is NULL");
+    return launch_moe_decode_noalloc(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x,
+                                     norm_w, eps, hidden, eff, n_experts, k, out, topk_idx, topk_w, s);
 }
 
 }  // extern "C"

@@ -24,6 +24,7 @@
 //   down    T*k rows of hidden fp32
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
@@ -351,6 +352,77 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     a.ex.n_experts = E;
     if ((rc = launch_gemv_experts(a, s))) return rc;
     return kOk;
+}
+
+// ------------------------------------------------------------------ decode without allocation
+// The decode MoE block for callers that cannot allocate or pass a workspace (code under
+// graph capture, serving loops): the workspace is the file-scope device array below, one
+// copy per GPU, held until the process ends.  Every call on a GPU uses that GPU's copy, so
+// calls that overlap on one GPU (other streams, other threads) race; the counters the
+// kernels need at zero (the router's arrival counter; the gate/up launch clears the tile
+// counters itself) are zeroed when a GPU's copy is first set up and every call leaves them
+// zero.  Sizes: moe_decode_layout(hidden, eff, n_experts, k) must fit kDecodeScratchBytes
+// (hidden 8192, eff 4096, 1024 experts, k 16 fit).
+constexpr size_t kDecodeScratchBytes = (size_t)1152 * 1024;
+static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static void *g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+__global__ void zero_words_kernel(uint32_t *__restrict__ p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// The device address of this GPU's scratch (hipGetSymbolAddress: the array's name is a
+// host-side stand-in that kernels cannot use).  `s`: the stream that zeroes a first-time
+// copy with a fill kernel (stream-ordered and capture-safe), or null to zero it
+// synchronously (set-up from cuda_kernels_init, outside any capture).
+static int decode_scratch(hipStream_t s, bool sync, void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+        return set_error(kErrLaunch, "moe_decode scratch: no usable HIP device");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(kErrLaunch, "moe_decode scratch: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+        const int words = (int)(kDecodeScratchBytes / 4);
+        if (sync) {
+            if (hipMemset(p, 0, kDecodeScratchBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+                return set_error(kErrLaunch, "moe_decode scratch: zeroing failed");
+        } else {
+            hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, s, (uint32_t *)p, words);
+            if (int rc = check_launch("moe_decode scratch zero")) return rc;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return kOk;
+}
+
+int moe_decode_scratch_init() {
+    void *p;
+    return decode_scratch(nullptr, true, &p);
+}
+
+int launch_moe_decode_noalloc(const float *router_w, const void *experts, size_t expert_stride, size_t gate_off,
+                              size_t up_off, size_t down_off, int down_type, const float *x, const float *norm_w,
+                              float eps, int hidden, int eff, int E, int k, float *out, int *idx_out, float *w_out,
+                              hipStream_t s) {
+    if (hidden <= 0 || eff <= 0 || E <= 0 || k <= 0)
+        return set_error(kErrBadArg, "moe_decode_rmsnorm_noalloc: non-positive size");
+    const size_t need = moe_decode_layout(hidden, eff, E, k).total;
+    if (need > kDecodeScratchBytes)
+        return set_error(kErrBadArg,
+                         "moe_decode_rmsnorm_noalloc: hidden %d, eff %d, %d experts, k %d need %zu bytes of scratch, "
+                         "the library holds %zu",
+                         hidden, eff, E, k, need, kDecodeScratchBytes);
+    void *ws = nullptr;
+    if (int rc = decode_scratch(s, false, &ws)) return rc;
+    return launch_moe_decode(router_w, experts, expert_stride, gate_off, up_off, down_off, down_type, x, norm_w, eps,
+                             hidden, eff, E, k, ws, kDecodeScratchBytes, out, idx_out, w_out, s);
 }
 
 }  // namespace mnemo

@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "mnemo_moe_decode": (i32, [fp, vp, sz, sz, sz, sz, i32, fp, i32, i32, i32, i32, vp, sz, fp, ip, fp, stream_t]),
     "mnemo_moe_decode_rmsnorm": (i32, [fp, vp, sz, sz, sz, sz, i32, fp, fp, f32, i32, i32, i32, i32, vp, sz, fp,
                                         ip, fp, stream_t]),
+    "mnemo_moe_decode_rmsnorm_noalloc": (i32, [fp, vp, sz, sz, sz, sz, i32, fp, fp, f32, i32, i32, i32, i32, fp, ip,
+                                                fp, stream_t]),
     # attention chain
     "cuda_rms_norm": (None, [fp, fp, fp, i32, f32, stream_t]),
     "cuda_rms_norm_residual": (None, [fp, fp, fp, fp, i32, f32, stream_t]),
