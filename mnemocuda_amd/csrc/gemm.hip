@@ -742,192 +742,252 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
 
 // ------------------------------------------------------------------ skinny grouped kernel
 // The grouped expert GEMMs of the MoE prefill: an expert receives a few tens of tokens, so a
-// tile is at most kGroupTile (64) token rows and the weights dominate the traffic.  Every
-// lane loads the raw bytes of its own A-operand values and converts them in registers;
-// nothing but the tile's activation rows is staged in LDS.  Each MFMA covers one sub-block
-// (the running scale needs the exact per-sub-block sums): lane group q = lane/16 holds
-// values 8q .. 8q+7 of the sub-block, i.e.
+// tile is at most kGroupTile (64) token rows and the weights dominate the traffic.  A
+// workgroup of 8 waves multiplies one token tile with 8 x 16R weight rows; every wave owns R
+// row tiles of 16 and converts its own A operands in registers, and the tile's staged
+// activation rows are shared through LDS.  Each MFMA covers one sub-block (the running scale
+// needs the exact per-sub-block sums): lane group q = lane/16 holds values 8q .. 8q+7 of the
+// sub-block, i.e.
 //   Q4_K sub-block j = 2g + h: qs bytes 32g + 8q .. +7, nibble h;
 //   Q6_K sub-block j = 4H + grp: ql bytes 64H + 32(grp%2) + 8q .. +7 (nibble grp/2), qh bytes
 //        32H + 8q .. +7 (bits 2grp), scale 8H + 2grp + q/2;
 // and the activation fragment is the staged row's values 32j + 8q .. +7 (natural order).
+// Q4_K weights reach the wave through its own LDS area: the 16 rows x 144 B of a tile's
+// block are 144 row-contiguous 16-byte chunks copied with global_load_lds (whole cache lines
+// per request, no registers held while they are in flight -- lanes loading their own 8-byte
+// pieces touch 16 rows per instruction and kept the L1 busy at ~3 TB/s in a read test
+// against ~4.8 TB/s for the copies), then read back per lane.  Q6_K blocks are 210 B and
+// only 2-byte aligned, so the lanes load them directly.
 constexpr int kSkThreads = 512;  // 8 waves
 constexpr int kSkWaves = kSkThreads / 64;
-constexpr int kSkTok = kGroupTile;  // token rows per tile: up to 4 column tiles of 16
+constexpr int kSkTok = kGroupTile;         // token rows per tile: up to 4 column tiles of 16
 constexpr int kSkStage = kSkThreads / 32;  // activation rows staged per pass (32 chunks each)
 // weight rows per wave: SwiGLU one gate and one up tile of 16 (same features); grouped two
 // tiles of 16 (Q4_K) or one (Q6_K, whose raw blocks take more registers)
 template <int TYPE, int MODE>
 constexpr int sk_rows_per_wave() { return MODE == 1 || TYPE == kTypeQ4K ? 32 : 16; }
+// One block of a 16-row tile is 2304 B = 144 chunks of 16 B.  Every copy instruction is
+// issued by the whole wave (a lane-predicated copy invites the compiler to merge it with its
+// neighbour and derive the wave-uniform LDS address from the wrong lane): chunks 0-127 of
+// tile a go to bytes 2048a .. of the wave's area with two copies, chunks 128-143 of all
+// tiles to the tail at 2048R + 256a with one copy, whose lanes past 16R repeat a chunk into
+// the unused rest of the tail.
+constexpr int kSkQ4Tile = 16 * kQ4KBytes;
+template <int R>
+constexpr int sk_q4_area() { return 2048 * R + 1024; }
+template <int R>
+constexpr int sk_q4_copies() { return 2 * R + 1; }
 
-// raw bytes of one row tile's lane values for one 256-value block
-struct SkRaw {
-    uint4 h;      // Q4_K: header (d, dmin, 12 scale bytes);  Q6_K: h.x / h.y the lane's scale
-                  // bytes of halves 0 / 1 (byte grp: scale 8H + 2grp + q/2)
-    uint2 a[4];   // Q4_K: qs bytes 32g + 8q .. +7;  Q6_K: ql bytes 64H + 32p + 8q .. (index 2H + p)
-    uint2 b[2];   // Q6_K: qh bytes 32H + 8q .. +7
-    uint32_t d;   // Q6_K: f16 d
+// Q6_K raw bytes of one row tile's lane values for one block
+struct SkRaw6 {
+    uint2 ql[4];  // ql bytes 64H + 32p + 8q .. +7 (index 2H + p)
+    uint2 qh[2];  // qh bytes 32H + 8q .. +7
+    uint32_t sc[2];  // the lane's scale bytes of halves 0 / 1 (byte grp: scale 8H + 2grp + q/2)
+    uint32_t d;      // f16 d
 };
+// vector memory instructions of sk_load6: six 8-byte and one 16-byte unaligned loads (two
+// instructions each: ld8_a2, ld16_a2) and the 2-byte d
+constexpr int kSk6Loads = 15;
 
-// vector memory instructions sk_load issues per row tile: Q4_K one 16-byte header and four
-// 8-byte loads; Q6_K six 8-byte and one 16-byte unaligned loads (two instructions each:
-// ld8_a2, ld16_a2) and the 2-byte d
-template <int TYPE>
-constexpr int sk_loads_per_tile() { return TYPE == kTypeQ4K ? 5 : 15; }
-
-template <int TYPE>
-__device__ __forceinline__ void sk_load(const uint8_t *__restrict__ blk, int q, SkRaw &r) {
-    if (TYPE == kTypeQ4K) {
-        r.h = ld16(blk);
+__device__ __forceinline__ void sk_load6(const uint8_t *__restrict__ blk, int q, SkRaw6 &r) {
 #pragma unroll
-        for (int g = 0; g < 4; g++) r.a[g] = ld8(blk + 16 + 32 * g + 8 * q);
-    } else {
+    for (int i = 0; i < 4; i++) r.ql[i] = ld8_a2(blk + 64 * (i >> 1) + 32 * (i & 1) + 8 * q);
 #pragma unroll
-        for (int i = 0; i < 4; i++) r.a[i] = ld8_a2(blk + 64 * (i >> 1) + 32 * (i & 1) + 8 * q);
-#pragma unroll
-        for (int H = 0; H < 2; H++) r.b[H] = ld8_a2(blk + 128 + 32 * H + 8 * q);
-        // of the 16 scale bytes the lane needs 8H + 2grp + q/2: bytes q/2, 2 + q/2, .. of each
-        // dword, packed into h.x (half 0) and h.y (half 1)
-        const uint4 sc = ld16_a2(blk + 192);
-        const uint32_t sel = 0x06040200u + 0x01010101u * (uint32_t)(q >> 1);
-        r.h.x = __builtin_amdgcn_perm(sc.y, sc.x, sel);
-        r.h.y = __builtin_amdgcn_perm(sc.w, sc.z, sel);
-        uint16_t dd;
-        __builtin_memcpy(&dd, blk + 208, 2);
-        r.d = dd;
-    }
+    for (int H = 0; H < 2; H++) r.qh[H] = ld8_a2(blk + 128 + 32 * H + 8 * q);
+    // of the 16 scale bytes the lane needs 8H + 2grp + q/2: bytes q/2, 2 + q/2, .. of each
+    // dword, packed per half
+    const uint4 sc = ld16_a2(blk + 192);
+    const uint32_t sel = 0x06040200u + 0x01010101u * (uint32_t)(q >> 1);
+    r.sc[0] = __builtin_amdgcn_perm(sc.y, sc.x, sel);
+    r.sc[1] = __builtin_amdgcn_perm(sc.w, sc.z, sel);
+    uint16_t dd;
+    __builtin_memcpy(&dd, blk + 208, 2);
+    r.d = dd;
 }
 
-// the block's d (0 when absent)
-template <int TYPE>
-__device__ __forceinline__ float sk_d(const SkRaw &r) {
-    return TYPE == kTypeQ4K ? h2f(r.h.x & 0xFFFFu) : h2f(r.d);
+// Q4_K lane view of a tile's block: the header (d, dmin, scales) and the lane's qs bytes
+struct SkQ4 {
+    uint4 h;
+    uint2 a[4];  // qs bytes 32g + 8q .. +7
+};
+// byte o of tile a's block in the wave's LDS area (reads of 8 or 16 aligned bytes never
+// straddle the split at 2048)
+template <int R>
+__device__ __forceinline__ const uint8_t *sk_q4_at(const uint8_t *area, int a, int o) {
+    return o < 2048 ? area + 2048 * a + o : area + 2048 * R + 256 * a + (o - 2048);
 }
-
-// A operand(s) of sub-block j: Q4_K sc*q; Q6_K the planes (sc - b)(q - 32), b(q - 32)
-template <int TYPE>
-__device__ __forceinline__ void sk_operand(const SkRaw &r, int j, int q, bool dzero, h8 &a1, h8 &a2) {
-    uint32_t o1[4], o2[4];
-    if (TYPE == kTypeQ4K) {
-        uint32_t sc, m;
-        q4k_scale_min(r.h.y, r.h.z, r.h.w, j, sc, m);
-        if (dzero) sc = 0;
-        const _Float16 s = (_Float16)(float)sc, ns = (_Float16)(-1024.0f * (float)sc);
-        const h2 S = {s, s}, N = {ns, ns};
-        const uint2 c = r.a[j >> 1];
-        const int sh = 4 * (j & 1);
-        const uint32_t w0 = (c.x >> sh) & 0x0F0F0F0Fu, w1 = (c.y >> sh) & 0x0F0F0F0Fu;
-        o1[0] = q4_scaled(w0, kSelLo, S, N);
-        o1[1] = q4_scaled(w0, kSelHi, S, N);
-        o1[2] = q4_scaled(w1, kSelLo, S, N);
-        o1[3] = q4_scaled(w1, kSelHi, S, N);
-        a1 = __builtin_bit_cast(h8, make_uint4(o1[0], o1[1], o1[2], o1[3]));
-    } else {
-        const int H = j >> 2, grp = j & 3;
-        int sc = (int)(int8_t)(((H ? r.h.y : r.h.x) >> (8 * grp)) & 0xFF);  // scale 8H + 2grp + q/2
-        if (dzero) sc = 0;
-        const int b1 = sc & 1;
-        const _Float16 e = (_Float16)(float)(sc - b1), bb = (_Float16)(float)b1;
-        const h2 E = {e, e}, B = {bb, bb};
-        const uint2 l = r.a[2 * H + (grp & 1)], hq = r.b[H];
-        const int shl = 4 * (grp >> 1), shh = 2 * grp;
-        const uint32_t v0 = ((l.x >> shl) & 0x0F0F0F0Fu) | (((hq.x >> shh) & 0x03030303u) << 4);
-        const uint32_t v1 = ((l.y >> shl) & 0x0F0F0F0Fu) | (((hq.y >> shh) & 0x03030303u) << 4);
-        const h2 c0 = q6_centered(v0, kSelLo), c1 = q6_centered(v0, kSelHi), c2 = q6_centered(v1, kSelLo),
-                 c3 = q6_centered(v1, kSelHi);
-        o1[0] = h2u(c0 * E); o1[1] = h2u(c1 * E); o1[2] = h2u(c2 * E); o1[3] = h2u(c3 * E);
-        o2[0] = h2u(c0 * B); o2[1] = h2u(c1 * B); o2[2] = h2u(c2 * B); o2[3] = h2u(c3 * B);
-        a1 = __builtin_bit_cast(h8, make_uint4(o1[0], o1[1], o1[2], o1[3]));
-        a2 = __builtin_bit_cast(h8, make_uint4(o2[0], o2[1], o2[2], o2[3]));
-    }
+template <int R>
+__device__ __forceinline__ SkQ4 sk_read_q4(const uint8_t *area, int a, int c, int q) {
+    SkQ4 r;
+    const int row = c * kQ4KBytes;
+    r.h = *(const uint4 *)sk_q4_at<R>(area, a, row);
+#pragma unroll
+    for (int g = 0; g < 4; g++) r.a[g] = *(const uint2 *)sk_q4_at<R>(area, a, row + 16 + 32 * g + 8 * q);
+    return r;
+}
+// the 8 six-bit scales of a Q4_K block as bytes (get_scale_min_k4, kernels.cu:45-53): sub-blocks
+// 0-3 are the low 6 bits of bytes 0-3, 4-7 the low nibbles of bytes 8-11 with bits 6-7 of
+// bytes 0-3 above them (the packed form of gemm_q4k.cu:53-56)
+__device__ __forceinline__ void q4k_scales8(const uint4 &h, uint32_t &lo, uint32_t &hi) {
+    lo = h.y & 0x3F3F3F3Fu;
+    hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+}
+// sub-block j's A operand, sc*q for its 8 values: the pair (1024 + sc) from the scale byte
+// under 0x64, so that (sc, -1024 sc) cost three packed operations
+__device__ __forceinline__ h8 sk_operand4(const SkQ4 &r, uint32_t slo, uint32_t shi, int j) {
+    const uint32_t sel = 0x04000400u + 0x00010001u * (uint32_t)(j & 3);
+    const h2 S = magic_pair(j < 4 ? slo : shi, sel) + h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2 N = S * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const uint2 c = r.a[j >> 1];
+    const int sh = 4 * (j & 1);
+    const uint32_t w0 = (c.x >> sh) & 0x0F0F0F0Fu, w1 = (c.y >> sh) & 0x0F0F0F0Fu;
+    return __builtin_bit_cast(h8, make_uint4(q4_scaled(w0, kSelLo, S, N), q4_scaled(w0, kSelHi, S, N),
+                                             q4_scaled(w1, kSelLo, S, N), q4_scaled(w1, kSelHi, S, N)));
+}
+// Q6_K: the planes (sc - b)(q - 32) and b(q - 32) of sub-block j
+__device__ __forceinline__ void sk_operand6(const SkRaw6 &r, int j, bool dzero, h8 &a1, h8 &a2) {
+    const int H = j >> 2, grp = j & 3;
+    int sc = (int)(int8_t)((r.sc[H] >> (8 * grp)) & 0xFF);
+    if (dzero) sc = 0;
+    const int b1 = sc & 1;
+    const _Float16 e = (_Float16)(float)(sc - b1), bb = (_Float16)(float)b1;
+    const h2 E = {e, e}, B = {bb, bb};
+    const uint2 l = r.ql[2 * H + (grp & 1)], hq = r.qh[H];
+    const int shl = 4 * (grp >> 1), shh = 2 * grp;
+    const uint32_t v0 = ((l.x >> shl) & 0x0F0F0F0Fu) | (((hq.x >> shh) & 0x03030303u) << 4);
+    const uint32_t v1 = ((l.y >> shl) & 0x0F0F0F0Fu) | (((hq.y >> shh) & 0x03030303u) << 4);
+    const h2 c0 = q6_centered(v0, kSelLo), c1 = q6_centered(v0, kSelHi), c2 = q6_centered(v1, kSelLo),
+             c3 = q6_centered(v1, kSelHi);
+    a1 = __builtin_bit_cast(h8, make_uint4(h2u(c0 * E), h2u(c1 * E), h2u(c2 * E), h2u(c3 * E)));
+    a2 = __builtin_bit_cast(h8, make_uint4(h2u(c0 * B), h2u(c1 * B), h2u(c2 * B), h2u(c3 * B)));
 }
 
 // staged activation chunk u (16 B = 8 values) of token row r, XOR-swizzled by the row so
 // that the 16 rows of a fragment read hit distinct banks
 __device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r & 31)) << 3); }
 
+template <int TYPE, int R>
 struct SkLds {
+    static constexpr int kW = TYPE == kTypeQ4K ? sk_q4_area<R>() : 16;
     _Float16 b[2][kSkTok * 256];  // staged q8 of one 256-value block, double-buffered
     float rho[2][kSkTok * 8];     // the rows' scale ratios of that block's 8 sub-blocks
+    uint8_t w[2][kSkWaves][kW];   // Q4_K: each wave's row tiles of one block, double-buffered
 };
 
-// One 256-value block: multiply block k (raw weights in `cur`, activations in LDS buffer
-// k%2) while the weights of block k+1 load into `nxt` and its activations into the other
-// LDS buffer (straight from memory, global_load_lds: lane l of a wave fills 16 bytes at
-// base + 16l).  The wait for those LDS writes before the barrier also covers the weight
-// loads issued after them (memory loads complete in issue order), so one block ahead is
-// what the pipeline can hold.
+// the running row scales at a block start: lane c owns A row c of each tile (its running d
+// and the ratio for this block); the lane's outputs are rows 4q + e, whose ratios come from
+// lanes 4q + e
+template <int NB, int R>
+__device__ __forceinline__ void sk_row_scales(const float (&d)[R], int q, float (&deff)[R], f4 (&acc)[R][NB]) {
+#pragma unroll
+    for (int a = 0; a < R; a++) {
+        const float nd = d[a] == 0.0f ? deff[a] : d[a];
+        const float sg = deff[a] * __builtin_amdgcn_rcpf(nd);
+        deff[a] = nd;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float se = __shfl(sg, 4 * q + e);
+#pragma unroll
+            for (int b = 0; b < NB; b++) acc[a][b][e] *= se;
+        }
+    }
+}
+
+// copies of block kb of the wave's Q4_K row tiles into its LDS area: copy 2a + i moves
+// chunk 64i + lane of tile a, copy 2R the tail chunks (sources from sk_tile's tile_src)
+template <int R>
+__device__ __forceinline__ void sk_copy_q4(const uint8_t *const (&src)[sk_q4_copies<R>()], int kb, uint8_t *dst) {
+#pragma unroll
+    for (int i = 0; i < sk_q4_copies<R>(); i++)
+        __builtin_amdgcn_global_load_lds((const void *)(src[i] + (size_t)kb * kQ4KBytes),
+                                         (__attribute__((address_space(3))) void *)(dst + 1024 * i), 16, 0, 0);
+}
+
+// One 256-value block k: the activations (and ratios) of block k+1 are copied into the other
+// LDS buffer, the weights of block k+1 into the wave's other LDS area (Q4_K) or registers
+// (Q6_K), then block k is multiplied.  The barrier at the end waits for the activation
+// copies only (they were issued first; memory operations complete in issue order): the
+// weights stay in flight until the next block needs them.
 template <int TYPE, int NB, int R>
-__device__ __forceinline__ void sk_block(int k, int nkb, int bbytes, int q, int c, int wave, int tid,
+__device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave, int lane, int tid,
                                          const uint8_t *const (&wrow)[R],
+                                         const uint8_t *const (&tile_src)[sk_q4_copies<R>()],
                                          const _Float16 *const (&arow)[NB * 16 / kSkStage], const float *rrow,
-                                         SkLds &L, const SkRaw (&cur)[R], SkRaw (&nxt)[R], float (&deff)[R][4],
-                                         f4 (&acc)[R][NB]) {
-    // past the end the last block is loaded again (into the idle buffer and registers)
+                                         SkLds<TYPE, R> &L, const SkRaw6 (&cur)[R], SkRaw6 (&nxt)[R],
+                                         float (&deff)[R], f4 (&acc)[R][NB]) {
+    // past the end the last block is copied again (into the idle buffers)
     const int kn = min(k + 1, nkb - 1);
+    // block k's weights have landed in the wave's LDS area (the memory clobber keeps the
+    // compiler from moving the LDS reads above the wait)
+    if constexpr (TYPE == kTypeQ4K) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int i = 0; i < NB * 16 / kSkStage; i++)
         __builtin_amdgcn_global_load_lds((const void *)(arow[i] + kn * 256),
                                          (__attribute__((address_space(3))) void *)&L.b[(k + 1) & 1][(2 * wave + kSkStage * i) * 256],
                                          16, 0, 0);
-    if (tid < NB * 16 * 2)  // the ratios: two 16-byte chunks per row
+    if (wave < (NB * 32 + 63) / 64)  // the ratios: two 16-byte chunks per row, whole waves
         __builtin_amdgcn_global_load_lds((const void *)(rrow + kn * 8),
                                          (__attribute__((address_space(3))) void *)&L.rho[(k + 1) & 1][(tid & ~63) * 4], 16,
                                          0, 0);
-    __builtin_amdgcn_sched_barrier(0);  // the LDS loads go first (the barrier below counts on it)
+    __builtin_amdgcn_sched_barrier(0);  // the shared copies go first (the barrier below counts on it)
+    if constexpr (TYPE == kTypeQ4K) {
+        sk_copy_q4<R>(tile_src, kn, L.w[(k + 1) & 1][wave]);
+    } else {
 #pragma unroll
-    for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a] + (size_t)kn * bbytes, q, nxt[a]);
+        for (int a = 0; a < R; a++) sk_load6(wrow[a] + (size_t)kn * kQ6KBytes, q, nxt[a]);
+    }
     // keep the loads here, ahead of the multiplication (the scheduler would otherwise sink
     // them past it to save registers, and nothing would be in flight during the MFMAs)
     __builtin_amdgcn_sched_barrier(0);
-    // row scales: lane c owns A row c of each tile; the lane's outputs are rows 4q + e
-    bool dz[R];
+
+    SkQ4 w4[R];
+    uint32_t slo[R], shi[R];
+    float d[R];
 #pragma unroll
     for (int a = 0; a < R; a++) {
-        const float d = sk_d<TYPE>(cur[a]);
-        dz[a] = d == 0.0f;
-        const float dn = dz[a] ? 0.0f : d;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float dr = __shfl(dn, 4 * q + e);
-            const float nd = dr != 0.0f ? dr : deff[a][e];
-            const float sg = deff[a][e] / nd;
-            deff[a][e] = nd;
-#pragma unroll
-            for (int b = 0; b < NB; b++) acc[a][b][e] *= sg;
+        if constexpr (TYPE == kTypeQ4K) {
+            w4[a] = sk_read_q4<R>(L.w[k & 1][wave], a, c, q);
+            d[a] = h2f(w4[a].h.x & 0xFFFFu);
+            q4k_scales8(w4[a].h, slo[a], shi[a]);
+            if (d[a] == 0.0f) slo[a] = shi[a] = 0u;  // the block's products are zero
+        } else {
+            d[a] = h2f(cur[a].d);
         }
     }
+    sk_row_scales<NB, R>(d, q, deff, acc);
     const _Float16 *bb = L.b[k & 1];
     const float *rb = L.rho[k & 1];
+    // the 8 ratios of each token column: two 16-byte reads
+    f4 rr[NB][2];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        rr[b][0] = *(const f4 *)(rb + (16 * b + c) * 8);
+        rr[b][1] = *(const f4 *)(rb + (16 * b + c) * 8 + 4);
+    }
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         h8 bf[NB];
-        float rho[NB];
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            bf[b] = *(const h8 *)(bb + sk_slot(16 * b + c, 4 * j + q));
-            rho[b] = rb[(16 * b + c) * 8 + j];
-        }
+        for (int b = 0; b < NB; b++) bf[b] = *(const h8 *)(bb + sk_slot(16 * b + c, 4 * j + q));
 #pragma unroll
         for (int a = 0; a < R; a++) {
             h8 a1, a2;
-            sk_operand<TYPE>(cur[a], j, q, dz[a], a1, a2);
+            if constexpr (TYPE == kTypeQ4K) a1 = sk_operand4(w4[a], slo[a], shi[a], j);
+            else sk_operand6(cur[a], j, d[a] == 0.0f, a1, a2);
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                acc[a][b] *= rho[b];
+                acc[a][b] *= rr[b][j >> 2][j & 3];
                 acc[a][b] = mfma(a1, bf[b], acc[a][b]);
                 if constexpr (TYPE == kTypeQ6K) acc[a][b] = mfma(a2, bf[b], acc[a][b]);
             }
         }
     }
-    // block k+1's activations are in LDS once at most the weight loads issued after them are
-    // outstanding; those stay in flight across the barrier
-    lds_dma_barrier<R * sk_loads_per_tile<TYPE>()>();
+    lds_dma_barrier<TYPE == kTypeQ4K ? sk_q4_copies<R>() : R * kSk6Loads>();
 }
 
 template <int TYPE, int MODE, int NB>
-__device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds &L, int wave, int lane, int tid, int e, int j0,
-                                        int n_rows, int row_base) {
+__device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_per_wave<TYPE, MODE>() / 16> &L,
+                                        int wave, int lane, int tid, int e, int j0, int n_rows, int row_base) {
     constexpr int R = sk_rows_per_wave<TYPE, MODE>() / 16;
     constexpr int H = R / 2;  // SwiGLU: gate tiles 0 .. H-1, up tiles H .. 2H-1
     const int q = lane >> 4, c = lane & 15;
@@ -937,21 +997,25 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds &L, int wave, i
     const uint8_t *Wm = g.W + (size_t)e * g.expert_stride + g.w_off;
     const uint8_t *Wm2 = g.W + (size_t)e * g.expert_stride + g.w_off2;
 
-    // this lane's weight row of each row tile (rows past M re-read the last)
-    const uint8_t *wrow[R];
+    // weight row r of tile a (rows past M re-read the last)
     int base;  // SwiGLU: first feature of the wave; grouped: first row
-    if (MODE == 1) {
-        base = (blockIdx.x * kSkWaves + wave) * (16 * H);
+    if (MODE == 1) base = (blockIdx.x * kSkWaves + wave) * (16 * H);
+    else base = (blockIdx.x * kSkWaves + wave) * (16 * R);
+    auto row_ptr = [&](int a, int r) {
+        if (MODE == 1) return (a < H ? Wm : Wm2) + (size_t)min(base + 16 * (a % H) + r, g.M - 1) * wrow_bytes;
+        return Wm + (size_t)min(base + 16 * a + r, g.M - 1) * wrow_bytes;
+    };
+    const uint8_t *wrow[R];  // the lane's own A row c of each tile
+    // Q4_K copy sources: chunk ch of a tile is row ch/9, bytes 16(ch%9) .. of the block
+    const uint8_t *tile_src[sk_q4_copies<R>()];
+    auto chunk_ptr = [&](int a, int ch) { return row_ptr(a, ch / 9) + 16 * (ch % 9); };
 #pragma unroll
-        for (int a = 0; a < R; a++) {
-            const int f = min(base + 16 * (a % H) + c, g.M - 1);
-            wrow[a] = (a < H ? Wm : Wm2) + (size_t)f * wrow_bytes;
-        }
-    } else {
-        base = (blockIdx.x * kSkWaves + wave) * (16 * R);
+    for (int a = 0; a < R; a++) {
+        wrow[a] = row_ptr(a, c);
 #pragma unroll
-        for (int a = 0; a < R; a++) wrow[a] = Wm + (size_t)min(base + 16 * a + c, g.M - 1) * wrow_bytes;
+        for (int i = 0; i < 2; i++) tile_src[2 * a + i] = chunk_ptr(a, 64 * i + lane);
     }
+    tile_src[2 * R] = lane < 16 * R ? chunk_ptr(lane >> 4, 128 + (lane & 15)) : chunk_ptr(R - 1, 143);
     // activation staging role: physical slot tid % 32 of rows r = tid/32 + kSkStage i, which
     // holds the logical slot (tid % 32) ^ (r % 32); ratio staging: threads below 2 NB 16 copy
     // 16-byte chunk tid % 2 of row tid / 2
@@ -968,71 +1032,87 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds &L, int wave, i
     }
     const float *rrow = g.a_rho + (size_t)stage_row(min(tid >> 1, NB * 16 - 1)) * (K / 32) + 4 * (tid & 1);
     f4 acc[R][NB];
-    float deff[R][4];
+    float deff[R];  // running d of the lane's A row c of each tile
 #pragma unroll
     for (int a = 0; a < R; a++) {
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int x = 0; x < 4; x++) deff[a][x] = 1.0f;
+        deff[a] = 1.0f;
     }
-    SkRaw r0[R], r1[R];
+    int tok[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) tok[b] = stage_row(16 * b + c);
+    // Q4_K's min term, sum_s -(dmin*m_s)_i * ds_js, first: the accumulator starts as this
+    // absolute value (the running scales start at 1 and their ratios telescope to
+    // 1 / (last d * last d8), which the epilogue multiplies back).  Windows of 32 sub-blocks,
+    // lane group q holding super-block 4w + q of its A row / token; the loads of up to four
+    // windows are issued together.
+    if constexpr (TYPE == kTypeQ4K) {
+        const int nwin = (nkb + 3) / 4;
+        for (int w0 = 0; w0 < nwin; w0 += 4) {
+            uint4 hdr[4][R], dsv[4][NB];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int sb = 4 * (w0 + u) + q;
+                const bool valid = sb < nkb;
+#pragma unroll
+                for (int a = 0; a < R; a++)
+                    hdr[u][a] = valid ? ld16(wrow[a] + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+                    dsv[u][b] = valid ? ld16((const uint8_t *)(g.a_ds + (size_t)tok[b] * (K / 32) + 8 * sb))
+                                      : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int a = 0; a < R; a++) {
+                    h8 hi, lo;
+                    q4k_min_operand(hdr[u][a], hi, lo);
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        const h8 bd = __builtin_bit_cast(h8, dsv[u][b]);
+                        acc[a][b] = mfma(lo, bd, mfma(hi, bd, acc[a][b]));
+                    }
+                }
+        }
+    }
+    SkRaw6 r0[R], r1[R];
 #pragma unroll
     for (int i = 0; i < NB * 16 / kSkStage; i++)
         __builtin_amdgcn_global_load_lds((const void *)arow[i],
                                          (__attribute__((address_space(3))) void *)&L.b[0][(2 * wave + kSkStage * i) * 256],
                                          16, 0, 0);
-    if (tid < NB * 16 * 2)
+    if (wave < (NB * 32 + 63) / 64)  // whole waves (rows past NB 16 repeat the last)
         __builtin_amdgcn_global_load_lds((const void *)rrow,
                                          (__attribute__((address_space(3))) void *)&L.rho[0][(tid & ~63) * 4], 16, 0,
                                          0);
+    if constexpr (TYPE == kTypeQ4K) {
+        sk_copy_q4<R>(tile_src, 0, L.w[0][wave]);
+    } else {
 #pragma unroll
-    for (int a = 0; a < R; a++) sk_load<TYPE>(wrow[a], q, r0[a]);
+        for (int a = 0; a < R; a++) sk_load6(wrow[a], q, r0[a]);
+    }
     __syncthreads();
-    // two raw slots, the loop unrolled by two so that both are static
+    // two raw slots (Q6_K), the loop unrolled by two so that both are static
     for (int k = 0; k < nkb; k += 2) {
-        sk_block<TYPE, NB, R>(k, nkb, bbytes, q, c, wave, tid, wrow, arow, rrow, L, r0, r1, deff, acc);
+        sk_block<TYPE, NB, R>(k, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r0, r1, deff, acc);
         if (k + 1 >= nkb) break;
-        sk_block<TYPE, NB, R>(k + 1, nkb, bbytes, q, c, wave, tid, wrow, arow, rrow, L, r1, r0, deff, acc);
+        sk_block<TYPE, NB, R>(k + 1, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r1, r0, deff, acc);
     }
 
-    // absolute values, then Q4_K's min term over windows of 32 sub-blocks (lane group q:
-    // super-block 4w + q of its A row / token)
+    // absolute values: the last nonzero d of the rows (from lanes 4q + x) and d8 of the tokens
     float dt[NB];
-    int tok[NB];
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        const int j = min(j0 + 16 * b + c, n_rows - 1);
-        tok[b] = MODE == 1 ? g.perm[row_base + j] : row_base + j;
-        dt[b] = g.a_dlast[tok[b]];
-    }
+    for (int b = 0; b < NB; b++) dt[b] = g.a_dlast[tok[b]];
 #pragma unroll
     for (int a = 0; a < R; a++)
 #pragma unroll
-        for (int b = 0; b < NB; b++)
+        for (int x = 0; x < 4; x++) {
+            const float dr = __shfl(deff[a], 4 * q + x);
 #pragma unroll
-            for (int x = 0; x < 4; x++) acc[a][b][x] *= deff[a][x] * dt[b];
-    if constexpr (TYPE == kTypeQ4K) {
-        for (int w = 0; w < (nkb + 3) / 4; w++) {
-            const int sb = 4 * w + q;
-            const bool valid = sb < nkb;
-            h8 bd[NB];
-#pragma unroll
-            for (int b = 0; b < NB; b++) {
-                const uint4 v = valid ? ld16((const uint8_t *)(g.a_ds + (size_t)tok[b] * (K / 32) + 8 * sb))
-                                      : make_uint4(0, 0, 0, 0);
-                bd[b] = __builtin_bit_cast(h8, v);
-            }
-#pragma unroll
-            for (int a = 0; a < R; a++) {
-                const uint4 hdr = valid ? ld16(wrow[a] + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
-                h8 hi, lo;
-                q4k_min_operand(hdr, hi, lo);
-#pragma unroll
-                for (int b = 0; b < NB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
-            }
+            for (int b = 0; b < NB; b++) acc[a][b][x] *= dr * dt[b];
         }
-    }
 
     // D layout: lane holds weight rows 4q + x of each 16-row tile, token column c
 #pragma unroll
@@ -1066,7 +1146,7 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds &L, int wave, i
 // perm[], out[q*ld + f] = silu(gate) * up); MODE 2: the expert-sorted rows themselves.
 template <int TYPE, int MODE>
 __global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmArgs g) {
-    __shared__ __align__(16) SkLds L;
+    __shared__ __align__(16) SkLds<TYPE, sk_rows_per_wave<TYPE, MODE>() / 16> L;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if ((int)blockIdx.y >= g.tiles[-1]) return;
     const int tl = g.tiles[blockIdx.y];
