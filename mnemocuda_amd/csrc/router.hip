@@ -213,15 +213,19 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     const float v = block_sum(nw ? row_dot_norm(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
                                  : row_dot(w + (size_t)row * n_cols, x, n_cols, vec4),
                               part);
+    // arrival protocol: the logit store happens-before the release half of the agent-scope
+    // fetch-add; the workgroup that sees n - 1 arrivals acquires them all (the acquire half of
+    // its fetch-add, then an agent-scope acquire fence in every thread after the barrier that
+    // hands them is_last), so its loads below see every workgroup's logit across the XCDs' L2s
     if (tid == 0) {
         __hip_atomic_store(logits + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         is_last = old == n - 1;
         if (is_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!is_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     for (int i = tid; i < n; i += kRowThreads) {
         const float l = __hip_atomic_load(logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         z[i] = l > -1e30f ? l : -1e30f;  // NaN and <= -1e30 never win

@@ -193,3 +193,90 @@ def test_repeat_calls_are_deterministic(gpu):
         gpu.ops.matvec_q4k(wd, x, y, 2048, 4096)
         ys.append(host(y))
     assert all(np.array_equal(ys[0], t) for t in ys[1:])
+
+
+# ---------------------------------------------------------------- adversarial x
+# x is carried as two int8 digits per 32-value block scaled by the block's max |x|
+# (step max|x| / 32258), so a block that mixes one huge value with small ones quantises the
+# small ones coarsely.  These inputs stress that encoding; the bar stays relative L2 1e-3
+# against the fp64 oracle of the reference's fp32-x product (kernels.cu:124-135).
+def _adversarial_x(kind: str, n: int, rng) -> np.ndarray:
+    x = rng.standard_normal(n)
+    if kind == "outlier_per_block":  # one 1e3-times value in every 32-value block
+        pos = np.arange(0, n, 32) + rng.integers(0, 32, size=(n + 31) // 32)
+        pos = pos[pos < n]
+        x[pos] *= 1e3
+    elif kind == "student_t2":
+        x = rng.standard_t(2.0, size=n)
+    elif kind == "massive_channels":  # a few channels at 1e4 over N(0, 1)
+        x[rng.choice(n, size=4, replace=False)] = 1e4 * rng.choice([-1.0, 1.0], size=4)
+    elif kind == "zero_blocks":  # every other 32-block (and a whole 256 block) all zero
+        x = x.reshape(-1, 32)
+        x[::2] = 0.0
+        x = x.reshape(-1)
+        x[256:512] = 0.0
+    else:
+        raise ValueError(kind)
+    return x.astype(np.float32)
+
+
+ADV = ["outlier_per_block", "student_t2", "massive_channels", "zero_blocks"]
+
+
+@pytest.mark.parametrize("kind", ADV)
+@pytest.mark.parametrize("type_id,rows,cols", [(12, 4096, 4096), (14, 4096, 4096), (12, 1536, 4096), (14, 512, 1536)])
+def test_matvec_adversarial_x(gpu, oracle, kind, type_id, rows, cols):
+    rng = np.random.default_rng(abs(hash(kind)) % 1000 + rows + type_id)
+    w, wd = _mk(rng, type_id, rows, cols)
+    x = _adversarial_x(kind, cols, rng)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    case(f"matvec adversarial {kind} type={type_id} {rows}x{cols}")
+    (gpu.ops.matvec_q4k if type_id == 12 else gpu.ops.matvec_q6k)(wd, dev(x), y, rows, cols)
+    err = rel_l2(host(y), oracle.gemv(type_id, w, x, rows, cols))
+    print(f"{kind} rel_l2={err:.2e}")
+    assert err < TOL
+
+
+@pytest.mark.parametrize("kind", ADV)
+def test_qkv_adversarial_x(gpu, oracle, kind):
+    rng = np.random.default_rng(11 + ADV.index(kind))
+    types, rows, cols = (12, 12, 14), (8192, 512, 512), 4096
+    ws = [_mk(rng, t, r, cols) for t, r in zip(types, rows)]
+    x = _adversarial_x(kind, cols, rng)
+    outs = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    case(f"qkv adversarial {kind}")
+    gpu.ops.matvec_qkv(ws[0][1], types[0], ws[1][1], types[1], ws[2][1], types[2], dev(x), *outs, 8192, 512, cols)
+    for (w, _), t, o, r in zip(ws, types, outs, rows):
+        err = rel_l2(host(o), oracle.gemv(t, w, x, r, cols))
+        print(f"{kind} type={t} rel_l2={err:.2e}")
+        assert err < TOL
+
+
+@pytest.mark.parametrize("kind", ADV)
+def test_dual_adversarial_x(gpu, oracle, kind):
+    rng = np.random.default_rng(23 + ADV.index(kind))
+    wa, wad = _mk(rng, 12, 1536, 4096)
+    wb, wbd = _mk(rng, 14, 1536, 4096)
+    x = _adversarial_x(kind, 4096, rng)
+    ya, yb = torch.zeros(1536, device="cuda"), torch.zeros(1536, device="cuda")
+    case(f"dual adversarial {kind}")
+    gpu.ops.matvec_dual(wad, 12, wbd, 14, dev(x), ya, yb, 1536, 4096)
+    assert rel_l2(host(ya), oracle.gemv(12, wa, x, 1536, 4096)) < TOL
+    assert rel_l2(host(yb), oracle.gemv(14, wb, x, 1536, 4096)) < TOL
+
+
+@pytest.mark.parametrize("kind", ADV)
+def test_qkv_rmsnorm_adversarial_x(gpu, oracle, kind):
+    rng = np.random.default_rng(37 + ADV.index(kind))
+    types, rows, cols = (12, 12, 14), (8192, 512, 512), 4096
+    ws = [_mk(rng, t, r, cols) for t, r in zip(types, rows)]
+    x = _adversarial_x(kind, cols, rng)
+    nw = (1.0 + 0.3 * rng.standard_normal(cols)).astype(np.float32)
+    eps = 1e-6
+    xn = oracle.rms_norm(x, nw, eps)
+    outs = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    case(f"qkv rmsnorm adversarial {kind}")
+    gpu.ops.matvec_qkv_rmsnorm(ws[0][1], types[0], ws[1][1], types[1], ws[2][1], types[2], dev(x), dev(nw), eps,
+                               *outs, 8192, 512, cols)
+    for (w, _), t, o, r in zip(ws, types, outs, rows):
+        assert rel_l2(host(o), oracle.gemv(t, w, xn, r, cols)) < TOL
