@@ -772,7 +772,6 @@ constexpr int sk_rows_per_wave() { return MODE == 1 || TYPE == kTypeQ4K ? 32 : 1
 // tile a go to bytes 2048a .. of the wave's area with two copies, chunks 128-143 of all
 // tiles to the tail at 2048R + 256a with one copy, whose lanes past 16R repeat a chunk into
 // the unused rest of the tail.
-constexpr int kSkQ4Tile = 16 * kQ4KBytes;
 template <int R>
 constexpr int sk_q4_area() { return 2048 * R + 1024; }
 template <int R>

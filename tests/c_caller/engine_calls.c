@@ -8,10 +8,12 @@
  * writes every input and output to one binary file that tests/test_gpu_c_caller.py checks
  * against the oracle.  Exit status: 0 on success, 1 on a library or HIP error.
  *
- * File layout (little endian): int32 R, RK, C, E, K, then the bytes of Wq4 (R x C Q4_K),
+ * File layout (little endian): int32 R, RK, C, E, K, NT, then the bytes of Wq4 (R x C Q4_K),
  * Wq6 (R x C Q6_K), Wk (RK x C Q4_K), Wv (RK x C Q6_K), fp32 x[C], res[R], router[E][C],
- * then the outputs y4[R], y6[R], yadd[R], ya[R], yb[R], q[R], k[RK], v[RK], logits[E],
- * int32 idx[K], fp32 w[K].
+ * x2[C], act[NT][C], then the outputs y4[R], y6[R], yadd[R], ya[R], yb[R], q[R], k[RK],
+ * v[RK], logits[E], int32 idx[K], fp32 w[K], then q2[R], k2[RK], v2[RK] (all-Q4_K QKV),
+ * ysa[R] (res + 0.37 Wq4 x), sw[C] (silu(x) * x2), ysc[R] (res + 0.5 y4), the Q8_1 bytes of
+ * act [NT][C/128][144] and the GEMM output gout[NT][R] of Wq4 with them.
  */
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
@@ -26,6 +28,7 @@
 #define C 4096
 #define E 64
 #define K 8
+#define NT 32
 #define Q4_BYTES ((size_t)(C / 256) * 144)
 #define Q6_BYTES ((size_t)(C / 256) * 210)
 
@@ -73,6 +76,7 @@ int main(int argc, char **argv) {
     uint8_t *wq4 = malloc(R * Q4_BYTES), *wq6 = malloc(R * Q6_BYTES);
     uint8_t *wk = malloc(RK * Q4_BYTES), *wv = malloc(RK * Q6_BYTES);
     float *x = malloc(C * 4), *res = malloc(R * 4), *router = malloc((size_t)E * C * 4);
+    float *x2 = malloc(C * 4), *act = malloc((size_t)NT * C * 4);
     fill_q4k(wq4, R);
     fill_q6k(wq6, R);
     fill_q4k(wk, RK);
@@ -80,22 +84,33 @@ int main(int argc, char **argv) {
     for (int i = 0; i < C; i++) x[i] = 2.0f * uniform() - 1.0f;
     for (int i = 0; i < R; i++) res[i] = 2.0f * uniform() - 1.0f;
     for (int i = 0; i < E * C; i++) router[i] = (2.0f * uniform() - 1.0f) * 0.03f;
+    for (int i = 0; i < C; i++) x2[i] = 2.0f * uniform() - 1.0f;
+    for (int i = 0; i < NT * C; i++) act[i] = 4.0f * uniform() - 2.0f;
 
     void *d_wq4 = dev_copy(wq4, R * Q4_BYTES), *d_wq6 = dev_copy(wq6, R * Q6_BYTES);
     void *d_wk = dev_copy(wk, RK * Q4_BYTES), *d_wv = dev_copy(wv, RK * Q6_BYTES);
     float *d_x = dev_copy(x, C * 4), *d_res = dev_copy(res, R * 4), *d_router = dev_copy(router, (size_t)E * C * 4);
-    float *d_out = NULL;
+    float *d_x2 = dev_copy(x2, C * 4), *d_act = dev_copy(act, (size_t)NT * C * 4);
+    float *d_out = NULL, *d_out2 = NULL;
     int *d_idx = NULL;
+    void *d_q8 = NULL;
     const size_t n_out = 5 * R + R + 2 * RK + E + K;
-    if (!d_wq4 || !d_wq6 || !d_wk || !d_wv || !d_x || !d_res || !d_router ||
-        hipMalloc((void **)&d_out, n_out * 4) != hipSuccess || hipMalloc((void **)&d_idx, K * 4) != hipSuccess) {
+    const size_t n_out2 = R + 2 * RK + R + C + R + (size_t)NT * R;
+    const size_t q8_bytes = (size_t)NT * (C / 128) * 144;
+    if (!d_wq4 || !d_wq6 || !d_wk || !d_wv || !d_x || !d_res || !d_router || !d_x2 || !d_act ||
+        hipMalloc((void **)&d_out, n_out * 4) != hipSuccess || hipMalloc((void **)&d_idx, K * 4) != hipSuccess ||
+        hipMalloc((void **)&d_out2, n_out2 * 4) != hipSuccess || hipMalloc(&d_q8, q8_bytes) != hipSuccess) {
         fprintf(stderr, "hip allocation or copy failed\n");
         return 1;
     }
     float *y4 = d_out, *y6 = y4 + R, *yadd = y6 + R, *ya = yadd + R, *yb = ya + R, *q = yb + R;
     float *k = q + R, *v = k + RK, *logits = v + RK, *w = logits + E;
+    float *q2 = d_out2, *k2 = q2 + R, *v2 = k2 + RK, *ysa = v2 + RK, *sw = ysa + R, *ysc = sw + C, *gout = ysc + R;
     hipStream_t s;
     if (hipStreamCreate(&s) != hipSuccess) return 1;
+    if (hipMemcpy(ysa, d_res, R * 4, hipMemcpyDeviceToDevice) != hipSuccess ||
+        hipMemcpy(ysc, d_res, R * 4, hipMemcpyDeviceToDevice) != hipSuccess)
+        return 1;
 
     /* the engine's calls (reference argument lists) */
     cuda_matvec_q4k(d_wq4, d_x, y4, R, C, s);
@@ -105,21 +120,30 @@ int main(int argc, char **argv) {
     mnemo_matvec_qkv(d_wq4, 12, d_wk, 12, d_wv, 14, d_x, q, k, v, R, RK, C, s);
     cuda_matvec_f32(d_router, d_x, logits, E, C, s);
     cuda_topk_softmax(logits, d_idx, w, E, K, s);
+    cuda_matvec_q4k_qkv(d_wq4, d_wk, d_wk, d_x, q2, k2, v2, R, RK, C, s);  /* forward.c:701 */
+    cuda_matvec_q4k_scaled_add(d_wq4, d_x, ysa, R, C, 0.37f, s);          /* forward.c:1134 */
+    cuda_swiglu(d_x, d_x2, sw, C, s);                                      /* forward.c:1130 */
+    cuda_scaled_add(ysc, y4, 0.5f, R, s);                                  /* forward.c:1140 */
+    cuda_quantize_mmq_q8_1(d_act, d_q8, C, NT, s);                         /* forward.c:691 */
+    cuda_gemm_q4k(d_wq4, d_q8, gout, R, C, NT, s);                         /* forward.c:693-697 */
     if (hipStreamSynchronize(s) != hipSuccess) return 1;
     if (mnemo_last_error() != MNEMO_OK) {
         fprintf(stderr, "library error: %s\n", mnemo_last_error_string());
         return 1;
     }
 
-    float *out = malloc(n_out * 4);
+    float *out = malloc(n_out * 4), *out2 = malloc(n_out2 * 4);
+    uint8_t *q8 = malloc(q8_bytes);
     int idx[K];
     if (hipMemcpy(out, d_out, n_out * 4, hipMemcpyDeviceToHost) != hipSuccess ||
-        hipMemcpy(idx, d_idx, K * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        hipMemcpy(idx, d_idx, K * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(out2, d_out2, n_out2 * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(q8, d_q8, q8_bytes, hipMemcpyDeviceToHost) != hipSuccess)
         return 1;
     FILE *f = fopen(argv[1], "wb");
     if (!f) return 1;
-    const int32_t hdr[5] = {R, RK, C, E, K};
-    fwrite(hdr, 4, 5, f);
+    const int32_t hdr[6] = {R, RK, C, E, K, NT};
+    fwrite(hdr, 4, 6, f);
     fwrite(wq4, 1, R * Q4_BYTES, f);
     fwrite(wq6, 1, R * Q6_BYTES, f);
     fwrite(wk, 1, RK * Q4_BYTES, f);
@@ -127,9 +151,14 @@ int main(int argc, char **argv) {
     fwrite(x, 4, C, f);
     fwrite(res, 4, R, f);
     fwrite(router, 4, (size_t)E * C, f);
+    fwrite(x2, 4, C, f);
+    fwrite(act, 4, (size_t)NT * C, f);
     fwrite(out, 4, 5 * R + R + 2 * RK + E, f);
     fwrite(idx, 4, K, f);
     fwrite(out + 5 * R + R + 2 * RK + E, 4, K, f);
+    fwrite(out2, 4, R + 2 * RK + R + C + R, f);
+    fwrite(q8, 1, q8_bytes, f);
+    fwrite(out2 + (gout - d_out2), 4, (size_t)NT * R, f);
     fclose(f);
     printf("%s: ok\n", mnemo_version());
     return 0;

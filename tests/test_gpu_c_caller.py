@@ -24,8 +24,8 @@ def test_c_caller_matches_oracle(gpu, oracle, tmp_path):
     r = subprocess.run([str(CALLER), str(out)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     buf = out.read_bytes()
-    R, RK, C, E, K = np.frombuffer(buf[:20], np.int32)
-    off = 20
+    R, RK, C, E, K, NT = np.frombuffer(buf[:24], np.int32)
+    off = 24
 
     def take(n, dtype):
         nonlocal off
@@ -37,9 +37,14 @@ def test_c_caller_matches_oracle(gpu, oracle, tmp_path):
     wq4, wq6 = take(R * q4b, np.uint8), take(R * q6b, np.uint8)
     wk, wv = take(RK * q4b, np.uint8), take(RK * q6b, np.uint8)
     x, res, router = take(C, np.float32), take(R, np.float32), take(E * C, np.float32)
+    x2, act = take(C, np.float32), take(NT * C, np.float32).reshape(NT, C)
     y4, y6, yadd, ya, yb, q = (take(R, np.float32) for _ in range(6))
     k, v, logits = take(RK, np.float32), take(RK, np.float32), take(E, np.float32)
     idx, w = take(K, np.int32), take(K, np.float32)
+    q2, k2, v2 = take(R, np.float32), take(RK, np.float32), take(RK, np.float32)
+    ysa, sw, ysc = take(R, np.float32), take(C, np.float32), take(R, np.float32)
+    q8 = take(NT * (C // 128) * 144, np.uint8)
+    gout = take(NT * R, np.float32).reshape(NT, R)
     assert off == len(buf)
 
     g4, g6 = oracle.gemv(12, wq4, x, R, C), oracle.gemv(14, wq6, x, R, C)
@@ -53,3 +58,16 @@ def test_c_caller_matches_oracle(gpu, oracle, tmp_path):
     ridx, rw = oracle.topk_softmax(logits, int(K))
     assert sorted(idx.tolist()) == sorted(ridx.tolist())
     assert np.allclose(w[np.argsort(idx)], rw[np.argsort(ridx)], rtol=1e-5, atol=1e-6)
+
+    # cuda_matvec_q4k_qkv (all three Q4_K; V reuses the K matrix)
+    gk = oracle.gemv(12, wk, x, RK, C)
+    assert rel_l2(q2, g4) < TOL and rel_l2(k2, gk) < TOL and rel_l2(v2, gk) < TOL
+    # cuda_matvec_q4k_scaled_add: res + 0.37 W x
+    assert rel_l2(ysa - res, 0.37 * g4) < TOL
+    # cuda_swiglu and cuda_scaled_add: elementwise fp32, against the oracle's restatement
+    assert np.allclose(sw, oracle.swiglu(x, x2), rtol=2e-6, atol=1e-7)
+    assert np.array_equal(ysc, (res + np.float32(0.5) * y4).astype(np.float32))
+    # cuda_quantize_mmq_q8_1 byte-identical, cuda_gemm_q4k against the oracle GEMM
+    ref_q8 = oracle.quantize_q8_1(act)
+    assert np.array_equal(q8, ref_q8.reshape(-1))
+    assert rel_l2(gout, oracle.gemm(12, wq4, ref_q8, R, C, NT)) < 1e-5
