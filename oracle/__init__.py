@@ -254,3 +254,45 @@ def load() -> Oracle:
     if _oracle is None:
         _oracle = Oracle()
     return _oracle
+
+
+# ---------------------------------------------------------------- CPU baseline
+def _has_avx512() -> bool:
+    try:
+        flags = next(l for l in open("/proc/cpuinfo") if l.startswith("flags")).split()
+    except (OSError, StopIteration):
+        return False
+    return all(f in flags for f in ("avx512f", "avx512bw", "avx512dq", "avx512vl"))
+
+
+class Baseline:
+    """The vectorised CPU GEMV bench.py times (cpu_baseline.c), built for x86-64-v4 and
+    x86-64-v3; the AVX-512 build is used where the host CPU has it."""
+
+    def __init__(self):
+        level = "v4" if _has_avx512() else "v3"
+        path = HERE / "_build" / f"libmnemo_baseline_{level}.so"
+        if not path.exists():
+            build()
+        self.level = level
+        self.L = C.CDLL(str(path))
+        self.L.mo_base_gemv.restype = C.c_int
+        self.L.mo_base_gemv.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int]
+
+    def gemv(self, type_id: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, nthreads: int = 0) -> np.ndarray:
+        w = np.ascontiguousarray(w, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(rows, np.float32)
+        if self.L.mo_base_gemv(type_id, w.ctypes.data, x.ctypes.data, y.ctypes.data, rows, cols, nthreads):
+            raise ValueError((type_id, cols))
+        return y
+
+
+_baseline: Baseline | None = None
+
+
+def load_baseline() -> Baseline:
+    global _baseline
+    if _baseline is None:
+        _baseline = Baseline()
+    return _baseline

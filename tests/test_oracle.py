@@ -195,6 +195,20 @@ def test_gemv_f32acc_baseline_close(oracle, rng):
     assert rel_l2(y, oracle.gemv(12, w, x, 64, 4096)) < 1e-5
 
 
+@pytest.mark.parametrize("type_id", [12, 14])
+def test_vectorised_cpu_baseline_close(oracle, rng, type_id):
+    """bench.py's CPU baseline (cpu_baseline.c: vectorised, FMA-contracted) computes the same
+    product as the checker within fp32 rounding."""
+    import oracle as O
+
+    w = synth.weights(rng, type_id, 96, 4096)
+    x = rng.standard_normal(4096).astype(np.float32)
+    ref = oracle.gemv(type_id, w, x, 96, 4096)
+    b = O.load_baseline()
+    for nthreads in (1, 4):
+        assert rel_l2(b.gemv(type_id, w, x, 96, 4096, nthreads), ref) < 1e-5
+
+
 def test_matvec_f32(oracle, rng):
     w = rng.standard_normal((128, 512)).astype(np.float32)
     x = rng.standard_normal(512).astype(np.float32)
