@@ -268,7 +268,7 @@ struct LoaderState {
 __device__ __forceinline__ void row_scale_step(float d, int ks, int p, float *sig, int row, LoaderState &ls, bool live) {
     if (p == 0 && (ks & 3) == 0 && live) {  // super-block start: the row scale changes
         const float dn = d != 0.0f ? d : ls.deff;
-        sig[row] = ls.deff / dn;
+        sig[row] = ls.deff * __builtin_amdgcn_rcpf(dn);
         ls.deff = dn;
     }
 }
@@ -336,7 +336,7 @@ __device__ __forceinline__ void store_a(const RawA &r, int p, Stage<TYPE> &st, i
     const int c = kVP * p;
     if ((c & 31) == 0 && live) {  // first part of a sub-block: its token scale ratio
         const float dn = zero ? ls.d8eff : d8;
-        st.rho[c >> 5][row] = ls.d8eff / dn;
+        st.rho[c >> 5][row] = ls.d8eff * __builtin_amdgcn_rcpf(dn);
         ls.d8eff = dn;
     }
 }

@@ -2,10 +2,17 @@
 
     python -m mnemocuda_amd.profiling stats <trace_dir> <out.md> "<command>" [<top> <name filter>]
     python -m mnemocuda_amd.profiling traffic <fetch_dir> <write_dir> <out.json> <out.md> "<command>"
-    python -m mnemocuda_amd.profiling probe
+    python -m mnemocuda_amd.profiling probe [qkv|gemm|moe]
+    python -m mnemocuda_amd.profiling counters <out.md> "<command>" <filter> <pmc_dir>...
 
-`probe` is the program the two `--pmc` passes profile: the fused QKV GEMV of bench.py's
-workload (one layer's weights, 4 launches), then the calibration copy.
+`probe` is the program the `--pmc` passes profile, each ending with the calibration copy:
+  qkv  -- the fused QKV GEMV of bench.py's workload (one layer's weights, 4 launches);
+  gemm -- the M=512 Q4_K prefill GEMMs of bench.py (N=8192 and N=1536, 4 launches each);
+  moe  -- bench.py's grouped-expert prefill (configs[4], 3 calls).
+`counters` merges several `--pmc` runs of one probe into a table per kernel (counters summed
+over a dispatch's XCD / shader-engine instances, averaged over dispatches) with derived
+figures: VALU and MFMA instructions per wave, the share of wave time waiting on counters,
+the LDS bank-conflict ratio, and HBM bytes per launch from FETCH_SIZE scaled by the copy.
 
 `stats` turns a `rocprofv3 --kernel-trace --stats --output-format csv` run into a table of
 kernel durations.  `traffic` reads two `--pmc` runs (FETCH_SIZE, then WRITE_SIZE) of
@@ -105,7 +112,55 @@ def traffic(fetch_dir: str, write_dir: str, out_json: str, out_md: str, command:
     return out
 
 
-def probe(launches: int = 4) -> None:
+def counters(out_md: str, command: str, only: str, *pmc_dirs: str) -> None:
+    per: dict[tuple[str, int], dict[str, list[float]]] = defaultdict(lambda: defaultdict(list))
+    copy: dict[str, float] = {}
+    for d in pmc_dirs:
+        cur: dict[tuple[str, int, str, str], float] = defaultdict(float)
+        for r in csv.DictReader(open(_find(Path(d), "counter_collection.csv"))):
+            cur[(r["Kernel_Name"], int(r["Grid_Size"]), r["Dispatch_Id"], r["Counter_Name"])] += float(r["Counter_Value"])
+        for (name, grid, _, c), v in cur.items():
+            if "neg_kernel" in name and c == "FETCH_SIZE":
+                copy[c] = max(copy.get(c, 0.0), v)
+            elif only in name:
+                per[(name, grid)][c].append(v)
+    lines = [f"command: `{command}`", ""]
+    for (name, grid), cs in sorted(per.items(), key=lambda kv: kv[0][0]):
+        avg = {c: sum(v) / len(v) for c, v in cs.items()}
+        lines += [f"`{name[:150]}` grid={grid}", "", "| counter | per dispatch |", "|---|---|"]
+        lines += [f"| {c} | {v:.6g} |" for c, v in sorted(avg.items())]
+        waves = avg.get("SQ_WAVES")
+        derived = []
+        if waves:
+            for c, label in (("SQ_INSTS_VALU", "VALU instructions per wave"), ("SQ_INSTS_MFMA", "MFMA instructions per wave"),
+                             ("SQ_INSTS_LDS", "LDS instructions per wave"), ("SQ_INSTS_VMEM_RD", "vector memory reads per wave")):
+                if c in avg:
+                    derived.append(f"| {label} | {avg[c] / waves:.1f} |")
+        if "SQ_INSTS_VALU" in avg and avg.get("SQ_INSTS_MFMA"):
+            derived.append(f"| VALU per MFMA instruction | {avg['SQ_INSTS_VALU'] / avg['SQ_INSTS_MFMA']:.2f} |")
+        if "SQ_WAIT_INST_ANY" in avg and avg.get("SQ_WAVE_CYCLES"):
+            derived.append(f"| share of wave time waiting on counters | {avg['SQ_WAIT_INST_ANY'] / avg['SQ_WAVE_CYCLES']:.2f} |")
+        if "SQ_LDS_BANK_CONFLICT" in avg and avg.get("SQ_LDS_IDX_ACTIVE"):
+            derived.append(f"| LDS bank-conflict cycles / LDS active cycles | {avg['SQ_LDS_BANK_CONFLICT'] / avg['SQ_LDS_IDX_ACTIVE']:.2f} |")
+        if "FETCH_SIZE" in avg and copy.get("FETCH_SIZE"):
+            derived.append(f"| HBM bytes fetched per launch (FETCH_SIZE x {COPY_BYTES / copy['FETCH_SIZE']:.1f} B, the copy's factor) | "
+                           f"{avg['FETCH_SIZE'] * COPY_BYTES / copy['FETCH_SIZE']:.4g} |")
+        if derived:
+            lines += ["", "| derived | value |", "|---|---|", *derived]
+        lines.append("")
+    Path(out_md).write_text("\n".join(lines) + "\n")
+
+
+def _copy_tail() -> None:
+    import torch
+    src = torch.ones(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def probe(which: str = "qkv", launches: int = 4) -> None:
     import torch
     from mnemocuda_amd import ops, synth
     Q4K, Q6K, H, QD, KVD = 12, 14, 4096, 8192, 512
@@ -113,6 +168,34 @@ def probe(launches: int = 4) -> None:
     ops.init()
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
+    if which == "gemm":
+        T = 512
+        acts = torch.randn(T, H, device="cuda", generator=gen)
+        aq = torch.empty(T * (H // 128) * 144, dtype=torch.uint8, device="cuda")
+        ops.quantize_q8_1(acts, aq, H, T)
+        for n in (QD, 1536):
+            w = synth.weights_torch(gen, Q4K, n, H, "cuda")
+            out = torch.empty(T, n, device="cuda")
+            for _ in range(launches):
+                ops.gemm(w, Q4K, aq, out, n, H, T)
+        _copy_tail()
+        print("probe done", flush=True)
+        return
+    if which == "moe":
+        import numpy as np
+        T, E, k, EFF = 512, 128, 8, 1536
+        idx, wt = synth.zipf_routing(np.random.default_rng(7), T, E, k)
+        table = synth.expert_table_torch(gen, E, H, EFF, Q6K, "cuda")
+        stride, g_off, u_off, d_off = synth.expert_layout(H, EFF, Q6K)
+        x = torch.randn(T, H, device="cuda", generator=gen)
+        out = torch.zeros(T, H, device="cuda")
+        idx_d, w_d = torch.from_numpy(idx).cuda(), torch.from_numpy(wt).cuda()
+        ws = torch.empty(ops.moe_prefill_workspace_bytes(T, H, EFF, E, k), dtype=torch.uint8, device="cuda")
+        for _ in range(3):
+            ops.moe_prefill(table, stride, g_off, u_off, d_off, Q6K, x, idx_d, w_d, T, H, EFF, E, k, ws, out)
+        _copy_tail()
+        print("probe done", flush=True)
+        return
     wq, wk = synth.weights_torch(gen, Q4K, QD, H, "cuda"), synth.weights_torch(gen, Q4K, KVD, H, "cuda")
     wv = synth.weights_torch(gen, Q6K, KVD, H, "cuda")
     x = torch.randn(H, device="cuda", generator=gen)
@@ -133,6 +216,8 @@ if __name__ == "__main__":
     elif sys.argv[1] == "traffic":
         traffic(sys.argv[2], sys.argv[3], sys.argv[4], sys.argv[5], sys.argv[6])
     elif sys.argv[1] == "probe":
-        probe()
+        probe(*sys.argv[2:3])
+    elif sys.argv[1] == "counters":
+        counters(sys.argv[2], sys.argv[3], sys.argv[4], *sys.argv[5:])
     else:
         raise SystemExit(__doc__)
