@@ -454,44 +454,6 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
 #pragma unroll
         for (int b = 0; b < kNB; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // Q4_K min term, sum_s -(dmin*m_s)_i * ds_js, first: the accumulator starts as this
-    // absolute value (the running scales start at 1, their ratios telescope to
-    // 1 / (last d8 * last d), which the epilogue multiplies back).  Windows of 32 sub-blocks
-    // (4 super-blocks), wave parity kh taking windows kh, kh+2, ...; lane group q = lane/16
-    // holds super-block 4w + q of its row / token (K index 8q + s of the MFMA = sub-block s of
-    // that super-block).
-    if constexpr (TYPE == kTypeQ4K) {
-        const int q = lane >> 4;
-        const int nwin = (sb1 - sb0 + 3) / 4;
-        for (int w = kh; w < nwin; w += 2) {
-            const int sb = sb0 + 4 * w + q;
-            const bool valid = sb < sb1;
-            uint4 hdr[4], blk[kNB][2];
-#pragma unroll
-            for (int a = 0; a < 4; a++) {
-                const uint8_t *rp = g.W + (size_t)min(i0 + wi + 16 * a + (lane & 15), g.M - 1) * wrow_bytes;
-                hdr[a] = valid ? ld16(rp + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int b = 0; b < kNB; b++) {
-                const uint8_t *ap = (const uint8_t *)g.A +
-                                    (size_t)min(j0 + wj + 16 * b + (lane & 15), g.N - 1) * (K / 128) * kQ81Bytes;
-                blk[b][0] = valid ? ld16(ap + (size_t)(2 * sb) * kQ81Bytes) : make_uint4(0, 0, 0, 0);
-                blk[b][1] = valid ? ld16(ap + (size_t)(2 * sb + 1) * kQ81Bytes) : make_uint4(0, 0, 0, 0);
-            }
-            h8 bd[kNB];
-#pragma unroll
-            for (int b = 0; b < kNB; b++) bd[b] = ds_operand(blk[b][0], blk[b][1]);
-#pragma unroll
-            for (int a = 0; a < 4; a++) {
-                h8 hi, lo;
-                q4k_min_operand(hdr[a], hi, lo);
-#pragma unroll
-                for (int b = 0; b < kNB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
-            }
-        }
-    }
-
     // Pipeline: three LDS stages.  In step ks a wave multiplies the fragments of step ks
     // (read during step ks-1), reads the fragments of step ks+1 (its stage was completed
     // before the previous barrier), converts step ks+2 into the third stage, then meets
@@ -537,6 +499,44 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
             const float dt = d8last[kh][wj + 16 * b + (lane & 15)];
 #pragma unroll
             for (int e = 0; e < 4; e++) acc[a][b][e] *= dr[e] * dt;
+        }
+    }
+
+    // Q4_K min term, sum_s -(dmin*m_s)_i * ds_js, added to the absolute accumulator after
+    // the loop (its header reads touch every weight line again; in front of the pipeline
+    // they cost ~2 us more on the M=8192 GEMM).  Windows of 32 sub-blocks
+    // (4 super-blocks), wave parity kh taking windows kh, kh+2, ...; lane group q = lane/16
+    // holds super-block 4w + q of its row / token (K index 8q + s of the MFMA = sub-block s of
+    // that super-block).
+    if constexpr (TYPE == kTypeQ4K) {
+        const int q = lane >> 4;
+        const int nwin = (sb1 - sb0 + 3) / 4;
+        for (int w = kh; w < nwin; w += 2) {
+            const int sb = sb0 + 4 * w + q;
+            const bool valid = sb < sb1;
+            uint4 hdr[4], blk[kNB][2];
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                const uint8_t *rp = g.W + (size_t)min(i0 + wi + 16 * a + (lane & 15), g.M - 1) * wrow_bytes;
+                hdr[a] = valid ? ld16(rp + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < kNB; b++) {
+                const uint8_t *ap = (const uint8_t *)g.A +
+                                    (size_t)min(j0 + wj + 16 * b + (lane & 15), g.N - 1) * (K / 128) * kQ81Bytes;
+                blk[b][0] = valid ? ld16(ap + (size_t)(2 * sb) * kQ81Bytes) : make_uint4(0, 0, 0, 0);
+                blk[b][1] = valid ? ld16(ap + (size_t)(2 * sb + 1) * kQ81Bytes) : make_uint4(0, 0, 0, 0);
+            }
+            h8 bd[kNB];
+#pragma unroll
+            for (int b = 0; b < kNB; b++) bd[b] = ds_operand(blk[b][0], blk[b][1]);
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+                h8 hi, lo;
+                q4k_min_operand(hdr[a], hi, lo);
+#pragma unroll
+                for (int b = 0; b < kNB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
+            }
         }
     }
 
