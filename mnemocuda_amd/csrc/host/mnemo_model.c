@@ -247,6 +247,18 @@ int mnemo_parse_config(const char *json_text, mnemo_model_config *cfg) {
         return fail(MNEMO_ERR_BAD_ARG, "config.json: invalid block count %d", cfg->n_layers);
     if (cfg->n_heads <= 0 || cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads)
         return fail(MNEMO_ERR_BAD_ARG, "config.json: head counts %d / %d", cfg->n_heads, cfg->n_kv_heads);
+    /* the expert table is split by n_experts and the kernels size their tables by these */
+    if (cfg->n_experts <= 0 || cfg->n_experts > 512)
+        return fail(MNEMO_ERR_BAD_ARG, "config.json: invalid expert count %d (1..512)", cfg->n_experts);
+    if (cfg->experts_per_tok <= 0 || cfg->experts_per_tok > cfg->n_experts || cfg->experts_per_tok > 16)
+        return fail(MNEMO_ERR_BAD_ARG, "config.json: invalid expert_used_count %d (1..min(16, %d))",
+                    cfg->experts_per_tok, cfg->n_experts);
+    if (cfg->eff <= 0 || cfg->eff > 65536)
+        return fail(MNEMO_ERR_BAD_ARG, "config.json: invalid expert_feed_forward_length %d", cfg->eff);
+    if (cfg->head_dim <= 0 || cfg->head_dim > 512 || cfg->head_dim % 2)
+        return fail(MNEMO_ERR_BAD_ARG, "config.json: invalid key_length %d (even, 2..512)", cfg->head_dim);
+    if (cfg->context_length <= 0)
+        return fail(MNEMO_ERR_BAD_ARG, "config.json: invalid context_length %d", cfg->context_length);
     return 0;
 }
 

@@ -202,7 +202,9 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
     if (E > kMaxMoeExperts) return set_error(kErrBadArg, "moe_prefill: at most %d experts", kMaxMoeExperts);
     if (hidden % 256 != 0 || eff % 256 != 0)
         return set_error(kErrBadArg, "moe_prefill: hidden and eff must be multiples of 256");
-    if ((long)T * k > (long)1 << 24) return set_error(kErrBadArg, "moe_prefill: too many token-expert pairs");
+    // a tile-list entry is (expert << 16) | tile: an expert's tiles must stay below 65536
+    if ((long)T * k > 65536L * kMoeTileRows)
+        return set_error(kErrBadArg, "moe_prefill: more than %ld token-expert pairs", 65536L * kMoeTileRows);
     if (down_type != kTypeQ4K && down_type != kTypeQ6K)
         return set_error(kErrUnsupportedType, "moe_prefill: unsupported down type %d", down_type);
     if ((((uintptr_t)ws | (uintptr_t)x | (uintptr_t)out) & 15) != 0)

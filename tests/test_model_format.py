@@ -44,6 +44,20 @@ def test_config_whole_key_match_and_missing():
                                     "qwen3moe.attention.head_count": 6, "qwen3moe.attention.head_count_kv": 4}))
 
 
+@pytest.mark.parametrize("key,value,match", [
+    ("expert_count", 0, "expert count"), ("expert_count", -3, "expert count"), ("expert_count", 513, "expert count"),
+    ("expert_used_count", 0, "expert_used_count"), ("expert_used_count", 200, "expert_used_count"),
+    ("expert_feed_forward_length", 0, "expert_feed_forward_length"), ("attention.key_length", -128, "key_length"),
+    ("attention.key_length", 129, "key_length"), ("context_length", 0, "context_length")])
+def test_config_rejects_invalid_sizes(key, value, match):
+    """Sizes the loader divides or indexes by are range-checked (an expert_count of 0 would
+    otherwise divide the expert file size by zero)."""
+    cfg = {"qwen3moe.embedding_length": 4096, "qwen3moe.block_count": 2, "qwen3moe.attention.head_count": 4,
+           "qwen3moe.attention.head_count_kv": 2, f"qwen3moe.{key}": value}
+    with pytest.raises(MnemoError, match=match):
+        mm.parse_config(json.dumps(cfg))
+
+
 def test_resident_manifest_fields():
     big = 2**40 + 3  # offsets beyond 2^32 (and exact beyond 2^53 would need integers: parsed as such)
     text = json.dumps({"version": 2, "tensors": [
