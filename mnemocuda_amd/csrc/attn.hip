@@ -264,8 +264,18 @@ int launch_head_pass(HeadPassArgs a, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ attention (entry-point form)
-constexpr int kAttnThreads = 256;
-constexpr int kAttnTile = 1024;
+// One 1024-thread workgroup per query head, split-K inside the workgroup: wave w takes the
+// positions [w*C, (w+1)*C) of the sequence.  In a wave, G = hd/8 lanes hold 8 dims each of a
+// position (16-byte f16 loads) and the wave covers 64/G positions per step (one per lane
+// group, "slot"); every slot keeps its own online softmax (running max m, sum l and the
+// 8-dim slice of acc), so the loop has no barrier and no cross-slot exchange.  The slots of a
+// wave are merged with shuffles and the 16 waves through LDS at the end (the merge of two
+// partial softmaxes: m = max, l and acc rescaled by exp(m_i - m)).  The reference runs one
+// 256-thread block per head and walks the whole sequence in tiles
+// (src/kernels.cu:1382-1481, 1550-1673); the result is the same softmax(q.K^T * scale).V.
+constexpr int kAttnThreads = 1024;
+constexpr int kAttnWaves = kAttnThreads / 64;
+constexpr int kAttnUnroll = 4;  // positions per slot per step (loads in flight)
 
 template <int KV>
 __device__ __forceinline__ void load8(const void *cache, size_t off, const float *scales, size_t si, float (&k)[8]) {
@@ -285,88 +295,88 @@ __device__ __forceinline__ void load8(const void *cache, size_t off, const float
     }
 }
 
-template <int KV>
-__device__ __forceinline__ float load1(const void *cache, size_t off, const float *scales, size_t si) {
-    if (KV == kKvF16) return (float)((const _Float16 *)cache)[off];
-    return (float)((const int8_t *)cache)[off] * scales[si];
-}
-
-__device__ __forceinline__ float block_reduce(float v, float *part, bool is_max) {
-    v = is_max ? wave_max_all(v) : wave_sum_all(v);
-    __syncthreads();  // part[] may still be read from the previous reduction
-    if (lane_id() == 0) part[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = part[0];
-#pragma unroll
-    for (int i = 1; i < kAttnThreads / 64; i++) r = is_max ? fmaxf(r, part[i]) : r + part[i];
-    return r;
-}
-
-// One workgroup per query head.  Scores: hd/8 lanes per position, 8 dims each (16-byte f16
-// loads).  Softmax: online over tiles of kAttnTile positions.  P.V: kAttnThreads/hd threads
-// per dim, each over every tpd-th position of the tile; summed through LDS at the end.
-template <int KV>
+template <int KV, int HD>
 __global__ void __launch_bounds__(kAttnThreads) attention_kernel(AttnArgs a) {
-    __shared__ float qs[256];
-    __shared__ float sc[kAttnTile];
-    __shared__ float part[kAttnThreads / 64];
-    __shared__ float accs[kAttnThreads];
+    constexpr int G = HD / 8;   // lanes per position
+    constexpr int S = 64 / G;   // slots (positions per wave step)
+    __shared__ float wm[kAttnWaves], wl[kAttnWaves];
+    __shared__ float wacc[kAttnWaves][HD];
     const int head = blockIdx.x, kvh = head / a.gqa, tid = threadIdx.x, lane = lane_id();
-    const int hd = a.hd;
+    const int wave = tid >> 6, gi = lane % G, slot = lane / G;
     const int seq = (a.seq_dev ? *a.seq_dev : 0) + a.seq;
-    const size_t stride = (size_t)a.nkv * hd;
-    for (int d = tid; d < hd; d += kAttnThreads) qs[d] = a.q[(size_t)head * hd + d];
-    __syncthreads();
-    const int G = hd / 8;                    // lanes per position
-    const int ppw = 64 / G;                  // positions per wave per step
-    const int pps = ppw * (kAttnThreads / 64);
-    const int gi = lane % G, gp = lane / G;  // lane's 8-dim group, position slot in the wave
-    const int tpd = kAttnThreads / hd;       // threads per output dim
-    const int d = tid % hd, dpart = tid / hd;
-    float m = -INFINITY, l = 0.0f, acc = 0.0f;
-    for (int t0 = 0; t0 < seq; t0 += kAttnTile) {
-        const int tl = min(kAttnTile, seq - t0);
-        for (int i0 = 0; i0 < tl; i0 += pps) {
-            const int i = i0 + (tid >> 6) * ppw + gp;
-            const int p = t0 + min(i, tl - 1);
-            float k[8];
-            load8<KV>(a.kc, (size_t)p * stride + (size_t)kvh * hd + 8 * gi, a.ksc, (size_t)p * a.nkv + kvh, k);
-            float s = 0.0f;
+    const size_t stride = (size_t)a.nkv * HD;
+    float q[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) s = fmaf(qs[8 * gi + e], k[e], s);
-            for (int o = G / 2; o > 0; o >>= 1) s += __shfl_xor(s, o);
-            if (gi == 0 && i < tl) sc[i] = s * a.scale;
+    for (int e = 0; e < 8; e++) q[e] = a.q[(size_t)head * HD + 8 * gi + e] * a.scale;
+    const int chunk = (seq + kAttnWaves - 1) / kAttnWaves;
+    const int p0 = wave * chunk, p1 = min(seq, p0 + chunk);
+    float m = -INFINITY, l = 0.0f, acc[8] = {};
+    for (int pb = p0; pb < p1; pb += S * kAttnUnroll) {
+        float s[kAttnUnroll], v[kAttnUnroll][8];
+#pragma unroll
+        for (int u = 0; u < kAttnUnroll; u++) {
+            const int p = pb + u * S + slot;
+            const int pc = min(p, p1 - 1);  // past the chunk: the last position again, masked below
+            float k[8];
+            load8<KV>(a.kc, (size_t)pc * stride + (size_t)kvh * HD + 8 * gi, a.ksc, (size_t)pc * a.nkv + kvh, k);
+            load8<KV>(a.vc, (size_t)pc * stride + (size_t)kvh * HD + 8 * gi, a.vsc, (size_t)pc * a.nkv + kvh, v[u]);
+            float d = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) d = fmaf(q[e], k[e], d);
+#pragma unroll
+            for (int o = G / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
+            s[u] = p < p1 ? d : -INFINITY;
         }
-        __syncthreads();
-        float tm = -INFINITY;
-        for (int i = tid; i < tl; i += kAttnThreads) tm = fmaxf(tm, sc[i]);
-        tm = block_reduce(tm, part, true);
-        const float mn = fmaxf(m, tm);
-        const float rescale = l > 0.0f ? expf(m - mn) : 0.0f;
-        float ts = 0.0f;
-        for (int i = tid; i < tl; i += kAttnThreads) {
-            const float e = expf(sc[i] - mn);
-            sc[i] = e;
-            ts += e;
+        float mt = m;
+#pragma unroll
+        for (int u = 0; u < kAttnUnroll; u++) mt = fmaxf(mt, s[u]);
+        if (mt == -INFINITY) continue;  // nothing valid in this slot yet (uniform per slot)
+        const float r = expf(m - mt);   // m = -inf: 0
+        l *= r;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] *= r;
+#pragma unroll
+        for (int u = 0; u < kAttnUnroll; u++) {
+            const float w = expf(s[u] - mt);
+            l += w;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[e] = fmaf(w, v[u][e], acc[e]);
         }
-        ts = block_reduce(ts, part, false);  // its barriers also publish sc[]
-        float v = 0.0f;
-        for (int i = dpart; i < tl; i += tpd) {
-            const int p = t0 + i;
-            v = fmaf(sc[i], load1<KV>(a.vc, (size_t)p * stride + (size_t)kvh * hd + d, a.vsc, (size_t)p * a.nkv + kvh),
-                     v);
-        }
-        acc = acc * rescale + v;
-        l = l * rescale + ts;
-        m = mn;
-        __syncthreads();  // sc[] is rewritten by the next tile
+        m = mt;
     }
-    accs[tid] = acc;
+    // merge the slots of the wave (lanes gi + G * slot)
+#pragma unroll
+    for (int o = G; o < 64; o <<= 1) {
+        const float mo = __shfl_xor(m, o), lo = __shfl_xor(l, o);
+        const float mn = fmaxf(m, mo);
+        const float ra = mn == -INFINITY ? 0.0f : expf(m - mn), rb = mn == -INFINITY ? 0.0f : expf(mo - mn);
+        l = l * ra + lo * rb;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = acc[e] * ra + __shfl_xor(acc[e], o) * rb;
+        m = mn;
+    }
+    if (slot == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) wacc[wave][8 * gi + e] = acc[e];
+        if (gi == 0) {
+            wm[wave] = m;
+            wl[wave] = l;
+        }
+    }
     __syncthreads();
-    if (tid < hd) {
-        float o = 0.0f;
-        for (int j = 0; j < tpd; j++) o += accs[tid + j * hd];
-        a.out[(size_t)head * hd + tid] = seq > 0 && l > 0.0f ? o / l : 0.0f;
+    // merge the waves: thread d < HD owns output dim d
+    if (tid < HD) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; w++) mx = fmaxf(mx, wm[w]);
+        float lt = 0.0f, o = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; w++) {
+            const float r = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - mx);
+            lt = fmaf(wl[w], r, lt);
+            o = fmaf(wacc[w][tid], r, o);
+        }
+        a.out[(size_t)head * HD + tid] = seq > 0 && lt > 0.0f ? o / lt : 0.0f;
     }
 }
 
@@ -377,10 +387,15 @@ int launch_attention(AttnArgs a, int kv_type, hipStream_t s) {
         return set_error(kErrBadArg, "attention: head_dim %d not supported (64, 128, 256)", a.hd);
     if (a.seq < 0) return set_error(kErrBadArg, "attention: seq_len < 0");
     if (kv_type == kKvInt8 && (!a.ksc || !a.vsc)) return set_error(kErrBadArg, "attention: int8 cache needs scales");
-    if (kv_type == kKvF16)
-        hipLaunchKernelGGL(attention_kernel<kKvF16>, dim3(a.nh), dim3(kAttnThreads), 0, s, a);
-    else
-        hipLaunchKernelGGL(attention_kernel<kKvInt8>, dim3(a.nh), dim3(kAttnThreads), 0, s, a);
+#define MNEMO_ATTN(HD_)                                                                                  \
+    do {                                                                                                 \
+        if (kv_type == kKvF16) hipLaunchKernelGGL((attention_kernel<kKvF16, HD_>), dim3(a.nh), dim3(kAttnThreads), 0, s, a); \
+        else hipLaunchKernelGGL((attention_kernel<kKvInt8, HD_>), dim3(a.nh), dim3(kAttnThreads), 0, s, a); \
+    } while (0)
+    if (a.hd == 64) MNEMO_ATTN(64);
+    else if (a.hd == 128) MNEMO_ATTN(128);
+    else MNEMO_ATTN(256);
+#undef MNEMO_ATTN
     return check_launch("attention");
 }
 

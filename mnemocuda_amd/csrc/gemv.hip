@@ -141,7 +141,7 @@ __device__ __forceinline__ void build_x(const XRegs<XPT> &R, const XRegs<XPT> &R
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) v[j] = t[j];
-        } else {
+        } else if (n != kp) {  // uniform: columns n .. kp-1 of the last super-block are zero
             const uint32_t keep = e < n ? ~0u : 0u;
 #pragma unroll
             for (int j = 0; j < 4; j++) v[j] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[j]) & keep);
