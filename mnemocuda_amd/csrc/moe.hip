@@ -38,8 +38,8 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
 
 int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s);
 int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k, hipStream_t s);
-int launch_router_topk(const float *w, const float *x, const float *nw, float eps, float *logits, int n, int n_cols,
-                       int k, int *cnt, int *idx, float *wts, hipStream_t stream);
+int launch_router_topk(const float *w, const float *x, const float *nw, float eps, unsigned long long *slots, int n,
+                       int n_cols, int k, unsigned long long *cnt, int *idx, float *wts, hipStream_t stream);
 
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
@@ -252,12 +252,13 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
 // launches (router + top-k, gate + up, down + combine) with no synchronisation,
 // graph-capturable.
 //
-// Workspace: logits[E] | idx[k] | w[k] | gate/up rows [k][2][eff] | partial [k][hidden] |
-// tile counters [hidden] | router arrival counter, each 256-byte aligned.  The router
-// counter must be zero before the first call (zero the workspace once when allocating it);
-// every call leaves it zero.
+// Workspace: router arrival counter (64 bits) | tagged logit slots [E] (64 bits each) |
+// idx[k] | w[k] | gate/up rows [k][2][eff] | partial [k][hidden] | tile counters [hidden],
+// each 256-byte aligned.  The counter sits at offset 0 whatever the sizes, so a workspace
+// shared by calls of different shapes never finds other data there.  Zero the workspace
+// once when allocating it; calls keep the counter and slots valid from then on.
 struct MoeDecodeLayout {
-    size_t logits, idx, w, gu, partial, cnt, rcnt, total;
+    size_t rcnt, logits, idx, w, gu, partial, cnt, total;
 };
 
 static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
@@ -268,13 +269,13 @@ static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
         o = align256(o + bytes);
         return at;
     };
-    L.logits = take((size_t)E * 4);
+    L.rcnt = take(8);
+    L.logits = take((size_t)E * 8);
     L.idx = take((size_t)k * 4);
     L.w = take((size_t)k * 4);
     L.gu = take((size_t)k * 2 * eff * 4);
     L.partial = take((size_t)k * hidden * 4);
     L.cnt = take((size_t)hidden * 4);
-    L.rcnt = take(4);
     L.total = o;
     return L;
 }
@@ -300,14 +301,16 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     uint8_t *w8 = (uint8_t *)ws;
     // the routing goes to the caller's arrays when given (the engine logs expert use),
     // else to the workspace
-    float *logits = (float *)(w8 + L.logits), *wts = w_out ? w_out : (float *)(w8 + L.w);
+    unsigned long long *slots = (unsigned long long *)(w8 + L.logits);
+    float *wts = w_out ? w_out : (float *)(w8 + L.w);
     int *idx = idx_out ? idx_out : (int *)(w8 + L.idx);
     float *gu = (float *)(w8 + L.gu), *partial = (float *)(w8 + L.partial);
     int *cnt = (int *)(w8 + L.cnt);
 
     // with norm_w, x is the raw hidden state and both the router and the gate/up launch apply
     // the RMS norm themselves (the reference's separate rms_norm launch, forward.c:800-806)
-    int rc = launch_router_topk(router_w, x, norm_w, eps, logits, E, hidden, k, (int *)(w8 + L.rcnt), idx, wts, s);
+    int rc = launch_router_topk(router_w, x, norm_w, eps, slots, E, hidden, k,
+                                (unsigned long long *)(w8 + L.rcnt), idx, wts, s);
     if (rc) return rc;
 
     GemvArgs a;
@@ -360,10 +363,10 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
 // The decode MoE block for callers that cannot allocate or pass a workspace (code under
 // graph capture, serving loops): the workspace is the file-scope device array below, one
 // copy per GPU, held until the process ends.  Every call on a GPU uses that GPU's copy, so
-// calls that overlap on one GPU (other streams, other threads) race; the counters the
-// kernels need at zero (the router's arrival counter; the gate/up launch clears the tile
-// counters itself) are zeroed when a GPU's copy is first set up and every call leaves them
-// zero.  Sizes: moe_decode_layout(hidden, eff, n_experts, k) must fit kDecodeScratchBytes
+// calls that overlap on one GPU (other streams, other threads) race.  The array is zeroed
+// when a GPU's copy is first set up; from then on every call keeps the router's counter
+// (at offset 0 for every shape) and logit slots valid, and the gate/up launch clears the
+// tile counters itself.  Sizes: moe_decode_layout(hidden, eff, n_experts, k) must fit kDecodeScratchBytes
 // (hidden 8192, eff 4096, 1024 experts, k 16 fit).
 constexpr size_t kDecodeScratchBytes = (size_t)1152 * 1024;
 static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];

@@ -149,13 +149,22 @@ int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k,
 
 // ---------------------------------------------------------------- router + top-k, one launch
 // The decode MoE block's router (kernels.cu:859-880) and top-k softmax (kernels.cu:993-1057)
-// in one launch: workgroup r computes logit r; the last workgroup to finish (an arrival
+// in one launch: workgroup r computes logit r; the last workgroup to count in (an arrival
 // counter) selects the top k by rank -- logit i's rank is the number of logits ordered
 // before it by (value desc, index asc), so the k winners come out sorted and ties go to the
 // lower index, as topk_wave orders them -- and writes the softmax over the winners.
-// Logits <= -1e30 and NaN never win.  The counter must be zero before the first launch;
-// the last workgroup resets it.  Logits cross workgroups (and XCDs) as agent-scope atomic
-// stores/loads; each writer waits for its store before counting in.
+// Logits <= -1e30 and NaN never win.
+//
+// Arrival without fences (an agent-scope release/acquire pair writes back and invalidates
+// the XCDs' L2s, ~2.5 us a launch): the counter is 64 bits, the launch number in the high
+// half and the arrivals of this launch in the low half.  Each workgroup counts in with a
+// relaxed fetch-add, which hands it the launch number g, and then stores its logit as one
+// 64-bit atomic slot {g + 1, logit bits}.  The workgroup that sees n - 1 earlier arrivals
+// is the last; it moves the counter on to {g + 1, 0} (every workgroup of the launch has
+// counted in, and the next launch on the stream starts after this one ends) and reads
+// each slot until it carries the tag g + 1 -- a store that the fetch-add order says was
+// issued, so the wait ends without any ordering between the two locations.  A zero-filled
+// counter and slots are a valid start (tag 0 never matches g + 1 before 2^32 launches).
 // With nw, x is first RMS-normalised (x * rsqrt(mean(x^2) + eps) * nw, the reference's
 // rms_norm_kernel, kernels.cu:692-722) inside every workgroup: each holds all of x.
 __device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, const float *__restrict__ x,
@@ -196,15 +205,21 @@ __device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, cons
     return acc;
 }
 
+// upper bound on one slot's wait (s_sleep rounds of ~64 cycles): the slot stores were all
+// issued before the last arrival, so a wait ends in well under a microsecond; the bound only
+// guarantees that no wave spins for ever
+constexpr int kRouterSlotWait = 1 << 22;
+
 __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *__restrict__ w,
                                                                  const float *__restrict__ x,
                                                                  const float *__restrict__ nw, float eps,
-                                                                 float *__restrict__ logits, int n, int n_cols,
-                                                                 int k, int *__restrict__ cnt,
+                                                                 unsigned long long *__restrict__ slots, int n,
+                                                                 int n_cols, int k,
+                                                                 unsigned long long *__restrict__ cnt,
                                                                  int *__restrict__ idx, float *__restrict__ wts,
                                                                  int vec4) {
     __shared__ float part[kRowThreads / 64];
-    __shared__ int is_last;
+    __shared__ unsigned int is_last, tag;
     __shared__ float z[64 * kTopkMaxPerLane];
     __shared__ float sel_v[kTopkMaxK];
     __shared__ int sel_i[kTopkMaxK];
@@ -213,21 +228,27 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     const float v = block_sum(nw ? row_dot_norm(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
                                  : row_dot(w + (size_t)row * n_cols, x, n_cols, vec4),
                               part);
-    // arrival protocol: the logit store happens-before the release half of the agent-scope
-    // fetch-add; the workgroup that sees n - 1 arrivals acquires them all (the acquire half of
-    // its fetch-add, then an agent-scope acquire fence in every thread after the barrier that
-    // hands them is_last), so its loads below see every workgroup's logit across the XCDs' L2s
     if (tid == 0) {
-        __hip_atomic_store(logits + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        is_last = old == n - 1;
-        if (is_last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned int g1 = (unsigned int)(old >> 32) + 1u;
+        __hip_atomic_store(slots + row, ((unsigned long long)g1 << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        is_last = (unsigned int)old == (unsigned int)(n - 1);
+        tag = g1;
+        if (is_last)  // {g, n - 1} + 1 + (2^32 - n) = {g + 1, 0}
+            __hip_atomic_fetch_add(cnt, (1ull << 32) - (unsigned long long)n, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!is_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const unsigned int g1 = tag;
     for (int i = tid; i < n; i += kRowThreads) {
-        const float l = __hip_atomic_load(logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned long long sv = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int t = 0; (unsigned int)(sv >> 32) != g1 && t < kRouterSlotWait; t++) {
+            __builtin_amdgcn_s_sleep(1);
+            sv = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const float l = __uint_as_float((unsigned int)sv);
         z[i] = l > -1e30f ? l : -1e30f;  // NaN and <= -1e30 never win
     }
     if (tid < k) sel_i[tid] = -1;
@@ -265,9 +286,9 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     }
 }
 
-int launch_router_topk(const float *w, const float *x, const float *nw, float eps, float *logits, int n, int n_cols,
-                       int k, int *cnt, int *idx, float *wts, hipStream_t stream) {
-    if (!w || !x || !logits || !cnt || !idx || !wts || n <= 0 || n_cols <= 0 || k <= 0 || k > kTopkMaxK ||
+int launch_router_topk(const float *w, const float *x, const float *nw, float eps, unsigned long long *slots, int n,
+                       int n_cols, int k, unsigned long long *cnt, int *idx, float *wts, hipStream_t stream) {
+    if (!w || !x || !slots || !cnt || !idx || !wts || n <= 0 || n_cols <= 0 || k <= 0 || k > kTopkMaxK ||
         k > n || n > 64 * kTopkMaxPerLane)
         return set_error(kErrBadArg, "router_topk: need 0 < k <= min(%d, n_experts), n_experts <= %d", kTopkMaxK,
                          64 * kTopkMaxPerLane);
@@ -276,7 +297,7 @@ int launch_router_topk(const float *w, const float *x, const float *nw, float ep
     if (nw && !vec4)
         return set_error(kErrBadArg, "router_topk: the fused RMS norm needs n_cols %% 4 == 0, <= %d and aligned vectors",
                          4 * kRowMaxV4 * kRowThreads);
-    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, nw, eps, logits, n,
+    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, nw, eps, slots, n,
                        n_cols, k, cnt, idx, wts, vec4);
     return check_launch("router_topk");
 }

@@ -232,6 +232,35 @@ def test_moe_decode_graph_replays(gpu):
         del junk
 
 
+def test_moe_decode_workspace_shared_across_shapes(gpu):
+    """One workspace (sized for the largest call) shared by calls of different shapes and
+    expert counts, in an order where each call's layout overlaps data the previous call left:
+    every call matches the same call on a fresh zero-filled workspace bit for bit (the router's
+    arrival counter and tagged logit slots stay valid whatever came before)."""
+    shapes = [(4096, 1536, 128, 8, 14), (1024, 512, 16, 4, 12), (2048, 1024, 64, 6, 14),
+              (1024, 512, 16, 4, 12), (4096, 1536, 128, 8, 14)]
+    big = max(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k) for H, EFF, E, k, _ in shapes)
+    shared = torch.zeros(big, dtype=torch.uint8, device="cuda")
+    for i, (H, EFF, E, k, DT) in enumerate(shapes):
+        rng = np.random.default_rng(100 + i)
+        table = dev(synth.expert_table(rng, E, H, EFF, DT))
+        lay = synth.expert_layout(H, EFF, DT)
+        router = dev((rng.standard_normal((E, H)) / np.sqrt(H)).astype(np.float32))
+        x = dev(rng.standard_normal(H).astype(np.float32))
+        outs = []
+        for ws in (torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8,
+                               device="cuda"), shared):
+            out = torch.zeros(H, device="cuda")
+            idx = torch.full((k,), -1, dtype=torch.int32, device="cuda")
+            w = torch.zeros(k, device="cuda")
+            case(f"moe_decode shared workspace call {i}: H={H} EFF={EFF} E={E} k={k} fresh={ws is not shared}")
+            gpu.ops.moe_decode(router, table, *lay, DT, x, H, EFF, E, k, ws, out, idx, w)
+            outs.append((host(out).copy(), host(idx).copy(), host(w).copy()))
+        (o0, i0, w0), (o1, i1, w1) = outs
+        assert (i0 >= 0).all() and np.array_equal(i0, i1) and np.array_equal(w0, w1)
+        assert np.array_equal(o0, o1)
+
+
 @pytest.mark.parametrize("H,EFF,E,k,DT,alias", [(512, 256, 16, 4, 14, False), (4096, 1536, 24, 8, 14, True),
                                                 (1024, 512, 8, 8, 12, True)])
 def test_moe_decode_rmsnorm_vs_oracle(gpu, oracle, H, EFF, E, k, DT, alias):
