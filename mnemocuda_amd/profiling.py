@@ -8,7 +8,10 @@
 `probe` is the program the `--pmc` passes profile, each ending with the calibration copy:
   qkv  -- the fused QKV GEMV of bench.py's workload (one layer's weights, 4 launches);
   gemm -- the M=512 Q4_K prefill GEMMs of bench.py (N=8192 and N=1536, 4 launches each);
-  moe  -- bench.py's grouped-expert prefill (configs[4], 3 calls).
+  moe  -- bench.py's grouped-expert prefill (configs[4], 3 calls);
+  decode -- bench.py's decode layer (fused QKV with the norm, attention at position 2048, O +
+          residual, the MoE block with 128 resident experts) over 4 layers of distinct
+          weights, 3 tokens, then the lm_head Q6_K 151,936 x 4096 GEMV and top-p sampling.
 `counters` merges several `--pmc` runs of one probe into a table per kernel (counters summed
 over a dispatch's XCD / shader-engine instances, averaged over dispatches) with derived
 figures: VALU and MFMA instructions per wave, the share of wave time waiting on counters,
@@ -160,6 +163,45 @@ def _copy_tail() -> None:
     torch.cuda.synchronize()
 
 
+def _decode_probe(torch, ops, synth, gen, layers: int = 4, tokens: int = 3, pos0: int = 2048) -> None:
+    """the calls of bench.py's decode step, eager, on `layers` layers of distinct weights"""
+    Q4K, Q6K, H, QD, KVD = 12, 14, 4096, 8192, 512
+    E, k, EFF, VOCAB = 128, 8, 1536, 151936
+    NH, NKV, HD, EPS, THETA, max_ctx = 64, 4, 128, 1e-6, 1e6, 4096
+    stride, g_off, u_off, d_off = synth.expert_layout(H, EFF, Q6K)
+    L = [dict(q=synth.weights_torch(gen, Q4K, QD, H, "cuda"), k=synth.weights_torch(gen, Q4K, KVD, H, "cuda"),
+              v=synth.weights_torch(gen, Q6K, KVD, H, "cuda"), o=synth.weights_torch(gen, Q4K, H, QD, "cuda"),
+              table=synth.expert_table_torch(gen, E, H, EFF, Q6K, "cuda"),
+              router=torch.randn(E, H, device="cuda", generator=gen) / 64,
+              kc=torch.randn(max_ctx * NKV * HD, device="cuda", generator=gen).half(),
+              vc=torch.randn(ops.v_cache_bytes(NKV, HD, max_ctx, 0, 1) // 2, device="cuda", generator=gen).half())
+         for _ in range(layers)]
+    nw = 1 + 0.05 * torch.randn(H, device="cuda", generator=gen)
+    qn = 1 + 0.05 * torch.randn(HD, device="cuda", generator=gen)
+    lm_head = synth.weights_torch(gen, Q6K, VOCAB, H, "cuda")
+    bufs = (torch.randn(H, device="cuda", generator=gen), torch.empty(H, device="cuda"))
+    q, kk, v = torch.empty(QD, device="cuda"), torch.empty(KVD, device="cuda"), torch.empty(KVD, device="cuda")
+    attn, normed, logits = torch.empty(QD, device="cuda"), torch.empty(H, device="cuda"), torch.empty(VOCAB, device="cuda")
+    tok, pos = torch.zeros(1, dtype=torch.int32, device="cuda"), torch.full((1,), pos0, dtype=torch.int32, device="cuda")
+    ws = torch.zeros(ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    aws = torch.empty(ops.attention_decode_workspace_bytes(NKV, max_ctx), dtype=torch.uint8, device="cuda")
+    sws = torch.empty(ops.sample_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    for _ in range(tokens):
+        for li, W in enumerate(L):
+            src, dst = bufs[li % 2], bufs[(li + 1) % 2]
+            ops.matvec_qkv_rmsnorm(W["q"], Q4K, W["k"], Q4K, W["v"], Q6K, src, nw, EPS, q, kk, v, QD, KVD, H)
+            ops.attention_decode_prep(q, kk, v, qn, qn, EPS, THETA, W["kc"], W["vc"], attn, NH, HD, NKV, max_ctx, pos,
+                                      1.0 / HD ** 0.5, aws, v_layout=1)
+            ops.matvec_q4k_add(W["o"], attn, src, dst, H, QD)
+            ops.moe_decode_rmsnorm(W["router"], W["table"], stride, g_off, u_off, d_off, Q6K, dst, nw, EPS, H, EFF,
+                                   E, k, ws, dst)
+        ops.rms_norm(bufs[layers % 2], nw, normed, EPS)
+        ops.matvec_q6k(lm_head, normed, logits, VOCAB, H)
+        ops.sample_token_ws(logits, VOCAB, 0.7, 0.9, 12345, sws, tok)
+        pos.add_(1)
+    torch.cuda.synchronize()
+
+
 def probe(which: str = "qkv", launches: int = 4) -> None:
     import torch
     from mnemocuda_amd import ops, synth
@@ -193,6 +235,11 @@ def probe(which: str = "qkv", launches: int = 4) -> None:
         ws = torch.empty(ops.moe_prefill_workspace_bytes(T, H, EFF, E, k), dtype=torch.uint8, device="cuda")
         for _ in range(3):
             ops.moe_prefill(table, stride, g_off, u_off, d_off, Q6K, x, idx_d, w_d, T, H, EFF, E, k, ws, out)
+        _copy_tail()
+        print("probe done", flush=True)
+        return
+    if which == "decode":
+        _decode_probe(torch, ops, synth, gen)
         _copy_tail()
         print("probe done", flush=True)
         return
