@@ -204,7 +204,7 @@ int mnemo_moe_decode_rmsnorm(const float *router_w, const void *experts, size_t 
  * allocate or hold a workspace (code under hipGraph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  It allocates nothing: the workspace is a device array inside the
  * library, one copy per GPU kept until the process ends, set up by cuda_kernels_init (or by
- * the first call on a GPU).  Sizes must fit that array, 1,179,648 bytes of workspace
+ * the first call on a GPU).  Sizes must fit that array, 1,703,936 bytes of workspace
  * (mnemo_moe_decode_workspace_bytes(hidden, eff, n_experts, k) <= that: hidden 8192,
  * eff 4096, 1024 experts, k 16 fit); larger sizes are rejected with an error.  Every call on
  * a GPU shares that GPU's array, so calls that overlap on one GPU (other streams or host

@@ -406,7 +406,8 @@ __device__ __forceinline__ GemvMat pass_mat(const GemvArgs &args, int base, int 
         M.mode = kEpiStore;
         M.scale = 0.0f;
     } else {
-        M.y = E.y + (size_t)s * E.rows;
+        M.part = E.part + (size_t)s * E.rows;
+        M.tag = (unsigned int)(*E.gen >> 32);
         M.mode = kEpiScaledStore;
         M.scale = ok ? E.wt[s] : 0.0f;
     }
@@ -470,25 +471,28 @@ __device__ __forceinline__ void finish_pass(const GemvMat &M, int bpr, const Pas
         if (M.mode == kEpiStore) M.y[ps.lrow] = acc;
         else if (M.mode == kEpiResidual) M.y[ps.lrow] = acc + M.res[ps.lrow];
         else if (M.mode == kEpiScaledAdd) M.y[ps.lrow] += M.scale * acc;
-        else  // expert partials: written through to the device coherence point (see experts_combine)
-            __hip_atomic_store(M.y + ps.lrow, M.scale * acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else  // expert partials: tagged 64-bit slots (see experts_combine)
+            __hip_atomic_store(M.part + ps.lrow, ((unsigned long long)M.tag << 32) | __float_as_uint(M.scale * acc),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
 // Expert-mode down launch: after a workgroup has stored its rows' partials, the last of
 // the `slots` workgroups that cover the same row tile (one per slot) adds the slot sum,
 // in slot order, into out -- deterministic, and no separate combine launch.
-// Visibility across the XCDs' separate L2s without a device-scope fence (a fence writes
-// back and invalidates a whole L2 per workgroup; it cost ~48 us per MoE layer): the
-// partials are agent-scope atomic stores, which go through to the coherence point, every
-// thread waits for its stores to complete before the barrier, the counter is an
-// agent-scope atomic, and the last workgroup reads the partials with agent-scope atomic
-// loads.
+// Visibility across the XCDs' separate L2s without fences (an agent-scope fence writes back
+// and invalidates a whole L2 per workgroup; it cost ~48 us per MoE layer): every partial is
+// one 64-bit atomic slot {tag, value} whose tag is this call's number (the high half of the
+// router's arrival counter, which the router of the same call moved on), the tile counter
+// only elects the last workgroup, and that workgroup reads each slot until it carries the
+// call's tag.  The slot stores were issued before their workgroups counted in, so every
+// wait ends; no ordering between two locations is assumed.
+constexpr int kPartialWait = 1 << 22;  // bound on one slot's wait (s_sleep rounds)
+
 template <int RPB>
 __device__ __forceinline__ void experts_combine(const GemvExperts &E) {
     __shared__ int is_last;
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-    __syncthreads();
+    __syncthreads();  // every wave of the workgroup has issued its partial stores
     const int tile = (int)blockIdx.x % E.ntiles;
     if (threadIdx.x == 0) {
         const int old = __hip_atomic_fetch_add(&E.tile_cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -497,11 +501,19 @@ __device__ __forceinline__ void experts_combine(const GemvExperts &E) {
     }
     __syncthreads();
     if (!is_last) return;
+    const unsigned int tag = (unsigned int)(*E.gen >> 32);
     for (int r = threadIdx.x; r < RPB; r += kGemvThreads) {
         const int row = tile * RPB + r;
         float sum = 0.0f;
-        for (int s = 0; s < E.slots; s++)
-            sum += __hip_atomic_load(E.y + (size_t)s * E.rows + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int s = 0; s < E.slots; s++) {
+            const unsigned long long *slot = E.part + (size_t)s * E.rows + row;
+            unsigned long long v = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int t = 0; (unsigned int)(v >> 32) != tag && t < kPartialWait; t++) {
+                __builtin_amdgcn_s_sleep(1);
+                v = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            sum += __uint_as_float((unsigned int)v);
+        }
         E.out[row] += sum;
     }
 }

@@ -44,6 +44,9 @@ struct GemvMat {
     // further (gate, up, gate, up, ...); lrow counts row pairs (kEpiSwiGLU)
     int pair;
     long long mstride;
+    // kEpiScaledStore: the expert partials as tagged 64-bit slots {tag, fp32 bits}
+    unsigned long long *part;
+    unsigned int tag;
 };
 
 // Expert mode (GemvArgs::experts != 0): the matrices are chosen on the device from the
@@ -67,6 +70,10 @@ struct GemvExperts {
     const float *xs;
     float *y;
     float *out;
+    // down launch with per-slot partials: the tagged partial slots [slots][rows] and the
+    // 64-bit counter whose high half is this call's tag (the router's arrival counter)
+    unsigned long long *part;
+    const unsigned long long *gen;
     int *tile_cnt;
     int slots, nm, rows, type, n_experts;
     int act;

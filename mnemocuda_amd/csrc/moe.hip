@@ -253,7 +253,8 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
 // graph-capturable.
 //
 // Workspace: router arrival counter (64 bits) | tagged logit slots [E] (64 bits each) |
-// idx[k] | w[k] | gate/up rows [k][2][eff] | partial [k][hidden] | tile counters [hidden],
+// idx[k] | w[k] | gate/up rows [k][2][eff] | tagged partial slots [k][hidden] (64 bits
+// each, used when the down launch combines through partials) | tile counters [hidden],
 // each 256-byte aligned.  The counter sits at offset 0 whatever the sizes, so a workspace
 // shared by calls of different shapes never finds other data there.  Zero the workspace
 // once when allocating it; calls keep the counter and slots valid from then on.
@@ -274,7 +275,7 @@ static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
     L.idx = take((size_t)k * 4);
     L.w = take((size_t)k * 4);
     L.gu = take((size_t)k * 2 * eff * 4);
-    L.partial = take((size_t)k * hidden * 4);
+    L.partial = take((size_t)k * hidden * 8);
     L.cnt = take((size_t)hidden * 4);
     L.total = o;
     return L;
@@ -304,7 +305,8 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     unsigned long long *slots = (unsigned long long *)(w8 + L.logits);
     float *wts = w_out ? w_out : (float *)(w8 + L.w);
     int *idx = idx_out ? idx_out : (int *)(w8 + L.idx);
-    float *gu = (float *)(w8 + L.gu), *partial = (float *)(w8 + L.partial);
+    float *gu = (float *)(w8 + L.gu);
+    unsigned long long *partial = (unsigned long long *)(w8 + L.partial);
     int *cnt = (int *)(w8 + L.cnt);
 
     // with norm_w, x is the raw hidden state and both the router and the gate/up launch apply
@@ -346,7 +348,8 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
     a.ex.idx = idx;
     a.ex.wt = wts;
     a.ex.xs = gu;
-    a.ex.y = partial;
+    a.ex.part = partial;
+    a.ex.gen = (const unsigned long long *)(w8 + L.rcnt);
     a.ex.out = out;
     a.ex.tile_cnt = cnt;
     a.ex.slots = k;
@@ -368,7 +371,7 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
 // (at offset 0 for every shape) and logit slots valid, and the gate/up launch clears the
 // tile counters itself.  Sizes: moe_decode_layout(hidden, eff, n_experts, k) must fit kDecodeScratchBytes
 // (hidden 8192, eff 4096, 1024 experts, k 16 fit).
-constexpr size_t kDecodeScratchBytes = (size_t)1152 * 1024;
+constexpr size_t kDecodeScratchBytes = (size_t)1664 * 1024;
 static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
 
 constexpr int kMaxScratchDevices = 64;

@@ -237,8 +237,9 @@ def test_moe_decode_workspace_shared_across_shapes(gpu):
     expert counts, in an order where each call's layout overlaps data the previous call left:
     every call matches the same call on a fresh zero-filled workspace bit for bit (the router's
     arrival counter and tagged logit slots stay valid whatever came before)."""
-    shapes = [(4096, 1536, 128, 8, 14), (1024, 512, 16, 4, 12), (2048, 1024, 64, 6, 14),
-              (1024, 512, 16, 4, 12), (4096, 1536, 128, 8, 14)]
+    # (2048, 2560, 16, 10): the down launch combines through the tagged partial slots
+    shapes = [(4096, 1536, 128, 8, 14), (1024, 512, 16, 4, 12), (2048, 2560, 16, 10, 14),
+              (1024, 512, 16, 4, 12), (2048, 2560, 16, 10, 14), (4096, 1536, 128, 8, 14)]
     big = max(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k) for H, EFF, E, k, _ in shapes)
     shared = torch.zeros(big, dtype=torch.uint8, device="cuda")
     for i, (H, EFF, E, k, DT) in enumerate(shapes):

@@ -62,8 +62,8 @@ def test_noalloc_matches_workspace_entry_point(gpu, order):
 def test_noalloc_rejects_oversize(gpu):
     lib = gpu.load_library()
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
-    H, EFF, E, k = 16384, 8192, 128, 16  # needs ~2.2 MB of workspace
-    assert gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k) > 1179648
+    H, EFF, E, k = 16384, 8192, 128, 16  # needs ~3.2 MB of workspace
+    assert gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k) > 1703936
     out = torch.zeros(H, device="cuda")
     before = out.clone()
     rc = lib.mnemo_moe_decode_rmsnorm_noalloc(None, None, 0, 0, 0, 0, 14, None, _ptr(out), C.c_float(1e-6), H, EFF,
