@@ -7,12 +7,14 @@
 // (store | store + residual | y += scale * acc).
 //
 // Design (CDNA4, wave64):
-//  * x is re-expressed per 32-element sub-block as two int8 digits,
-//      x ~= u * (254*d1 + d2),  u = amax/(127*254),  |x - xhat| <= ~amax/64516,
+//  * x is re-expressed per 32-element sub-block as a 16-bit integer in two bytes,
+//      x ~= u * (256*d1 + d2),  u = amax/32767,  |x - xhat| <= amax/65534,
+//    d1 the signed high byte and d2 the unsigned low byte of rne(x/u),
 //    held in LDS together with fp32 sums of x per 32 and per 16 elements.  Each
 //    workgroup (512 threads, two per CU) builds this image once for all of its rows.
-//    Weight nibbles / 6-bit values are multiplied with v_dot4_i32_i8 (4 MACs per
-//    instruction, two per digit) and the integer partial of each sub-block is rescaled
+//    Weight nibbles / 6-bit values (unsigned) are multiplied with v_dot4_i32_i8 (high
+//    bytes) and v_dot4_u32_u8 (low bytes), 4 MACs per instruction, and the integer
+//    partial of each sub-block is rescaled
 //    in fp32:
 //      Q4_K: w = d*sc*q - dmin*m   ->  acc += d*sc*u*I - dmin*m*sum32(x)
 //      Q6_K: w = d*sc*(q-32)       ->  acc += d*sc*(u*I - 32*sum16(x))
@@ -47,7 +49,7 @@ constexpr int xpt_for(int kp_max) { return (kp_max + 4 * kGemvThreads - 1) / (4 
 
 // ------------------------------------------------------------------ x preparation
 // LDS image of x for a padded length kp (multiple of 256):
-//   int8 d1[kp + 128] | int8 d2[kp + 128] | float u[kp/32] | float s32[kp/32] | float s16[kp/16]
+//   int8 d1[kp + 128] | uint8 d2[kp + 128] | float u[kp/32] | float s32[kp/32] | float s16[kp/16]
 // The digit planes are stored in 16-byte words, interleaved by 128-column chunk: column c
 // lives in word ((c % 128) / 16) * (kp/128 + 1) + c / 128.  Lane ul reads chunk ul, so the
 // 16-byte reads of one instruction hit consecutive words (no bank conflicts); the +1
@@ -150,30 +152,23 @@ __device__ __forceinline__ void build_x(const XRegs<XPT> &R, const XRegs<XPT> &R
         // two instructions; non-negative floats order like their bits for the DPP max)
         const float a4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
         const float amax = __builtin_bit_cast(float, umax_dpp8(__builtin_bit_cast(uint32_t, a4)));
-        const float s = amax * (1.0f / 127.0f);
-        const float u = s * (1.0f / 254.0f);
-        const float inv1 = amax > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.0f;
-        const float inv2 = inv1 * 254.0f;
-        // d1 = rne(v * inv1), d2 = rne((v - d1*s) * inv2); |v * inv1| <= 127 (1 + 2^-22) and
-        // |r * inv2| <= 127 (1 + 2^-21), so both land in [-127, 127] without a clamp.  The
-        // low byte of (t + magic) is the digit in two's complement.
-        uint32_t b1[4], b2[4];
+        const float u = amax * (1.0f / 32767.0f);
+        const float inv = amax > 0.0f ? 32767.0f * __builtin_amdgcn_rcpf(amax) : 0.0f;
+        // q = rne(v * inv): |v * inv| <= 32767 (1 + 2^-22), so |q| <= 32767.  The low half of
+        // (t + magic) is q in two's complement: byte 1 is the signed digit d1 = q >> 8, byte 0
+        // the unsigned digit d2 = q & 255, and q = 256 d1 + d2.
+        uint32_t b1[4];
         float s4 = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const float t1 = fmaf(v[j], inv1, kMagic);
-            const float a = t1 - kMagic;
-            const float r = fmaf(-a, s, v[j]);
-            const float t2 = fmaf(r, inv2, kMagic);
-            b1[j] = __builtin_bit_cast(uint32_t, t1);
-            b2[j] = __builtin_bit_cast(uint32_t, t2);
+            b1[j] = __builtin_bit_cast(uint32_t, fmaf(v[j], inv, kMagic));
             s4 += v[j];
         }
-        // gather the low bytes: selector byte k picks byte sel_k of {src0 (4..7), src1 (0..3)}
-        const uint32_t w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0C0C0400u) |
+        // gather bytes: selector byte k picks byte sel_k of {src0 (4..7), src1 (0..3)}
+        const uint32_t w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0C0C0501u) |
+                            __builtin_amdgcn_perm(b1[3], b1[2], 0x05010C0Cu);
+        const uint32_t w2 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0C0C0400u) |
                             __builtin_amdgcn_perm(b1[3], b1[2], 0x04000C0Cu);
-        const uint32_t w2 = __builtin_amdgcn_perm(b2[1], b2[0], 0x0C0C0400u) |
-                            __builtin_amdgcn_perm(b2[3], b2[2], 0x04000C0Cu);
         const float s16 = sum4(s4);                             // 4 lanes x 4 = 16 elements
         const float s32 = s16 + dpp_f<kDppRowHalfMirror>(s16);  // 8 lanes = 32 elements
         if (store) {
@@ -261,6 +256,14 @@ __device__ __forceinline__ int dot16(const uint32_t (&q)[4], const int4 &d, int 
     acc = sdot4((int)q[3], d.w, acc);
     return acc;
 }
+// the same with the unsigned low-byte digits (the weights are unsigned as well)
+__device__ __forceinline__ int dot16u(const uint32_t (&q)[4], const int4 &d, int acc) {
+    acc = (int)__builtin_amdgcn_udot4(q[0], (uint32_t)d.x, (uint32_t)acc, false);
+    acc = (int)__builtin_amdgcn_udot4(q[1], (uint32_t)d.y, (uint32_t)acc, false);
+    acc = (int)__builtin_amdgcn_udot4(q[2], (uint32_t)d.z, (uint32_t)acc, false);
+    acc = (int)__builtin_amdgcn_udot4(q[3], (uint32_t)d.w, (uint32_t)acc, false);
+    return acc;
+}
 
 // Sum over the 128 weights of a Q4_K half super-block whose first column is c.
 // Sub-block t of the half: nibble t%2 of qs dwords 8(t/2) .. +7.
@@ -278,8 +281,8 @@ __device__ __forceinline__ float q4k_dot(const RawH &r, int hf, int c, const XLd
         const uint32_t nb[4] = {(qb.x >> sh) & 0x0F0F0F0Fu, (qb.y >> sh) & 0x0F0F0F0Fu,
                                 (qb.z >> sh) & 0x0F0F0F0Fu, (qb.w >> sh) & 0x0F0F0F0Fu};
         const int a1 = dot16(nb, d1b, dot16(na, d1a, 0));
-        const int a2 = dot16(nb, d2b, dot16(na, d2a, 0));
-        I[t] = 254 * a1 + a2;
+        const int a2 = dot16u(nb, d2b, dot16u(na, d2a, 0));
+        I[t] = 256 * a1 + a2;
         // one sub-block's digit reads at a time: hoisting all of them costs ~64 VGPRs and
         // occupancy.  The sched_barrier alone does not hold: the compiler sinks the
         // arithmetic below later reads; the empty asm with the sub-block's result as an
@@ -333,8 +336,8 @@ __device__ __forceinline__ float q6k_dot(const RawH &r, int hf, int c, const XLd
         const int4 d1a = *(const int4 *)(X.d1 + oa), d1b = *(const int4 *)(X.d1 + ob);
         const int4 d2a = *(const int4 *)(X.d2 + oa), d2b = *(const int4 *)(X.d2 + ob);
         const uint32_t qa[4] = {q[0], q[1], q[2], q[3]}, qb[4] = {q[4], q[5], q[6], q[7]};
-        const int i0 = 254 * dot16(qa, d1a, 0) + dot16(qa, d2a, 0);
-        const int i1 = 254 * dot16(qb, d1b, 0) + dot16(qb, d2b, 0);
+        const int i0 = 256 * dot16(qa, d1a, 0) + dot16u(qa, d2a, 0);
+        const int i1 = 256 * dot16(qb, d1b, 0) + dot16u(qb, d2b, 0);
         // scale bytes 8hf + 2g, 8hf + 2g + 1 (the 16-value groups of group g)
         const uint32_t sw = hf ? (g < 2 ? r.h.z : r.h.w) : (g < 2 ? r.h.x : r.h.y);
         const int sc0 = (int8_t)(sw >> (16 * (g & 1)));
