@@ -1,6 +1,6 @@
 """GPU parity of the decode GEMV family against the CPU oracle (fp64 of fp32-dequantised
-weights).  Bar: relative L2 <= 1e-3; the int8-digit x encoding is
-expected to land near 1e-5, which is also recorded."""
+weights).  Bar: relative L2 <= 1e-3; the 16-bit x encoding (two
+bytes per value) is expected to land near 1e-5, which is also recorded."""
 import numpy as np
 import pytest
 import torch
@@ -196,8 +196,8 @@ def test_repeat_calls_are_deterministic(gpu):
 
 
 # ---------------------------------------------------------------- adversarial x
-# x is carried as two int8 digits per 32-value block scaled by the block's max |x|
-# (step max|x| / 32258), so a block that mixes one huge value with small ones quantises the
+# x is carried as a 16-bit integer (two bytes) per value, scaled per 32-value block by the
+# block's max |x| (step max|x| / 32767), so a block that mixes one huge value with small ones quantises the
 # small ones coarsely.  These inputs stress that encoding; the bar stays relative L2 1e-3
 # against the fp64 oracle of the reference's fp32-x product (kernels.cu:124-135).
 def _adversarial_x(kind: str, n: int, rng) -> np.ndarray:
