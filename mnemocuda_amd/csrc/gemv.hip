@@ -551,7 +551,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs &args, uint8_t *smem) {
     const GemvMat M = pass_mat(args, bc, row0);
     Pass<UPL> ps;
     load_pass<LPR, UPL, TM>(M, row0, bc, bpr, ps);
+    // the x image gates every wave of the workgroup at the barrier, while a wave's dot
+    // products gate only its own rows: the image is built at raised wave priority, so a
+    // SIMD shared with other workgroups' dot products finishes it first (~0.4 us of the
+    // fused QKV launch)
+    __builtin_amdgcn_s_setprio(3);
     const float oscale = finish_x<XPT, XM>(xr, xr2, args.n_cols, kp, X, args.eps);
+    __builtin_amdgcn_s_setprio(0);
     if (base < args.total_rows) finish_pass<LPR, UPL, TM>(M, bpr, ps, X, oscale);
     if (args.experts && args.ex.nm == 2 && blockIdx.x == 0) {
         // clear the tile counters of the down launch that follows on the stream
