@@ -280,3 +280,53 @@ def test_qkv_rmsnorm_adversarial_x(gpu, oracle, kind):
                                *outs, 8192, 512, cols)
     for (w, _), t, o, r in zip(ws, types, outs, rows):
         assert rel_l2(host(o), oracle.gemv(t, w, xn, r, cols)) < TOL
+
+
+# ---------------------------------------------------------------- x encoding, value by value
+def _diag_q4k(n: int) -> np.ndarray:
+    """Q4_K matrix n x n with W[r][r] = 15 and every other weight 0: d = 1, dmin = 0, all
+    (sc, m) = (1, 0); the nibble of value v in its block sits in qs[32(v//64) + v%32], low
+    half for v%64 < 32 (kernels.cu:114-136)."""
+    bpr = n // 256
+    blk = np.zeros((n, bpr, 144), dtype=np.uint8)
+    blk[:, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), dtype=np.uint8)
+    # packed scales: sub-blocks 0-3 sc in bytes 0-3 (m in 4-7), 4-7 in the nibbles of 8-11
+    blk[:, :, 4:8] = 1
+    blk[:, :, 12:16] = 1
+    for r in range(n):
+        b, v = divmod(r, 256)
+        byte = 16 + 32 * (v // 64) + v % 32
+        blk[r, b, byte] = 0x0F if v % 64 < 32 else 0xF0
+    return blk.reshape(-1)
+
+
+def test_x_encoding_value_by_value(gpu, oracle):
+    """Each output of the one-hot diagonal Q4_K matrix is 15 * (x as the kernel encodes it),
+    so every value of x is checked against the encoding's bound |xhat - x| <= u/2,
+    u = amax/32767 of its 32-value block, at the byte boundaries of the 16-bit integer
+    (q = +-1, +-255, +-256, -257, +-32767, 0) and for random values."""
+    n = 4096
+    rng = np.random.default_rng(11)
+    W = _diag_q4k(n)
+    # the matrix is what the oracle decodes: 15 on the diagonal
+    dense = oracle.dequant(12, W, n, n)
+    assert np.array_equal(np.diag(dense), np.full(n, 15.0)) and np.count_nonzero(dense) == n
+    del dense
+    x = np.zeros(n, dtype=np.float32)
+    qs = [32767, -32767, 255, 256, -256, -257, 1, -1, 0, 127, 128, -128, -129, 16383, -16384]
+    for blk in range(n // 32):
+        amax = np.float32(10.0 ** rng.uniform(-3, 3))
+        vals = rng.uniform(-1, 1, 32).astype(np.float32) * amax
+        vals[0] = amax if blk % 2 else -amax
+        for i, q in enumerate(qs):
+            vals[1 + i] = np.float32(amax * (q / 32767.0))
+        x[32 * blk: 32 * blk + 32] = vals
+    y = torch.zeros(n, device="cuda")
+    case("matvec_q4k one-hot diagonal, x at the encoding's byte boundaries")
+    gpu.ops.matvec_q4k(dev(W), dev(x), y, n, n)
+    xhat = host(y).astype(np.float64) / 15.0
+    amax = np.abs(x.reshape(-1, 32)).max(axis=1).repeat(32).astype(np.float64)
+    bound = 0.5 * amax / 32767.0 * (1 + 1e-5) + 1e-7 * np.abs(x)
+    err = np.abs(xhat - x.astype(np.float64))
+    worst = int(np.argmax(err / bound))
+    assert (err <= bound).all(), f"x[{worst}]={x[worst]!r} decoded {xhat[worst]!r}, bound {bound[worst]:.3e}"
