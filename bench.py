@@ -382,7 +382,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the hot path "
-              "shards by weight rows / experts with no exchange, see DESIGN.md", file=sys.stderr)
+              "would shard by weight rows and experts with no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
     r = gpu_bench(args)
     if args.copy_calibration:
@@ -414,7 +414,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "i8 dot4 (q4/q6 weights x int8 digits of x), fp32 rescale and accumulate",
-        "data": "synthetic (seeded GGUF Q4_K/Q6_K blocks with the BASELINE distributions, generated in HBM)",
+        "data": "synthetic (seeded GGUF Q4_K/Q6_K blocks with the benchmark configs' value distributions, generated in HBM)",
         "config": {"workload": "configs[1]: Qwen3-235B attention projections, decode batch=1, hidden 4096, "
                                "94 layers per step (Q 4096->8192 Q4_K + K Q4_K + V Q6_K 4096->512 in one "
                                "launch, O 8192->4096 Q4_K + residual), hipGraph replay",

@@ -14,7 +14,7 @@
 //
 // Build: hipcc -O3 -std=c++17 --offload-arch=gfx950 -Xclang -target-feature -Xclang -packed-fp32-ops
 //        -I mnemocuda_amd/csrc mnemocuda_amd/probes/gemm_int8.hip -o gemm_int8
-// Prints, for M = 8192 weight rows, K = 4096, N = 512 tokens (BASELINE's prefill GEMM; one
+// Prints, for M = 8192 weight rows, K = 4096, N = 512 tokens (the benchmark's prefill GEMM; one
 // K split in both kernels): the time per launch of both kernels (HIP events, 40 launches
 // over 8 copies of the weights) and the relative L2 difference between their outputs.
 #include "gemm.hip"

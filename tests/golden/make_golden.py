@@ -5,7 +5,7 @@ The reference ships no golden vectors or kernel known-answer tests for this path
 tests/ hold engine, heat-map and server tests only), so these fixtures are produced by
 the C oracle (oracle/mnemo_oracle.c) and cross-checked here against the independent
 numpy restatement (oracle/oracle_np.py) before they are written; they then pin both
-restatements against regressions.  Inputs use the BASELINE value distributions.
+restatements against regressions.  Inputs use the benchmark configs' value distributions.
 
 Run:  python tests/golden/make_golden.py
 """

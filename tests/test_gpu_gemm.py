@@ -3,7 +3,7 @@
 Reference value: the product gemm_q4k.cu:103-112, 164-166 computes (mo_gemm_q8_1: exact
 integer sub-block sums scaled by d*sc*d8, minus dmin*m*ds for Q4_K).  Contract bar: relative
 L2 <= 1e-3 (north_star).  The kernel sums each sub-block exactly and rescales in fp32, so the
-tests hold it to 1e-5.  Small shapes against the fp64 C oracle; the BASELINE shapes against
+tests hold it to 1e-5.  Small shapes against the fp64 C oracle; the benchmark shapes against
 the fp64 torch restatement (tests/torch_ref.py, pinned against the oracle on the CPU) plus
 size-independent properties."""
 import numpy as np

@@ -1,5 +1,5 @@
 """GPU parity of the decode GEMV family against the CPU oracle (fp64 of fp32-dequantised
-weights).  Bar (BASELINE north star): relative L2 <= 1e-3; the 16-bit x encoding (two
+weights).  Bar (the north-star contract): relative L2 <= 1e-3; the 16-bit x encoding (two
 bytes per value) is expected to land near 1e-5, which is also recorded."""
 import numpy as np
 import pytest

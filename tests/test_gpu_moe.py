@@ -3,7 +3,7 @@
 Reference for the added delta out - out0: the reference's expert chain applied token by token
 (src/forward.c:876-893 per expert, src/forward.c:1783-1830 per token) in the Q8_1 GEMM
 semantics -- Oracle.moe_prefill (fp64, C) at test sizes and its torch restatement
-(tests/torch_ref.py, fp64 on the GPU, pinned against the oracle on the CPU) at the BASELINE
+(tests/torch_ref.py, fp64 on the GPU, pinned against the oracle on the CPU) at the benchmark
 cfg5 shape.  Bar: relative L2 <= 1e-3 (north_star).  The GEMMs sum every sub-block exactly,
 so the remaining difference is the SwiGLU's exp rounding moving a requantized value by one
 step now and then (measured ~1e-6); a wrong expert, slot or weight is an O(1) error.
@@ -82,7 +82,7 @@ def test_moe_prefill_vs_oracle(gpu, oracle, T, H, EFF, E, k, down_type, skew):
     x = rng.standard_normal((T, H)).astype(np.float32)
     if down_type == 12:
         # a Q4_K down projection takes its min term from the Q8_1 ds field (d8 * sum of the
-        # SwiGLU values, an f16): with the BASELINE weight distribution and x ~ N(0, 1) the
+        # SwiGLU values, an f16): with the benchmark weight distribution and x ~ N(0, 1) the
         # SwiGLU values reach ~1e3 and ds overflows to inf, in the reference's formula as here
         x *= np.float32(0.05)
     out0 = rng.standard_normal((T, H)).astype(np.float32)

@@ -1,4 +1,4 @@
-"""Pins tests/torch_ref.py (the GPU-side restatement used at full BASELINE sizes) against the
+"""Pins tests/torch_ref.py (the GPU-side restatement used at the benchmark's full sizes) against the
 C oracle on the CPU."""
 import numpy as np
 import pytest
