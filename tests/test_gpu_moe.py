@@ -177,7 +177,8 @@ def _routable(rng, E, H, k):
 
 
 @pytest.mark.parametrize("H,EFF,E,k,DT", [(512, 256, 16, 4, 14), (1024, 512, 8, 8, 12), (4096, 1536, 24, 8, 14),
-                                        (1024, 768, 24, 12, 14), (2048, 2560, 16, 6, 12), (4608, 512, 8, 4, 14)])
+                                        (1024, 768, 24, 12, 14), (2048, 2560, 16, 6, 12), (4608, 512, 8, 4, 14),
+                                        (256, 256, 1024, 16, 14), (256, 256, 1, 1, 12)])
 def test_moe_decode_vs_oracle(gpu, oracle, H, EFF, E, k, DT):
     rng = np.random.default_rng(H + E * k)
     table = synth.expert_table(rng, E, H, EFF, DT)
