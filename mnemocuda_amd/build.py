@@ -34,6 +34,12 @@ HIPCC_FLAGS = [
 ]
 
 
+# per-source flags: the router's count-in atomic is issued by one lane before the row's
+# loads; LLVM's atomic optimizer would rewrite it into a wave-wide form that reads the
+# result back at once, waiting for the round trip before the loads go out
+SOURCE_FLAGS = {"router.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]}
+
+
 def _run(cmd: list[str]) -> None:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -53,7 +59,7 @@ def build(jobs: int = 4) -> Path:
     cmds: list[list[str]] = []
     for src in HIP_SOURCES:
         obj = BUILD / (Path(src).stem + ".hip.o")
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([hipcc, *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(obj)
     # the GEMV kernels, once per workgroup size (gemv_launch.hip picks per launch)
     for threads in (512, 256):

@@ -158,12 +158,13 @@ int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k,
 // Arrival without fences (an agent-scope release/acquire pair writes back and invalidates
 // the XCDs' L2s, ~2.5 us a launch): the counter is 64 bits, the launch number in the high
 // half and the arrivals of this launch in the low half.  Each workgroup counts in with a
-// relaxed fetch-add, which hands it the launch number g, and then stores its logit as one
-// 64-bit atomic slot {g + 1, logit bits}.  The workgroup that sees n - 1 earlier arrivals
-// is the last; it moves the counter on to {g + 1, 0} (every workgroup of the launch has
-// counted in, and the next launch on the stream starts after this one ends) and reads
-// each slot until it carries the tag g + 1 -- a store that the fetch-add order says was
-// issued, so the wait ends without any ordering between the two locations.  A zero-filled
+// relaxed fetch-add as it starts, which hands it the launch number g, and stores its logit
+// as one 64-bit atomic slot {g + 1, logit bits} when it has it.  The workgroup that sees
+// n - 1 earlier arrivals ranks the logits: it moves the counter on to {g + 1, 0} (every
+// workgroup of the launch has counted in, and the next launch on the stream starts after
+// this one ends) and reads each slot until it carries the tag g + 1.  Every workgroup that
+// counted in is running and stores its slot, so the wait ends, without any ordering
+// between the two locations.  A zero-filled
 // counter and slots are a valid start (tag 0 never matches g + 1 before 2^32 launches).
 // With nw, x is first RMS-normalised (x * rsqrt(mean(x^2) + eps) * nw, the reference's
 // rms_norm_kernel, kernels.cu:692-722) inside every workgroup: each holds all of x.
@@ -225,11 +226,14 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     __shared__ int sel_i[kTopkMaxK];
     const int tid = threadIdx.x;
     const int row = blockIdx.x;
+    // count in before the row's dot product, so that the atomic's round trip overlaps the
+    // row's loads
+    unsigned long long old = 0;
+    if (tid == 0) old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float v = block_sum(nw ? row_dot_norm(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
                                  : row_dot(w + (size_t)row * n_cols, x, n_cols, vec4),
                               part);
     if (tid == 0) {
-        const unsigned long long old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned int g1 = (unsigned int)(old >> 32) + 1u;
         __hip_atomic_store(slots + row, ((unsigned long long)g1 << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
