@@ -7,7 +7,8 @@
 // whole sequence.  Here:
 //  * one wave per (KV head, 64-position chunk): the gqa (<= 16) query heads that share the
 //    KV head are the 16 rows of v_mfma_f32_16x16x32_f16, so K and V are read once per
-//    chunk, and the chunks of a long sequence spread over the whole chip;
+//    chunk, and the chunks of a long sequence spread over the whole chip (the chunk's
+//    workgroup has more waves, which only prepare the query heads);
 //  * S = Q K^T: K fragments come straight from the cache (8 consecutive dims per lane);
 //    Q is split into f16 hi + lo parts (two MFMAs) so the product keeps ~fp32 precision;
 //  * softmax over the chunk in registers (16-lane row reductions), P split hi + lo;
@@ -99,13 +100,19 @@ __device__ __forceinline__ float store_new_row(float x0, float x1, void *cache, 
 // the same values head_pass_kernel would have written, formed in registers: every chunk
 // prepares its query heads itself, the chunk holding *pos_dev stores the new K / V rows
 // and uses them in place of what it loaded from the cache.
+// Workgroups of kChunkWaves waves: all of them prepare kRows / kChunkWaves query heads each
+// (the per-head norm and RoPE are serial wave work), then wave 0 alone runs the chunk.
+constexpr int kChunkWaves = 8;
+constexpr int kChunkThreads = 64 * kChunkWaves;
+constexpr int kPrepHeads = kRows / kChunkWaves;
 template <int KV, int VL, bool PREP>
-__global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
+__global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArgs a) {
     __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
     __shared__ __align__(16) _Float16 vt[VL == kVRows ? kChunk : 1][kHd + 8];  // V tile [pos][dim]
     __shared__ __align__(16) _Float16 ps[2][kRows][kChunk + 8];
     __shared__ __align__(16) uint8_t knew[PREP ? 2 : 1][PREP ? 2 * kHd : 1];  // new K, V rows as stored
-    const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x;
+    const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pos = *a.pos_dev;
     const int seq = min(pos + 1, a.max_ctx);
     const int p0 = chunk * kChunk;
@@ -117,13 +124,13 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
 
     // ---- PREP: the new token's raw rows, loaded before the cache so that waiting for them
     // does not wait for the cache
-    float qx0[PREP ? kRows : 1], qx1[PREP ? kRows : 1];
+    float qx0[PREP ? kPrepHeads : 1], qx1[PREP ? kPrepHeads : 1];
     float k0 = 0.0f, k1 = 0.0f, v0 = 0.0f, v1 = 0.0f, qw0 = 1.0f, qw1 = 1.0f, kw0 = 1.0f, kw1 = 1.0f, fr = 0.0f;
     const bool norm = PREP && a.qw != nullptr;  // uniform
     if (PREP) {
 #pragma unroll
-        for (int h = 0; h < kRows; h++) {
-            const float *qh = a.q + (size_t)(kvh * G + min(h, G - 1)) * kHd;
+        for (int h = 0; h < kPrepHeads; h++) {
+            const float *qh = a.q + (size_t)(kvh * G + min(kPrepHeads * wave + h, G - 1)) * kHd;
             qx0[h] = qh[lane];
             qx1[h] = qh[lane + kHd / 2];
         }
@@ -145,6 +152,9 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     constexpr int EB = KV == kKvF16 ? 2 : 1;  // bytes per cache element
     const uint8_t *kc = (const uint8_t *)a.kc, *vc = (const uint8_t *)a.vc;
     uint4 kr[16];  // f16: 8 halves; int8: 8 bytes in .x/.y
+    uint4 vr[16];
+    float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, vsc = 1.0f;
+    if (wave == 0) {  // the chunk's wave
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int p = min(p0 + 16 * t + r, seq - 1);
@@ -160,7 +170,6 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
     // 16n + r, positions 32kk + 8kg .. +7 of this chunk (rows past the sequence are read as
     // stored and weighted by P = 0, so the cache must hold finite values there; the caller
     // zero-fills the blocked cache once)
-    uint4 vr[16];
 #pragma unroll
     for (int u = 0; u < 16; u++) {
         size_t off;
@@ -175,10 +184,10 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
         if (KV == kKvF16) __builtin_memcpy(&vr[u], vc + off, 16);
         else __builtin_memcpy(&vr[u], vc + off, 8);
     }
-    float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, vsc = 1.0f;
     if (KV == kKvInt8) {
 #pragma unroll
         for (int t = 0; t < 4; t++) ksc[t] = a.ksc[(size_t)min(p0 + 16 * t + r, seq - 1) * a.nkv + kvh];
+    }
     }
 
     // ---- Q rows (heads kvh*G .. +G-1) as f16 hi + lo
@@ -187,8 +196,9 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
         float sn, cs;
         sincosf((float)pos * fr, &sn, &cs);
 #pragma unroll
-        for (int h = 0; h < kRows; h++) {
-            float x0 = qx0[h], x1 = qx1[h];
+        for (int j = 0; j < kPrepHeads; j++) {
+            const int h = kPrepHeads * wave + j;
+            float x0 = qx0[j], x1 = qx1[j];
             prep_head(x0, x1, norm, qw0, qw1, a.eps, cs, sn);
             if (h >= G) x0 = x1 = 0.0f;
             const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
@@ -197,14 +207,14 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
             qs[1][h][lane] = (_Float16)(x0 - (float)h0);
             qs[1][h][lane + kHd / 2] = (_Float16)(x1 - (float)h1);
         }
-        if (mine) {
+        if (mine && wave == 0) {
             prep_head(k0, k1, norm, kw0, kw1, a.eps, cs, sn);
             const size_t si = (size_t)pos * a.nkv + kvh;
             new_ksc = store_new_row<KV>(k0, k1, a.kcw, a.kscw, si * kHd, 1, si, knew[0]);
             const size_t vb = VL == kVBlocked ? (((size_t)(pos / 64) * a.nkv + kvh) * kHd) * 64 + pos % 64 : si * kHd;
             new_vsc = store_new_row<KV>(v0, v1, a.vcw, a.vscw, vb, VL == kVBlocked ? 64 : 1, si, knew[1]);
         }
-    } else for (int e = lane; e < kRows * kHd / 4; e += 64) {
+    } else for (int e = threadIdx.x; e < kRows * kHd / 4; e += kChunkThreads) {
         const int h = e / (kHd / 4), d = 4 * (e % (kHd / 4));
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (h < G) v = *(const float4 *)(a.q + (size_t)(kvh * G + h) * kHd + d);
@@ -219,6 +229,10 @@ __global__ void __launch_bounds__(64) attn_chunk_kernel(AttnDecodeArgs a) {
         __builtin_memcpy(&qs[1][h][d], lo, 8);
     }
     __syncthreads();
+    if (wave != 0) {  // the Q rows are in LDS: the rest is wave 0's (it meets one more barrier)
+        __syncthreads();
+        return;
+    }
     if (mine) {
         // the loaded cache rows at pos are stale: take the new K / V rows from LDS (also
         // where a position past pos was clamped to pos)
@@ -464,12 +478,12 @@ static int launch_decode(const AttnDecodeArgs &a, int kv_type, hipStream_t s) {
     const dim3 grid(a.max_chunks, a.nkv);
     if (kv_type == kKvF16) {
         if (a.v_layout == kVBlocked)
-            hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVBlocked, PREP>), grid, dim3(64), 0, s, a);
-        else hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVRows, PREP>), grid, dim3(64), 0, s, a);
+            hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVBlocked, PREP>), grid, dim3(kChunkThreads), 0, s, a);
+        else hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVRows, PREP>), grid, dim3(kChunkThreads), 0, s, a);
     } else {
         if (a.v_layout == kVBlocked)
-            hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVBlocked, PREP>), grid, dim3(64), 0, s, a);
-        else hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVRows, PREP>), grid, dim3(64), 0, s, a);
+            hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVBlocked, PREP>), grid, dim3(kChunkThreads), 0, s, a);
+        else hipLaunchKernelGGL((attn_chunk_kernel<kKvInt8, kVRows, PREP>), grid, dim3(kChunkThreads), 0, s, a);
     }
     hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, kHd / kCombDims), dim3(kCombThreads), 0, s, a);
     return check_launch("attention_decode");
