@@ -5,10 +5,10 @@
 // positions 0..*pos_dev of the cache [pos][n_kv_heads][head_dim].  The reference runs one
 // block per query head, so each KV head is streamed gqa times and one block walks the
 // whole sequence.  Here:
-//  * one wave per (KV head, 64-position chunk): the gqa (<= 16) query heads that share the
-//    KV head are the 16 rows of v_mfma_f32_16x16x32_f16, so K and V are read once per
-//    chunk, and the chunks of a long sequence spread over the whole chip (the chunk's
-//    workgroup has more waves, which only prepare the query heads);
+//  * one workgroup per (KV head, 64-position chunk): the gqa (<= 16) query heads that share
+//    the KV head are the 16 rows of v_mfma_f32_16x16x32_f16, so K and V are read once per
+//    chunk, and the chunks of a long sequence spread over the whole chip; the workgroup's
+//    waves split the chunk by position tiles (S) and by dims (O);
 //  * S = Q K^T: K fragments come straight from the cache (8 consecutive dims per lane);
 //    Q is split into f16 hi + lo parts (two MFMAs) so the product keeps ~fp32 precision;
 //  * softmax over the chunk in registers (16-lane row reductions), P split hi + lo;
@@ -100,17 +100,24 @@ __device__ __forceinline__ float store_new_row(float x0, float x1, void *cache, 
 // the same values head_pass_kernel would have written, formed in registers: every chunk
 // prepares its query heads itself, the chunk holding *pos_dev stores the new K / V rows
 // and uses them in place of what it loaded from the cache.
-// Workgroups of kChunkWaves waves: all of them prepare kRows / kChunkWaves query heads each
-// (the per-head norm and RoPE are serial wave work), then wave 0 alone runs the chunk.
+//
+// A chunk's workgroup has 8 waves.  All of them prepare 2 of the 16 query heads (the
+// per-head norm and RoPE are serial wave work).  Waves 0-3 then own one 16-position tile
+// each: its K fragments, its column of S = Q K^T and its share of the softmax; waves 4-7
+// own 32 of the 128 dims each: their V fragments and their columns of O = P V.  The waves
+// meet through LDS: the Q rows, the tiles' row maxima and sums, P.
 constexpr int kChunkWaves = 8;
 constexpr int kChunkThreads = 64 * kChunkWaves;
 constexpr int kPrepHeads = kRows / kChunkWaves;
+constexpr int kTiles = kChunk / 16;  // position tiles = S waves
 template <int KV, int VL, bool PREP>
 __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArgs a) {
     __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
     __shared__ __align__(16) _Float16 vt[VL == kVRows ? kChunk : 1][kHd + 8];  // V tile [pos][dim]
     __shared__ __align__(16) _Float16 ps[2][kRows][kChunk + 8];
     __shared__ __align__(16) uint8_t knew[PREP ? 2 : 1][PREP ? 2 * kHd : 1];  // new K, V rows as stored
+    __shared__ float tmax[kTiles][kRows], tsum[kTiles][kRows];
+    __shared__ float new_sc[2];  // int8 scales of the new K / V rows
     const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pos = *a.pos_dev;
@@ -121,6 +128,10 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
     const size_t stride = (size_t)a.nkv * kHd;
     const int r = lane & 15, kg = lane >> 4;
     const bool mine = PREP && pos < a.max_ctx && pos / kChunk == chunk;  // uniform
+    const bool swave = wave < kTiles;        // S wave: position tile t
+    const int t = wave & (kTiles - 1);
+    const int nv = wave - kTiles;            // O wave: dims 32 nv .. 32 nv + 31 (n-tiles 2nv, 2nv+1)
+    constexpr int EB = KV == kKvF16 ? 2 : 1;  // bytes per cache element
 
     // ---- PREP: the new token's raw rows, loaded before the cache so that waiting for them
     // does not wait for the cache
@@ -148,50 +159,54 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
         fr = a.freq[lane];
     }
 
-    // ---- loads first: K fragments (4 tiles of 16 positions x 4 steps of 32 dims) and the V tile
-    constexpr int EB = KV == kKvF16 ? 2 : 1;  // bytes per cache element
+    // ---- loads first.  S waves: the K fragments of tile t (4 steps of 32 dims; lane: position
+    // p0 + 16t + r, dims 32s + 8kg .. +7) and, for int8, the positions' K and V scales.
     const uint8_t *kc = (const uint8_t *)a.kc, *vc = (const uint8_t *)a.vc;
-    uint4 kr[16];  // f16: 8 halves; int8: 8 bytes in .x/.y
-    uint4 vr[16];
-    float ksc[4] = {1.0f, 1.0f, 1.0f, 1.0f}, vsc = 1.0f;
-    if (wave == 0) {  // the chunk's wave
+    const int pt = min(p0 + 16 * t + r, seq - 1);  // this lane's position in tile t (clamped)
+    uint4 kr[4];  // f16: 8 halves; int8: 8 bytes in .x/.y
+    float ksc = 1.0f, vsc = 1.0f;
+    if (swave) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int p = min(p0 + 16 * t + r, seq - 1);
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
-            const size_t off = ((size_t)p * stride + (size_t)kvh * kHd + 32 * s + 8 * kg) * EB;
-            if (KV == kKvF16) __builtin_memcpy(&kr[4 * t + s], kc + off, 16);
-            else __builtin_memcpy(&kr[4 * t + s], kc + off, 8);
+        for (int st = 0; st < 4; st++) {
+            const size_t off = ((size_t)pt * stride + (size_t)kvh * kHd + 32 * st + 8 * kg) * EB;
+            if (KV == kKvF16) __builtin_memcpy(&kr[st], kc + off, 16);
+            else __builtin_memcpy(&kr[st], kc + off, 8);
+        }
+        if (KV == kKvInt8) {
+            ksc = a.ksc[(size_t)pt * a.nkv + kvh];
+            vsc = a.vsc[(size_t)pt * a.nkv + kvh];
         }
     }
-    // V: rows layout -- 16-element chunk c = lane + 64u of the tile (position c / 16, dims
-    // 8 (c % 16)); blocked layout -- the O = P V fragments themselves: u = 2n + kk holds dim
-    // 16n + r, positions 32kk + 8kg .. +7 of this chunk (rows past the sequence are read as
-    // stored and weighted by P = 0, so the cache must hold finite values there; the caller
-    // zero-fills the blocked cache once)
+    // V.  Blocked layout (O waves): the O = P V fragments themselves, u = 2j + kk holds dim
+    // 16(2nv + j) + r, positions 32kk + 8kg .. +7 of this chunk (rows past the sequence are
+    // read as stored and weighted by P = 0, so the cache must hold finite values there; the
+    // caller zero-fills the blocked cache once).  Rows layout (every wave): 16-element pieces
+    // c = lane + 64u, u = 2 wave + i, of the tile (position c / 16, dims 8 (c % 16)), staged
+    // through LDS.
+    uint4 vr[4];
+    if (VL == kVBlocked) {
+        if (!swave) {
 #pragma unroll
-    for (int u = 0; u < 16; u++) {
-        size_t off;
-        if (VL == kVRows) {
-            const int c = lane + 64 * u;
+            for (int u = 0; u < 4; u++) {
+                const int n = 2 * nv + (u >> 1), kk = u & 1;
+                const size_t off =
+                    ((((size_t)chunk * a.nkv + kvh) * kHd + 16 * n + r) * kChunk + 32 * kk + 8 * kg) * EB;
+                if (KV == kKvF16) __builtin_memcpy(&vr[u], vc + off, 16);
+                else __builtin_memcpy(&vr[u], vc + off, 8);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = lane + 64 * (2 * wave + i);
             const int p = min(p0 + (c >> 4), seq - 1);
-            off = ((size_t)p * stride + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
-        } else {
-            const int n = u >> 1, kk = u & 1;
-            off = ((((size_t)chunk * a.nkv + kvh) * kHd + 16 * n + r) * kChunk + 32 * kk + 8 * kg) * EB;
+            const size_t off = ((size_t)p * stride + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
+            if (KV == kKvF16) __builtin_memcpy(&vr[i], vc + off, 16);
+            else __builtin_memcpy(&vr[i], vc + off, 8);
         }
-        if (KV == kKvF16) __builtin_memcpy(&vr[u], vc + off, 16);
-        else __builtin_memcpy(&vr[u], vc + off, 8);
-    }
-    if (KV == kKvInt8) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) ksc[t] = a.ksc[(size_t)min(p0 + 16 * t + r, seq - 1) * a.nkv + kvh];
-    }
     }
 
     // ---- Q rows (heads kvh*G .. +G-1) as f16 hi + lo
-    float new_ksc = 1.0f, new_vsc = 1.0f;
     if (PREP) {
         float sn, cs;
         sincosf((float)pos * fr, &sn, &cs);
@@ -210,9 +225,13 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
         if (mine && wave == 0) {
             prep_head(k0, k1, norm, kw0, kw1, a.eps, cs, sn);
             const size_t si = (size_t)pos * a.nkv + kvh;
-            new_ksc = store_new_row<KV>(k0, k1, a.kcw, a.kscw, si * kHd, 1, si, knew[0]);
+            const float nk = store_new_row<KV>(k0, k1, a.kcw, a.kscw, si * kHd, 1, si, knew[0]);
             const size_t vb = VL == kVBlocked ? (((size_t)(pos / 64) * a.nkv + kvh) * kHd) * 64 + pos % 64 : si * kHd;
-            new_vsc = store_new_row<KV>(v0, v1, a.vcw, a.vscw, vb, VL == kVBlocked ? 64 : 1, si, knew[1]);
+            const float nvs = store_new_row<KV>(v0, v1, a.vcw, a.vscw, vb, VL == kVBlocked ? 64 : 1, si, knew[1]);
+            if (lane == 0) {
+                new_sc[0] = nk;
+                new_sc[1] = nvs;
+            }
         }
     } else for (int e = threadIdx.x; e < kRows * kHd / 4; e += kChunkThreads) {
         const int h = e / (kHd / 4), d = 4 * (e % (kHd / 4));
@@ -228,161 +247,143 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
         __builtin_memcpy(&qs[0][h][d], hi, 8);
         __builtin_memcpy(&qs[1][h][d], lo, 8);
     }
-    __syncthreads();
-    if (wave != 0) {  // the Q rows are in LDS: the rest is wave 0's (it meets one more barrier)
-        __syncthreads();
-        return;
-    }
+    __syncthreads();  // 1: Q rows, the new K / V rows and their scales
     if (mine) {
-        // the loaded cache rows at pos are stale: take the new K / V rows from LDS (also
-        // where a position past pos was clamped to pos)
-        constexpr int EB = KV == kKvF16 ? 2 : 1;
+        // the loaded cache rows at pos are stale: take the new K / V rows from LDS (also where
+        // a position past pos was clamped to pos)
         const int o = pos - p0;
+        if (swave && 16 * t + r >= o) {
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            if (16 * t + r >= o) {
-#pragma unroll
-                for (int s = 0; s < 4; s++) __builtin_memcpy(&kr[4 * t + s], &knew[0][(32 * s + 8 * kg) * EB], 8 * EB);
-                ksc[t] = new_ksc;
-            }
+            for (int st = 0; st < 4; st++) __builtin_memcpy(&kr[st], &knew[0][(32 * st + 8 * kg) * EB], 8 * EB);
+            ksc = new_sc[0];
+            vsc = new_sc[1];
         }
         if (VL == kVRows) {
 #pragma unroll
-            for (int u = 0; u < 16; u++)
-                if (4 * u + (lane >> 4) >= o)  // position of the 16-element piece, clamped
-                    __builtin_memcpy(&vr[u], &knew[1][8 * (lane & 15) * EB], 8 * EB);
-        } else if (kg == ((o >> 3) & 3)) {
-            // vr[2n + kk] holds dim 16n + r at positions 32kk + 8kg .. +7
+            for (int i = 0; i < 2; i++)
+                if (4 * (2 * wave + i) + (lane >> 4) >= o)  // position of the 16-element piece, clamped
+                    __builtin_memcpy(&vr[i], &knew[1][8 * (lane & 15) * EB], 8 * EB);
+        } else if (!swave && kg == ((o >> 3) & 3)) {
 #pragma unroll
-            for (int n = 0; n < 8; n++) {
+            for (int u = 0; u < 4; u++) {
+                const int n = 2 * nv + (u >> 1), kk = u & 1;
+                if (kk != (o >> 5)) continue;
+                uint8_t *vb = (uint8_t *)&vr[u];
 #pragma unroll
-                for (int kk = 0; kk < 2; kk++) {
-                    if (kk != (o >> 5)) continue;
-                    uint8_t *vb = (uint8_t *)&vr[2 * n + kk];
-#pragma unroll
-                    for (int j = 0; j < 8; j++)
-                        if (j == (o & 7)) __builtin_memcpy(vb + j * EB, &knew[1][(16 * n + r) * EB], EB);
-                }
+                for (int j = 0; j < 8; j++)
+                    if (j == (o & 7)) __builtin_memcpy(vb + j * EB, &knew[1][(16 * n + r) * EB], EB);
             }
         }
     }
 
-    // ---- S = Q K^T for 4 tiles of 16 positions
-    f4 sc[4];
+    // ---- S waves: tile t of S = Q K^T (lane: heads 4kg + i, position p0 + 16t + r) and its
+    // row maxima
+    f4 sc = {0.f, 0.f, 0.f, 0.f};
+    if (swave) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        f4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; s++) {
+        for (int st = 0; st < 4; st++) {
             h8 b;
             if (KV == kKvF16) {
-                __builtin_memcpy(&b, &kr[4 * t + s], 16);
+                __builtin_memcpy(&b, &kr[st], 16);
             } else {
-                const int8_t *kb = (const int8_t *)&kr[4 * t + s];
+                const int8_t *kb = (const int8_t *)&kr[st];
 #pragma unroll
                 for (int j = 0; j < 8; j++) b[j] = (_Float16)kb[j];
             }
             h8 ah, al;
-            __builtin_memcpy(&ah, &qs[0][r][32 * s + 8 * kg], 16);
-            __builtin_memcpy(&al, &qs[1][r][32 * s + 8 * kg], 16);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, c, 0, 0, 0);
+            __builtin_memcpy(&ah, &qs[0][r][32 * st + 8 * kg], 16);
+            __builtin_memcpy(&al, &qs[1][r][32 * st + 8 * kg], 16);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, sc, 0, 0, 0);
         }
-        sc[t] = c;
-    }
-    // lane holds heads 4kg + i, position p0 + 16t + r
-    float m[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const bool ok = p0 + 16 * t + r < seq;
-            const float s = ok ? sc[t][i] * (a.scale * ksc[t]) : -INFINITY;
-            sc[t][i] = s;
-            mx = fmaxf(mx, s);
-        }
-        m[i] = max16(mx);  // every row has position p0 < seq, so m is finite
-        float sum = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const float e = expf(sc[t][i] - m[i]);  // exp(-inf) = 0 for masked positions
-            sc[t][i] = e;
-            sum += e;
-        }
-        l[i] = sum16(sum);
-    }
-    // ---- P (times the V scale for int8) to LDS as hi + lo, V tile to LDS
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        if (KV == kKvInt8) {
-            const int p = min(p0 + 16 * t + r, seq - 1);
-            vsc = mine && p == pos ? new_vsc : a.vsc[(size_t)p * a.nkv + kvh];
-        }
+        const bool ok = p0 + 16 * t + r < seq;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float pv = sc[t][i] * vsc;
+            sc[i] = ok ? sc[i] * (a.scale * ksc) : -INFINITY;
+            const float mx = max16(sc[i]);
+            if (r == 0) tmax[t][4 * kg + i] = mx;
+        }
+    }
+    __syncthreads();  // 2: the tiles' row maxima
+    if (swave) {
+        // P = exp(S - m) (times the V scale for int8) to LDS as hi + lo; the tile's row sums
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = 4 * kg + i;
+            float m = tmax[0][h];
+#pragma unroll
+            for (int u = 1; u < kTiles; u++) m = fmaxf(m, tmax[u][h]);  // finite: position p0 < seq
+            const float e = expf(sc[i] - m);  // exp(-inf) = 0 for masked positions
+            const float sum = sum16(e);
+            if (r == 0) tsum[t][h] = sum;
+            const float pv = e * vsc;
             const _Float16 hi = (_Float16)pv;
-            ps[0][4 * kg + i][16 * t + r] = hi;
-            ps[1][4 * kg + i][16 * t + r] = (_Float16)(pv - (float)hi);
+            ps[0][h][16 * t + r] = hi;
+            ps[1][h][16 * t + r] = (_Float16)(pv - (float)hi);
         }
     }
     if (VL == kVRows) {
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int c = lane + 64 * u;
+        for (int i = 0; i < 2; i++) {
+            const int c = lane + 64 * (2 * wave + i);
             h8 v;
             if (KV == kKvF16) {
-                __builtin_memcpy(&v, &vr[u], 16);
+                __builtin_memcpy(&v, &vr[i], 16);
             } else {
-                const int8_t *vb = (const int8_t *)&vr[u];
+                const int8_t *vb = (const int8_t *)&vr[i];
 #pragma unroll
                 for (int j = 0; j < 8; j++) v[j] = (_Float16)vb[j];
             }
             __builtin_memcpy(&vt[c >> 4][8 * (c & 15)], &v, 16);
         }
     }
-    __syncthreads();
+    __syncthreads();  // 3: P, the row sums and (rows layout) the V tile
 
-    // ---- O = P V: 8 tiles of 16 dims, 2 steps of 32 positions
-    f4 o[8];
+    float *part = a.ws + ((size_t)kvh * a.max_chunks + chunk) * kPart;
+    if (swave) {
+        // partial m and l: the 16 heads' maxima and sums over the tiles, in tile order
+        if (wave == 0 && lane < kRows) {
+            float m = tmax[0][lane], l = tsum[0][lane];
 #pragma unroll
-    for (int n = 0; n < 8; n++) o[n] = (f4){0.f, 0.f, 0.f, 0.f};
+            for (int u = 1; u < kTiles; u++) {
+                m = fmaxf(m, tmax[u][lane]);
+                l += tsum[u][lane];
+            }
+            part[lane] = m;
+            part[kRows + lane] = l;
+        }
+        return;
+    }
+    // ---- O waves: O = P V for n-tiles 2nv, 2nv + 1 (16 dims each), 2 steps of 32 positions
+    f4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int kk = 0; kk < 2; kk++) {
         h8 ah, al;
         __builtin_memcpy(&ah, &ps[0][r][32 * kk + 8 * kg], 16);
         __builtin_memcpy(&al, &ps[1][r][32 * kk + 8 * kg], 16);
 #pragma unroll
-        for (int n = 0; n < 8; n++) {
+        for (int j = 0; j < 2; j++) {
+            const int n = 2 * nv + j;
             h8 b;
             if (VL == kVRows) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) b[j] = vt[32 * kk + 8 * kg + j][16 * n + r];
+                for (int q = 0; q < 8; q++) b[q] = vt[32 * kk + 8 * kg + q][16 * n + r];
             } else if (KV == kKvF16) {
-                __builtin_memcpy(&b, &vr[2 * n + kk], 16);
+                __builtin_memcpy(&b, &vr[2 * j + kk], 16);
             } else {
-                const int8_t *vb = (const int8_t *)&vr[2 * n + kk];
+                const int8_t *vb = (const int8_t *)&vr[2 * j + kk];
 #pragma unroll
-                for (int j = 0; j < 8; j++) b[j] = (_Float16)vb[j];
+                for (int q = 0; q < 8; q++) b[q] = (_Float16)vb[q];
             }
-            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, o[n], 0, 0, 0);
-            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, o[n], 0, 0, 0);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, o[j], 0, 0, 0);
+            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, o[j], 0, 0, 0);
         }
     }
-    // ---- partial: m[16], l[16], o[16][128]
-    float *part = a.ws + ((size_t)kvh * a.max_chunks + chunk) * kPart;
-    if (r == 0) {
+    // ---- partial O[16][128]: this wave's 32 dims
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            part[4 * kg + i] = m[i];
-            part[kRows + 4 * kg + i] = l[i];
-        }
-    }
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-    for (int n = 0; n < 8; n++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * n + r] = o[n][i];
+        for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * (2 * nv + j) + r] = o[j][i];
 }
 
 // Merge of the chunks' (max, sum, O): grid (query head, quarter of head_dim), 256 threads =
