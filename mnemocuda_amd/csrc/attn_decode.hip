@@ -110,6 +110,8 @@ constexpr int kChunkWaves = 8;
 constexpr int kChunkThreads = 64 * kChunkWaves;
 constexpr int kPrepHeads = kRows / kChunkWaves;
 constexpr int kTiles = kChunk / 16;  // position tiles = S waves
+static_assert(kChunkWaves == 2 * kTiles && kHd == 32 * (kChunkWaves - kTiles) && kRows % kChunkWaves == 0,
+              "4 S waves (16 positions each), 4 O waves (32 dims each), whole query heads per wave");
 template <int KV, int VL, bool PREP>
 __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArgs a) {
     __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
