@@ -288,7 +288,8 @@ def attention_bench(stream, lengths=(1024, 4096, 16384, 32768)):
     """Decode attention for one layer (64 query heads, 4 KV heads, head_dim 128, f16 cache)
     at several sequence lengths: the GQA-batched split kernel with V in the blocked layout
     (the decode path) and in the reference's row layout, and the reference-form entry point
-    (one workgroup per query head), graph-timed over 20 launches."""
+    cuda_attention_f16kv (host sequence length, the reference's caches), graph-timed over 20
+    launches."""
     import torch
     from mnemocuda_amd import ops
     NH, NKV, HD = 64, 4, 128
@@ -306,7 +307,7 @@ def attention_bench(stream, lengths=(1024, 4096, 16384, 32768)):
         ref = time_launches(lambda i: ops.attention(q, kc, vc, o, NH, HD, NKV, L, 0.088), 20, stream)
         kv = 2 * L * NKV * HD * 2
         out[str(L)] = {"gqa_split_us": round(fast * 1e6, 2), "gqa_split_rowsV_us": round(rows * 1e6, 2),
-                       "per_head_us": round(ref * 1e6, 2), "gqa_split_kv_GBps": round(kv / fast / 1e9, 1)}
+                       "entry_point_us": round(ref * 1e6, 2), "gqa_split_kv_GBps": round(kv / fast / 1e9, 1)}
         del kc, vc
     return out
 

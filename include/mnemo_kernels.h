@@ -248,7 +248,12 @@ void cuda_f32_to_int8_kv_dual(const float *k, const float *v, void *out_k, void 
                               hipStream_t stream);
 /* kernels.cu:1662-1673 (:1550-1660) and :1536-1546 (:1382-1481): softmax(scale q.k) v over
  * positions 0..seq_len-1 of the cache [pos][n_kv_heads][head_dim] for every query head
- * (kv head = head / gqa_ratio).  head_dim 64, 128 or 256. */
+ * (kv head = head / gqa_ratio).  head_dim 64, 128 or 256.  With head_dim 128, gqa <= 16 and
+ * seq_len <= 65536 the call runs the split-chunk kernels of mnemo_attention_decode (two
+ * launches, capture-safe) on a 64 MiB workspace that cuda_kernels_init allocates per GPU;
+ * that workspace belongs to the first stream that uses it, and calls from other streams (or
+ * without cuda_kernels_init, or longer than the workspace holds) run the per-head kernel.
+ * The two paths agree to ~1e-6 relative (not bit for bit). */
 void cuda_attention_f16kv(const void *q, const void *kv_k, const void *kv_v, float *out,
                           int n_heads_q, int head_dim, int n_kv_heads, int seq_len, int gqa_ratio,
                           float scale, hipStream_t stream);

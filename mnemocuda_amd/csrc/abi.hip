@@ -121,6 +121,7 @@ void cuda_kernels_init(void) {
         return;
     }
     moe_decode_scratch_init();  // this device's copy of the no-allocation decode scratch
+    attn_rows_ws_init();        // partials of the split-chunk path of cuda_attention_*
 }
 
 void cuda_matvec_q4k(const void *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s) {
@@ -351,6 +352,9 @@ void cuda_f32_to_int8_kv_dual(const float *k, const float *v, void *out_k, void 
 
 void cuda_attention_f16kv(const void *q, const void *kv_k, const void *kv_v, float *out, int n_heads_q, int head_dim,
                           int n_kv_heads, int seq_len, int gqa_ratio, float scale, hipStream_t s) {
+    if (launch_attention_rows((const float *)q, kv_k, kv_v, nullptr, nullptr, kKvF16, out, n_heads_q, head_dim,
+                              n_kv_heads, gqa_ratio, seq_len, scale, s) != kErrBadArg)
+        return;
     AttnArgs a = {};
     a.q = (const float *)q;
     a.kc = kv_k;
@@ -368,6 +372,10 @@ void cuda_attention_f16kv(const void *q, const void *kv_k, const void *kv_v, flo
 void cuda_attention_int8kv(const float *q, const void *kv_k, const void *kv_v, const float *k_scales,
                            const float *v_scales, float *out, int n_heads_q, int head_dim, int n_kv_heads,
                            int seq_len, int gqa_ratio, float scale, hipStream_t s) {
+    if (k_scales && v_scales &&
+        launch_attention_rows(q, kv_k, kv_v, k_scales, v_scales, kKvInt8, out, n_heads_q, head_dim, n_kv_heads,
+                              gqa_ratio, seq_len, scale, s) != kErrBadArg)
+        return;
     AttnArgs a = {};
     a.q = q;
     a.kc = kv_k;

@@ -20,6 +20,8 @@
 // the score column, the V scale is folded into P.
 #include <math.h>
 
+#include <mutex>
+
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
 
@@ -122,7 +124,7 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
     __shared__ float new_sc[2];  // int8 scales of the new K / V rows
     const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int pos = *a.pos_dev;
+    const int pos = a.pos_dev ? *a.pos_dev : a.seq_fixed - 1;
     const int seq = min(pos + 1, a.max_ctx);
     const int p0 = chunk * kChunk;
     if (p0 >= seq) return;  // the combine reads ceil(seq / 64) chunks only
@@ -405,7 +407,7 @@ __global__ void __launch_bounds__(kCombThreads) attn_combine_kernel(AttnDecodeAr
     __shared__ float part_o[kCombThreads];
     const int h = blockIdx.x, tid = threadIdx.x;
     const int kvh = h / a.gqa, hh = h % a.gqa;
-    const int seq = min(*a.pos_dev + 1, a.max_ctx);
+    const int seq = min((a.pos_dev ? *a.pos_dev : a.seq_fixed - 1) + 1, a.max_ctx);
     const int nc = (seq + kChunk - 1) / kChunk;
     const float *base = a.ws + (size_t)kvh * a.max_chunks * kPart;
     const int dl = tid % kCombDims, g = tid / kCombDims;
@@ -458,7 +460,7 @@ __global__ void __launch_bounds__(kCombThreads) attn_combine_kernel(AttnDecodeAr
 }
 
 static int check_decode_args(AttnDecodeArgs &a, int kv_type) {
-    if (!a.q || !a.kc || !a.vc || !a.out || !a.pos_dev || !a.ws)
+    if (!a.q || !a.kc || !a.vc || !a.out || (!a.pos_dev && a.seq_fixed <= 0) || !a.ws)
         return set_error(kErrBadArg, "attention_decode: NULL pointer");
     if (a.hd != kHd) return set_error(kErrBadArg, "attention_decode: head_dim %d (this kernel: %d)", a.hd, kHd);
     if (a.nkv <= 0 || a.gqa <= 0 || a.gqa > kRows || a.nh != a.nkv * a.gqa)
@@ -508,6 +510,76 @@ int launch_attention_decode_prep(AttnDecodeArgs a, int kv_type, float theta, hip
     // the frequencies of head_pass_kernel's RoPE, computed the same way
     for (int j = 0; j < kHd / 2; j++) a.freq[j] = 1.0f / powf(theta, (float)(2 * j) / (float)kHd);
     return launch_decode<true>(a, kv_type, s);
+}
+
+// ------------------------------------------------------------------ the reference's entry points
+// cuda_attention_f16kv / _int8kv (the reference's caches: K and V rows [pos][n_kv][hd], the
+// sequence length a host value) run on the split-chunk kernels above when head_dim is 128 and
+// gqa <= 16, with the partials in a workspace the library allocates at cuda_kernels_init
+// (kRowsWsBytes per GPU, outside any graph capture).  The workspace belongs to the first
+// stream that uses it on a GPU; calls from other streams, or larger than the workspace, take
+// the per-head kernel (attn.hip), so calls on different streams never share it.
+constexpr size_t kRowsWsBytes = (size_t)64 << 20;
+constexpr int kMaxRowsDevices = 64;
+static float *g_rows_ws[kMaxRowsDevices];
+static hipStream_t g_rows_owner[kMaxRowsDevices];
+static bool g_rows_owned[kMaxRowsDevices];
+static std::mutex g_rows_mu;
+
+int attn_rows_ws_init() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxRowsDevices) return kErrLaunch;
+    std::lock_guard<std::mutex> lock(g_rows_mu);
+    if (g_rows_ws[dev]) return kOk;
+    void *p = nullptr;
+    if (hipMalloc(&p, kRowsWsBytes) != hipSuccess) {
+        (void)hipGetLastError();  // the per-head kernel stays the path on this GPU
+        return kErrLaunch;
+    }
+    g_rows_ws[dev] = (float *)p;
+    return kOk;
+}
+
+// Returns kErrBadArg without recording an error when the split kernels do not apply.
+int launch_attention_rows(const float *q, const void *kc, const void *vc, const float *ksc, const float *vsc,
+                          int kv_type, float *out, int nh, int hd, int nkv, int gqa, int seq, float scale,
+                          hipStream_t s) {
+    if (hd != kHd || gqa <= 0 || gqa > kRows || nkv <= 0 || nh != nkv * gqa || seq <= 0 || seq > kMaxChunks * kChunk)
+        return kErrBadArg;
+    if (attn_decode_workspace_bytes(nkv, seq) > kRowsWsBytes) return kErrBadArg;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxRowsDevices) return kErrBadArg;
+    float *ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_rows_mu);
+        if (!g_rows_ws[dev]) return kErrBadArg;
+        if (!g_rows_owned[dev]) {
+            g_rows_owner[dev] = s;
+            g_rows_owned[dev] = true;
+        }
+        if (g_rows_owner[dev] != s) return kErrBadArg;
+        ws = g_rows_ws[dev];
+    }
+    AttnDecodeArgs a{};
+    a.q = q;
+    a.kc = kc;
+    a.vc = vc;
+    a.ksc = ksc;
+    a.vsc = vsc;
+    a.out = out;
+    a.ws = ws;
+    a.ws_bytes = kRowsWsBytes;
+    a.nh = nh;
+    a.hd = hd;
+    a.nkv = nkv;
+    a.gqa = gqa;
+    a.max_ctx = seq;
+    a.pos_dev = nullptr;
+    a.seq_fixed = seq;
+    a.scale = scale;
+    a.v_layout = kVRows;
+    if (int rc = check_decode_args(a, kv_type)) return rc;
+    return launch_decode<false>(a, kv_type, s);
 }
 
 }  // namespace mnemo

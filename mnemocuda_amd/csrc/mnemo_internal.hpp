@@ -143,6 +143,7 @@ struct AttnDecodeArgs {
     int nh, hd, nkv, gqa;
     int max_ctx, max_chunks;
     const int *pos_dev;  // sequence length = min(*pos_dev + 1, max_ctx)
+    int seq_fixed;       // with pos_dev NULL: the sequence length (a host value)
     float scale;
     int v_layout;        // 0: V rows [pos][n_kv][hd]; 1: blocked [pos/64][n_kv][hd][pos%64]
     // the new token's preparation inside the launch (launch_attention_decode_prep): q is
@@ -156,6 +157,10 @@ struct AttnDecodeArgs {
 };
 size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx);
 int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s);
+int attn_rows_ws_init();
+int launch_attention_rows(const float *q, const void *kc, const void *vc, const float *ksc, const float *vsc,
+                          int kv_type, float *out, int nh, int hd, int nkv, int gqa, int seq, float scale,
+                          hipStream_t s);
 int launch_attention_decode_prep(AttnDecodeArgs a, int kv_type, float theta, hipStream_t s);
 
 int launch_embedding(const void *table, int type, const int *tok_dev, int tok, int n_vocab, float *out, int hidden,

@@ -170,12 +170,13 @@ def test_attn_prep_and_dev_attention(gpu, oracle, rng, kind):
         wvq, wvs = oracle.kv_quant_int8(v, HD)
         assert np.array_equal(ck[pos], wkq) and np.array_equal(host(tks).reshape(ctx, -1)[pos], wks)
         assert np.array_equal(cv[pos], wvq) and np.array_equal(host(tvs).reshape(ctx, -1)[pos], wvs)
-    # attention over 0..pos with the length read on the device = the entry point with seq = pos + 1
+    # attention over 0..pos with the length read on the device (the per-head kernel) against the
+    # entry point with seq = pos + 1 (the split-chunk kernels at head_dim 128): both ~fp32
     out = torch.empty(NH * HD, device="cuda")
     out2 = torch.empty(NH * HD, device="cuda")
     gpu.ops.attention_dev(tq, tkc, tvc, out, NH, HD, NKV, pos_dev, 1 / np.sqrt(HD), tks, tvs)
     gpu.ops.attention(tq, tkc, tvc, out2, NH, HD, NKV, pos + 1, 1 / np.sqrt(HD), tks, tvs)
-    assert torch.equal(out, out2)
+    assert rel_l2(host(out2), host(out)) < 1e-5
     if kind == "f16":
         kk, vv = host(tkc).view(np.uint16), host(tvc).view(np.uint16)
         want = oracle.attention(gq, kk, vv, NH, HD, NKV, pos + 1, 1 / np.sqrt(HD))
