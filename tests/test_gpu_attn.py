@@ -486,3 +486,24 @@ def test_attention_decode_prep_bad_args(gpu):
     with pytest.raises(gpu.MnemoError):  # int8 caches without scales
         kc8 = torch.zeros(64 * NKV * HD, dtype=torch.int8, device="cuda")
         gpu.ops.attention_decode_prep(q, k, k, None, None, 1e-6, 1e6, kc8, kc8, out, NH, HD, NKV, 64, pos, 0.1, ws)
+
+
+@pytest.mark.parametrize("kind", ["f16", "int8"])
+def test_attention_entry_point_paths(gpu, oracle, rng, kind):
+    """cuda_attention_* runs the split-chunk kernels on the stream that owns the library's
+    workspace and the per-head kernel elsewhere (another stream, or a sequence longer than
+    65,536 positions): every path matches the oracle."""
+    nh, hd, nkv, scale = NH, 128, NKV, 1.0 / np.sqrt(128)
+    for seq, streams in [(3000, ("current", "side")), (66000, ("current",))]:
+        q = rng.standard_normal(nh * hd).astype(np.float32)
+        kc, vc, ks, vs = _caches(rng, seq, nkv, hd, kind)
+        want = oracle.attention(q, kc, vc, nh, hd, nkv, seq, scale, ks, vs)
+        tkc, tvc, tks, tvs = _to_dev(kc), _to_dev(vc), _to_dev(ks), _to_dev(vs)
+        for which in streams:
+            s = torch.cuda.current_stream() if which == "current" else torch.cuda.Stream()
+            out = torch.full((nh * hd,), np.nan, device="cuda")
+            case(f"attention entry point {kind} seq={seq} stream={which}")
+            with torch.cuda.stream(s):
+                gpu.ops.attention(dev(q), tkc, tvc, out, nh, hd, nkv, seq, scale, tks, tvs)
+            torch.cuda.synchronize()
+            assert rel_l2(host(out), want) < 1e-5, (seq, which)
