@@ -37,69 +37,178 @@ __device__ __forceinline__ bool before(float pa, int ia, float pb, int ib) {
     return pa > pb || (pa == pb && ia < ib);
 }
 
-// Top-p draw from the 2048 candidates (cp[] = p, ci[] = token id; p < 0 marks an empty slot)
-// with total = the sum of all p: bitonic sort by (p desc, id asc), running sums, nucleus,
-// draw.  All kSampleThreads threads call this; cs (2048 floats) and red (2 ints) are LDS
-// scratch.
-__device__ void select_candidates(float *cp, int *ci, float *cs, int *red_i, float total, float top_p,
-                                  unsigned long long seed, int *__restrict__ out) {
-    const int tid = threadIdx.x;
-    __syncthreads();
-    // bitonic sort of the candidates by (p desc, id asc)
-    for (int k = 2; k <= kCands; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = tid; t < kCands / 2; t += kSampleThreads) {
-                const int a = ((t & ~(j - 1)) << 1) | (t & (j - 1)), b = a + j;  // j is a power of two
-                const bool up = (a & k) == 0;
-                const float pa = cp[a], pb = cp[b];
-                const int ia = ci[a], ib = ci[b];
-                if (before(pa, ia, pb, ib) != up) {
-                    cp[a] = pb;
-                    cp[b] = pa;
-                    ci[a] = ib;
-                    ci[b] = ia;
+// ------------------------------------------------------------------ top-p selection
+// The 2048 candidates are sorted by (p desc, id asc) on 256 threads, 8 per thread: thread t
+// holds sorted positions 8t .. 8t+7 in registers.  A candidate's order is that of one 64-bit
+// key, {p bits, ~id} (p >= 0 orders like its bits); an empty slot (p < 0, NaN) is key 0 and
+// sorts last.  Bitonic network: strides below 8 inside a thread, 8 .. 256 between the lanes
+// of a wave (DPP up to 64, permutes at 128 and 256), 512 and 1024 through LDS.  Then the running sums (inclusive, in
+// sorted order: sequential within a thread, a scan over the threads), the nucleus and the
+// draw.
+constexpr int kSelThreads = kCands / 8;  // 256
+constexpr int kSelWaves = kSelThreads / 64;
+
+__device__ __forceinline__ uint64_t cand_key(float p, int id) {
+    if (!(p >= 0.0f)) return 0ull;
+    return ((uint64_t)__float_as_uint(fabsf(p)) << 32) | (uint32_t)~(uint32_t)id;
+}
+
+// keep the better (larger key) of a and b in a when `better_here`, the other one otherwise
+__device__ __forceinline__ uint64_t keep(uint64_t a, uint64_t b, bool better_here) {
+    const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+    return better_here ? hi : lo;
+}
+
+// v of lane ^ M: DPP within rows of 16 lanes (quad permutes; row rotations, where lane i
+// reads lane (i - n) mod 16), a cross-lane permute beyond
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor1, 0xF, 0xF, false);
+    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor2, 0xF, 0xF, false);
+    else if constexpr (M == 4) {
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false);  // i - 4
+        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x12C, 0xF, 0xF, false);  // i + 4
+        return (lane_id() & 4) ? dn : up;
+    } else if constexpr (M == 8) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);
+    else return (uint32_t)__shfl_xor((int)v, M);
+}
+
+// a bitonic pass between lanes t and t ^ M (strides 8M): every key's partner first, then
+// the choices (one wait for the exchanged values, not one per key)
+template <int M>
+__device__ __forceinline__ void lane_pass(uint64_t (&k)[8], bool better_here) {
+    uint64_t o[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+        o[r] = ((uint64_t)xor_lane<M>((uint32_t)(k[r] >> 32)) << 32) | xor_lane<M>((uint32_t)k[r]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < 8; r++) k[r] = keep(k[r], o[r], better_here);
+}
+
+// a bitonic pass of stride J < 8: pairs inside the thread's 8 keys (sorted positions 8t + r)
+template <int J>
+__device__ __forceinline__ void reg_pass(uint64_t (&k)[8], int t, int kk) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        if (r & J) continue;
+        const bool up = ((8 * t + r) & kk) == 0;
+        const uint64_t a = k[r], b = k[r | J];
+        k[r] = keep(a, b, up);
+        k[r | J] = keep(a, b, !up);
+    }
+}
+
+struct SelLds {
+    uint64_t xch[kCands];
+    float wsum[kSelWaves];
+    int wmin[2][kSelWaves];
+    float cs_last;
+};
+
+// Every thread of the NT-thread workgroup calls this (it holds barriers); threads
+// t < kSelThreads hold candidates 8t .. 8t+7 in k (any order).  total = the sum of all p.
+template <int NT>
+__device__ void select_sorted(uint64_t (&k)[8], float total, float top_p, unsigned long long seed, SelLds &L,
+                              int *__restrict__ out) {
+    static_assert(NT % 64 == 0 && NT >= kSelThreads, "the selection needs 256 threads");
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const bool act = t < kSelThreads;
+    // bitonic sort, best first: at level kk the pair (e, e ^ j), e < e ^ j, puts the better
+    // key at e when (e & kk) == 0
+    for (int kk = 2; kk <= kCands; kk <<= 1) {
+        for (int j = kk >> 1; j >= 8; j >>= 1) {
+            const int m = j >> 3;  // partner thread t ^ m
+            const bool up = ((8 * t) & kk) == 0, lower = (t & m) == 0;
+            if (j < 512) {  // partner in the same wave (m is uniform)
+                const bool b = up == lower;
+                switch (m) {
+                case 1: lane_pass<1>(k, b); break;
+                case 2: lane_pass<2>(k, b); break;
+                case 4: lane_pass<4>(k, b); break;
+                case 8: lane_pass<8>(k, b); break;
+                case 16: lane_pass<16>(k, b); break;
+                default: lane_pass<32>(k, b); break;
                 }
+            } else {
+                if (act)
+#pragma unroll
+                    for (int r = 0; r < 8; r++) L.xch[8 * t + r] = k[r];
+                __syncthreads();
+                if (act)
+#pragma unroll
+                    for (int r = 0; r < 8; r++) k[r] = keep(k[r], L.xch[8 * (t ^ m) + r], up == lower);
+                __syncthreads();
             }
-            __syncthreads();
         }
+        // strides 4, 2, 1 inside the thread
+        if (kk > 4) reg_pass<4>(k, t, kk);
+        if (kk > 2) reg_pass<2>(k, t, kk);
+        reg_pass<1>(k, t, kk);
     }
-    // inclusive running sums of the positive p (Hillis-Steele, two elements per thread)
-    for (int t = tid; t < kCands; t += kSampleThreads) cs[t] = fmaxf(cp[t], 0.0f);
+    // inclusive running sums of the positive p in sorted order
+    float p[8], c[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) p[r] = act ? __uint_as_float((uint32_t)(k[r] >> 32)) : 0.0f;
+    c[0] = p[0];
+#pragma unroll
+    for (int r = 1; r < 8; r++) c[r] = c[r - 1] + p[r];
+    float s = c[7];  // inclusive scan of the thread totals over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float v = __shfl_up(s, o);
+        if (lane >= o) s += v;
+    }
+    float excl = __shfl_up(s, 1);
+    if (lane == 0) excl = 0.0f;
+    if (act && lane == 63) L.wsum[w] = s;
     __syncthreads();
-    for (int off = 1; off < kCands; off <<= 1) {
-        float v[2];
+    float off = 0.0f;
+    for (int i = 0; i < w && i < kSelWaves; i++) off += L.wsum[i];
+    const float pre = off + excl;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int t = tid + q * kSampleThreads;
-            v[q] = cs[t] + (t >= off ? cs[t - off] : 0.0f);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < 2; q++) cs[tid + q * kSampleThreads] = v[q];
-        __syncthreads();
-    }
-    // nucleus size n: 1 + the first position whose running sum reaches top_p * total, or
-    // the number of positive candidates
-    uint64_t s0 = seed, s1 = seed ^ 0xDEADBEEFCAFEBABEull;
-    for (int w = 0; w < 3; w++) xoro_next(s0, s1);
-    const float r = (float)(xoro_next(s0, s1) >> 11) * (1.0f / 9007199254740992.0f);
+    for (int r = 0; r < 8; r++) c[r] = pre + c[r];
+    // nucleus size n: 1 + the first position whose running sum reaches top_p * total, the
+    // position of the first candidate with p <= 0, or all of them
     const float mass = top_p * total;
-    if (tid == 0) {
-        red_i[0] = kCands;
-        red_i[1] = 0x7FFFFFFF;
+    int nc = kCands;
+#pragma unroll
+    for (int r = 7; r >= 0; r--)
+        if (act && (p[r] <= 0.0f || c[r] >= mass)) nc = p[r] <= 0.0f ? 8 * t + r : 8 * t + r + 1;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) nc = min(nc, __shfl_xor(nc, o));
+    if (act && lane == 0) L.wmin[0][w] = nc;
+    __syncthreads();
+    int n = kCands;
+    for (int i = 0; i < kSelWaves; i++) n = min(n, L.wmin[0][i]);
+    if (act && n > 0 && t == (n - 1) >> 3) {
+        float v = c[0];
+#pragma unroll
+        for (int r = 1; r < 8; r++) v = r == ((n - 1) & 7) ? c[r] : v;
+        L.cs_last = v;
     }
     __syncthreads();
-    for (int t = tid; t < kCands; t += kSampleThreads)
-        if (cp[t] <= 0.0f || cs[t] >= mass) atomicMin(&red_i[0], cp[t] <= 0.0f ? t : t + 1);
+    uint64_t s0 = seed, s1 = seed ^ 0xDEADBEEFCAFEBABEull;
+    for (int i = 0; i < 3; i++) xoro_next(s0, s1);
+    const float u = (float)(xoro_next(s0, s1) >> 11) * (1.0f / 9007199254740992.0f);
+    const float target = u * (n > 0 ? L.cs_last : 0.0f);
+    // the draw: the first position below n whose running sum reaches the target
+    int pk = 0x7FFFFFFF;
+#pragma unroll
+    for (int r = 7; r >= 0; r--)
+        if (act && 8 * t + r < n && c[r] >= target) pk = 8 * t + r;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) pk = min(pk, __shfl_xor(pk, o));
+    if (act && lane == 0) L.wmin[1][w] = pk;
     __syncthreads();
-    const int n = red_i[0];
-    const float target = r * (n > 0 ? cs[n - 1] : 0.0f);
-    for (int t = tid; t < n; t += kSampleThreads)
-        if (cs[t] >= target) atomicMin(&red_i[1], t);
-    __syncthreads();
-    if (tid == 0) {
-        const int pick = red_i[1] == 0x7FFFFFFF ? 0 : red_i[1];
-        const int id = ci[pick];
+    int pick = 0x7FFFFFFF;
+    for (int i = 0; i < kSelWaves; i++) pick = min(pick, L.wmin[1][i]);
+    if (pick == 0x7FFFFFFF) pick = 0;
+    if (act && t == pick >> 3) {
+        uint64_t kv = k[0];
+#pragma unroll
+        for (int r = 1; r < 8; r++) kv = r == (pick & 7) ? k[r] : kv;
+        const int id = kv ? (int)~(uint32_t)kv : -1;
         *out = (id < 0 || id == 0x7FFFFFFF) ? 0 : id;
     }
 }
@@ -229,7 +338,11 @@ __global__ void __launch_bounds__(kSampleThreads) sample_token_kernel(const floa
     }
     const float total = red_f[0];
 
-    select_candidates(cp, ci, mp, red_i, total, top_p, seed, out);
+    __shared__ SelLds sel;
+    uint64_t key[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) key[r] = tid < kSelThreads ? cand_key(cp[8 * tid + r], ci[8 * tid + r]) : 0ull;
+    select_sorted<kSampleThreads>(key, total, top_p, seed, sel, out);
 }
 
 // ------------------------------------------------------------------ workspace form
@@ -361,13 +474,12 @@ __global__ void __launch_bounds__(kClsThreads) sample_classes_kernel(const float
     }
 }
 
-__global__ void __launch_bounds__(kSampleThreads) sample_finish_kernel(const SampleWs *__restrict__ ws,
-                                                                       float temperature, float top_p,
-                                                                       unsigned long long seed, int *__restrict__ out) {
-    __shared__ float cp[kCands];
-    __shared__ int ci[kCands];
-    __shared__ float cs[kCands];
-    __shared__ int red_i[2];
+__global__ void __launch_bounds__(kSelThreads) sample_finish_kernel(const SampleWs *__restrict__ ws,
+                                                                    float temperature, float top_p,
+                                                                    unsigned long long seed, int *__restrict__ out) {
+    __shared__ SelLds sel;
+    __shared__ float wv[kSelWaves];
+    __shared__ int wi[kSelWaves];
     __shared__ float tot;
     __shared__ float Ms;
     const int tid = threadIdx.x;
@@ -386,43 +498,43 @@ __global__ void __launch_bounds__(kSampleThreads) sample_finish_kernel(const Sam
     __syncthreads();
     const float M = Ms;
     if (temperature <= 0.0f) {  // argmax: the best class winner (ties to the lower id)
-        if (tid < kClasses) {  // thread c holds class c's first winner
-            float bv = ws->z[tid * kPerClass];
-            int bi = ws->id[tid * kPerClass];
+        static_assert(kClasses == kSelThreads, "thread c holds class c's first winner");
+        float bv = ws->z[tid * kPerClass];
+        int bi = ws->id[tid * kPerClass];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int oi = __shfl_xor(bi, o);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
             }
-            if ((tid & 63) == 0) {
-                cp[tid >> 6] = bv;
-                ci[tid >> 6] = bi;
-            }
+        }
+        if ((tid & 63) == 0) {
+            wv[tid >> 6] = bv;
+            wi[tid >> 6] = bi;
         }
         __syncthreads();
         if (tid == 0) {
-            float bv = cp[0];
-            int bi = ci[0];
-            for (int w = 1; w < kClasses / 64; w++)
-                if (cp[w] > bv || (cp[w] == bv && ci[w] < bi)) {
-                    bv = cp[w];
-                    bi = ci[w];
+            bv = wv[0];
+            bi = wi[0];
+            for (int w = 1; w < kSelWaves; w++)
+                if (wv[w] > bv || (wv[w] == bv && wi[w] < bi)) {
+                    bv = wv[w];
+                    bi = wi[w];
                 }
             *out = bi == 0x7FFFFFFF ? 0 : bi;
         }
         return;
     }
-    for (int t = tid; t < kCands; t += kSampleThreads) {
-        const int id = ws->id[t];
-        cp[t] = id == 0x7FFFFFFF ? -1.0f : expf((ws->z[t] - M) / temperature);
-        ci[t] = id;
+    // thread t: class t's 8 winners, p as the one-launch form computes it
+    uint64_t key[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const int id = ws->id[8 * tid + r];
+        key[r] = cand_key(id == 0x7FFFFFFF ? -1.0f : expf((ws->z[8 * tid + r] - M) / temperature), id);
     }
-    __syncthreads();
-    select_candidates(cp, ci, cs, red_i, tot, top_p, seed, out);
+    select_sorted<kSelThreads>(key, tot, top_p, seed, sel, out);
 }
 
 int launch_sample_token_ws(const float *logits, int V, float temperature, float top_p, unsigned long long seed,
@@ -436,8 +548,7 @@ int launch_sample_token_ws(const float *logits, int V, float temperature, float 
     SampleWs *w = (SampleWs *)ws;
     hipLaunchKernelGGL(sample_classes_kernel, dim3(kClsGroups), dim3(kClsThreads), 0, stream, logits, V,
                        temperature > 0.0f ? temperature : 1.0f, w);
-    hipLaunchKernelGGL(sample_finish_kernel, dim3(1), dim3(kSampleThreads), 0, stream, w, temperature, top_p, seed,
-                       out);
+    hipLaunchKernelGGL(sample_finish_kernel, dim3(1), dim3(kSelThreads), 0, stream, w, temperature, top_p, seed, out);
     return check_launch("sample_token_ws");
 }
 

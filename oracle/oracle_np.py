@@ -169,7 +169,7 @@ def sample_candidates(logits: np.ndarray, temperature: float):
     """The 2048 candidates of kernels.cu:2085-2104 as a set: for every residue class
     i mod 256, the 8 largest p with earlier indices winning ties (a scan that replaces its
     minimum only by a strictly larger value keeps exactly those).  Returns (p, ids) sorted
-    by p descending, p in fp64."""
+    by (p descending, id ascending), p in fp64."""
     z = logits.astype(np.float64)
     p = np.exp((z - z.max()) / temperature)
     V = p.size
@@ -182,7 +182,10 @@ def sample_candidates(logits: np.ndarray, temperature: float):
         ids.extend(idx[order].tolist())
         ps.extend(p[idx[order]].tolist())
     ids, ps = np.array(ids), np.array(ps)
-    o = np.argsort(-ps, kind="stable")
+    # equal p: the lower token id first.  (The reference's selection sort, kernels.cu:2145-2166,
+    # orders equal p by where its swaps left them in the class-slot array; both orders give
+    # the same running sums at every position, only the token drawn at a tie can differ.)
+    o = np.lexsort((ids, -ps))
     return ps[o], ids[o], p.sum()
 
 

@@ -93,6 +93,29 @@ def test_top_p_ws(gpu, oracle, V, scale, T, top_p, data):
     assert checked >= 16
 
 
+@pytest.mark.parametrize("V,step,T,top_p", [(151936, 0.5, 0.7, 0.9), (3000, 0.25, 1.0, 0.8)])
+def test_top_p_ties(gpu, V, step, T, top_p):
+    """logits on a coarse grid, so that most candidates share their p with others: both
+    forms take equal p in increasing token id and draw the token of the numpy restatement,
+    which orders them so.  (The reference orders equal p by where its selection sort's
+    swaps left them, kernels.cu:2145-2166 -- the C oracle follows that -- so at a tie the
+    token can differ from the reference's, while the running sums at every position agree.)"""
+    rng = np.random.default_rng(V + 7)
+    z = (np.round(rng.standard_normal(V) * 2.0 / step) * step).astype(np.float32)
+    seeds = rng.integers(0, 2**63, 32).tolist()
+    ws = torch.empty(gpu.ops.sample_workspace_bytes(), dtype=torch.uint8, device="cuda")
+    case(f"sample top-p ties V={V} step={step}")
+    checked = 0
+    for seed in seeds:
+        tok, margin = onp.sample_token(z, T, top_p, seed)
+        if margin < 1e-5:
+            continue
+        assert _gpu_sample(gpu, z, T, top_p, seed) == tok, seed
+        assert _gpu_sample_ws(gpu, z, T, top_p, seed, ws) == tok, seed
+        checked += 1
+    print(f"checked {checked} seeds")
+    assert checked >= 16
+
 def test_sample_ws_bad_args(gpu):
     case("sample_ws bad args")
     z = torch.zeros(300000, device="cuda")
