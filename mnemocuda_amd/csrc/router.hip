@@ -20,6 +20,7 @@ namespace mnemo {
 constexpr int kRowThreads = 1024;
 constexpr int kRowMaxV4 = 4;  // float4 per thread: n_cols <= 16384 on the vector path
 
+template <int T = kRowThreads, int V4 = kRowMaxV4>
 __device__ __forceinline__ float row_dot(const float *__restrict__ wr, const float *__restrict__ x, int n_cols,
                                          bool vec4) {
     typedef float fv4 __attribute__((ext_vector_type(4)));
@@ -29,35 +30,36 @@ __device__ __forceinline__ float row_dot(const float *__restrict__ wr, const flo
         const fv4 *w4 = (const fv4 *)wr;
         const fv4 *x4 = (const fv4 *)x;
         const int n4 = n_cols / 4;
-        fv4 a[kRowMaxV4], b[kRowMaxV4];
+        fv4 a[V4], b[V4];
 #pragma unroll
-        for (int i = 0; i < kRowMaxV4; i++) {
-            const int c = min(tid + i * kRowThreads, n4 - 1);  // clamped: branch-free loads
+        for (int i = 0; i < V4; i++) {
+            const int c = min(tid + i * T, n4 - 1);  // clamped: branch-free loads
             a[i] = __builtin_nontemporal_load(w4 + c);
             b[i] = x4[c];
         }
 #pragma unroll
-        for (int i = 0; i < kRowMaxV4; i++) {
+        for (int i = 0; i < V4; i++) {
             float t = fmaf(a[i].x, b[i].x, acc);
             t = fmaf(a[i].y, b[i].y, t);
             t = fmaf(a[i].z, b[i].z, t);
             t = fmaf(a[i].w, b[i].w, t);
-            acc = tid + i * kRowThreads < n4 ? t : acc;
+            acc = tid + i * T < n4 ? t : acc;
         }
     } else {
-        for (int c = tid; c < n_cols; c += kRowThreads) acc = fmaf(wr[c], x[c], acc);
+        for (int c = tid; c < n_cols; c += T) acc = fmaf(wr[c], x[c], acc);
     }
     return acc;
 }
 
-// Workgroup sum in a fixed order (wave sums, then wave 0 .. 15): deterministic.
+// Workgroup sum in a fixed order (wave sums, then wave 0, 1, ..): deterministic.
+template <int T = kRowThreads>
 __device__ __forceinline__ float block_sum(float v, float *part) {
     v = sum64_lane63(v);
     if (lane_id() == 63) part[threadIdx.x >> 6] = v;
     __syncthreads();
     float s = 0.0f;
     if (threadIdx.x == 0)
-        for (int i = 0; i < kRowThreads / 64; i++) s += part[i];
+        for (int i = 0; i < T / 64; i++) s += part[i];
     return s;
 }
 
@@ -168,40 +170,41 @@ int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k,
 // counter and slots are a valid start (tag 0 never matches g + 1 before 2^32 launches).
 // With nw, x is first RMS-normalised (x * rsqrt(mean(x^2) + eps) * nw, the reference's
 // rms_norm_kernel, kernels.cu:692-722) inside every workgroup: each holds all of x.
+template <int T, int V4>
 __device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, const float *__restrict__ x,
                                               const float *__restrict__ nw, int n_cols, float eps, float *part) {
     typedef float fv4 __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x;
     const fv4 *w4 = (const fv4 *)wr, *x4 = (const fv4 *)x, *n4w = (const fv4 *)nw;
     const int n4 = n_cols / 4;
-    fv4 a[kRowMaxV4], b[kRowMaxV4], c[kRowMaxV4];
+    fv4 a[V4], b[V4], c[V4];
 #pragma unroll
-    for (int i = 0; i < kRowMaxV4; i++) {
-        const int j = min(tid + i * kRowThreads, n4 - 1);
+    for (int i = 0; i < V4; i++) {
+        const int j = min(tid + i * T, n4 - 1);
         a[i] = __builtin_nontemporal_load(w4 + j);
         b[i] = x4[j];
         c[i] = n4w[j];
     }
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kRowMaxV4; i++)
-        if (tid + i * kRowThreads < n4) ss += b[i].x * b[i].x + b[i].y * b[i].y + b[i].z * b[i].z + b[i].w * b[i].w;
+    for (int i = 0; i < V4; i++)
+        if (tid + i * T < n4) ss += b[i].x * b[i].x + b[i].y * b[i].y + b[i].z * b[i].z + b[i].w * b[i].w;
     ss = sum64_lane63(ss);
     if (lane_id() == 63) part[tid >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kRowThreads / 64; i++) tot += part[i];
+    for (int i = 0; i < T / 64; i++) tot += part[i];
     __syncthreads();  // part[] is reused by block_sum
     const float scale = __builtin_amdgcn_rsqf(tot / (float)n_cols + eps);  // rsqrtf, as the reference (kernels.cu:718)
     float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kRowMaxV4; i++) {
+    for (int i = 0; i < V4; i++) {
         float t = fmaf(a[i].x, b[i].x * scale * c[i].x, acc);
         t = fmaf(a[i].y, b[i].y * scale * c[i].y, t);
         t = fmaf(a[i].z, b[i].z * scale * c[i].z, t);
         t = fmaf(a[i].w, b[i].w * scale * c[i].w, t);
-        acc = tid + i * kRowThreads < n4 ? t : acc;
+        acc = tid + i * T < n4 ? t : acc;
     }
     return acc;
 }
@@ -211,17 +214,23 @@ __device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, cons
 // guarantees that no wave spins for ever
 constexpr int kRouterSlotWait = 1 << 22;
 
-__global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *__restrict__ w,
-                                                                 const float *__restrict__ x,
-                                                                 const float *__restrict__ nw, float eps,
-                                                                 unsigned long long *__restrict__ slots, int n,
-                                                                 int n_cols, int k,
-                                                                 unsigned long long *__restrict__ cnt,
-                                                                 int *__restrict__ idx, float *__restrict__ wts,
-                                                                 int vec4) {
-    __shared__ float part[kRowThreads / 64];
+// One workgroup of kRouterThreads per row (fewer waves than kRowThreads: the row's loads are
+// as many, and the barriers before the logit is ready shorter).
+constexpr int kRouterThreads = 512;
+
+template <int T, int V4>
+__global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict__ w, const float *__restrict__ x,
+                                                        const float *__restrict__ nw, float eps,
+                                                        unsigned long long *__restrict__ slots, int n, int n_cols,
+                                                        int k, unsigned long long *__restrict__ cnt,
+                                                        int *__restrict__ idx, float *__restrict__ wts, int vec4) {
+    __shared__ float part[T / 64];
     __shared__ unsigned int is_last, tag;
     __shared__ float z[64 * kTopkMaxPerLane];
+    // rank keys: {order-preserving bits of the logit, ~index} -- a larger key is a better
+    // logit, equal logits the lower index (as `better`); 0 for a logit that never wins
+    __shared__ __align__(16) unsigned long long zk[64 * kTopkMaxPerLane];
+    static_assert((64 * kTopkMaxPerLane) % 16 == 0, "whole 16-key blocks");
     __shared__ float sel_v[kTopkMaxK];
     __shared__ int sel_i[kTopkMaxK];
     const int tid = threadIdx.x;
@@ -230,9 +239,9 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     // row's loads
     unsigned long long old = 0;
     if (tid == 0) old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float v = block_sum(nw ? row_dot_norm(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
-                                 : row_dot(w + (size_t)row * n_cols, x, n_cols, vec4),
-                              part);
+    const float v = block_sum<T>(nw ? row_dot_norm<T, V4>(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
+                                    : row_dot<T, V4>(w + (size_t)row * n_cols, x, n_cols, vec4),
+                                 part);
     if (tid == 0) {
         const unsigned int g1 = (unsigned int)(old >> 32) + 1u;
         __hip_atomic_store(slots + row, ((unsigned long long)g1 << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
@@ -246,63 +255,92 @@ __global__ void __launch_bounds__(kRowThreads) router_topk_kernel(const float *_
     __syncthreads();
     if (!is_last) return;
     const unsigned int g1 = tag;
-    for (int i = tid; i < n; i += kRowThreads) {
-        unsigned long long sv = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int t = 0; (unsigned int)(sv >> 32) != g1 && t < kRouterSlotWait; t++) {
-            __builtin_amdgcn_s_sleep(1);
-            sv = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int n16 = (n + 15) & ~15;
+    for (int i = tid; i < n16; i += T) {
+        unsigned long long key = 0;
+        if (i < n) {
+            unsigned long long sv = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int t = 0; (unsigned int)(sv >> 32) != g1 && t < kRouterSlotWait; t++) {
+                __builtin_amdgcn_s_sleep(1);
+                sv = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            const float l = __uint_as_float((unsigned int)sv);
+            const bool ok = l > -1e30f;  // NaN and <= -1e30 never win
+            z[i] = ok ? l : -1e30f;
+            const uint32_t bits = __float_as_uint(l + 0.0f);  // -0 as +0: they compare equal
+            const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+            key = ok ? ((unsigned long long)ord << 32) | (uint32_t)~(uint32_t)i : 0ull;
         }
-        const float l = __uint_as_float((unsigned int)sv);
-        z[i] = l > -1e30f ? l : -1e30f;  // NaN and <= -1e30 never win
+        zk[i] = key;
     }
     if (tid < k) sel_i[tid] = -1;
     __syncthreads();
-    // G threads per candidate (a power of two, within a wave) count the candidates ordered
-    // before it over a strided share of j; the counts meet in G-lane shuffle sums
+    // G threads per candidate (a power of two <= 64) count the keys above its own, each over
+    // its share of the blocks of 16 keys; the counts meet in G-lane sums
     int G = 1;
-    while (G < 64 && G * 2 * n <= kRowThreads) G *= 2;
+    while (G < 64 && G * 2 * n <= T && 16 * G < n) G *= 2;
     const int sub = tid & (G - 1);
-    for (int i = tid / G; i < n; i += kRowThreads / G) {
-        const float zi = z[i];
+    for (int i = tid / G; i < n; i += T / G) {
+        const unsigned long long ki = zk[i];
         int rank = 0;
-        for (int j = sub; j < n; j += G) {
-            const float zj = z[j];
-            rank += (zj > -1e30f) && better(zj, j, zi, i);
+        for (int j0 = 16 * sub; j0 < n; j0 += 16 * G) {
+            unsigned long long kb[16];
+#pragma unroll
+            for (int q = 0; q < 8; q++) *(ulonglong2 *)&kb[2 * q] = *(const ulonglong2 *)&zk[j0 + 2 * q];
+#pragma unroll
+            for (int u = 0; u < 16; u++) rank += kb[u] > ki;
         }
-        for (int o = 1; o < G; o <<= 1) rank += __shfl_xor(rank, o);
-        if (sub == 0 && zi > -1e30f && rank < k) {
-            sel_v[rank] = zi;
+        // the group's partial counts: DPP within 8 lanes (quad exchanges, then the half-row
+        // mirror pairs the two quads), lane permutes beyond
+        if (G >= 2) rank += __builtin_amdgcn_update_dpp(0, rank, kDppXor1, 0xF, 0xF, false);
+        if (G >= 4) rank += __builtin_amdgcn_update_dpp(0, rank, kDppXor2, 0xF, 0xF, false);
+        if (G >= 8) rank += __builtin_amdgcn_update_dpp(0, rank, kDppRowHalfMirror, 0xF, 0xF, false);
+        for (int o = 8; o < G; o <<= 1) rank += __shfl_xor(rank, o);
+        if (sub == 0 && ki != 0 && rank < k) {
+            sel_v[rank] = z[i];
             sel_i[rank] = i;
         }
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid < 64) {
+        // softmax over the winners: lane r takes winner r; the sum runs in rank order, as a
+        // sequential loop over the winners forms it
+        static_assert(kTopkMaxK <= 64, "one winner per lane");
+        const int r = tid;
         const float mx = sel_v[0];
-        float e[kTopkMaxK], sum = 0.0f;
-        for (int r = 0; r < k; r++) {
-            e[r] = sel_i[r] >= 0 ? expf(sel_v[r] - mx) : 0.0f;
-            sum += e[r];
-        }
-        for (int r = 0; r < k; r++) {
+        const float e = r < k && sel_i[r] >= 0 ? expf(sel_v[r] - mx) : 0.0f;
+        float sum = 0.0f;
+        for (int q = 0; q < k; q++)
+            sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), q));
+        if (r < k) {
             idx[r] = sel_i[r];
-            wts[r] = sum > 0.0f ? e[r] / sum : 0.0f;
+            wts[r] = sum > 0.0f ? e / sum : 0.0f;
         }
     }
 }
 
 int launch_router_topk(const float *w, const float *x, const float *nw, float eps, unsigned long long *slots, int n,
                        int n_cols, int k, unsigned long long *cnt, int *idx, float *wts, hipStream_t stream) {
+    constexpr int T = kRouterThreads, kMaxV4 = 8;
     if (!w || !x || !slots || !cnt || !idx || !wts || n <= 0 || n_cols <= 0 || k <= 0 || k > kTopkMaxK ||
         k > n || n > 64 * kTopkMaxPerLane)
         return set_error(kErrBadArg, "router_topk: need 0 < k <= min(%d, n_experts), n_experts <= %d", kTopkMaxK,
                          64 * kTopkMaxPerLane);
-    const int vec4 = (n_cols % 4 == 0) && (n_cols <= 4 * kRowMaxV4 * kRowThreads) &&
+    const int vec4 = (n_cols % 4 == 0) && (n_cols <= 4 * kMaxV4 * T) &&
                      (((uintptr_t)w | (uintptr_t)x | (uintptr_t)nw) % 16 == 0);
     if (nw && !vec4)
         return set_error(kErrBadArg, "router_topk: the fused RMS norm needs n_cols %% 4 == 0, <= %d and aligned vectors",
-                         4 * kRowMaxV4 * kRowThreads);
-    hipLaunchKernelGGL(router_topk_kernel, dim3(n), dim3(kRowThreads), 0, stream, w, x, nw, eps, slots, n,
-                       n_cols, k, cnt, idx, wts, vec4);
+                         4 * kMaxV4 * T);
+    // float4s per thread: the fewest that cover the row
+    if (n_cols <= 4 * 2 * T)
+        hipLaunchKernelGGL((router_topk_kernel<T, 2>), dim3(n), dim3(T), 0, stream, w, x, nw, eps, slots, n, n_cols, k,
+                           cnt, idx, wts, vec4);
+    else if (n_cols <= 4 * 4 * T)
+        hipLaunchKernelGGL((router_topk_kernel<T, 4>), dim3(n), dim3(T), 0, stream, w, x, nw, eps, slots, n, n_cols, k,
+                           cnt, idx, wts, vec4);
+    else
+        hipLaunchKernelGGL((router_topk_kernel<T, kMaxV4>), dim3(n), dim3(T), 0, stream, w, x, nw, eps, slots, n,
+                           n_cols, k, cnt, idx, wts, vec4);
     return check_launch("router_topk");
 }
 
