@@ -122,7 +122,7 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
     __shared__ __align__(16) uint8_t knew[PREP ? 2 : 1][PREP ? 2 * kHd : 1];  // new K, V rows as stored
     __shared__ float tmax[kTiles][kRows], tsum[kTiles][kRows];
     __shared__ float new_sc[2];  // int8 scales of the new K / V rows
-    const int chunk = blockIdx.x, kvh = blockIdx.y, lane = threadIdx.x & 63;
+    const int chunk = blockIdx.y, kvh = blockIdx.x, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int pos = a.pos_dev ? *a.pos_dev : a.seq_fixed - 1;
     const int seq = min(pos + 1, a.max_ctx);
@@ -480,7 +480,12 @@ static int check_decode_args(AttnDecodeArgs &a, int kv_type) {
 
 template <bool PREP>
 static int launch_decode(const AttnDecodeArgs &a, int kv_type, hipStream_t s) {
-    const dim3 grid(a.max_chunks, a.nkv);
+    // KV heads fastest: the workgroups are dispatched in order, so the chunks inside the
+    // sequence (the lowest chunk indices) start first and those past it (which exit at once)
+    // queue behind them -- with chunks fastest, a KV head's live chunks waited for the
+    // previous head's whole chunk range to be dispatched (2 K positions of a 40 K cache:
+    // 9.4 -> 8.3 us for the chunk and merge launches)
+    const dim3 grid(a.nkv, a.max_chunks);
     if (kv_type == kKvF16) {
         if (a.v_layout == kVBlocked)
             hipLaunchKernelGGL((attn_chunk_kernel<kKvF16, kVBlocked, PREP>), grid, dim3(kChunkThreads), 0, s, a);
