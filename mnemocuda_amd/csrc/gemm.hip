@@ -112,13 +112,6 @@ __device__ __forceinline__ h8 ds_operand(const uint4 &b0, const uint4 &b1) {
     return __builtin_bit_cast(h8, u);
 }
 
-// Workgroup barrier for LDS hand-offs that leaves global loads in flight.  __syncthreads()
-// is a release/acquire fence plus s_barrier, and the release makes every wave wait for all
-// of its outstanding global loads (vmcnt(0)) -- the loads of the next steps included, which
-// drains the prefetch pipeline at every step.  Here only the wave's own LDS accesses
-// (lgkmcnt) are waited for; the asm's memory clobber keeps the compiler from moving memory
-// accesses across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 // The same after LDS writes made by global_load_lds: those complete with the wave's vector
 // memory counter, so the wave waits until at most N vector memory operations (the ones it
 // issued after the LDS loads) are outstanding.

@@ -210,7 +210,7 @@ __device__ __forceinline__ float finish_x(const XRegs<XPT> &R, const XRegs<XPT> 
         if (lane_id() == 63) part[threadIdx.x >> 6] = ss;
     }
     build_x<XPT, XM, kGemvThreads>(R, R2, n, kp, X, threadIdx.x);
-    __syncthreads();
+    lds_barrier();  // the image only: each wave's dot products wait for its own weights
     if (XM != 2) return 1.0f;
     float tot = 0.0f;
 #pragma unroll
@@ -599,11 +599,16 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_down_slots_kernel(GemvArgs 
     M.pair = 0;
     M.mstride = 0;
     const int base = (int)blockIdx.x * P;
-    Pass<UPL> ps;
-    load_pass<LPR, UPL, TM>(M, 0, base, bpr, ps);
+    // the image before the weight loads: a wave's 33 loads fill the memory queue and stall
+    // its instruction issue until they are accepted, so an image built after them starts
+    // only then (and the barrier waits for the slowest wave's issue); built first, it
+    // costs the weight loads ~0.4 us of delay and the dot products start at once when the
+    // loads are in (16.0 -> 14.7 us for 8 experts of 4096 x 1536 Q6_K)
     const XLds X(smem + (size_t)w * xlds_bytes(kp), kp);
     build_x<XPW, XM, 64>(xr, xr2, n, kp, X, lane);
-    __syncthreads();
+    lds_barrier();
+    Pass<UPL> ps;
+    load_pass<LPR, UPL, TM>(M, 0, base, bpr, ps);
     const float wt = ok && w < E.slots ? E.wt[s] : 0.0f;
     const float acc = pass_dot<LPR, UPL, TM>(bpr, ps, X);
     if (lane % LPR == LPR - 1) red[w][lane / LPR] = wt * acc;

@@ -172,4 +172,13 @@ __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u,
 // signed 4 x int8 dot product accumulate (v_dot4_i32_i8)
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// Workgroup barrier for LDS hand-offs that leaves global loads in flight.  __syncthreads()
+// is a release/acquire fence plus s_barrier, and the release makes every wave wait for all
+// of its outstanding global loads (vmcnt(0)) -- loads that the barrier does not protect
+// included, so every wave then waits for the slowest wave's data.  Here only the wave's own
+// LDS accesses (lgkmcnt) are waited for; the asm's memory clobber keeps the compiler from
+// moving memory accesses across it, and the compiler still waits for each load before the
+// first use of its registers.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 }  // namespace mnemo
