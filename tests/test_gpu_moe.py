@@ -178,7 +178,9 @@ def _routable(rng, E, H, k):
 
 @pytest.mark.parametrize("H,EFF,E,k,DT", [(512, 256, 16, 4, 14), (1024, 512, 8, 8, 12), (4096, 1536, 24, 8, 14),
                                         (1024, 768, 24, 12, 14), (2048, 2560, 16, 6, 12), (4608, 512, 8, 4, 14),
-                                        (256, 256, 1024, 16, 14), (256, 256, 1, 1, 12)])
+                                        (256, 256, 1024, 16, 14), (256, 256, 1, 1, 12),
+                                        (1024, 512, 128, 8, 14), (512, 256, 64, 6, 12), (512, 256, 256, 8, 14),
+                                        (512, 256, 40, 8, 14)])
 def test_moe_decode_vs_oracle(gpu, oracle, H, EFF, E, k, DT):
     rng = np.random.default_rng(H + E * k)
     table = synth.expert_table(rng, E, H, EFF, DT)
@@ -200,6 +202,35 @@ def test_moe_decode_vs_oracle(gpu, oracle, H, EFF, E, k, DT):
     # a second call on the same workspace (tile counters must have been reset) adds again
     gpu.ops.moe_decode(dev(router), dev(table), *lay, DT, dev(x), H, EFF, E, k, ws, out, idx, w)
     assert rel_l2(host(out).astype(np.float64) - out0, 2 * delta) < TOL
+
+
+def test_moe_decode_router_ties(gpu, oracle):
+    """Router logits with exact ties (x one-hot, so each logit is one router weight): equal
+    logits rank by lower expert index, also across the k-th place, as the oracle's top-k."""
+    H, EFF, E, k, DT = 256, 256, 64, 8, 14
+    rng = np.random.default_rng(5)
+    table = synth.expert_table(rng, E, H, EFF, DT)
+    lay = synth.expert_layout(H, EFF, DT)
+    router = np.zeros((E, H), dtype=np.float32)
+    col = -np.abs(rng.standard_normal(E)).astype(np.float32) - 4.0  # all below the winners
+    col[[50, 3, 33, 12]] = [2.0, 2.0, 1.5, 1.5]  # ties inside the top k
+    col[[7, 9, 60]] = [1.0, 0.5, 0.25]
+    col[[44, 21, 30]] = 0.125  # three-way tie for the 8th place: 21 wins
+    router[:, 0] = col
+    x = np.zeros(H, dtype=np.float32)
+    x[0] = 1.0
+    out0 = rng.standard_normal(H).astype(np.float32)
+    ws = torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    out = dev(out0)
+    idx = torch.full((k,), -1, dtype=torch.int32, device="cuda")
+    w = torch.zeros(k, device="cuda")
+    case("moe_decode router ties")
+    gpu.ops.moe_decode(dev(router), dev(table), *lay, DT, dev(x), H, EFF, E, k, ws, out, idx, w)
+    _, ridx, rw, delta = _decode_ref(oracle, table, lay, DT, router, x, H, EFF, E, k)
+    assert host(idx).tolist() == [3, 50, 12, 33, 7, 9, 60, 21]
+    assert sorted(ridx.tolist()) == sorted(host(idx).tolist())
+    assert np.allclose(host(w)[np.argsort(host(idx))], rw[np.argsort(ridx)], rtol=1e-5, atol=1e-6)
+    assert rel_l2(host(out).astype(np.float64) - out0, delta) < TOL
 
 
 def test_moe_decode_graph_replays(gpu):
