@@ -13,7 +13,13 @@
  * x2[C], act[NT][C], then the outputs y4[R], y6[R], yadd[R], ya[R], yb[R], q[R], k[RK],
  * v[RK], logits[E], int32 idx[K], fp32 w[K], then q2[R], k2[RK], v2[RK] (all-Q4_K QKV),
  * ysa[R] (res + 0.37 Wq4 x), sw[C] (silu(x) * x2), ysc[R] (res + 0.5 y4), the Q8_1 bytes of
- * act [NT][C/128][144] and the GEMM output gout[NT][R] of Wq4 with them.
+ * act [NT][C/128][144] and the GEMM output gout[NT][R] of Wq4 with them.  Then the attention
+ * chain: int32 HH, NH, NKV, HD, SEQ, VOC, VT, the inputs xin[HH], anorm[HH], q[NH*HD],
+ * k[NKV*HD], v[NKV*HD], qw[HD], kw[HD], the f16 caches K, V [SEQ][NKV][HD] and the int8
+ * caches K, V with their scales [SEQ][NKV] before the call, logits[VOC], the Q4_K embedding
+ * table [VT][HH], and the outputs normed, resid, normed2, radd [HH], att, att8 [NH*HD],
+ * emb[HH], q and k after the QK norm and RoPE, the four caches and two scale arrays after
+ * the stores, and the sampled token.
  */
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
@@ -31,6 +37,15 @@
 #define NT 32
 #define Q4_BYTES ((size_t)(C / 256) * 144)
 #define Q6_BYTES ((size_t)(C / 256) * 210)
+/* the attention chain (forward.c:725-823, :1145-1280 embedding, :1702-1707 sampling) */
+#define HH 512   /* hidden size of the norms and the embedding */
+#define NH 8     /* query heads */
+#define NKV 2    /* KV heads */
+#define HD 128   /* head_dim */
+#define SEQ 70   /* positions attended: the new token at POS = SEQ - 1 */
+#define POS (SEQ - 1)
+#define VOC 3000 /* vocabulary of the sampled logits */
+#define VT 16    /* rows of the Q4_K embedding table */
 
 static uint64_t lcg = 0x9E3779B97F4A7C15ull;
 static uint32_t next32(void) {
@@ -60,6 +75,10 @@ static void fill_q6k(uint8_t *w, size_t rows) {
         memcpy(blk + 208, &d, 2);
     }
 }
+
+/* f16 bits of a value in +-[0.125, 1) */
+static uint16_t kv_f16(void) { return (uint16_t)((next32() & 0x8000u) | (0x3000u + next32() % 0x0C00u)); }
+static float sym(float a) { return a * (2.0f * uniform() - 1.0f); }
 
 static void *dev_copy(const void *h, size_t n) {
     void *d = NULL;
@@ -159,6 +178,107 @@ int main(int argc, char **argv) {
     fwrite(out2, 4, R + 2 * RK + R + C + R, f);
     fwrite(q8, 1, q8_bytes, f);
     fwrite(out2 + (gout - d_out2), 4, (size_t)NT * R, f);
+
+    /* ---- the attention chain of one decode layer, then sampling and the embedding ---- */
+    const size_t nkv = (size_t)SEQ * NKV * HD;
+    float *xin = malloc(HH * 4), *anorm = malloc(HH * 4), *qraw = malloc(NH * HD * 4);
+    float *knraw = malloc(NKV * HD * 4), *vnraw = malloc(NKV * HD * 4), *qw = malloc(HD * 4), *kw = malloc(HD * 4);
+    uint16_t *kc = malloc(nkv * 2), *vc = malloc(nkv * 2);
+    int8_t *kc8 = malloc(nkv), *vc8 = malloc(nkv);
+    float *ksc = malloc(SEQ * NKV * 4), *vsc = malloc(SEQ * NKV * 4), *lg = malloc(VOC * 4);
+    uint8_t *table = malloc((size_t)VT * (HH / 256) * 144);
+    for (int i = 0; i < HH; i++) { xin[i] = sym(2.0f); anorm[i] = 1.0f + sym(0.1f); }
+    for (int i = 0; i < NH * HD; i++) qraw[i] = sym(2.0f);
+    for (int i = 0; i < NKV * HD; i++) { knraw[i] = sym(2.0f); vnraw[i] = sym(2.0f); }
+    for (int i = 0; i < HD; i++) { qw[i] = 1.0f + sym(0.1f); kw[i] = 1.0f + sym(0.1f); }
+    for (size_t i = 0; i < nkv; i++) {
+        kc[i] = kv_f16();
+        vc[i] = kv_f16();
+        kc8[i] = (int8_t)((int)(next32() % 255) - 127);
+        vc8[i] = (int8_t)((int)(next32() % 255) - 127);
+    }
+    for (int i = 0; i < SEQ * NKV; i++) { ksc[i] = 0.001f + 0.01f * uniform(); vsc[i] = 0.001f + 0.01f * uniform(); }
+    for (int i = 0; i < VOC; i++) lg[i] = sym(6.0f);
+    fill_q4k(table, (size_t)VT * (HH / 256) / (C / 256)); /* VT rows of HH/256 blocks */
+    float *d_xin = dev_copy(xin, HH * 4), *d_anorm = dev_copy(anorm, HH * 4), *d_q = dev_copy(qraw, NH * HD * 4);
+    float *d_kn = dev_copy(knraw, NKV * HD * 4), *d_vn = dev_copy(vnraw, NKV * HD * 4);
+    float *d_qw = dev_copy(qw, HD * 4), *d_kw = dev_copy(kw, HD * 4), *d_lg = dev_copy(lg, VOC * 4);
+    uint16_t *d_kc = dev_copy(kc, nkv * 2), *d_vc = dev_copy(vc, nkv * 2);
+    int8_t *d_kc8 = dev_copy(kc8, nkv), *d_vc8 = dev_copy(vc8, nkv);
+    float *d_ksc = dev_copy(ksc, SEQ * NKV * 4), *d_vsc = dev_copy(vsc, SEQ * NKV * 4);
+    void *d_table = dev_copy(table, (size_t)VT * (HH / 256) * 144);
+    float *d_chain = NULL; /* normed, resid, normed2, radd [HH], att, att8 [NH*HD], emb [HH] */
+    int *d_tok = NULL;
+    const size_t n_chain = 5 * (size_t)HH + 2 * NH * HD;
+    if (!d_xin || !d_anorm || !d_q || !d_kn || !d_vn || !d_qw || !d_kw || !d_lg || !d_kc || !d_vc || !d_kc8 ||
+        !d_vc8 || !d_ksc || !d_vsc || !d_table || hipMalloc((void **)&d_chain, n_chain * 4) != hipSuccess ||
+        hipMalloc((void **)&d_tok, 4) != hipSuccess) {
+        fprintf(stderr, "hip allocation or copy failed (attention chain)\n");
+        return 1;
+    }
+    float *normed = d_chain, *resid = normed + HH, *normed2 = resid + HH, *radd = normed2 + HH;
+    float *att = radd + HH, *att8 = att + NH * HD, *emb = att8 + NH * HD;
+    const float scale = 0.08838834764831845f; /* 1 / sqrt(128) */
+    cuda_rms_norm_residual(d_xin, d_anorm, normed, resid, HH, 1e-6f, s);           /* forward.c:727 */
+    cuda_rms_norm(d_xin, d_anorm, normed2, HH, 1e-6f, s);
+    cuda_residual_add(d_xin, d_anorm, radd, HH, s);
+    cuda_rms_norm_qk(d_q, d_kn, d_qw, d_kw, HD, NH, NKV, 1e-6f, s);                 /* forward.c:742 */
+    cuda_rope(d_q, d_kn, HD, POS, 1e6f, NH, NKV, s);                                /* forward.c:748 */
+    cuda_f32_to_f16_dual(d_kn, d_vn, d_kc + (size_t)POS * NKV * HD, d_vc + (size_t)POS * NKV * HD, NKV * HD, s);
+    cuda_attention_f16kv(d_q, d_kc, d_vc, att, NH, HD, NKV, SEQ, NH / NKV, scale, s); /* forward.c:772 */
+    cuda_f32_to_int8_kv_dual(d_kn, d_vn, d_kc8 + (size_t)POS * NKV * HD, d_vc8 + (size_t)POS * NKV * HD,
+                             d_ksc + POS * NKV, d_vsc + POS * NKV, HD, NKV, s);
+    cuda_attention_int8kv(d_q, d_kc8, d_vc8, d_ksc, d_vsc, att8, NH, HD, NKV, SEQ, NH / NKV, scale, s);
+    cuda_sample_token(d_lg, VOC, 0.8f, 0.9f, 12345ull, d_tok, s);                  /* forward.c:1703 */
+    cuda_embedding_lookup_q4k(d_table, emb, 5, HH, (HH / 256) * 144, s);           /* forward.c:1160 */
+    if (hipStreamSynchronize(s) != hipSuccess) return 1;
+    if (mnemo_last_error() != MNEMO_OK) {
+        fprintf(stderr, "library error: %s\n", mnemo_last_error_string());
+        return 1;
+    }
+    float *chain = malloc(n_chain * 4), *qpost = malloc(NH * HD * 4), *kpost = malloc(NKV * HD * 4);
+    uint16_t *kc_o = malloc(nkv * 2), *vc_o = malloc(nkv * 2);
+    int8_t *kc8_o = malloc(nkv), *vc8_o = malloc(nkv);
+    float *ksc_o = malloc(SEQ * NKV * 4), *vsc_o = malloc(SEQ * NKV * 4);
+    int tok = -1;
+    if (hipMemcpy(chain, d_chain, n_chain * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(qpost, d_q, NH * HD * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(kpost, d_kn, NKV * HD * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(kc_o, d_kc, nkv * 2, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(vc_o, d_vc, nkv * 2, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(kc8_o, d_kc8, nkv, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(vc8_o, d_vc8, nkv, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(ksc_o, d_ksc, SEQ * NKV * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(vsc_o, d_vsc, SEQ * NKV * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(&tok, d_tok, 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return 1;
+    const int32_t hdr2[7] = {HH, NH, NKV, HD, SEQ, VOC, VT};
+    fwrite(hdr2, 4, 7, f);
+    fwrite(xin, 4, HH, f);
+    fwrite(anorm, 4, HH, f);
+    fwrite(qraw, 4, NH * HD, f);
+    fwrite(knraw, 4, NKV * HD, f);
+    fwrite(vnraw, 4, NKV * HD, f);
+    fwrite(qw, 4, HD, f);
+    fwrite(kw, 4, HD, f);
+    fwrite(kc, 2, nkv, f);
+    fwrite(vc, 2, nkv, f);
+    fwrite(kc8, 1, nkv, f);
+    fwrite(vc8, 1, nkv, f);
+    fwrite(ksc, 4, SEQ * NKV, f);
+    fwrite(vsc, 4, SEQ * NKV, f);
+    fwrite(lg, 4, VOC, f);
+    fwrite(table, 1, (size_t)VT * (HH / 256) * 144, f);
+    fwrite(chain, 4, n_chain, f);
+    fwrite(qpost, 4, NH * HD, f);
+    fwrite(kpost, 4, NKV * HD, f);
+    fwrite(kc_o, 2, nkv, f);
+    fwrite(vc_o, 2, nkv, f);
+    fwrite(kc8_o, 1, nkv, f);
+    fwrite(vc8_o, 1, nkv, f);
+    fwrite(ksc_o, 4, SEQ * NKV, f);
+    fwrite(vsc_o, 4, SEQ * NKV, f);
+    fwrite(&tok, 4, 1, f);
     fclose(f);
     printf("%s: ok\n", mnemo_version());
     return 0;

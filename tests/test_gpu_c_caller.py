@@ -45,6 +45,20 @@ def test_c_caller_matches_oracle(gpu, oracle, tmp_path):
     ysa, sw, ysc = take(R, np.float32), take(C, np.float32), take(R, np.float32)
     q8 = take(NT * (C // 128) * 144, np.uint8)
     gout = take(NT * R, np.float32).reshape(NT, R)
+    HH, NH, NKV, HD, SEQ, VOC, VT = (int(v) for v in take(7, np.int32))
+    nkv = SEQ * NKV * HD
+    xin, anorm = take(HH, np.float32), take(HH, np.float32)
+    qraw, kraw, vraw = take(NH * HD, np.float32), take(NKV * HD, np.float32), take(NKV * HD, np.float32)
+    qw, kw = take(HD, np.float32), take(HD, np.float32)
+    kc, vc, kc8, vc8 = take(nkv, np.uint16), take(nkv, np.uint16), take(nkv, np.int8), take(nkv, np.int8)
+    ksc, vsc, lg = take(SEQ * NKV, np.float32), take(SEQ * NKV, np.float32), take(VOC, np.float32)
+    table = take(VT * (HH // 256) * 144, np.uint8)
+    normed, resid, normed2, radd = (take(HH, np.float32) for _ in range(4))
+    att, att8, emb = take(NH * HD, np.float32), take(NH * HD, np.float32), take(HH, np.float32)
+    qpost, kpost = take(NH * HD, np.float32), take(NKV * HD, np.float32)
+    kc_o, vc_o, kc8_o, vc8_o = take(nkv, np.uint16), take(nkv, np.uint16), take(nkv, np.int8), take(nkv, np.int8)
+    ksc_o, vsc_o = take(SEQ * NKV, np.float32), take(SEQ * NKV, np.float32)
+    tok = int(take(1, np.int32)[0])
     assert off == len(buf)
 
     g4, g6 = oracle.gemv(12, wq4, x, R, C), oracle.gemv(14, wq6, x, R, C)
@@ -71,3 +85,40 @@ def test_c_caller_matches_oracle(gpu, oracle, tmp_path):
     ref_q8 = oracle.quantize_q8_1(act)
     assert np.array_equal(q8, ref_q8.reshape(-1))
     assert rel_l2(gout, oracle.gemm(12, wq4, ref_q8, R, C, NT)) < 1e-5
+
+    # ---- the attention chain (forward.c:725-823), sampling and the embedding, from C
+    pos, row = SEQ - 1, slice((SEQ - 1) * NKV * HD, SEQ * NKV * HD)
+    wn, wr = oracle.rms_norm_residual(xin, anorm, 1e-6)
+    np.testing.assert_allclose(normed, wn, rtol=2e-6, atol=1e-7)
+    assert np.array_equal(resid, xin) and np.array_equal(resid, wr)
+    np.testing.assert_allclose(normed2, oracle.rms_norm(xin, anorm, 1e-6), rtol=2e-6, atol=1e-7)
+    assert np.array_equal(radd, (xin + anorm).astype(np.float32))
+    rq, rk = oracle.rope(oracle.rms_norm_heads(qraw, qw, HD, 1e-6), oracle.rms_norm_heads(kraw, kw, HD, 1e-6),
+                         HD, pos, 1e6)
+    tol = 1e-5 * max(np.abs(rq).max(), np.abs(rk).max())
+    np.testing.assert_allclose(qpost, rq, rtol=0, atol=tol)
+    np.testing.assert_allclose(kpost, rk, rtol=0, atol=tol)
+    # f16 stores at the new position only; attention over the stored caches
+    keep = np.ones(nkv, bool)
+    keep[row] = False
+    assert np.array_equal(kc_o[keep], kc[keep]) and np.array_equal(vc_o[keep], vc[keep])
+    assert np.array_equal(kc_o[row], kpost.astype(np.float16).view(np.uint16))
+    assert np.array_equal(vc_o[row], vraw.astype(np.float16).view(np.uint16))
+    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    assert rel_l2(att, oracle.attention(qpost, kc_o, vc_o, NH, HD, NKV, SEQ, scale)) < 1e-5
+    # int8 stores and the int8 attention
+    qk, sk = oracle.kv_quant_int8(kpost, HD)
+    qv, sv = oracle.kv_quant_int8(vraw, HD)
+    assert np.array_equal(kc8_o[keep], kc8[keep]) and np.array_equal(vc8_o[keep], vc8[keep])
+    assert np.array_equal(kc8_o[row], qk) and np.array_equal(vc8_o[row], qv)
+    assert np.array_equal(ksc_o[pos * NKV:], sk) and np.array_equal(vsc_o[pos * NKV:], sv)
+    assert np.array_equal(ksc_o[:pos * NKV], ksc[:pos * NKV]) and np.array_equal(vsc_o[:pos * NKV], vsc[:pos * NKV])
+    ref8 = oracle.attention(qpost, kc8_o, vc8_o, NH, HD, NKV, SEQ, scale, k_scales=ksc_o, v_scales=vsc_o)
+    assert rel_l2(att8, ref8) < 1e-5
+    # sampling: the oracle's token unless the draw lies within rounding of a boundary
+    from oracle import oracle_np as onp
+    want, margin = onp.sample_token(lg, 0.8, 0.9, 12345)
+    if margin >= 1e-5:
+        assert tok == want == oracle.sample_token(lg, 0.8, 0.9, 12345)[0]
+    # embedding row 5 of the Q4_K table, bit-exact
+    assert np.array_equal(emb, oracle.dequant(12, table, VT, HH)[5])
