@@ -19,7 +19,7 @@
  * caches K, V with their scales [SEQ][NKV] before the call, logits[VOC], the Q4_K embedding
  * table [VT][HH], and the outputs normed, resid, normed2, radd [HH], att, att8 [NH*HD],
  * emb[HH], q and k after the QK norm and RoPE, the four caches and two scale arrays after
- * the stores, and the sampled token.
+ * the stores, the sampled token, and the head-wise RMS norm of the raw q [NH*HD].
  */
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
@@ -229,6 +229,9 @@ int main(int argc, char **argv) {
     cuda_f32_to_int8_kv_dual(d_kn, d_vn, d_kc8 + (size_t)POS * NKV * HD, d_vc8 + (size_t)POS * NKV * HD,
                              d_ksc + POS * NKV, d_vsc + POS * NKV, HD, NKV, s);
     cuda_attention_int8kv(d_q, d_kc8, d_vc8, d_ksc, d_vsc, att8, NH, HD, NKV, SEQ, NH / NKV, scale, s);
+    float *d_qb = dev_copy(qraw, NH * HD * 4), *d_qbo = NULL;
+    if (!d_qb || hipMalloc((void **)&d_qbo, NH * HD * 4) != hipSuccess) return 1;
+    cuda_rms_norm_batched(d_qb, d_qw, d_qbo, HD, NH, 1e-6f, s);
     cuda_sample_token(d_lg, VOC, 0.8f, 0.9f, 12345ull, d_tok, s);                  /* forward.c:1703 */
     cuda_embedding_lookup_q4k(d_table, emb, 5, HH, (HH / 256) * 144, s);           /* forward.c:1160 */
     if (hipStreamSynchronize(s) != hipSuccess) return 1;
@@ -252,6 +255,8 @@ int main(int argc, char **argv) {
         hipMemcpy(vsc_o, d_vsc, SEQ * NKV * 4, hipMemcpyDeviceToHost) != hipSuccess ||
         hipMemcpy(&tok, d_tok, 4, hipMemcpyDeviceToHost) != hipSuccess)
         return 1;
+    float *qb = malloc(NH * HD * 4);
+    if (hipMemcpy(qb, d_qbo, NH * HD * 4, hipMemcpyDeviceToHost) != hipSuccess) return 1;
     const int32_t hdr2[7] = {HH, NH, NKV, HD, SEQ, VOC, VT};
     fwrite(hdr2, 4, 7, f);
     fwrite(xin, 4, HH, f);
@@ -279,6 +284,7 @@ int main(int argc, char **argv) {
     fwrite(ksc_o, 4, SEQ * NKV, f);
     fwrite(vsc_o, 4, SEQ * NKV, f);
     fwrite(&tok, 4, 1, f);
+    fwrite(qb, 4, NH * HD, f);
     fclose(f);
     printf("%s: ok\n", mnemo_version());
     return 0;

@@ -59,6 +59,7 @@ def test_c_caller_matches_oracle(gpu, oracle, tmp_path):
     kc_o, vc_o, kc8_o, vc8_o = take(nkv, np.uint16), take(nkv, np.uint16), take(nkv, np.int8), take(nkv, np.int8)
     ksc_o, vsc_o = take(SEQ * NKV, np.float32), take(SEQ * NKV, np.float32)
     tok = int(take(1, np.int32)[0])
+    qb = take(NH * HD, np.float32)
     assert off == len(buf)
 
     g4, g6 = oracle.gemv(12, wq4, x, R, C), oracle.gemv(14, wq6, x, R, C)
@@ -122,3 +123,4 @@ def test_c_caller_matches_oracle(gpu, oracle, tmp_path):
         assert tok == want == oracle.sample_token(lg, 0.8, 0.9, 12345)[0]
     # embedding row 5 of the Q4_K table, bit-exact
     assert np.array_equal(emb, oracle.dequant(12, table, VT, HH)[5])
+    np.testing.assert_allclose(qb, oracle.rms_norm_heads(qraw, qw, HD, 1e-6), rtol=2e-6, atol=1e-7)
