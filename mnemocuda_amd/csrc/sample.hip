@@ -55,8 +55,7 @@ __device__ __forceinline__ uint64_t cand_key(float p, int id) {
 
 // keep the better (larger key) of a and b in a when `better_here`, the other one otherwise
 __device__ __forceinline__ uint64_t keep(uint64_t a, uint64_t b, bool better_here) {
-    const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
-    return better_here ? hi : lo;
+    return (a > b) == better_here ? a : b;  // one compare, one select (keys are distinct or equal)
 }
 
 // v of lane ^ M: DPP within rows of 16 lanes (quad permutes; row rotations, where lane i
