@@ -241,6 +241,22 @@ void cuda_rope(float *q, float *k, int head_dim, int pos, float theta, int n_hea
 /* kernels.cu:1328-1335 (:1320-1326): oa = f16(a), ob = f16(b), round to nearest even. */
 void cuda_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n,
                           hipStream_t stream);
+/* kernels.cu:2243-2245: the kernels an engine finds in a captured graph by function pointer
+ * (forward.c:1395-1412) and patches before every replay (forward.c:633-668).
+ * cuda_get_rope_kernel_ptr: the kernel of cuda_rope, parameter 3 = pos.
+ * cuda_get_f16dual_kernel_ptr: the kernel of cuda_f32_to_f16_dual, parameters 2 and 3 = the
+ * f16 destinations.  cuda_get_attn_f16kv_kernel_ptr: the first kernel of cuda_attention_f16kv
+ * (head_dim 128, gqa <= 16), parameter 6 = seq_len. */
+void *cuda_get_rope_kernel_ptr(void);
+void *cuda_get_f16dual_kernel_ptr(void);
+void *cuda_get_attn_f16kv_kernel_ptr(void);
+/* No counterpart in the reference: workspace slots of cuda_attention_f16kv / _int8kv.  Makes
+ * at least n_slots free slots exist on the current GPU (allocates; call outside any graph
+ * capture), for an engine that captures more attention calls than cuda_kernels_init's 16.
+ * Returns 0 or an error code. */
+int mnemo_attention_reserve(int n_slots);
+/* bytes of one slot (device memory held until the process ends) */
+size_t mnemo_attention_slot_bytes(void);
 /* kernels.cu:1526-1534 (:1493-1524): per head absmax a, scale = a/127, q = rne(x*127/a)
  * clamped to +-127; out_* and *_scales point at the current position's row and slots. */
 void cuda_f32_to_int8_kv_dual(const float *k, const float *v, void *out_k, void *out_v,
@@ -249,11 +265,14 @@ void cuda_f32_to_int8_kv_dual(const float *k, const float *v, void *out_k, void 
 /* kernels.cu:1662-1673 (:1550-1660) and :1536-1546 (:1382-1481): softmax(scale q.k) v over
  * positions 0..seq_len-1 of the cache [pos][n_kv_heads][head_dim] for every query head
  * (kv head = head / gqa_ratio).  head_dim 64, 128 or 256.  With head_dim 128, gqa <= 16 and
- * seq_len <= 65536 the call runs the split-chunk kernels of mnemo_attention_decode (two
- * launches, capture-safe) on a 64 MiB workspace that cuda_kernels_init allocates per GPU;
- * that workspace belongs to the first stream that uses it, and calls from other streams (or
- * without cuda_kernels_init, or longer than the workspace holds) run the per-head kernel.
- * The two paths agree to ~1e-6 relative (not bit for bit). */
+ * n_kv_heads <= 256 the call is two launches: the split kernel (the function
+ * cuda_get_attn_f16kv_kernel_ptr returns, with the reference kernel's parameters first and
+ * seq_len as parameter 6, and a grid that does not depend on seq_len) and the merge of its
+ * partials.  They run on a workspace slot of mnemo_attention_slot_bytes(): eager calls use a
+ * slot bound to their stream, and a call made under graph capture takes a free slot of its own
+ * (cuda_kernels_init reserves 16, mnemo_attention_reserve more), so a captured graph can be
+ * replayed on any stream next to eager calls.  Other shapes run the per-head kernel.  The two
+ * paths agree to ~1e-6 relative (not bit for bit). */
 void cuda_attention_f16kv(const void *q, const void *kv_k, const void *kv_v, float *out,
                           int n_heads_q, int head_dim, int n_kv_heads, int seq_len, int gqa_ratio,
                           float scale, hipStream_t stream);

@@ -20,6 +20,7 @@ CSRC = PKG / "csrc"
 BUILD = ROOT / "_build"
 LIB = PKG / "libmnemo_hip.so"
 CALLER = PKG / "engine_calls"  # tests/c_caller/engine_calls.c, linked against LIB
+GRAPH_CALLER = PKG / "attn_graph"  # tests/c_caller/attn_graph.c, linked against LIB
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 HIP_SOURCES = ["abi.hip", "gemv_launch.hip", "router.hip", "gemm.hip", "moe.hip", "sample.hip", "attn.hip", "attn_decode.hip", "embed.hip"]
@@ -78,12 +79,13 @@ def build(jobs: int = 4) -> Path:
     _run([hipcc, "-shared", "-fPIC", "--offload-arch=gfx950", *map(str, objs), "-o", str(tmp),
           f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}"])
     tmp.replace(LIB)
-    # the C caller of the C-ABI that the GPU tests run (tests/c_caller/engine_calls.c)
-    caller = ROOT / "tests" / "c_caller" / "engine_calls.c"
-    if caller.exists():
-        _run([cc, "-O2", "-std=c11", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
-              str(caller), "-o", str(CALLER), f"-L{LIB.parent}", "-lmnemo_hip", f"-L{ROCM / 'lib'}", "-lamdhip64",
-              "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}"])
+    # the C callers of the C-ABI that the GPU tests run (tests/c_caller/)
+    for name, exe in (("engine_calls.c", CALLER), ("attn_graph.c", GRAPH_CALLER)):
+        src = ROOT / "tests" / "c_caller" / name
+        if src.exists():
+            _run([cc, "-O2", "-std=c11", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
+                  str(src), "-o", str(exe), f"-L{LIB.parent}", "-lmnemo_hip", f"-L{ROCM / 'lib'}", "-lamdhip64",
+                  "-lm", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}"])
     return LIB
 
 

@@ -316,17 +316,26 @@ void cuda_residual_add(const float *a, const float *b, float *out, int n, hipStr
 }
 
 void cuda_rope(float *q, float *k, int head_dim, int pos, float theta, int n_heads_q, int n_heads_k, hipStream_t s) {
-    HeadPassArgs a = {};
-    a.q = q;
-    a.k = k;
-    a.hd = head_dim;
-    a.nq = n_heads_q;
-    a.nk = n_heads_k;
-    a.theta = theta;
-    a.pos = pos;
-    a.flags = kHeadRope;
-    launch_head_pass(a, s);
+    launch_rope(q, k, head_dim, pos, theta, n_heads_q, n_heads_k, s);
 }
+
+// The kernels whose graph nodes the reference engine finds by function pointer and patches
+// before every replay (kernels.cu:2243-2245; forward.c:1291-1297, 1395-1412, 633-668):
+// parameter 3 of the RoPE node (pos), 2 and 3 of the f16 KV store (destinations), 6 of the
+// attention node (seq_len).  Each is the kernel its entry point launches, with those parameters
+// at those positions.
+void *cuda_get_rope_kernel_ptr(void) { return rope_kernel_ptr(); }
+void *cuda_get_f16dual_kernel_ptr(void) { return f16_dual_kernel_ptr(); }
+void *cuda_get_attn_f16kv_kernel_ptr(void) { return attn_rows_kernel_ptr(); }
+
+int mnemo_attention_reserve(int n_slots) {
+    if (n_slots < 0) return set_error(kErrBadArg, "attention_reserve: n_slots < 0");
+    const int rc = attn_rows_reserve(n_slots);
+    if (rc != kOk) return set_error(rc, "attention_reserve: could not hold %d free slots", n_slots);
+    return kOk;
+}
+
+size_t mnemo_attention_slot_bytes(void) { return attn_rows_slot_bytes(); }
 
 void cuda_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, int n, hipStream_t s) {
     launch_f32_to_f16_dual(a, b, oa, ob, n, s);

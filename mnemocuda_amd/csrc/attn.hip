@@ -133,6 +133,48 @@ int launch_f32_to_f16_dual(const float *a, const float *b, void *oa, void *ob, i
     return check_launch("f32_to_f16_dual");
 }
 
+void *f16_dual_kernel_ptr() { return reinterpret_cast<void *>(&f32_to_f16_dual_kernel); }
+
+// ------------------------------------------------------------------ RoPE entry point
+// cuda_rope launches this kernel.  Its first seven parameters are those of the reference's
+// rope_kernel in the same order (kernels.cu:818-822: q, k, head_dim, pos, theta, n_heads_q,
+// n_heads_k), because the reference patches parameter 3 (pos) of the captured node before each
+// graph replay (forward.c:635-640).  The frequencies 1 / powf(theta, 2j / head_dim) come by value
+// after them, computed on the host as the reference does (kernels.cu:1259-1266; it keeps them in
+// constant memory).  One thread per rotated pair; the rotation is head_pass_kernel's, bit for bit.
+struct RopeFreqs {
+    float f[kMaxRopeFreqs];
+};
+
+__global__ void __launch_bounds__(256) rope_kernel(float *__restrict__ q, float *__restrict__ k, int head_dim, int pos,
+                                                   float theta, int n_heads_q, int n_heads_k, RopeFreqs fr) {
+    (void)theta;  // folded into fr
+    const int half = head_dim / 2;
+    const int tid = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (tid >= (n_heads_q + n_heads_k) * half) return;
+    const int head = tid / half, j = tid - head * half;
+    float *v = head < n_heads_q ? q + (size_t)head * head_dim : k + (size_t)(head - n_heads_q) * head_dim;
+    float sn, cs;
+    sincosf((float)pos * fr.f[j], &sn, &cs);
+    const float v0 = v[j], v1 = v[j + half];
+    v[j] = fmaf(v0, cs, -(v1 * sn));
+    v[j + half] = fmaf(v0, sn, v1 * cs);
+}
+
+void *rope_kernel_ptr() { return reinterpret_cast<void *>(&rope_kernel); }
+
+int launch_rope(float *q, float *k, int head_dim, int pos, float theta, int nq, int nk, hipStream_t s) {
+    if (head_dim <= 0 || (head_dim & 1) || head_dim / 2 > kMaxRopeFreqs || nq < 0 || nk < 0 || nq + nk <= 0 ||
+        (nq && !q) || (nk && !k))
+        return set_error(kErrBadArg, "rope: need an even head_dim <= %d, heads > 0 and q / k", 2 * kMaxRopeFreqs);
+    RopeFreqs fr = {};
+    for (int j = 0; j < head_dim / 2; j++) fr.f[j] = 1.0f / powf(theta, (float)(2 * j) / (float)head_dim);
+    const int total = (nq + nk) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3((total + 255) / 256), dim3(256), 0, s, q, k, head_dim, pos, theta, nq, nk,
+                       fr);
+    return check_launch("rope");
+}
+
 // ------------------------------------------------------------------ per-head pass
 constexpr int kHeadPairs = 4;  // RoPE pairs per lane: head_dim <= 512
 

@@ -518,73 +518,316 @@ int launch_attention_decode_prep(AttnDecodeArgs a, int kv_type, float theta, hip
 }
 
 // ------------------------------------------------------------------ the reference's entry points
-// cuda_attention_f16kv / _int8kv (the reference's caches: K and V rows [pos][n_kv][hd], the
-// sequence length a host value) run on the split-chunk kernels above when head_dim is 128 and
-// gqa <= 16, with the partials in a workspace the library allocates at cuda_kernels_init
-// (kRowsWsBytes per GPU, outside any graph capture).  The workspace belongs to the first
-// stream that uses it on a GPU; calls from other streams, or larger than the workspace, take
-// the per-head kernel (attn.hip), so calls on different streams never share it.
-constexpr size_t kRowsWsBytes = (size_t)64 << 20;
+// cuda_attention_f16kv / _int8kv: the reference's row caches (K and V [pos][n_kv][hd]) and a
+// host sequence length.  At head_dim 128 and gqa <= 16 they run attention_rows_kernel plus the
+// chunk merge above.  The reference captures cuda_attention_f16kv in a graph and patches the
+// sequence length of the captured node before every replay (forward.c:658-666: kernelParams[6]
+// of the node whose function is cuda_get_attn_f16kv_kernel_ptr(), kernels.cu:2245), so:
+//  * attention_rows_kernel takes the reference kernel's parameters in the reference's order
+//    (kernels.cu:1550-1554: q, kv_k, kv_v, out, head_dim, n_kv_heads, seq_len, gqa_ratio,
+//    scale), then its own (workspace, split count, int8 scales);
+//  * its grid does not depend on seq_len: (n_kv_heads, nsplit) workgroups, workgroup g taking
+//    the 64-position chunks g, g + nsplit, ... and merging them as it goes (running max, sum
+//    and O), so one workgroup leaves one partial whatever the length;
+//  * it writes the number of partials to the workspace header, from which the merge launch
+//    (whose arguments hold no length) reads it.
+// With at most nsplit chunks every workgroup takes one chunk and the partials are exactly
+// those of attn_chunk_kernel.
+constexpr int kSplitTarget = 256;  // workgroups per launch (one per CU)
+constexpr int kRowsMaxKv = kSplitTarget;
+static int rows_nsplit(int nkv) { return max(1, kSplitTarget / nkv); }
+// partials for nkv * nsplit <= kSplitTarget workgroups, then the header (one int)
+constexpr size_t kRowsSlotBytes = (size_t)kSplitTarget * kPart * sizeof(float) + 256;
+
+template <int KV>
+__global__ void __launch_bounds__(kChunkThreads)
+    attention_rows_kernel(const float *__restrict__ q, const void *__restrict__ kv_k, const void *__restrict__ kv_v,
+                          float *out, int head_dim, int n_kv_heads, int seq_len, int gqa_ratio, float scale,
+                          float *ws, int nsplit, const float *__restrict__ k_scales,
+                          const float *__restrict__ v_scales) {
+    (void)out;       // written by the merge launch
+    (void)head_dim;  // 128: checked by the host
+    __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];
+    __shared__ __align__(16) _Float16 vt[kChunk][kHd + 8];
+    __shared__ __align__(16) _Float16 ps[2][kRows][kChunk + 8];
+    __shared__ float tmax[kTiles][kRows], tsum[kTiles][kRows];
+    const int kvh = blockIdx.x, g = blockIdx.y, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int seq = max(seq_len, 1);
+    const int nchunks = (seq + kChunk - 1) / kChunk;
+    if (kvh == 0 && g == 0 && threadIdx.x == 0)  // the merge reads min(nchunks, nsplit) partials
+        *(int *)(ws + (size_t)n_kv_heads * nsplit * kPart) = kChunk * min(nchunks, nsplit) - 1;
+    if (g >= nchunks) return;
+    const int G = gqa_ratio;
+    const size_t stride = (size_t)n_kv_heads * kHd;
+    const int r = lane & 15, kg = lane >> 4;
+    const bool swave = wave < kTiles;
+    const int t = wave & (kTiles - 1);
+    const int nv = wave - kTiles;
+    constexpr int EB = KV == kKvF16 ? 2 : 1;
+    const uint8_t *kc = (const uint8_t *)kv_k, *vc = (const uint8_t *)kv_v;
+
+    // Q rows (heads kvh*G .. +G-1) as f16 hi + lo, once for all chunks
+    for (int e = threadIdx.x; e < kRows * kHd / 4; e += kChunkThreads) {
+        const int h = e / (kHd / 4), d = 4 * (e % (kHd / 4));
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (h < G) v = *(const float4 *)(q + (size_t)(kvh * G + h) * kHd + d);
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            hi[j] = (_Float16)vv[j];
+            lo[j] = (_Float16)(vv[j] - (float)hi[j]);
+        }
+        __builtin_memcpy(&qs[0][h][d], hi, 8);
+        __builtin_memcpy(&qs[1][h][d], lo, 8);
+    }
+
+    // running state of the O waves: rows (heads) 4kg + i, dims of n-tiles 2nv, 2nv + 1
+    float Mr[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, Lr[4] = {0.f, 0.f, 0.f, 0.f};
+    f4 oacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int chunk = g; chunk < nchunks; chunk += nsplit) {
+        const int p0 = chunk * kChunk;
+        // loads: K fragments of tile t (S waves), the 16-element V pieces of every wave
+        const int pt = min(p0 + 16 * t + r, seq - 1);
+        uint4 kr[4];
+        float ksc = 1.0f, vsc = 1.0f;
+        if (swave) {
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const size_t off = ((size_t)pt * stride + (size_t)kvh * kHd + 32 * st + 8 * kg) * EB;
+                if (KV == kKvF16) __builtin_memcpy(&kr[st], kc + off, 16);
+                else __builtin_memcpy(&kr[st], kc + off, 8);
+            }
+            if (KV == kKvInt8) {
+                ksc = k_scales[(size_t)pt * n_kv_heads + kvh];
+                vsc = v_scales[(size_t)pt * n_kv_heads + kvh];
+            }
+        }
+        uint4 vr[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = lane + 64 * (2 * wave + i);
+            const int p = min(p0 + (c >> 4), seq - 1);
+            const size_t off = ((size_t)p * stride + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
+            if (KV == kKvF16) __builtin_memcpy(&vr[i], vc + off, 16);
+            else __builtin_memcpy(&vr[i], vc + off, 8);
+        }
+        __syncthreads();  // 1: Q rows (first chunk); the previous chunk's LDS reads are done
+        f4 sc = {0.f, 0.f, 0.f, 0.f};
+        if (swave) {
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                h8 b;
+                if (KV == kKvF16) {
+                    __builtin_memcpy(&b, &kr[st], 16);
+                } else {
+                    const int8_t *kb = (const int8_t *)&kr[st];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) b[j] = (_Float16)kb[j];
+                }
+                h8 ah, al;
+                __builtin_memcpy(&ah, &qs[0][r][32 * st + 8 * kg], 16);
+                __builtin_memcpy(&al, &qs[1][r][32 * st + 8 * kg], 16);
+                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, sc, 0, 0, 0);
+            }
+            const bool ok = p0 + 16 * t + r < seq;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sc[i] = ok ? sc[i] * (scale * ksc) : -INFINITY;
+                const float mx = max16(sc[i]);
+                if (r == 0) tmax[t][4 * kg + i] = mx;
+            }
+        }
+        __syncthreads();  // 2: the tiles' row maxima
+        if (swave) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int h = 4 * kg + i;
+                float m = tmax[0][h];
+#pragma unroll
+                for (int u = 1; u < kTiles; u++) m = fmaxf(m, tmax[u][h]);
+                const float e = expf(sc[i] - m);
+                const float sum = sum16(e);
+                if (r == 0) tsum[t][h] = sum;
+                const float pv = e * vsc;
+                const _Float16 hi = (_Float16)pv;
+                ps[0][h][16 * t + r] = hi;
+                ps[1][h][16 * t + r] = (_Float16)(pv - (float)hi);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = lane + 64 * (2 * wave + i);
+            h8 v;
+            if (KV == kKvF16) {
+                __builtin_memcpy(&v, &vr[i], 16);
+            } else {
+                const int8_t *vb = (const int8_t *)&vr[i];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = (_Float16)vb[j];
+            }
+            __builtin_memcpy(&vt[c >> 4][8 * (c & 15)], &v, 16);
+        }
+        __syncthreads();  // 3: P, the row sums and the V tile
+        if (!swave) {
+            f4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                h8 ah, al;
+                __builtin_memcpy(&ah, &ps[0][r][32 * kk + 8 * kg], 16);
+                __builtin_memcpy(&al, &ps[1][r][32 * kk + 8 * kg], 16);
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int n = 2 * nv + j;
+                    h8 b;
+#pragma unroll
+                    for (int qq = 0; qq < 8; qq++) b[qq] = vt[32 * kk + 8 * kg + qq][16 * n + r];
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, o[j], 0, 0, 0);
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, o[j], 0, 0, 0);
+                }
+            }
+            // merge into the running state: the chunk's max and (tile-order) sum per head
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int h = 4 * kg + i;
+                float m = tmax[0][h], l = tsum[0][h];
+#pragma unroll
+                for (int u = 1; u < kTiles; u++) {
+                    m = fmaxf(m, tmax[u][h]);
+                    l += tsum[u][h];
+                }
+                const float mn = fmaxf(Mr[i], m);       // finite: the chunk holds position p0 < seq
+                const float a = expf(Mr[i] - mn);       // 0 on the first chunk
+                const float b = expf(m - mn);
+                Lr[i] = fmaf(Lr[i], a, l * b);
+#pragma unroll
+                for (int j = 0; j < 2; j++) oacc[j][i] = fmaf(oacc[j][i], a, o[j][i] * b);
+                Mr[i] = mn;
+            }
+        }
+    }
+    if (swave) return;
+    float *part = ws + ((size_t)kvh * nsplit + g) * kPart;
+    if (nv == 0 && r == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            part[4 * kg + i] = Mr[i];
+            part[kRows + 4 * kg + i] = Lr[i];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * (2 * nv + j) + r] = oacc[j][i];
+}
+
+// Workspaces of the entry points, kRowsSlotBytes each, per GPU.  A stream's eager calls use
+// the slot bound to that stream (bound at its first call); a call made while its stream is
+// being captured takes a free slot for good, so that the captured graph may be replayed on any
+// stream while other graphs and eager calls run.  cuda_kernels_init reserves kRowsPoolInit
+// free slots; mnemo_attention_reserve adds more (outside any capture: it allocates).  A capture
+// that finds no free slot shares its stream's slot (one warning is printed): such a graph must
+// then be replayed in order with the eager calls of that stream.  Calls that overlap in time
+// never share a slot otherwise.
+constexpr int kRowsPoolInit = 16;
 constexpr int kMaxRowsDevices = 64;
-static float *g_rows_ws[kMaxRowsDevices];
-static hipStream_t g_rows_owner[kMaxRowsDevices];
-static bool g_rows_owned[kMaxRowsDevices];
+constexpr int kMaxRowsStreams = 64;
+struct RowsPool {
+    float *free_slots[1024];
+    int nfree = 0;
+    hipStream_t stream[kMaxRowsStreams];
+    float *bound[kMaxRowsStreams];
+    int nbound = 0;
+    bool warned = false;
+};
+static RowsPool g_rows[kMaxRowsDevices];
 static std::mutex g_rows_mu;
 
-int attn_rows_ws_init() {
+static int rows_reserve_locked(RowsPool &P, int n) {
+    while (P.nfree < n && P.nfree < (int)(sizeof P.free_slots / sizeof P.free_slots[0])) {
+        void *p = nullptr;
+        if (hipMalloc(&p, kRowsSlotBytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return kErrLaunch;
+        }
+        P.free_slots[P.nfree++] = (float *)p;
+    }
+    return P.nfree >= n ? kOk : kErrBadArg;
+}
+
+int attn_rows_reserve(int n) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxRowsDevices) return kErrLaunch;
     std::lock_guard<std::mutex> lock(g_rows_mu);
-    if (g_rows_ws[dev]) return kOk;
-    void *p = nullptr;
-    if (hipMalloc(&p, kRowsWsBytes) != hipSuccess) {
-        (void)hipGetLastError();  // the per-head kernel stays the path on this GPU
-        return kErrLaunch;
-    }
-    g_rows_ws[dev] = (float *)p;
-    return kOk;
+    return rows_reserve_locked(g_rows[dev], n);
 }
+
+int attn_rows_ws_init() { return attn_rows_reserve(kRowsPoolInit); }
+
+size_t attn_rows_slot_bytes() { return kRowsSlotBytes; }
+
+// The slot for a call on stream s, or nullptr (then the per-head kernel runs).
+static float *rows_slot(hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxRowsDevices) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        cs = hipStreamCaptureStatusNone;
+    }
+    const bool capturing = cs == hipStreamCaptureStatusActive;
+    std::lock_guard<std::mutex> lock(g_rows_mu);
+    RowsPool &P = g_rows[dev];
+    if (capturing && P.nfree > 0) return P.free_slots[--P.nfree];  // the graph's own slot
+    for (int i = 0; i < P.nbound; i++)
+        if (P.stream[i] == s) {
+            if (capturing && !P.warned) {
+                P.warned = true;
+                fprintf(stderr,
+                        "[mnemo] cuda_attention_*: no free workspace slot for a graph capture; it shares its "
+                        "stream's slot (call mnemo_attention_reserve before capturing)\n");
+            }
+            return P.bound[i];
+        }
+    if (P.nbound == kMaxRowsStreams) return nullptr;
+    if (P.nfree == 0 && (capturing || rows_reserve_locked(P, 1) != kOk)) return nullptr;
+    P.stream[P.nbound] = s;
+    P.bound[P.nbound] = P.free_slots[--P.nfree];
+    return P.bound[P.nbound++];
+}
+
+void *attn_rows_kernel_ptr() { return reinterpret_cast<void *>(&attention_rows_kernel<kKvF16>); }
 
 // Returns kErrBadArg without recording an error when the split kernels do not apply.
 int launch_attention_rows(const float *q, const void *kc, const void *vc, const float *ksc, const float *vsc,
                           int kv_type, float *out, int nh, int hd, int nkv, int gqa, int seq, float scale,
                           hipStream_t s) {
-    if (hd != kHd || gqa <= 0 || gqa > kRows || nkv <= 0 || nh != nkv * gqa || seq <= 0 || seq > kMaxChunks * kChunk)
+    if (hd != kHd || gqa <= 0 || gqa > kRows || nkv <= 0 || nkv > kRowsMaxKv || nh != nkv * gqa || seq <= 0)
         return kErrBadArg;
-    if (attn_decode_workspace_bytes(nkv, seq) > kRowsWsBytes) return kErrBadArg;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxRowsDevices) return kErrBadArg;
-    float *ws = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(g_rows_mu);
-        if (!g_rows_ws[dev]) return kErrBadArg;
-        if (!g_rows_owned[dev]) {
-            g_rows_owner[dev] = s;
-            g_rows_owned[dev] = true;
-        }
-        if (g_rows_owner[dev] != s) return kErrBadArg;
-        ws = g_rows_ws[dev];
-    }
+    if (!q || !kc || !vc || !out || (kv_type == kKvInt8 && (!ksc || !vsc))) return kErrBadArg;
+    float *ws = rows_slot(s);
+    if (!ws) return kErrBadArg;
+    const int nsplit = rows_nsplit(nkv);
+    if (kv_type == kKvF16)
+        hipLaunchKernelGGL(attention_rows_kernel<kKvF16>, dim3(nkv, nsplit), dim3(kChunkThreads), 0, s, q, kc, vc,
+                           out, hd, nkv, seq, gqa, scale, ws, nsplit, ksc, vsc);
+    else
+        hipLaunchKernelGGL(attention_rows_kernel<kKvInt8>, dim3(nkv, nsplit), dim3(kChunkThreads), 0, s, q, kc, vc,
+                           out, hd, nkv, seq, gqa, scale, ws, nsplit, ksc, vsc);
     AttnDecodeArgs a{};
-    a.q = q;
-    a.kc = kc;
-    a.vc = vc;
-    a.ksc = ksc;
-    a.vsc = vsc;
     a.out = out;
     a.ws = ws;
-    a.ws_bytes = kRowsWsBytes;
     a.nh = nh;
     a.hd = hd;
     a.nkv = nkv;
     a.gqa = gqa;
-    a.max_ctx = seq;
-    a.pos_dev = nullptr;
-    a.seq_fixed = seq;
-    a.scale = scale;
-    a.v_layout = kVRows;
-    if (int rc = check_decode_args(a, kv_type)) return rc;
-    return launch_decode<false>(a, kv_type, s);
+    a.max_chunks = nsplit;
+    a.max_ctx = kChunk * nsplit;
+    a.pos_dev = (const int *)(ws + (size_t)nkv * nsplit * kPart);  // written by attention_rows_kernel
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nh, kHd / kCombDims), dim3(kCombThreads), 0, s, a);
+    return check_launch("cuda_attention (split)");
 }
 
 }  // namespace mnemo

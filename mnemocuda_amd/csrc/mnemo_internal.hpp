@@ -158,6 +158,12 @@ struct AttnDecodeArgs {
 size_t attn_decode_workspace_bytes(int n_kv_heads, int max_ctx);
 int launch_attention_decode(AttnDecodeArgs a, int kv_type, hipStream_t s);
 int attn_rows_ws_init();
+int attn_rows_reserve(int n);
+size_t attn_rows_slot_bytes();
+void *attn_rows_kernel_ptr();
+void *rope_kernel_ptr();
+void *f16_dual_kernel_ptr();
+int launch_rope(float *q, float *k, int head_dim, int pos, float theta, int nq, int nk, hipStream_t s);
 int launch_attention_rows(const float *q, const void *kc, const void *vc, const float *ksc, const float *vsc,
                           int kv_type, float *out, int nh, int hd, int nkv, int gqa, int seq, float scale,
                           hipStream_t s);

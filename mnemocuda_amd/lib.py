@@ -59,6 +59,11 @@ SIGNATURES: dict[str, tuple] = {
     "cuda_residual_add": (None, [fp, fp, fp, i32, stream_t]),
     "cuda_rope": (None, [fp, fp, i32, i32, f32, i32, i32, stream_t]),
     "cuda_f32_to_f16_dual": (None, [fp, fp, vp, vp, i32, stream_t]),
+    "cuda_get_rope_kernel_ptr": (vp, []),
+    "cuda_get_f16dual_kernel_ptr": (vp, []),
+    "cuda_get_attn_f16kv_kernel_ptr": (vp, []),
+    "mnemo_attention_reserve": (i32, [i32]),
+    "mnemo_attention_slot_bytes": (sz, []),
     "cuda_f32_to_int8_kv_dual": (None, [fp, fp, vp, vp, fp, fp, i32, i32, stream_t]),
     "cuda_attention_f16kv": (None, [vp, vp, vp, fp, i32, i32, i32, i32, i32, f32, stream_t]),
     "cuda_attention_int8kv": (None, [fp, vp, vp, fp, fp, fp, i32, i32, i32, i32, i32, f32, stream_t]),

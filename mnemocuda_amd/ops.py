@@ -389,6 +389,13 @@ def attention(q, kc, vc, out, n_heads: int, head_dim: int, n_kv_heads: int, seq_
         check(lib, "cuda_attention_int8kv")
 
 
+def attention_reserve(n_slots: int) -> None:
+    """mnemo_attention_reserve: at least n_slots free workspace slots for captured
+    cuda_attention_* calls on the current GPU (allocates; not under capture)."""
+    lib = load_library()
+    _check_rc(lib, lib.mnemo_attention_reserve(int(n_slots)), "mnemo_attention_reserve")
+
+
 def attn_prep(q, k, v, qw, kw, head_dim: int, eps: float, theta: float, pos_dev, kc, vc, ks=None, vs=None,
               v_layout: int = 0):
     """QK norm (when qw/kw are given) + RoPE + KV store at cache row pos_dev[0], one launch

@@ -490,9 +490,10 @@ def test_attention_decode_prep_bad_args(gpu):
 
 @pytest.mark.parametrize("kind", ["f16", "int8"])
 def test_attention_entry_point_paths(gpu, oracle, rng, kind):
-    """cuda_attention_* runs the split-chunk kernels on the stream that owns the library's
-    workspace and the per-head kernel elsewhere (another stream, or a sequence longer than
-    65,536 positions): every path matches the oracle."""
+    """cuda_attention_* runs the split kernel on a workspace slot bound to the calling stream:
+    on the current stream, on a second stream, and for a sequence longer than its workgroups
+    have chunks (66,000 positions: every workgroup merges several chunks), all match the
+    oracle."""
     nh, hd, nkv, scale = NH, 128, NKV, 1.0 / np.sqrt(128)
     for seq, streams in [(3000, ("current", "side")), (66000, ("current",))]:
         q = rng.standard_normal(nh * hd).astype(np.float32)
@@ -507,3 +508,36 @@ def test_attention_entry_point_paths(gpu, oracle, rng, kind):
                 gpu.ops.attention(dev(q), tkc, tvc, out, nh, hd, nkv, seq, scale, tks, tvs)
             torch.cuda.synchronize()
             assert rel_l2(host(out), want) < 1e-5, (seq, which)
+
+
+def test_attention_entry_graph_on_other_stream(gpu, rng):
+    """cuda_attention_f16kv captured on stream A and replayed on stream B while eager calls
+    with other inputs run on A: the captured call holds a workspace slot of its own, so both
+    give exactly the serial results."""
+    nh, hd, nkv, scale = NH, 128, NKV, 1.0 / np.sqrt(128)
+    q1, q2 = (dev(rng.standard_normal(nh * hd).astype(np.float32)) for _ in range(2))
+    c1 = [_to_dev(c) for c in _caches(rng, 3000, nkv, hd, "f16")[:2]]
+    c2 = [_to_dev(c) for c in _caches(rng, 2000, nkv, hd, "f16")[:2]]
+    A, B = torch.cuda.Stream(), torch.cuda.Stream()
+    ref1, ref2 = torch.empty(nh * hd, device="cuda"), torch.empty(nh * hd, device="cuda")
+    out_g, out_e = torch.empty(nh * hd, device="cuda"), torch.empty(nh * hd, device="cuda")
+    case("attention entry point: graph from stream A replayed on B next to eager calls on A")
+    with torch.cuda.stream(A):
+        gpu.ops.attention(q1, c1[0], c1[1], ref1, nh, hd, nkv, 3000, scale)
+        gpu.ops.attention(q2, c2[0], c2[1], ref2, nh, hd, nkv, 2000, scale)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=A):
+        gpu.ops.attention(q1, c1[0], c1[1], out_g, nh, hd, nkv, 3000, scale)
+    torch.cuda.synchronize()
+    for _ in range(20):
+        out_g.zero_()
+        out_e.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(B):
+            g.replay()
+        with torch.cuda.stream(A):
+            for _ in range(3):
+                gpu.ops.attention(q2, c2[0], c2[1], out_e, nh, hd, nkv, 2000, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ref1) and torch.equal(out_e, ref2)
