@@ -18,17 +18,20 @@
 //     split into two exact planes, (sc - b) * (q - 32) (even) and b * (q - 32) with
 //     b = sc & 1, and the two MFMAs chain into t (|t| < 2^24, still exact).
 //   * The fp32 rescale is a running scale: the accumulator holds the sum in units of the
-//     current (row scale d) x (token scale d8), and every sub-block does acc = acc * rho + t
-//     with rho = d8_prev / d8 of the token (one fma per output per sub-block); at a
-//     super-block boundary the rows' acc is multiplied by d_prev / d once.  The epilogue
+//     current (row scale d) x (token scale d8).  Every sub-block multiplies acc by
+//     rho = d8_prev / d8 of the token (one multiply per output per sub-block) and the MFMA
+//     then adds the sub-block's products straight into that rescaled accumulator, so t is
+//     never formed on its own: each step rounds like an fp32 sum of the exact products onto
+//     acc * rho.  At a super-block boundary the rows' acc is multiplied by d_prev / d once.  The epilogue
 //     multiplies by the last d8 * d.  A zero scale leaves the running scale unchanged and
 //     zeroes its block's operand (its products are zero).
 //   * Q4_K's min term, sum_s -(dmin*m_s) * ds_js, is one more product over the sub-block
 //     index: -dmin*m (an f16 times a 6-bit integer, 17 significant bits) is split into an
 //     f16 hi + lo pair that is exact, ds is an f16 already, and two MFMAs per 32 sub-blocks
 //     add it to the finished absolute accumulator.
-//   Against the fp64 value the only roundings are the fp32 fma per output per sub-block
-//   and the rho quotients (measured ~1e-7 relative L2).
+//   Against the fp64 value the roundings are the rescale multiply and the MFMA's fp32
+//   accumulation per output per sub-block, and the rho quotients (measured ~1e-7 relative
+//   L2).
 //
 // An int8 MFMA does not fit this product on gfx950: v_mfma_i32_16x16x64_i8 sums 64 values,
 // two sub-blocks with different token scales, and the 32-deep v_mfma_i32_16x16x32_i8 runs
@@ -375,8 +378,8 @@ __device__ __forceinline__ void read_frags(const Stage<TYPE> &st, int wi, int wj
     }
 }
 
-// acc = acc * rho + (the exact integer sub-block sums of the step): the MFMA adds its products
-// to the rescaled accumulator
+// acc = acc * rho, then the MFMA adds the step's exact products to the rescaled accumulator
+// (rounded as fp32 sums onto it)
 // (at a super-block start the row ratios come first, read from the step's own stage, which
 // no thread writes during the step)
 template <int TYPE>

@@ -515,7 +515,9 @@ __device__ __forceinline__ void experts_combine(const GemvExperts &E) {
                 __builtin_amdgcn_s_sleep(1);
                 v = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            sum += __uint_as_float((unsigned int)v);
+            // a slot still without this call's tag after the bound (a broken ordering, never
+            // seen) makes the row NaN instead of adding an earlier call's value
+            sum += (unsigned int)(v >> 32) == tag ? __uint_as_float((unsigned int)v) : __builtin_nanf("");
         }
         E.out[row] += sum;
     }

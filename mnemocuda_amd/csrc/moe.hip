@@ -401,6 +401,15 @@ static int decode_scratch(hipStream_t s, bool sync, void **out) {
             if (hipMemset(p, 0, kDecodeScratchBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
                 return set_error(kErrLaunch, "moe_decode scratch: zeroing failed");
         } else {
+            // a first call under graph capture would record the zeroing into the graph (run
+            // again on every replay): set-up belongs to cuda_kernels_init
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+                (void)hipGetLastError();
+                return set_error(kErrBadArg,
+                                 "moe_decode scratch: first use on this GPU under graph capture; call "
+                                 "cuda_kernels_init first");
+            }
             hipLaunchKernelGGL(zero_words_kernel, dim3(256), dim3(256), 0, s, (uint32_t *)p, words);
             if (int rc = check_launch("moe_decode scratch zero")) return rc;
         }

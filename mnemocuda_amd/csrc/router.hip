@@ -225,7 +225,7 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
                                                         int k, unsigned long long *__restrict__ cnt,
                                                         int *__restrict__ idx, float *__restrict__ wts, int vec4) {
     __shared__ float part[T / 64];
-    __shared__ unsigned int is_last, tag;
+    __shared__ unsigned int is_last, tag, stale;
     __shared__ float z[64 * kTopkMaxPerLane];
     // rank keys: {order-preserving bits of the logit, ~index} -- a larger key is a better
     // logit, equal logits the lower index (as `better`); 0 for a logit that never wins
@@ -238,6 +238,7 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
     // count in before the row's dot product, so that the atomic's round trip overlaps the
     // row's loads
     unsigned long long old = 0;
+    if (tid == 0) stale = 0;  // ordered before its uses by the barrier after the count-in
     if (tid == 0) old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const float v = block_sum<T>(nw ? row_dot_norm<T, V4>(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
                                     : row_dot<T, V4>(w + (size_t)row * n_cols, x, n_cols, vec4),
@@ -264,6 +265,9 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
                 __builtin_amdgcn_s_sleep(1);
                 sv = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            // a slot that never carried this call's tag (a broken ordering, never seen) marks
+            // the whole ranking stale: the weights come out NaN, so the error shows downstream
+            if ((unsigned int)(sv >> 32) != g1) stale = 1;
             const float l = __uint_as_float((unsigned int)sv);
             const bool ok = l > -1e30f;  // NaN and <= -1e30 never win
             z[i] = ok ? l : -1e30f;
@@ -314,7 +318,7 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
             sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), q));
         if (r < k) {
             idx[r] = sel_i[r];
-            wts[r] = sum > 0.0f ? e / sum : 0.0f;
+            wts[r] = stale ? __builtin_nanf("") : (sum > 0.0f ? e / sum : 0.0f);
         }
     }
 }
