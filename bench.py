@@ -411,7 +411,7 @@ def main():
     value = BYTES_LAYER * LAYERS / r["step_s"] / 1e9
     ach = BYTES_QKV / r["d_qkv"] / 1e9
     prof = ROOT / "profiles" / "gemv_qkv_fused_traffic.json"
-    traffic, kname = None, "gemv_kernel<32, 1, *, 0, 3>"
+    traffic, kname = None, "gemv_split_kernel<8, 4, 0, 3>"
     if prof.exists():
         try:
             pj = json.loads(prof.read_text())

@@ -640,6 +640,150 @@ static void launch_down_slots(const GemvArgs &a, int tm, hipStream_t stream) {
 }
 #endif
 
+#if MNEMO_GEMV_THREADS == 512
+// Split-columns form of the static GEMV.  A workgroup owns 64 / LPR rows; its W waves split
+// the columns, wave w taking the 128 * LPR columns [w * 128 LPR, (w + 1) * 128 LPR) of those
+// rows (one half super-block per lane, LPR lanes per row).  Each wave builds the x image of its
+// own columns only and reads it back alone (no workgroup barrier before the dot products);
+// the LPR lanes of a row read LPR different 16-byte words and the rows of the wave the same
+// ones (an LDS broadcast).  The waves' row sums meet in LDS once, at the end, and are added in
+// wave order.  TM: the workgroup's type, 1 Q4_K or 2 Q6_K.
+template <int LPR, int W, int XM, int TM>
+__device__ __forceinline__ void gemv_split_body(const GemvArgs &args, uint8_t (*img)[xlds_bytes(128 * LPR)],
+                                                float (*red)[64 / LPR], float *ssw) {
+    constexpr int R = 64 / LPR;
+    constexpr int CW = 128 * LPR;
+    constexpr int XPW = CW / 256;  // float4 of x per lane
+    const int w = threadIdx.x >> 6, lane = lane_id();
+    const int n = args.n_cols;
+    const int kp = (n + 255) & ~255;
+    const int uph = kp / 128;        // half super-blocks per row
+    const int c0 = w * CW;           // this wave's first column
+    const int nw = min(CW, n - c0);  // its columns (>= 4: n % 4 == 0 and c0 < n)
+    XRegs<XPW> xr, xr2;
+    load_x<XPW, XM, 64>(args.x + c0, args.x2 ? args.x2 + c0 : nullptr, nw, xr, xr2, lane);
+
+    // the weights: row base + lane / LPR, half super-block w * LPR + lane % LPR
+    const int base = (int)blockIdx.x * R;
+    int row0;
+    const GemvMat M = pass_mat(args, base, row0);
+    const int i = lane / LPR, ul = lane % LPR;
+    const int bb = TM == 1 ? kQ4KBytes : kQ6KBytes;
+    const int u = w * LPR + ul;
+    const int uc = min(u, uph - 1);
+    RawH raw;
+    {
+        const int lrow = min(base - row0 + i, M.rows - 1);
+        const uint8_t *blk = (const uint8_t *)M.w + ((size_t)lrow * (kp / 256) + (uc >> 1)) * bb;
+        if (TM == 1) load_q4k(blk, uc & 1, raw);
+        else load_q6k(blk, uc & 1, raw);
+    }
+
+    const XLds X(img[w], CW);
+    build_x<XPW, XM, 64>(xr, xr2, nw, CW, X, lane);
+    float ss = 0.0f;
+    if (XM == 2) {
+#pragma unroll
+        for (int j = 0; j < XPW; j++) {
+            if (4 * (lane + 64 * j) < nw) {
+                ss = fmaf(xr.v[j].x, xr.v[j].x, ss);
+                ss = fmaf(xr.v[j].y, xr.v[j].y, ss);
+                ss = fmaf(xr.v[j].z, xr.v[j].z, ss);
+                ss = fmaf(xr.v[j].w, xr.v[j].w, ss);
+            }
+        }
+    }
+    if (XM == 2) {
+        ss = sum64_lane63(ss);
+        if (lane == 63) ssw[w] = ss;
+    }
+    // the wave reads only what it wrote: its own LDS stores done is enough
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float v = TM == 1 ? q4k_dot(raw, uc & 1, ul * 128, X) : q6k_dot(raw, uc & 1, ul * 128, X);
+    v = u < uph ? v : 0.0f;
+    v = reduce_rows<LPR>(v);
+    if (ul == LPR - 1) red[w][i] = v;
+    __syncthreads();
+    if ((int)threadIdx.x < R) {
+        const int r = threadIdx.x;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < W; k++) acc += red[k][r];
+        if (XM == 2) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int k = 0; k < W; k++) tot += ssw[k];
+            acc *= __builtin_amdgcn_rsqf(tot / (float)n + args.eps);  // rsqrtf, as the reference (kernels.cu:718)
+        }
+        const int lr = base - row0 + r;
+        if (lr < M.rows) {
+            if (M.mode == kEpiStore) M.y[lr] = acc;
+            else if (M.mode == kEpiResidual) M.y[lr] = acc + M.res[lr];
+            else M.y[lr] += M.scale * acc;
+        }
+    }
+}
+
+// TM: types present in the launch, 1 Q4_K only, 2 Q6_K only, 3 both (each matrix then starts
+// at a multiple of the workgroup's rows, so the type is uniform per workgroup).
+template <int LPR, int W, int XM, int TM>
+__global__ void __launch_bounds__(64 * W) gemv_split_kernel(GemvArgs args) {
+    constexpr int R = 64 / LPR;
+    __shared__ __align__(16) uint8_t img[W][xlds_bytes(128 * LPR)];
+    __shared__ float red[W][R];
+    __shared__ float ssw[W];
+    if constexpr (TM == 3) {
+        const int mi = pass_matrix(args, (int)blockIdx.x * R);
+        if (args.m[mi].type == kTypeQ4K) gemv_split_body<LPR, W, XM, 1>(args, img, red, ssw);
+        else gemv_split_body<LPR, W, XM, 2>(args, img, red, ssw);
+    } else {
+        gemv_split_body<LPR, W, XM, TM>(args, img, red, ssw);
+    }
+}
+
+template <int LPR, int W, int TM>
+static void launch_split_tm(const GemvArgs &a, int blocks, hipStream_t stream) {
+    const dim3 g(blocks), b(64 * W);
+    if (a.xmode == 1) hipLaunchKernelGGL((gemv_split_kernel<LPR, W, 1, TM>), g, b, 0, stream, a);
+    else if (a.xmode == 2) hipLaunchKernelGGL((gemv_split_kernel<LPR, W, 2, TM>), g, b, 0, stream, a);
+    else hipLaunchKernelGGL((gemv_split_kernel<LPR, W, 0, TM>), g, b, 0, stream, a);
+}
+
+// LPR 8: 1024 columns per wave, 4 or 8 waves per workgroup (rows of 3076..4096 or
+// 7172..8192 columns).  Returns kErrBadArg (nothing launched, no error recorded) for launches
+// it does not take.
+int launch_gemv_split_impl(GemvArgs a, hipStream_t stream) {
+    constexpr int LPR = 8, R = 64 / LPR;
+    if (a.experts || a.n_cols < 4 || a.n_cols % 4 || a.n_cols > kMaxGemvCols) return kErrBadArg;
+    const int kp = (a.n_cols + 255) & ~255;
+    const int waves = (kp + 128 * LPR - 1) / (128 * LPR);
+    if ((waves != 4 && waves != 8) || kp <= (waves - 1) * 128 * LPR) return kErrBadArg;
+    int tm = 0;
+    for (int i = 0; i < a.nmat; i++) {
+        if (a.m[i].mode != kEpiStore && a.m[i].mode != kEpiResidual && a.m[i].mode != kEpiScaledAdd) return kErrBadArg;
+        tm |= a.m[i].type == kTypeQ4K ? 1 : 2;
+    }
+    int off = 0;
+    for (int i = 0; i < a.nmat; i++) {
+        a.off[i] = off;
+        off += (a.m[i].rows + R - 1) / R * R;  // a workgroup never spans two matrices
+    }
+    for (int i = a.nmat; i < 3; i++) a.off[i] = INT_MAX;
+    a.total_rows = off;
+    const int blocks = off / R;
+    if (waves == 4) {
+        if (tm == 1) launch_split_tm<LPR, 4, 1>(a, blocks, stream);
+        else if (tm == 2) launch_split_tm<LPR, 4, 2>(a, blocks, stream);
+        else launch_split_tm<LPR, 4, 3>(a, blocks, stream);
+    } else {
+        if (tm == 1) launch_split_tm<LPR, 8, 1>(a, blocks, stream);
+        else if (tm == 2) launch_split_tm<LPR, 8, 2>(a, blocks, stream);
+        else launch_split_tm<LPR, 8, 3>(a, blocks, stream);
+    }
+    return check_launch("gemv split");
+}
+#endif
+
 // TM: types present in the launch -- 1 Q4_K only, 2 Q6_K only, 3 both.  With both, every
 // matrix starts at a multiple of the rows of one workgroup, so the type is uniform per
 // workgroup and each workgroup runs the single-type code (the barrier of the x image

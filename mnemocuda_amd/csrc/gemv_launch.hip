@@ -1,4 +1,4 @@
-// gemv_launch.hip -- picks the GEMV workgroup size per launch.  gemv.hip is compiled for
+// gemv_launch.hip -- picks the GEMV kernel and workgroup size per launch.  gemv.hip is compiled for
 // 512-thread (g512) and 256-thread (g256) workgroups.  Measured on MI355X: 512 threads are
 // faster whenever the waves of a launch fit on the chip at once (16 per CU) or fill it many
 // times over; when they exceed one chip-full by a little (the fused Q+K+V launch: 4,608
@@ -11,6 +11,7 @@
 namespace mnemo {
 namespace g512 {
 int launch_gemv_impl(GemvArgs a, hipStream_t stream);
+int launch_gemv_split_impl(GemvArgs a, hipStream_t stream);
 int launch_gemv_experts_impl(GemvArgs a, hipStream_t stream);
 }  // namespace g512
 namespace g256 {
@@ -39,6 +40,16 @@ int launch_gemv(GemvArgs a, hipStream_t stream) {
     for (int i = 0; i < a.nmat; i++) rows += a.m[i].rows;
     const long waves = rows / (64 / lpr);
     const long chip = 16L * device_cus_launch();
+    // The split-columns kernel (8 rows x 1024 columns per wave, an x image per wave of its own
+    // columns) where the whole-row kernel leaves the chip short of work or a partial second
+    // round.  Measured on MI355X, 94 layers of distinct weights: fused Q 8192 + K 512 + V 512
+    // at 4096 columns 7.30 against 7.6-7.9 us (8.32 against 8.4-8.5 with the RMS norm); K + V
+    // 512 + 512 3.77 against 5.02; 1536 rows 3.51 against 3.83; but 4096 or 8192 rows alone
+    // 4.84 / 6.49 against 4.60 / 6.04, and O 4096 x 8192 6.61 against 6.25, stay whole-row.
+    if (waves <= chip / 4 || (waves > chip && waves <= chip + chip / 4)) {
+        const int rc = g512::launch_gemv_split_impl(a, stream);
+        if (rc != kErrBadArg) return rc;
+    }
     if (waves > chip && waves <= chip + chip / 4) return g256::launch_gemv_impl(a, stream);
     return g512::launch_gemv_impl(a, stream);
 }

@@ -32,14 +32,15 @@ import sys
 from collections import defaultdict
 from pathlib import Path
 
-# the fused QKV GEMV: a mixed-type launch (TM = 3) of the 32-lanes-per-row GEMV; the library
-# builds it for 512- and 256-thread workgroups and the QKV shape runs the 256-thread one
-QKV_KERNEL = "gemv_kernel<32, 1, *, 0, 3>"
+# the fused QKV GEMV: a mixed-type launch (TM = 3) of the split-columns GEMV (8 lanes per row,
+# 4 waves of 1024 columns, plain x), which the library picks for the QKV shape
+QKV_KERNEL = "gemv_split_kernel<8, 4, 0, 3>"
 
 
 def _is_qkv(name: str) -> bool:
-    # template arguments <LPR 32, UPL 1, XPT, x mode 0 (plain x), types 3 (Q4_K and Q6_K)>
-    return "gemv_kernel<32, 1, " in name and (", 0, 3>" in name or ", false, 3>" in name)
+    return "gemv_split_kernel<8, 4, 0, 3>" in name
+
+
 COPY_BYTES = 256 << 20  # bench.py --copy-calibration copies this many bytes
 
 
@@ -51,7 +52,8 @@ def _find(d: Path, suffix: str) -> Path:
 
 
 def stats(trace_dir: str, out_md: str, command: str, top: int = 16, only: str | None = None) -> None:
-    """only: keep the kernels whose name contains this text (e.g. 'mnemo::')"""
+    """only: keep the kernels whose name contains this text (e.g. 'mnemo::').  With the
+    kernel trace present, a kernel launched with several grid sizes gets a row per size."""
     rows = list(csv.DictReader(open(_find(Path(trace_dir), "kernel_stats.csv"))))
     if only:
         rows = [r for r in rows if only in r["Name"]]
@@ -61,6 +63,21 @@ def stats(trace_dir: str, out_md: str, command: str, top: int = 16, only: str | 
     for r in rows[:top]:
         lines.append(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                      f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f} |")
+    hits = sorted(Path(trace_dir).rglob("*kernel_trace.csv"))
+    if hits:
+        per: dict[tuple[str, int], list[float]] = defaultdict(list)
+        for r in csv.DictReader(open(hits[0])):
+            if only and only not in r["Kernel_Name"]:
+                continue
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            per[(r["Kernel_Name"], grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        names = [r["Name"] for r in rows[:top]]
+        split = [(k, v) for k, v in per.items() if k[0] in names and sum(1 for kk in per if kk[0] == k[0]) > 1]
+        if split:
+            lines += ["", "Per launch shape (kernel trace):", "", "| kernel | grid (threads) | calls | avg us | min us | max us |",
+                      "|---|---|---|---|---|---|"]
+            for (name, grid), v in sorted(split, key=lambda kv: (kv[0][0], -kv[0][1])):
+                lines.append(f"| `{name[:90]}` | {grid} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} |")
     Path(out_md).write_text("\n".join(lines) + "\n")
 
 

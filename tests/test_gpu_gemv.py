@@ -22,6 +22,9 @@ SHAPES = [
     (12, 4096, 4096), (12, 8192, 4096), (12, 512, 4096), (12, 1536, 4096), (12, 4096, 1536),
     (12, 4096, 8192), (14, 512, 4096), (14, 4096, 1536), (14, 333, 4096),
     (12, 1, 256), (14, 3, 512), (12, 7, 300), (14, 5, 1000), (12, 2, 16384),
+    # launches small enough for the split-columns kernel (1024 columns per wave), with the
+    # last wave's columns partly past n: 4000 and 3332 (4 waves), 7424 and 8192 (8 waves)
+    (12, 64, 4000), (14, 40, 3332), (12, 24, 7424), (14, 600, 8192), (12, 9, 4096),
 ]
 
 
