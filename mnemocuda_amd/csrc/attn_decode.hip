@@ -727,9 +727,10 @@ __global__ void __launch_bounds__(kChunkThreads)
 // the slot bound to that stream (bound at its first call); a call made while its stream is
 // being captured takes a free slot for good, so that the captured graph may be replayed on any
 // stream while other graphs and eager calls run.  cuda_kernels_init reserves kRowsPoolInit
-// free slots; mnemo_attention_reserve adds more (outside any capture: it allocates).  A capture
-// that finds no free slot shares its stream's slot (one warning is printed): such a graph must
-// then be replayed in order with the eager calls of that stream.  Calls that overlap in time
+// free slots; mnemo_attention_reserve adds more (outside any capture: it allocates); the calls
+// themselves never allocate.  A capture that finds no free slot shares its stream's slot (one
+// warning is printed): such a graph must then be replayed in order with the eager calls of
+// that stream.  A stream that finds none runs the per-head kernel.  Calls that overlap in time
 // never share a slot otherwise.
 constexpr int kRowsPoolInit = 16;
 constexpr int kMaxRowsDevices = 64;
@@ -791,8 +792,15 @@ static float *rows_slot(hipStream_t s) {
             }
             return P.bound[i];
         }
-    if (P.nbound == kMaxRowsStreams) return nullptr;
-    if (P.nfree == 0 && (capturing || rows_reserve_locked(P, 1) != kOk)) return nullptr;
+    if (P.nbound == kMaxRowsStreams || P.nfree == 0) {  // no allocation here: the per-head kernel runs
+        if (!P.warned) {
+            P.warned = true;
+            fprintf(stderr,
+                    "[mnemo] cuda_attention_*: no free workspace slot for this stream; the per-head kernel runs "
+                    "(call mnemo_attention_reserve)\n");
+        }
+        return nullptr;
+    }
     P.stream[P.nbound] = s;
     P.bound[P.nbound] = P.free_slots[--P.nfree];
     return P.bound[P.nbound++];
