@@ -7,7 +7,8 @@
 
 `probe` is the program the `--pmc` passes profile, each ending with the calibration copy:
   qkv  -- the fused QKV GEMV of bench.py's workload (one layer's weights, 4 launches);
-  gemm -- the M=512 Q4_K prefill GEMMs of bench.py (N=8192 and N=1536, 4 launches each);
+  gemm -- the M=512 Q4_K prefill GEMMs of bench.py (N=8192 and N=1536, one launch per weight
+          buffer over 600 MB of distinct buffers);
   moe  -- bench.py's grouped-expert prefill (configs[4], 3 calls);
   decode -- bench.py's decode layer (fused QKV with the norm, attention at position 2048, O +
           residual, the MoE block with 128 resident experts) over 4 layers of distinct
@@ -233,10 +234,14 @@ def probe(which: str = "qkv", launches: int = 4) -> None:
         aq = torch.empty(T * (H // 128) * 144, dtype=torch.uint8, device="cuda")
         ops.quantize_q8_1(acts, aq, H, T)
         for n in (QD, 1536):
-            w = synth.weights_torch(gen, Q4K, n, H, "cuda")
+            # distinct weight buffers over 600 MB (more than the 256 MB MALL), one launch each,
+            # as bench.py times them
+            nbuf = -(-(600 << 20) // (n * (H // 256) * 144))
             out = torch.empty(T, n, device="cuda")
-            for _ in range(launches):
+            for _ in range(nbuf):
+                w = synth.weights_torch(gen, Q4K, n, H, "cuda")
                 ops.gemm(w, Q4K, aq, out, n, H, T)
+                del w
         _copy_tail()
         print("probe done", flush=True)
         return
