@@ -28,7 +28,9 @@ def _run(gpu, type_id, wd, actd, M, K, N):
 @pytest.mark.parametrize("type_id,M,K,N", [(12, 256, 1024, 128), (12, 100, 512, 37), (14, 130, 768, 9),
                                            (12, 1, 256, 1), (14, 64, 1536, 200),
                                            # ragged tiles with K split 8 ways (summed with atomics)
-                                           (12, 200, 4096, 100), (14, 36, 2048, 68)])
+                                           (12, 200, 4096, 100), (14, 36, 2048, 68),
+                                           # 6 tiles of 9 super-blocks: uneven slices of K
+                                           (12, 384, 2304, 130)])
 def test_gemm_vs_oracle(gpu, oracle, type_id, M, K, N):
     rng = np.random.default_rng(M * N + K)
     w = synth.weights(rng, type_id, M, K)
