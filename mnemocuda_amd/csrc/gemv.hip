@@ -623,6 +623,134 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_down_slots_kernel(GemvArgs 
     }
 }
 
+// The same for Q6_K rows of 1536 values (the expert down projection of 1536-wide experts),
+// with the weights staged.  A 210-byte block starts at every even byte offset, so the
+// half-super-block loads of the kernel above are 16-byte loads from 4-byte aligned
+// addresses (ld16_a2), which stream at under half the rate of aligned ones here.  Instead
+// wave w reads its slot's 16-row tile (16 x 1260 contiguous bytes, 16-byte aligned) as
+// chunk 64 j + lane of the tile (aligned 16-byte loads, consecutive lanes on consecutive
+// chunks), all 20 loads issued at once, and passes the tile through LDS in two parts: the
+// first 128 half super-blocks (rows 0..9 and the first 8 of row 10, 13,440 bytes), then the
+// other 64.  Lane l takes half super-blocks l and 64 + l of the first part and 128 + l of
+// the second, reading each from LDS with the same 2-byte realignment as ld16_a2 and running
+// the kernel's dot code; the 12 partial sums of a row are added in order from LDS.
+constexpr int kStageRowBytes = 6 * kQ6KBytes;                  // 1260
+constexpr int kStageTile = 16 * kStageRowBytes;                // 20160
+constexpr int kStagePartA = 64 * kQ6KBytes;                    // 13440: 128 half super-blocks
+constexpr int kStageChunks = kStageTile / 16;                  // 1260
+constexpr int kStageChunksA = kStagePartA / 16;                // 840
+constexpr int kStageLoads = (kStageChunks + 63) / 64;          // 20 per lane
+constexpr int kStageBuf = kStagePartA + 16;                    // + a dummy 16-byte slot
+constexpr size_t kStageLds = (size_t)kSlotWaves * (kStageBuf + xlds_bytes(1536) + 192 * 4);
+
+// N 16-byte words from a 2-byte aligned LDS address (the LDS form of ld16_a2)
+template <int N>
+__device__ __forceinline__ void lds16_a2(const uint8_t *p, uint4 (&out)[N]) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 2u;
+    const uint32_t *a = (const uint32_t *)(p - sh);
+    uint32_t w[4 * N + 1];
+#pragma unroll
+    for (int i = 0; i < 4 * N + 1; i++) w[i] = a[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        out[i].x = __builtin_amdgcn_alignbyte(w[4 * i + 1], w[4 * i], sh);
+        out[i].y = __builtin_amdgcn_alignbyte(w[4 * i + 2], w[4 * i + 1], sh);
+        out[i].z = __builtin_amdgcn_alignbyte(w[4 * i + 3], w[4 * i + 2], sh);
+        out[i].w = __builtin_amdgcn_alignbyte(w[4 * i + 4], w[4 * i + 3], sh);
+    }
+}
+
+// Half super-block u (0..191) of the tile, staged at buf + its tile offset - base.
+__device__ __forceinline__ float stage_unit_dot(const uint8_t *buf, int base, int u, const XLds &X) {
+    const int row = u / 12, k = u - 12 * row, hf = k & 1;
+    const uint8_t *blk = buf + row * kStageRowBytes + (k >> 1) * kQ6KBytes - base;
+    RawH r;
+    lds16_a2<4>(blk + 64 * hf, r.q);
+    lds16_a2<2>(blk + 128 + 32 * hf, r.qh);
+    uint4 h[1];
+    lds16_a2<1>(blk + 192, h);
+    r.h = h[0];
+    r.dd = *(const uint16_t *)(blk + 208);
+    return q6k_dot(r, hf, k * 128, X);
+}
+
+template <int XM>
+__global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemv_down_stage_kernel(GemvArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int XPW = 6;  // 1536 values: 6 float4 per lane
+    __shared__ float red[kSlotWaves][16];
+    const GemvExperts &E = args.ex;
+    const int n = args.n_cols;
+    const int w = threadIdx.x >> 6, lane = lane_id();
+    uint8_t *buf = smem + (size_t)w * kStageBuf;
+    const XLds X(smem + (size_t)kSlotWaves * kStageBuf + (size_t)w * xlds_bytes(1536), 1536);
+    float *part = (float *)(smem + (size_t)kSlotWaves * (kStageBuf + xlds_bytes(1536))) + w * 192;
+    if (w < E.slots) {  // wave-uniform: waves past the slots load nothing
+        const int s = w;
+        const float *x0 = E.xs + (size_t)(2 * s) * n, *x1 = x0 + n;
+        if (XM == 0) x0 = E.xs + (size_t)s * n;  // the SwiGLU output of the gate/up launch
+        XRegs<XPW> xr, xr2;
+        load_x<XPW, XM, 64>(x0, x1, n, xr, xr2, lane);
+        int e = E.idx[s];
+        const bool ok = e >= 0 && e < E.n_experts;  // a dropped slot computes expert 0 with weight 0
+        e = ok ? e : 0;
+        const float wt = ok ? E.wt[s] : 0.0f;
+        const uint8_t *tile = E.table + (size_t)e * E.stride + E.off[0] + (size_t)blockIdx.x * kStageTile;
+        // The loads of part A, the image, then the loads of part B: all 20 loads before the
+        // image stall the issue of its instructions until the memory queue drains (13.9 us
+        // against 12.5 us for the 8-slot 4096 x 1536 launch), all of them after it start the
+        // tile late (12.9 us).  An LLVM vector type: an array of the HIP uint4 class is
+        // copied with memcpy and stays in scratch memory.
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        constexpr int kLoadsA = (kStageChunksA + 63) / 64;  // 14
+        u32x4 v[kStageLoads];
+#pragma unroll
+        for (int j = 0; j < kLoadsA; j++) v[j] = ((const u32x4 *)tile)[min(64 * j + lane, kStageChunks - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        build_x<XPW, XM, 64>(xr, xr2, n, 1536, X, lane);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = kLoadsA; j < kStageLoads; j++)
+            v[j] = ((const u32x4 *)tile)[min(64 * j + lane, kStageChunks - 1)];
+        // Every lane of a load stores (chunks of the other part into a dummy slot past the
+        // buffer): a load read only under a lane condition is sunk into it by the compiler,
+        // behind the waits of the loads before it.
+#pragma unroll
+        for (int j = 0; j < kStageLoads; j++) {
+            const int c = 64 * j + lane;
+            if (64 * j < kStageChunksA) *(u32x4 *)(buf + (c < kStageChunksA ? 16 * c : kStagePartA)) = v[j];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's image and part A are in LDS
+        part[lane] = stage_unit_dot(buf, 0, lane, X);
+        __builtin_amdgcn_sched_barrier(0);  // one unit's digit reads at a time
+        part[64 + lane] = stage_unit_dot(buf, 0, 64 + lane, X);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // part A read before it is overwritten
+#pragma unroll
+        for (int j = 0; j < kStageLoads; j++) {
+            const int c = 64 * j + lane - kStageChunksA;
+            if (64 * j + 63 >= kStageChunksA)
+                *(u32x4 *)(buf + (c >= 0 && c < kStageChunks - kStageChunksA ? 16 * c : kStagePartA)) = v[j];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        part[128 + lane] = stage_unit_dot(buf, kStagePartA, 128 + lane, X);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane < 16) {  // row lane: its 12 half super-blocks in order
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 12; k++) acc += part[12 * lane + k];
+            red[w][lane] = wt * acc;
+        }
+    }
+    __syncthreads();
+    const int row = (int)blockIdx.x * 16 + (int)threadIdx.x;
+    if (threadIdx.x < 16) {
+        float sum = 0.0f;
+        for (int k = 0; k < E.slots; k++) sum += red[k][threadIdx.x];
+        E.out[row] += sum;
+    }
+}
+
 template <int UPL, int XPW>
 static void launch_down_slots(const GemvArgs &a, int tm, hipStream_t stream) {
     constexpr int LPR = 4, P = 64 / LPR;
@@ -899,6 +1027,14 @@ int launch_gemv_experts_impl(GemvArgs a, hipStream_t stream) {
         a.total_rows = a.ex.rows;
         const int tm = a.ex.type == kTypeQ4K ? 1 : 2;
         // LPR 4: a row's uph half super-blocks over 4 lanes, UPL = uph / 4 each
+        // Q6_K 1536-value rows in whole 16-row tiles, 16-byte aligned: the staged kernel
+        if (tm == 2 && a.n_cols == 1536 && a.ex.rows % 16 == 0 &&
+            ((uintptr_t)a.ex.table % 16 | a.ex.stride % 16 | a.ex.off[0] % 16) == 0) {
+            const dim3 g(a.ex.rows / 16), b(kGemvThreads);
+            if (a.ex.act) hipLaunchKernelGGL((gemv_down_stage_kernel<0>), g, b, kStageLds, stream, a);
+            else hipLaunchKernelGGL((gemv_down_stage_kernel<1>), g, b, kStageLds, stream, a);
+            return check_launch("gemv_experts down (staged)");
+        }
         if (uph <= 4) launch_down_slots<1, 2>(a, tm, stream);
         else if (uph <= 8) launch_down_slots<2, 4>(a, tm, stream);
         else if (uph <= 12) launch_down_slots<3, 6>(a, tm, stream);

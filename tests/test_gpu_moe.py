@@ -180,7 +180,11 @@ def _routable(rng, E, H, k):
                                         (1024, 768, 24, 12, 14), (2048, 2560, 16, 6, 12), (4608, 512, 8, 4, 14),
                                         (256, 256, 1024, 16, 14), (256, 256, 1, 1, 12),
                                         (1024, 512, 128, 8, 14), (512, 256, 64, 6, 12), (512, 256, 256, 8, 14),
-                                        (512, 256, 40, 8, 14)])
+                                        (512, 256, 40, 8, 14),
+                                        # the staged Q6_K down kernel (1536-value rows): 3 of
+                                        # 8 slot waves live; the SwiGLU formed in the down
+                                        # launch (gate/up rows past 4096 values)
+                                        (2048, 1536, 16, 3, 14), (4608, 1536, 8, 4, 14)])
 def test_moe_decode_vs_oracle(gpu, oracle, H, EFF, E, k, DT):
     rng = np.random.default_rng(H + E * k)
     table = synth.expert_table(rng, E, H, EFF, DT)
