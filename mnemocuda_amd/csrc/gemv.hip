@@ -751,6 +751,101 @@ gemv_down_stage_kernel(GemvArgs args) {
     }
 }
 
+// Paired gate/up launch of the decode MoE block for rows of 4096 values (Q4_K), staged like
+// the down kernel above: a 4-wave workgroup owns 16 rows of one slot (wave w: rows
+// 4w .. 4w+3 of the gate and of the up matrix) and builds one x image (with the RMS norm,
+// XM 2) for all of them.  A wave reads its 4 gate rows (9,216 contiguous bytes, 9 aligned
+// 16-byte loads per lane, consecutive lanes on consecutive chunks), then its 4 up rows,
+// passes each part through a wave-private LDS area and runs the unchanged q4k_dot on half
+// super-blocks l and 64 + l of the part (rows l / 32 and 2 + l / 32).  768 workgroups for
+// 8 slots x 1536 rows, three per CU: one round.  Half the image builds and x reads of the
+// whole-row launch, and whole cache lines per load instruction.
+constexpr int kGuRowBytes = 16 * kQ4KBytes;        // 2304: 4096 values
+constexpr int kGuPart = 4 * kGuRowBytes;           // 9216: 4 rows
+constexpr int kGuLoads = kGuPart / 16 / 64;        // 9 per lane and part
+constexpr int kGuThreads = 256;
+constexpr size_t kGuLds = (size_t)(kGuThreads / 64) * kGuPart + xlds_bytes(4096);
+static_assert(kGuPart % 1024 == 0, "a part is whole 64-lane loads");
+
+template <int XM>
+__global__ void __launch_bounds__(kGuThreads) gemv_gateup_stage_kernel(GemvArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int XPT = 4096 / (4 * kGuThreads);  // 4 float4 of x per thread
+    __shared__ float part_ss[kGuThreads / 64];
+    const GemvExperts &E = args.ex;
+    const int w = threadIdx.x >> 6, lane = lane_id();
+    const int tiles = E.rows / 16;
+    const int s = (int)blockIdx.x / tiles, r0 = ((int)blockIdx.x - s * tiles) * 16 + 4 * w;
+    uint8_t *buf = smem + (size_t)w * kGuPart;
+    const XLds X(smem + (size_t)(kGuThreads / 64) * kGuPart, 4096);
+    XRegs<XPT> xr, xr2;
+    load_x<XPT, XM == 2 ? 2 : 0, kGuThreads>(args.x, args.x2, 4096, xr, xr2, threadIdx.x);
+    int e = E.idx[s];
+    e = e >= 0 && e < E.n_experts ? e : 0;  // a dropped slot computes expert 0 (weight 0 in the down)
+    const uint8_t *mat = E.table + (size_t)e * E.stride;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 *gsrc = (const u32x4 *)(mat + E.off[0] + (size_t)r0 * kGuRowBytes);
+    const u32x4 *usrc = (const u32x4 *)(mat + E.off[1] + (size_t)r0 * kGuRowBytes);
+    u32x4 vg[kGuLoads], vu[kGuLoads];
+#pragma unroll
+    for (int j = 0; j < kGuLoads; j++) vg[j] = gsrc[64 * j + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    // the image (every thread builds 16 values; the barrier ends it)
+    float ss = 0.0f;
+    if (XM == 2) {
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            ss = fmaf(xr.v[i].x, xr.v[i].x, ss);
+            ss = fmaf(xr.v[i].y, xr.v[i].y, ss);
+            ss = fmaf(xr.v[i].z, xr.v[i].z, ss);
+            ss = fmaf(xr.v[i].w, xr.v[i].w, ss);
+        }
+        ss = sum64_lane63(ss);
+        if (lane == 63) part_ss[w] = ss;
+    }
+    build_x<XPT, XM == 2 ? 2 : 0, kGuThreads>(xr, xr2, 4096, 4096, X, threadIdx.x);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kGuLoads; j++) vu[j] = usrc[64 * j + lane];
+    lds_barrier();  // the image (the waves' weights stay in flight)
+    float oscale = 1.0f;
+    if (XM == 2) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kGuThreads / 64; k++) tot += part_ss[k];
+        oscale = __builtin_amdgcn_rsqf(tot / 4096.0f + args.eps);  // rsqrtf, as the reference (kernels.cu:718)
+    }
+    float acc[2][2];  // [gate, up][unit l, unit 64 + l]
+#pragma unroll
+    for (int m = 0; m < 2; m++) {
+        const u32x4 *v = m == 0 ? vg : vu;
+#pragma unroll
+        for (int j = 0; j < kGuLoads; j++) *(u32x4 *)(buf + 16 * (64 * j + lane)) = v[j];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's part is in LDS
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int u = 64 * k + lane, row = u >> 5, hu = u & 31;
+            const uint8_t *blk = buf + row * kGuRowBytes + (hu >> 1) * kQ4KBytes;
+            RawH r;
+            r.h = *(const uint4 *)blk;
+#pragma unroll
+            for (int i = 0; i < 4; i++) r.q[i] = *(const uint4 *)(blk + 16 + 64 * (hu & 1) + 16 * i);
+            acc[m][k] = sum32_lane31(q4k_dot(r, hu & 1, hu * 128, X));
+            __builtin_amdgcn_sched_barrier(0);  // one unit's digit reads at a time
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the part is read before it is overwritten
+    }
+    if ((lane & 31) == 31) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int row = r0 + 2 * k + (lane >> 5);
+            E.y[(size_t)s * E.rows + row] = silu_mul(acc[0][k] * oscale, acc[1][k] * oscale);
+        }
+    }
+    if (blockIdx.x == 0)  // clear the tile counters of the down launch that follows on the stream
+        for (int t = threadIdx.x; t < E.ntiles; t += kGuThreads) E.tile_cnt[t] = 0;
+}
+
 template <int UPL, int XPW>
 static void launch_down_slots(const GemvArgs &a, int tm, hipStream_t stream) {
     constexpr int LPR = 4, P = 64 / LPR;
@@ -1040,6 +1135,18 @@ int launch_gemv_experts_impl(GemvArgs a, hipStream_t stream) {
         else if (uph <= 12) launch_down_slots<3, 6>(a, tm, stream);
         else launch_down_slots<4, 8>(a, tm, stream);
         return check_launch("gemv_experts down");
+    }
+#endif
+#if MNEMO_GEMV_THREADS == 512
+    // paired gate/up of 4096-value Q4_K rows in whole 16-row tiles, 16-byte aligned: staged
+    if (a.ex.nm == 2 && a.ex.act && a.ex.type == kTypeQ4K && a.n_cols == 4096 && a.ex.rows % 16 == 0 &&
+        a.ex.rows > 0 && ((uintptr_t)a.ex.table % 16 | a.ex.stride % 16 | a.ex.off[0] % 16 | a.ex.off[1] % 16) == 0) {
+        a.experts = 1;
+        a.nmat = 0;
+        const dim3 g(a.ex.slots * (a.ex.rows / 16)), b(kGuThreads);
+        if (a.x2) hipLaunchKernelGGL((gemv_gateup_stage_kernel<2>), g, b, kGuLds, stream, a);
+        else hipLaunchKernelGGL((gemv_gateup_stage_kernel<0>), g, b, kGuLds, stream, a);
+        return check_launch("gemv_experts gate/up (staged)");
     }
 #endif
     int lpr = 2;

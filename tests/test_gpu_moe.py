@@ -184,7 +184,9 @@ def _routable(rng, E, H, k):
                                         # the staged Q6_K down kernel (1536-value rows): 3 of
                                         # 8 slot waves live; the SwiGLU formed in the down
                                         # launch (gate/up rows past 4096 values)
-                                        (2048, 1536, 16, 3, 14), (4608, 1536, 8, 4, 14)])
+                                        (2048, 1536, 16, 3, 14), (4608, 1536, 8, 4, 14),
+                                        # the staged gate/up kernel (4096-value rows) with 3 slots
+                                        (4096, 512, 16, 3, 12)])
 def test_moe_decode_vs_oracle(gpu, oracle, H, EFF, E, k, DT):
     rng = np.random.default_rng(H + E * k)
     table = synth.expert_table(rng, E, H, EFF, DT)
