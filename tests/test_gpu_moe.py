@@ -386,3 +386,33 @@ def test_moe_decode_rmsnorm_in_place_graph(gpu, k):
         junk = torch.randn(1 << 18, device="cuda").sum()  # eager work between replays
         torch.cuda.synchronize()
         del junk
+
+
+def test_moe_decode_staged_adversarial_x(gpu, oracle):
+    """The staged gate/up (4096-value rows) and down (Q6_K 1536-value rows) launches on an
+    input with one 1e3-times value in every 32-value block, a run of zero blocks and
+    Student-t(2) tails: the two-byte x digits of each launch's image against the fp64 chain."""
+    H, EFF, E, k, DT = 4096, 1536, 16, 8, 14
+    rng = np.random.default_rng(77)
+    table = synth.expert_table(rng, E, H, EFF, DT)
+    lay = synth.expert_layout(H, EFF, DT)
+    while True:
+        x = rng.standard_t(2, H).astype(np.float32)
+        x[rng.integers(0, 32, H // 32) + 32 * np.arange(H // 32)] *= 1e3
+        x[512:768] = 0.0
+        router = (rng.standard_normal((E, H)) / np.sqrt(H) / 1e3).astype(np.float32)
+        z = np.sort(router.astype(np.float64) @ x)[::-1]
+        if z[k - 1] - z[k] > 1e-3 * max(1.0, abs(z[0])):
+            break
+    out0 = rng.standard_normal(H).astype(np.float32)
+    ws = torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    out = dev(out0)
+    idx = torch.full((k,), -1, dtype=torch.int32, device="cuda")
+    w = torch.zeros(k, device="cuda")
+    case("moe_decode staged launches, adversarial x")
+    gpu.ops.moe_decode(dev(router), dev(table), *lay, DT, dev(x), H, EFF, E, k, ws, out, idx, w)
+    _, ridx, rw, delta = _decode_ref(oracle, table, lay, DT, router, x, H, EFF, E, k)
+    assert sorted(host(idx).tolist()) == sorted(ridx.tolist())
+    err = rel_l2(host(out).astype(np.float64) - out0, delta)
+    print(f"rel_l2={err:.2e}")
+    assert err < TOL
