@@ -94,10 +94,13 @@ __device__ inline uint64_t match_mask(int v, int bits) {
     return m;
 }
 
-// One block of 1024 threads.  Pass 1 walks the pairs in chunks of 1024 (pair order = token
-// major, slot minor) and gives each pair its rank among the earlier pairs of the same
-// expert, so the expert-sorted order is deterministic: token ascending within an expert.
-// Pass 2 scans the counts, places the pairs and writes the tile list.
+// One block of 1024 threads.  Pass 1: wave w walks its own contiguous range of the pairs
+// (pair order = token major, slot minor) in steps of 64 and gives each pair its rank among
+// the earlier pairs of the same expert in that range (a wave-wide match, a per-wave count
+// per expert in LDS); the per-wave counts are then scanned across waves, so a pair's rank
+// among all earlier pairs of its expert is its wave's prefix plus its rank in the range:
+// the expert-sorted order is deterministic, token ascending within an expert.  Pass 2 scans
+// the counts, places the pairs and writes the tile list.
 __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const int *__restrict__ topk_idx, int pairs, int E,
                                                                   int bits, int *__restrict__ counts,
                                                                   int *__restrict__ offsets, int *__restrict__ rank,
@@ -105,64 +108,95 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const int *__r
                                                                   int *__restrict__ tiles, int k) {
     __shared__ int running[kMaxMoeExperts];
     __shared__ int wave_cnt[kRouteWaves][kMaxMoeExperts];
-    __shared__ int tile_base[kMaxMoeExperts];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += kRouteThreads) running[e] = 0;
+    for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wave_cnt[i / E][i % E] = 0;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-
-    for (int c0 = 0; c0 < pairs; c0 += kRouteThreads) {
-        for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) wave_cnt[i / E][i % E] = 0;
-        __syncthreads();
-        const int p = c0 + tid;
-        int e = p < pairs ? topk_idx[p] : -1;
-        if (e >= E) e = -1;  // out-of-range expert ids are dropped like empty slots
-        const int key = e < 0 ? E : e;  // E = "dropped" bucket, matched like any value
-        const uint64_t m = match_mask(key, bits);
-        const int r_wave = __popcll(m & lt);
-        if (e >= 0 && r_wave == 0) wave_cnt[wave][e] = __popcll(m);
-        __syncthreads();
-        if (e >= 0) {
-            int r = running[e] + r_wave;
-            for (int w = 0; w < wave; w++) r += wave_cnt[w][e];
-            rank[p] = r;
-        } else if (p < pairs) {
-            rank[p] = -1;
+    const int per = ((pairs + kRouteWaves - 1) / kRouteWaves + 63) & ~63;  // pairs per wave range
+    __syncthreads();
+    {
+        const int w0 = wave * per, w1 = min(w0 + per, pairs);
+        for (int c = w0; c < w1; c += 64) {  // wave-uniform
+            const int p = c + lane;
+            int e = p < w1 ? topk_idx[p] : -1;
+            if (e >= E) e = -1;  // out-of-range expert ids are dropped like empty slots
+            const int key = e < 0 ? E : e;  // E = "dropped" bucket, matched like any value
+            const uint64_t m = match_mask(key, bits);
+            const int r_in = __popcll(m & lt);
+            if (e >= 0) rank[p] = wave_cnt[wave][e] + r_in;
+            else if (p < w1) rank[p] = -1;
+            // the group's first lane adds the group; the next step's reads come after it
+            // (one wave's LDS operations complete in order)
+            if (e >= 0 && r_in == 0) wave_cnt[wave][e] += __popcll(m);
         }
-        __syncthreads();
-        for (int ex = tid; ex < E; ex += kRouteThreads) {
-            int s = 0;
-            for (int w = 0; w < kRouteWaves; w++) s += wave_cnt[w][ex];
-            running[ex] += s;
-        }
-        __syncthreads();
-    }
-    // exclusive scans of counts and of tiles per expert (E <= 512: one thread does it)
-    if (tid == 0) {
-        int acc = 0, tacc = 0;
-        for (int ex = 0; ex < E; ex++) {
-            const int c = running[ex];
-            counts[ex] = c;
-            offsets[ex] = acc;
-            tile_base[ex] = tacc;
-            acc += c;
-            tacc += (c + kMoeTileRows - 1) / kMoeTileRows;
-        }
-        tiles[0] = tacc;
     }
     __syncthreads();
-    for (int ex = 0; ex < E; ex++) {  // tiles of each expert, in expert order
-        const int nt = (running[ex] + kMoeTileRows - 1) / kMoeTileRows;
-        for (int j = tid; j < nt; j += kRouteThreads) tiles[1 + tile_base[ex] + j] = (ex << 16) | j;
-    }
-    for (int p = tid; p < pairs; p += kRouteThreads) {
-        const int r = rank[p];
-        if (r < 0) {
-            inv[p] = -1;
-            continue;
+    for (int ex = tid; ex < E; ex += kRouteThreads) {  // exclusive prefix over the waves
+        int acc = 0;
+        for (int w = 0; w < kRouteWaves; w++) {
+            const int t = wave_cnt[w][ex];
+            wave_cnt[w][ex] = acc;
+            acc += t;
         }
-        const int q = offsets[topk_idx[p]] + r;
-        inv[p] = q;
-        perm[q] = p / k;
+        running[ex] = acc;
+    }
+    __syncthreads();
+    // exclusive scans of the counts and of the tiles per expert: thread ex holds expert ex
+    // (E <= 512), a wave-wide scan (DPP shuffles), then the wave totals in wave order
+    __shared__ int wsum[2][kRouteWaves];
+    __shared__ int s_off[kMaxMoeExperts];
+    const int c = tid < E ? running[tid] : 0;
+    const int nt = (c + kMoeTileRows - 1) / kMoeTileRows;
+    int ic = c, it = nt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int a = __shfl_up(ic, o), b = __shfl_up(it, o);
+        if (lane >= o) {
+            ic += a;
+            it += b;
+        }
+    }
+    if (lane == 63) {
+        wsum[0][wave] = ic;
+        wsum[1][wave] = it;
+    }
+    __syncthreads();
+    int bc = 0, bt = 0;
+    for (int w = 0; w < wave; w++) {
+        bc += wsum[0][w];
+        bt += wsum[1][w];
+    }
+    if (tid < E) {
+        const int oc = bc + ic - c, ot = bt + it - nt;
+        counts[tid] = c;
+        offsets[tid] = oc;
+        s_off[tid] = oc;
+        for (int j = 0; j < nt; j++) tiles[1 + ot + j] = (tid << 16) | j;  // expert order
+        if (tid == E - 1) tiles[0] = ot + nt;
+    }
+    __syncthreads();
+    // place the pairs (loads of four pairs per thread in flight at a time)
+    for (int p0 = 0; p0 < pairs; p0 += 4 * kRouteThreads) {
+        int r[4], e[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = min(p0 + tid + i * kRouteThreads, pairs - 1);
+            r[i] = rank[p];
+            e[i] = topk_idx[p];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = p0 + tid + i * kRouteThreads;
+            if (p >= pairs) break;
+            if (r[i] < 0) {
+                inv[p] = -1;
+                continue;
+            }
+            const int rr = r[i] + wave_cnt[p / per][e[i]];
+            rank[p] = rr;
+            const int q = s_off[e[i]] + rr;
+            inv[p] = q;
+            perm[q] = p / k;
+        }
     }
 }
 
