@@ -972,6 +972,81 @@ static void launch_split_tm(const GemvArgs &a, int blocks, hipStream_t stream) {
     else hipLaunchKernelGGL((gemv_split_kernel<LPR, W, 0, TM>), g, b, 0, stream, a);
 }
 
+// One Q6_K matrix of 4096-value rows (the lm_head), staged: a 4-wave workgroup owns 16 rows
+// and builds one x image; wave w reads its 4 rows (13,440 contiguous, 16-byte aligned bytes:
+// 14 aligned lane-contiguous loads per lane, the chunks past the rows going to a dummy
+// slot), passes them through LDS and runs the unchanged q6k_dot on half super-blocks l and
+// 64 + l (rows l / 32 and 2 + l / 32), read with the 2-byte realignment of lds16_a2.
+constexpr int kQsRowBytes = 16 * kQ6KBytes;          // 3360: 4096 values
+constexpr int kQsPart = 4 * kQsRowBytes;             // 13440: a wave's 4 rows
+constexpr int kQsChunks = kQsPart / 16;              // 840
+constexpr int kQsLoads = (kQsChunks + 63) / 64;      // 14
+constexpr int kQsBuf = kQsPart + 16;                 // + a dummy 16-byte slot
+constexpr int kQsThreads = 256;
+constexpr size_t kQsLds = (size_t)(kQsThreads / 64) * kQsBuf + xlds_bytes(4096);
+
+__global__ void __launch_bounds__(kQsThreads) gemv_q6stage_kernel(GemvArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int XPT = 4096 / (4 * kQsThreads);  // 4 float4 of x per thread
+    const int w = threadIdx.x >> 6, lane = lane_id();
+    const GemvMat &M = args.m[0];
+    const int r0 = (int)blockIdx.x * 16 + 4 * w;
+    uint8_t *buf = smem + (size_t)w * kQsBuf;
+    const XLds X(smem + (size_t)(kQsThreads / 64) * kQsBuf, 4096);
+    XRegs<XPT> xr, xr2;
+    load_x<XPT, 0, kQsThreads>(args.x, nullptr, 4096, xr, xr2, threadIdx.x);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 *src = (const u32x4 *)((const uint8_t *)M.w + (size_t)r0 * kQsRowBytes);
+    u32x4 v[kQsLoads];
+#pragma unroll
+    for (int j = 0; j < kQsLoads; j++) v[j] = src[min(64 * j + lane, kQsChunks - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    build_x<XPT, 0, kQsThreads>(xr, xr2, 4096, 4096, X, threadIdx.x);
+    lds_barrier();  // the image only: each wave's rows wait for its own loads
+    // every lane of a load stores (a load read only under a lane condition is sunk into it)
+#pragma unroll
+    for (int j = 0; j < kQsLoads; j++) {
+        const int c = 64 * j + lane;
+        *(u32x4 *)(buf + (c < kQsChunks ? 16 * c : kQsPart)) = v[j];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    float acc[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int u = 64 * k + lane, row = u >> 5, hu = u & 31, hf = hu & 1;
+        const uint8_t *blk = buf + row * kQsRowBytes + (hu >> 1) * kQ6KBytes;
+        RawH r;
+        lds16_a2<4>(blk + 64 * hf, r.q);
+        lds16_a2<2>(blk + 128 + 32 * hf, r.qh);
+        uint4 h[1];
+        lds16_a2<1>(blk + 192, h);
+        r.h = h[0];
+        r.dd = *(const uint16_t *)(blk + 208);
+        acc[k] = sum32_lane31(q6k_dot(r, hf, hu * 128, X));
+        __builtin_amdgcn_sched_barrier(0);  // one unit's digit reads at a time
+    }
+    if ((lane & 31) == 31) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int row = r0 + 2 * k + (lane >> 5);
+            if (M.mode == kEpiStore) M.y[row] = acc[k];
+            else if (M.mode == kEpiResidual) M.y[row] = acc[k] + M.res[row];
+            else M.y[row] += M.scale * acc[k];
+        }
+    }
+}
+
+// Returns kErrBadArg (nothing launched, no error recorded) for launches it does not take.
+int launch_gemv_q6stage_impl(GemvArgs a, hipStream_t stream) {
+    if (a.experts || a.nmat != 1 || a.xmode != 0 || a.n_cols != 4096) return kErrBadArg;
+    const GemvMat &M = a.m[0];
+    if (M.type != kTypeQ6K || M.rows <= 0 || M.rows % 16 || (uintptr_t)M.w % 16 ||
+        (M.mode != kEpiStore && M.mode != kEpiResidual && M.mode != kEpiScaledAdd))
+        return kErrBadArg;
+    hipLaunchKernelGGL(gemv_q6stage_kernel, dim3(M.rows / 16), dim3(kQsThreads), kQsLds, stream, a);
+    return check_launch("gemv (staged Q6_K 4096-value rows)");
+}
+
 // LPR 8: 1024 columns per wave, 4 or 8 waves per workgroup (rows of 3076..4096 or
 // 7172..8192 columns).  Returns kErrBadArg (nothing launched, no error recorded) for launches
 // it does not take.

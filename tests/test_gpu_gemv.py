@@ -25,6 +25,9 @@ SHAPES = [
     # launches small enough for the split-columns kernel (1024 columns per wave), with the
     # last wave's columns partly past n: 4000 and 3332 (4 waves), 7424 and 8192 (8 waves)
     (12, 64, 4000), (14, 40, 3332), (12, 24, 7424), (14, 600, 8192), (12, 9, 4096),
+    # Q6_K rows of 4096 values over several rounds: the staged kernel (rows % 16 == 0), and the
+    # whole-row kernel for a row count it does not take
+    (14, 20480, 4096), (14, 20482, 4096),
 ]
 
 
