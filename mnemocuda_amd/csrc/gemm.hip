@@ -952,12 +952,15 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
     sk_row_scales<NB, R>(d, q, deff, acc);
     const _Float16 *bb = L.b[k & 1];
     const float *rb = L.rho[k & 1];
-    // the 8 ratios of each token column: two 16-byte reads
+    // the 8 ratios of each token column: two 16-byte reads (Q4_K); Q6_K reads each where it
+    // is used, to fit its 128-register budget
     f4 rr[NB][2];
+    if constexpr (TYPE == kTypeQ4K) {
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        rr[b][0] = *(const f4 *)(rb + (16 * b + c) * 8);
-        rr[b][1] = *(const f4 *)(rb + (16 * b + c) * 8 + 4);
+        for (int b = 0; b < NB; b++) {
+            rr[b][0] = *(const f4 *)(rb + (16 * b + c) * 8);
+            rr[b][1] = *(const f4 *)(rb + (16 * b + c) * 8 + 4);
+        }
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -971,11 +974,14 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
             else sk_operand6(cur[a], j, d[a] == 0.0f, a1, a2);
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                acc[a][b] *= rr[b][j >> 2][j & 3];
+                if constexpr (TYPE == kTypeQ4K) acc[a][b] *= rr[b][j >> 2][j & 3];
+                else acc[a][b] *= rb[(16 * b + c) * 8 + j];
                 acc[a][b] = mfma(a1, bf[b], acc[a][b]);
                 if constexpr (TYPE == kTypeQ6K) acc[a][b] = mfma(a2, bf[b], acc[a][b]);
             }
         }
+        // Q6_K: one sub-block's fragment reads at a time (fewer spills under the budget)
+        if constexpr (TYPE == kTypeQ6K) __builtin_amdgcn_sched_barrier(0);
     }
     lds_dma_barrier<TYPE == kTypeQ4K ? sk_q4_copies<R>() : R * kSk6Loads>();
 }
@@ -1139,8 +1145,12 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
 
 // MODE 1: SwiGLU (gate and up rows of the same features, activation rows gathered through
 // perm[], out[q*ld + f] = silu(gate) * up); MODE 2: the expert-sorted rows themselves.
+// The Q6_K kernel (70 KB of LDS) runs two workgroups per CU when it fits 128 registers: four
+// waves per SIMD instead of two (a few registers spill; 540 -> ~460 us for the cfg5 down GEMM).
+// The Q4_K kernels' 150 KB of LDS allow one workgroup per CU whatever the registers.
 template <int TYPE, int MODE>
-__global__ void __launch_bounds__(kSkThreads) gemm_skinny_kernel(GemmArgs g) {
+__global__ void __launch_bounds__(kSkThreads) __attribute__((amdgpu_waves_per_eu(TYPE == kTypeQ6K ? 4 : 1, 8)))
+gemm_skinny_kernel(GemmArgs g) {
     __shared__ __align__(16) SkLds<TYPE, sk_rows_per_wave<TYPE, MODE>() / 16> L;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if ((int)blockIdx.y >= g.tiles[-1]) return;
