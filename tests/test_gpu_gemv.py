@@ -336,3 +336,23 @@ def test_x_encoding_value_by_value(gpu, oracle):
     err = np.abs(xhat - x.astype(np.float64))
     worst = int(np.argmax(err / bound))
     assert (err <= bound).all(), f"x[{worst}]={x[worst]!r} decoded {xhat[worst]!r}, bound {bound[worst]:.3e}"
+
+
+def test_matvec_q6k_lm_head_unaligned(gpu, oracle):
+    """A Q6_K matrix of 4096-value rows over several chip rounds whose first block sits 2 bytes
+    past a 16-byte boundary: the staged kernel (aligned 16-byte loads) must decline it and the
+    whole-row kernel's realigned loads give the oracle's result."""
+    rows, cols = 20480, 4096
+    rng = np.random.default_rng(5)
+    w = synth.weights(rng, 14, rows, cols)
+    buf = torch.zeros(w.size + 210, dtype=torch.uint8, device="cuda")
+    buf[210:] = dev(w)
+    wd = buf[210:]
+    assert wd.data_ptr() % 16 == 2
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    case("matvec_q6k 20480x4096 at a 2-byte-aligned address")
+    gpu.ops.matvec_q6k(wd, dev(x), y, rows, cols)
+    err = rel_l2(host(y), oracle.gemv(14, w, x, rows, cols))
+    print(f"rel_l2={err:.2e}")
+    assert err < TOL

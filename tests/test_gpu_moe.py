@@ -416,3 +416,35 @@ def test_moe_decode_staged_adversarial_x(gpu, oracle):
     err = rel_l2(host(out).astype(np.float64) - out0, delta)
     print(f"rel_l2={err:.2e}")
     assert err < TOL
+
+
+def test_moe_decode_unaligned_table(gpu, oracle):
+    """The Qwen3 expert shape with the expert table 4 bytes past a 16-byte boundary: the
+    staged gate/up and down launches (aligned 16-byte loads) decline it and the whole-row /
+    slot-parallel kernels give the oracle chain's result."""
+    H, EFF, E, k, DT = 4096, 1536, 16, 8, 14
+    rng = np.random.default_rng(78)
+    table = synth.expert_table(rng, E, H, EFF, DT)
+    lay = synth.expert_layout(H, EFF, DT)
+    while True:
+        x = rng.standard_normal(H).astype(np.float32)
+        router = (rng.standard_normal((E, H)) / np.sqrt(H)).astype(np.float32)
+        z = np.sort(router.astype(np.float64) @ x)[::-1]
+        if z[k - 1] - z[k] > 1e-3 * max(1.0, abs(z[0])):
+            break
+    buf = torch.zeros(table.size + 4, dtype=torch.uint8, device="cuda")
+    buf[4:] = dev(table)
+    td = buf[4:]
+    assert td.data_ptr() % 16 == 4
+    out0 = rng.standard_normal(H).astype(np.float32)
+    ws = torch.zeros(gpu.ops.moe_decode_workspace_bytes(H, EFF, E, k), dtype=torch.uint8, device="cuda")
+    out = dev(out0)
+    idx = torch.full((k,), -1, dtype=torch.int32, device="cuda")
+    w = torch.zeros(k, device="cuda")
+    case("moe_decode, expert table at a 4-byte-aligned address")
+    gpu.ops.moe_decode(dev(router), td, *lay, DT, dev(x), H, EFF, E, k, ws, out, idx, w)
+    _, ridx, rw, delta = _decode_ref(oracle, table, lay, DT, router, x, H, EFF, E, k)
+    assert sorted(host(idx).tolist()) == sorted(ridx.tolist())
+    err = rel_l2(host(out).astype(np.float64) - out0, delta)
+    print(f"rel_l2={err:.2e}")
+    assert err < TOL
