@@ -15,7 +15,9 @@
 //  * O = P V: V goes through LDS so that each lane can gather 8 consecutive positions of
 //    one dim (the MFMA's K direction);
 //  * each chunk writes (max, sum, O) to the workspace; a second launch merges the chunks
-//    per query head (the flash-decoding combine).
+//    per query head (the flash-decoding combine).  Past 4 K positions (blocked V) each
+//    workgroup walks several chunks and merges them itself, so the partials stay at 64 or
+//    128 per KV head.
 // int8 caches: K and V bytes convert exactly to f16; the per-position K scale multiplies
 // the score column, the V scale is folded into P.
 #include <math.h>
@@ -31,6 +33,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 64;       // positions per wave
+
 constexpr int kHd = 128;         // head_dim of this kernel
 constexpr int kRows = 16;        // query heads per KV head handled (MFMA rows)
 constexpr int kPart = 2 * kRows + kRows * kHd;  // floats per (KV head, chunk) partial
@@ -114,24 +117,50 @@ constexpr int kPrepHeads = kRows / kChunkWaves;
 constexpr int kTiles = kChunk / 16;  // position tiles = S waves
 static_assert(kChunkWaves == 2 * kTiles && kHd == 32 * (kChunkWaves - kTiles) && kRows % kChunkWaves == 0,
               "4 S waves (16 positions each), 4 O waves (32 dims each), whole query heads per wave");
+// Long sequences (blocked V): past 64 chunks (4 K positions) a workgroup walks the chunks g,
+// g + S, g + 2S, ... of its KV head and merges them as it goes (running max, sum and O, the
+// flash-decoding update), so the launch leaves S partials per KV head instead of one per
+// chunk; the next chunk's K (S waves) and V (O waves) loads are issued as soon as the current
+// chunk's registers are free.  S = 64 up to 192 chunks, then 128 (one layer of 4 KV heads,
+// MI355X: 8 K positions 10.3 against 10.5 us, 16 K 13.5 against 15.1, 32 K 18.8 against 24.3;
+// S = 256 past 384 chunks was slower, 21.6 us at 32 K).  Shorter sequences take one chunk per
+// workgroup, with none of the loop's code.
+constexpr int kLoopChunks = 64;
+__host__ __device__ __forceinline__ int chunk_stride(int nc, bool looping) {
+    if (!looping || nc <= kLoopChunks) return nc;
+    return nc <= 192 ? 64 : 128;
+}
+
 template <int KV, int VL, bool PREP>
-__global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArgs a) {
-    __shared__ __align__(16) _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
-    __shared__ __align__(16) _Float16 vt[VL == kVRows ? kChunk : 1][kHd + 8];  // V tile [pos][dim]
-    __shared__ __align__(16) _Float16 ps[2][kRows][kChunk + 8];
-    __shared__ __align__(16) uint8_t knew[PREP ? 2 : 1][PREP ? 2 * kHd : 1];  // new K, V rows as stored
-    __shared__ float tmax[kTiles][kRows], tsum[kTiles][kRows];
-    __shared__ float new_sc[2];  // int8 scales of the new K / V rows
-    const int chunk = blockIdx.y, kvh = blockIdx.x, lane = threadIdx.x & 63;
+struct ChunkLds {
+    _Float16 qs[2][kRows][kHd + 8];  // Q hi / lo, rows padded by 16 B
+    _Float16 vt[VL == kVRows ? kChunk : 1][kHd + 8];  // V tile [pos][dim]
+    _Float16 ps[2][kRows][kChunk + 8];
+    uint8_t knew[PREP ? 2 : 1][PREP ? 2 * kHd : 1];  // new K, V rows as stored
+    float tmax[kTiles][kRows], tsum[kTiles][kRows];
+    float new_sc[2];  // int8 scales of the new K / V rows
+};
+
+// LOOP: the workgroup walks chunks g, g + stride, ... (else chunk g alone, the code of
+// one chunk with nothing of the loop left in it)
+template <int KV, int VL, bool PREP, bool LOOP>
+__device__ __forceinline__ void chunk_body(const AttnDecodeArgs &a, ChunkLds<KV, VL, PREP> &L, int pos, int seq,
+                                           int nc, int stride) {
+    auto &qs = L.qs;
+    auto &vt = L.vt;
+    auto &ps = L.ps;
+    auto &knew = L.knew;
+    auto &tmax = L.tmax;
+    auto &tsum = L.tsum;
+    auto &new_sc = L.new_sc;
+    const int g = blockIdx.y, kvh = blockIdx.x, lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int pos = a.pos_dev ? *a.pos_dev : a.seq_fixed - 1;
-    const int seq = min(pos + 1, a.max_ctx);
-    const int p0 = chunk * kChunk;
-    if (p0 >= seq) return;  // the combine reads ceil(seq / 64) chunks only
     const int G = a.gqa;
-    const size_t stride = (size_t)a.nkv * kHd;
+    const size_t stride_kv = (size_t)a.nkv * kHd;
     const int r = lane & 15, kg = lane >> 4;
-    const bool mine = PREP && pos < a.max_ctx && pos / kChunk == chunk;  // uniform
+    const int pchunk = pos / kChunk;
+    // this workgroup walks the chunk holding pos: it stores the new K / V rows
+    const bool mine_wg = PREP && pos < a.max_ctx && pchunk % stride == g;  // uniform
     const bool swave = wave < kTiles;        // S wave: position tile t
     const int t = wave & (kTiles - 1);
     const int nv = wave - kTiles;            // O wave: dims 32 nv .. 32 nv + 31 (n-tiles 2nv, 2nv+1)
@@ -163,16 +192,23 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
         fr = a.freq[lane];
     }
 
-    // ---- loads first.  S waves: the K fragments of tile t (4 steps of 32 dims; lane: position
-    // p0 + 16t + r, dims 32s + 8kg .. +7) and, for int8, the positions' K and V scales.
+    // ---- cache loads of one chunk.  S waves: the K fragments of tile t (4 steps of 32 dims;
+    // lane: position p0 + 16t + r, dims 32s + 8kg .. +7) and, for int8, the positions' K and V
+    // scales.  V, blocked layout (O waves): the O = P V fragments themselves, u = 2j + kk holds
+    // dim 16(2nv + j) + r, positions 32kk + 8kg .. +7 of the chunk (rows past the sequence are
+    // read as stored and weighted by P = 0, so the cache must hold finite values there; the
+    // caller zero-fills the blocked cache once).  Rows layout (every wave): 16-element pieces
+    // c = lane + 64u, u = 2 wave + i, of the tile (position c / 16, dims 8 (c % 16)), staged
+    // through LDS.
     const uint8_t *kc = (const uint8_t *)a.kc, *vc = (const uint8_t *)a.vc;
-    const int pt = min(p0 + 16 * t + r, seq - 1);  // this lane's position in tile t (clamped)
     uint4 kr[4];  // f16: 8 halves; int8: 8 bytes in .x/.y
     float ksc = 1.0f, vsc = 1.0f;
-    if (swave) {
+    uint4 vr[4];
+    auto load_k = [&](int p0) {
+        const int pt = min(p0 + 16 * t + r, seq - 1);  // this lane's position in tile t (clamped)
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            const size_t off = ((size_t)pt * stride + (size_t)kvh * kHd + 32 * st + 8 * kg) * EB;
+            const size_t off = ((size_t)pt * stride_kv + (size_t)kvh * kHd + 32 * st + 8 * kg) * EB;
             if (KV == kKvF16) __builtin_memcpy(&kr[st], kc + off, 16);
             else __builtin_memcpy(&kr[st], kc + off, 8);
         }
@@ -180,16 +216,10 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
             ksc = a.ksc[(size_t)pt * a.nkv + kvh];
             vsc = a.vsc[(size_t)pt * a.nkv + kvh];
         }
-    }
-    // V.  Blocked layout (O waves): the O = P V fragments themselves, u = 2j + kk holds dim
-    // 16(2nv + j) + r, positions 32kk + 8kg .. +7 of this chunk (rows past the sequence are
-    // read as stored and weighted by P = 0, so the cache must hold finite values there; the
-    // caller zero-fills the blocked cache once).  Rows layout (every wave): 16-element pieces
-    // c = lane + 64u, u = 2 wave + i, of the tile (position c / 16, dims 8 (c % 16)), staged
-    // through LDS.
-    uint4 vr[4];
-    if (VL == kVBlocked) {
-        if (!swave) {
+    };
+    auto load_v = [&](int chunk) {
+        const int p0 = chunk * kChunk;
+        if (VL == kVBlocked) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int n = 2 * nv + (u >> 1), kk = u & 1;
@@ -198,17 +228,19 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
                 if (KV == kKvF16) __builtin_memcpy(&vr[u], vc + off, 16);
                 else __builtin_memcpy(&vr[u], vc + off, 8);
             }
-        }
-    } else {
+        } else {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int c = lane + 64 * (2 * wave + i);
-            const int p = min(p0 + (c >> 4), seq - 1);
-            const size_t off = ((size_t)p * stride + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
-            if (KV == kKvF16) __builtin_memcpy(&vr[i], vc + off, 16);
-            else __builtin_memcpy(&vr[i], vc + off, 8);
+            for (int i = 0; i < 2; i++) {
+                const int c = lane + 64 * (2 * wave + i);
+                const int p = min(p0 + (c >> 4), seq - 1);
+                const size_t off = ((size_t)p * stride_kv + (size_t)kvh * kHd + 8 * (c & 15)) * EB;
+                if (KV == kKvF16) __builtin_memcpy(&vr[i], vc + off, 16);
+                else __builtin_memcpy(&vr[i], vc + off, 8);
+            }
         }
-    }
+    };
+    if (swave) load_k(g * kChunk);
+    if (VL == kVRows || !swave) load_v(g);
 
     // ---- Q rows (heads kvh*G .. +G-1) as f16 hi + lo
     if (PREP) {
@@ -226,7 +258,7 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
             qs[1][h][lane] = (_Float16)(x0 - (float)h0);
             qs[1][h][lane + kHd / 2] = (_Float16)(x1 - (float)h1);
         }
-        if (mine && wave == 0) {
+        if (mine_wg && wave == 0) {
             prep_head(k0, k1, norm, kw0, kw1, a.eps, cs, sn);
             const size_t si = (size_t)pos * a.nkv + kvh;
             const float nk = store_new_row<KV>(k0, k1, a.kcw, a.kscw, si * kHd, 1, si, knew[0]);
@@ -252,142 +284,202 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
         __builtin_memcpy(&qs[1][h][d], lo, 8);
     }
     __syncthreads();  // 1: Q rows, the new K / V rows and their scales
-    if (mine) {
-        // the loaded cache rows at pos are stale: take the new K / V rows from LDS (also where
-        // a position past pos was clamped to pos)
-        const int o = pos - p0;
-        if (swave && 16 * t + r >= o) {
+
+    // running state of the O waves: rows (heads) 4kg + i, dims of n-tiles 2nv, 2nv + 1
+    float Mr[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, Lr[4] = {0.f, 0.f, 0.f, 0.f};
+    f4 oacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int chunk = g;;) {
+        const int p0 = chunk * kChunk;
+        const int next = chunk + stride;
+        const bool more = LOOP && next < nc;  // uniform
+        if (PREP && mine_wg && chunk == pchunk) {
+            // the loaded cache rows at pos are stale: take the new K / V rows from LDS (also
+            // where a position past pos was clamped to pos)
+            const int o = pos - p0;
+            if (swave && 16 * t + r >= o) {
 #pragma unroll
-            for (int st = 0; st < 4; st++) __builtin_memcpy(&kr[st], &knew[0][(32 * st + 8 * kg) * EB], 8 * EB);
-            ksc = new_sc[0];
-            vsc = new_sc[1];
+                for (int st = 0; st < 4; st++) __builtin_memcpy(&kr[st], &knew[0][(32 * st + 8 * kg) * EB], 8 * EB);
+                ksc = new_sc[0];
+                vsc = new_sc[1];
+            }
+            if (VL == kVRows) {
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    if (4 * (2 * wave + i) + (lane >> 4) >= o)  // position of the 16-element piece, clamped
+                        __builtin_memcpy(&vr[i], &knew[1][8 * (lane & 15) * EB], 8 * EB);
+            } else if (!swave && kg == ((o >> 3) & 3)) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int n = 2 * nv + (u >> 1), kk = u & 1;
+                    if (kk != (o >> 5)) continue;
+                    uint8_t *vb = (uint8_t *)&vr[u];
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        if (j == (o & 7)) __builtin_memcpy(vb + j * EB, &knew[1][(16 * n + r) * EB], EB);
+                }
+            }
+        }
+
+        // ---- S waves: tile t of S = Q K^T (lane: heads 4kg + i, position p0 + 16t + r) and
+        // its row maxima
+        f4 sc = {0.f, 0.f, 0.f, 0.f};
+        if (swave) {
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                h8 b;
+                if (KV == kKvF16) {
+                    __builtin_memcpy(&b, &kr[st], 16);
+                } else {
+                    const int8_t *kb = (const int8_t *)&kr[st];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) b[j] = (_Float16)kb[j];
+                }
+                h8 ah, al;
+                __builtin_memcpy(&ah, &qs[0][r][32 * st + 8 * kg], 16);
+                __builtin_memcpy(&al, &qs[1][r][32 * st + 8 * kg], 16);
+                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, sc, 0, 0, 0);
+                sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, sc, 0, 0, 0);
+            }
+            const bool ok = p0 + 16 * t + r < seq;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sc[i] = ok ? sc[i] * (a.scale * ksc) : -INFINITY;
+                const float mx = max16(sc[i]);
+                if (r == 0) tmax[t][4 * kg + i] = mx;
+            }
+        }
+        __syncthreads();  // 2: the tiles' row maxima
+        if (swave) {
+            // P = exp(S - m) (times the V scale for int8) to LDS as hi + lo; the tile's row sums
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int h = 4 * kg + i;
+                float m = tmax[0][h];
+#pragma unroll
+                for (int u = 1; u < kTiles; u++) m = fmaxf(m, tmax[u][h]);  // finite: position p0 < seq
+                const float e = expf(sc[i] - m);  // exp(-inf) = 0 for masked positions
+                const float sum = sum16(e);
+                if (r == 0) tsum[t][h] = sum;
+                const float pv = e * vsc;
+                const _Float16 hi = (_Float16)pv;
+                ps[0][h][16 * t + r] = hi;
+                ps[1][h][16 * t + r] = (_Float16)(pv - (float)hi);
+            }
+            if (more) load_k(next * kChunk);  // this chunk's K and scales are used
         }
         if (VL == kVRows) {
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-                if (4 * (2 * wave + i) + (lane >> 4) >= o)  // position of the 16-element piece, clamped
-                    __builtin_memcpy(&vr[i], &knew[1][8 * (lane & 15) * EB], 8 * EB);
-        } else if (!swave && kg == ((o >> 3) & 3)) {
+            for (int i = 0; i < 2; i++) {
+                const int c = lane + 64 * (2 * wave + i);
+                h8 v;
+                if (KV == kKvF16) {
+                    __builtin_memcpy(&v, &vr[i], 16);
+                } else {
+                    const int8_t *vb = (const int8_t *)&vr[i];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int n = 2 * nv + (u >> 1), kk = u & 1;
-                if (kk != (o >> 5)) continue;
-                uint8_t *vb = (uint8_t *)&vr[u];
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    if (j == (o & 7)) __builtin_memcpy(vb + j * EB, &knew[1][(16 * n + r) * EB], EB);
+                    for (int j = 0; j < 8; j++) v[j] = (_Float16)vb[j];
+                }
+                __builtin_memcpy(&vt[c >> 4][8 * (c & 15)], &v, 16);
             }
+            if (more) load_v(next);  // the pieces are in LDS
         }
-    }
-
-    // ---- S waves: tile t of S = Q K^T (lane: heads 4kg + i, position p0 + 16t + r) and its
-    // row maxima
-    f4 sc = {0.f, 0.f, 0.f, 0.f};
-    if (swave) {
-#pragma unroll
-        for (int st = 0; st < 4; st++) {
-            h8 b;
-            if (KV == kKvF16) {
-                __builtin_memcpy(&b, &kr[st], 16);
-            } else {
-                const int8_t *kb = (const int8_t *)&kr[st];
-#pragma unroll
-                for (int j = 0; j < 8; j++) b[j] = (_Float16)kb[j];
-            }
-            h8 ah, al;
-            __builtin_memcpy(&ah, &qs[0][r][32 * st + 8 * kg], 16);
-            __builtin_memcpy(&al, &qs[1][r][32 * st + 8 * kg], 16);
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, sc, 0, 0, 0);
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, sc, 0, 0, 0);
-        }
-        const bool ok = p0 + 16 * t + r < seq;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            sc[i] = ok ? sc[i] * (a.scale * ksc) : -INFINITY;
-            const float mx = max16(sc[i]);
-            if (r == 0) tmax[t][4 * kg + i] = mx;
-        }
-    }
-    __syncthreads();  // 2: the tiles' row maxima
-    if (swave) {
-        // P = exp(S - m) (times the V scale for int8) to LDS as hi + lo; the tile's row sums
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int h = 4 * kg + i;
-            float m = tmax[0][h];
-#pragma unroll
-            for (int u = 1; u < kTiles; u++) m = fmaxf(m, tmax[u][h]);  // finite: position p0 < seq
-            const float e = expf(sc[i] - m);  // exp(-inf) = 0 for masked positions
-            const float sum = sum16(e);
-            if (r == 0) tsum[t][h] = sum;
-            const float pv = e * vsc;
-            const _Float16 hi = (_Float16)pv;
-            ps[0][h][16 * t + r] = hi;
-            ps[1][h][16 * t + r] = (_Float16)(pv - (float)hi);
-        }
-    }
-    if (VL == kVRows) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int c = lane + 64 * (2 * wave + i);
-            h8 v;
-            if (KV == kKvF16) {
-                __builtin_memcpy(&v, &vr[i], 16);
-            } else {
-                const int8_t *vb = (const int8_t *)&vr[i];
-#pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = (_Float16)vb[j];
-            }
-            __builtin_memcpy(&vt[c >> 4][8 * (c & 15)], &v, 16);
-        }
-    }
-    __syncthreads();  // 3: P, the row sums and (rows layout) the V tile
-
-    float *part = a.ws + ((size_t)kvh * a.max_chunks + chunk) * kPart;
-    if (swave) {
-        // partial m and l: the 16 heads' maxima and sums over the tiles, in tile order
-        if (wave == 0 && lane < kRows) {
+        __syncthreads();  // 3: P, the row sums and (rows layout) the V tile
+        constexpr bool single = !LOOP;  // the workgroup's only chunk (a looping one has >= 2)
+        if (single && wave == 0 && lane < kRows) {
+            // its m and l: the 16 heads' maxima and sums over the tiles, in tile order
             float m = tmax[0][lane], l = tsum[0][lane];
 #pragma unroll
             for (int u = 1; u < kTiles; u++) {
                 m = fmaxf(m, tmax[u][lane]);
                 l += tsum[u][lane];
             }
+            float *part = a.ws + ((size_t)kvh * a.max_chunks + g) * kPart;
             part[lane] = m;
             part[kRows + lane] = l;
         }
-        return;
-    }
-    // ---- O waves: O = P V for n-tiles 2nv, 2nv + 1 (16 dims each), 2 steps of 32 positions
-    f4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        if (!swave) {
+            // ---- O waves: O = P V for n-tiles 2nv, 2nv + 1 (16 dims each), 2 steps of 32
+            // positions, merged into the running state
+            f4 o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
-        h8 ah, al;
-        __builtin_memcpy(&ah, &ps[0][r][32 * kk + 8 * kg], 16);
-        __builtin_memcpy(&al, &ps[1][r][32 * kk + 8 * kg], 16);
+            for (int kk = 0; kk < 2; kk++) {
+                h8 ah, al;
+                __builtin_memcpy(&ah, &ps[0][r][32 * kk + 8 * kg], 16);
+                __builtin_memcpy(&al, &ps[1][r][32 * kk + 8 * kg], 16);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = 2 * nv + j;
-            h8 b;
-            if (VL == kVRows) {
+                for (int j = 0; j < 2; j++) {
+                    const int n = 2 * nv + j;
+                    h8 b;
+                    if (VL == kVRows) {
 #pragma unroll
-                for (int q = 0; q < 8; q++) b[q] = vt[32 * kk + 8 * kg + q][16 * n + r];
-            } else if (KV == kKvF16) {
-                __builtin_memcpy(&b, &vr[2 * j + kk], 16);
-            } else {
-                const int8_t *vb = (const int8_t *)&vr[2 * j + kk];
+                        for (int q = 0; q < 8; q++) b[q] = vt[32 * kk + 8 * kg + q][16 * n + r];
+                    } else if (KV == kKvF16) {
+                        __builtin_memcpy(&b, &vr[2 * j + kk], 16);
+                    } else {
+                        const int8_t *vb = (const int8_t *)&vr[2 * j + kk];
 #pragma unroll
-                for (int q = 0; q < 8; q++) b[q] = (_Float16)vb[q];
+                        for (int q = 0; q < 8; q++) b[q] = (_Float16)vb[q];
+                    }
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, o[j], 0, 0, 0);
+                    o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, o[j], 0, 0, 0);
+                }
             }
-            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, o[j], 0, 0, 0);
-            o[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, o[j], 0, 0, 0);
+            if (VL == kVBlocked && more) load_v(next);  // this chunk's fragments are used
+            if (single) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) oacc[j] = o[j];
+            } else {
+                // the chunk's max and (tile-order) sum per head, merged into the running state
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int h = 4 * kg + i;
+                    float m = tmax[0][h], l = tsum[0][h];
+#pragma unroll
+                    for (int u = 1; u < kTiles; u++) {
+                        m = fmaxf(m, tmax[u][h]);
+                        l += tsum[u][h];
+                    }
+                    const float mn = fmaxf(Mr[i], m);  // finite: the chunk holds position p0 < seq
+                    const float ea = expf(Mr[i] - mn);
+                    const float eb = expf(m - mn);
+                    Lr[i] = fmaf(Lr[i], ea, l * eb);
+#pragma unroll
+                    for (int j = 0; j < 2; j++) oacc[j][i] = fmaf(oacc[j][i], ea, o[j][i] * eb);
+                    Mr[i] = mn;
+                }
+            }
+        }
+        if (!more) break;
+        __syncthreads();  // 4: this chunk's P, maxima, sums and V tile are read
+        chunk = next;
+    }
+    if (swave) return;
+    // ---- the partial: m and l of the 16 heads (a single chunk's came from wave 0),
+    // O[16][128] (this wave's 32 dims)
+    float *part = a.ws + ((size_t)kvh * a.max_chunks + g) * kPart;
+    if (LOOP && nv == 0 && r == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            part[4 * kg + i] = Mr[i];
+            part[kRows + 4 * kg + i] = Lr[i];
         }
     }
-    // ---- partial O[16][128]: this wave's 32 dims
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * (2 * nv + j) + r] = o[j][i];
+        for (int i = 0; i < 4; i++) part[2 * kRows + (4 * kg + i) * kHd + 16 * (2 * nv + j) + r] = oacc[j][i];
+}
+
+template <int KV, int VL, bool PREP>
+__global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArgs a) {
+    __shared__ __align__(16) ChunkLds<KV, VL, PREP> L;
+    const int pos = a.pos_dev ? *a.pos_dev : a.seq_fixed - 1;
+    const int seq = min(pos + 1, a.max_ctx);
+    const int nc = (seq + kChunk - 1) / kChunk;
+    const int stride = chunk_stride(nc, VL == kVBlocked);
+    if ((int)blockIdx.y >= stride) return;  // the combine reads `stride` partials per KV head
+    if (stride < nc) chunk_body<KV, VL, PREP, VL == kVBlocked>(a, L, pos, seq, nc, stride);
+    else chunk_body<KV, VL, PREP, false>(a, L, pos, seq, nc, stride);
 }
 
 // Merge of the chunks' (max, sum, O): grid (query head, quarter of head_dim), 256 threads =
@@ -408,7 +500,8 @@ __global__ void __launch_bounds__(kCombThreads) attn_combine_kernel(AttnDecodeAr
     const int h = blockIdx.x, tid = threadIdx.x;
     const int kvh = h / a.gqa, hh = h % a.gqa;
     const int seq = min((a.pos_dev ? *a.pos_dev : a.seq_fixed - 1) + 1, a.max_ctx);
-    const int nc = (seq + kChunk - 1) / kChunk;
+    const int nchunks = (seq + kChunk - 1) / kChunk;
+    const int nc = chunk_stride(nchunks, a.loop_split != 0);  // partials per KV head
     const float *base = a.ws + (size_t)kvh * a.max_chunks * kPart;
     const int dl = tid % kCombDims, g = tid / kCombDims;
     const int d = (int)blockIdx.y * kCombDims + dl;
@@ -475,6 +568,7 @@ static int check_decode_args(AttnDecodeArgs &a, int kv_type) {
         return set_error(kErrBadArg, "attention_decode: workspace %zu < %zu bytes", a.ws_bytes,
                          attn_decode_workspace_bytes(a.nkv, a.max_ctx));
     a.max_chunks = (a.max_ctx + kChunk - 1) / kChunk;
+    a.loop_split = a.v_layout == kVBlocked;
     return 0;
 }
 

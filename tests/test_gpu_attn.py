@@ -266,7 +266,10 @@ def _blocked(v, max_ctx, nkv, hd):
 @pytest.mark.parametrize("kind", ["f16", "int8"])
 @pytest.mark.parametrize("seq,nh,nkv,max_ctx", [(1, NH, NKV, 8192), (63, NH, NKV, 8192), (64, NH, NKV, 8192),
                                                 (65, NH, NKV, 8192), (1000, NH, NKV, 8192), (4097, NH, NKV, 8192),
-                                                (300, 32, 4, 8192), (200, 8, 8, 8192), (1000, NH, NKV, 1000)])
+                                                (300, 32, 4, 8192), (200, 8, 8, 8192), (1000, NH, NKV, 1000),
+                                                # past 128 chunks each workgroup walks several (merged as it goes)
+                                                (8193, NH, NKV, 16384), (10000, NH, NKV, 16384),
+                                                (33000, NH, NKV, 40960), (20000, 8, 8, 20000)])
 def test_attention_decode(gpu, oracle, rng, kind, seq, nh, nkv, max_ctx, v_layout):
     q = rng.standard_normal(nh * HD).astype(np.float32)
     kc, vc, ks, vs = _caches(rng, max_ctx, nkv, HD, kind)
@@ -386,7 +389,7 @@ def _prep_inputs(rng, kind, max_ctx, nh, nkv, v_layout, pos):
 @pytest.mark.parametrize("kind", ["f16", "int8"])
 @pytest.mark.parametrize("pos,nh,nkv,max_ctx", [(0, NH, NKV, 4096), (63, NH, NKV, 4096), (64, NH, NKV, 4096),
                                                 (1000, NH, NKV, 4096), (130, 32, 4, 512), (77, 8, 8, 200),
-                                                (199, 8, 8, 200)])
+                                                (199, 8, 8, 200), (9000, NH, NKV, 12000), (8191, NH, NKV, 8192)])
 def test_attention_decode_prep_matches_two_step(gpu, rng, kind, v_layout, norm, pos, nh, nkv, max_ctx):
     """mnemo_attention_decode_prep == mnemo_attn_prep then mnemo_attention_decode, bit for bit:
     the output, both caches (and int8 scales); q, k, v are left unchanged."""
