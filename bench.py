@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the full decode-step tok/s (147 GB of experts)")
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--decode-pos", type=int, default=2048, help="KV-cache position of the first decoded token")
+    ap.add_argument("--decode-long-pos", type=int, default=32768,
+                    help="a second position the same graph is timed at (long-context decode; 0: skip)")
     ap.add_argument("--decode-max-ctx", type=int, default=40960,
                     help="KV-cache allocation in positions (the model's context length, as a server allocates it)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -205,12 +207,13 @@ def gpu_bench(args):
         decode = attn = None
         if not args.no_decode:
             attn = attention_bench(s)
-            decode = decode_bench(gen, s, layers, args.decode_tokens, args.decode_pos, args.decode_max_ctx)
+            decode = decode_bench(gen, s, layers, args.decode_tokens, args.decode_pos, args.decode_max_ctx,
+                                  args.decode_long_pos)
     return dict(step_s=step_s, wall=wall, d_qkv=d_qkv, d_q=d_q, d_kv=d_kv, d_o=d_o, gemm=gemm, moe=moe,
                 decode=decode, attn=attn)
 
 
-def decode_bench(gen, stream, layers, tokens, ctx_pos, cache_ctx=40960):
+def decode_bench(gen, stream, layers, tokens, ctx_pos, cache_ctx=40960, long_pos=0):
     """configs[2] inside a full decode step (forward.c:687-1077 per layer, then the lm_head
     and sampling, forward.c:1601-1707), one token at cache position ctx_pos, ctx_pos+1, ...:
     per layer  fused Q/K/V with the attention RMS norm -> GQA decode attention over 0..pos
@@ -219,7 +222,8 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos, cache_ctx=40960):
     Q4_K 4096->1536 x 8, down Q6_K 1536->4096 x 8, weighted sum added to the residual);
     then the final norm, lm_head Q6_K 151936 x 4096 and top-p sampling.  All 128 experts of
     all 94 layers are resident (147 GB); the KV cache rows below ctx_pos hold random
-    earlier tokens.  One hipGraph per token (the position advances on the device)."""
+    earlier tokens.  One hipGraph per token (the position advances on the device); with
+    long_pos the same graph is timed again from that position (long-context decode)."""
     import torch
     from mnemocuda_amd import ops, synth
     E, k, EFF, VOCAB = 128, 8, 1536, 151936
@@ -281,15 +285,20 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos, cache_ctx=40960):
             res.copy_(X0)
             g.replay()
         torch.cuda.synchronize()
-        pos.fill_(ctx_pos)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for t in range(tokens):
-            res.copy_(X0)
-            g.replay()
-        b.record(stream)
-        torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / tokens
+        def timed(p0):
+            pos.fill_(p0)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for t in range(tokens):
+                res.copy_(X0)
+                g.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / tokens
+
+        ms = timed(ctx_pos)
+        # the same graph later in the context (the position lives on the device)
+        long_ms = timed(long_pos) if 0 < long_pos and long_pos + tokens <= max_ctx else None
     moe_bytes = (E * H * 4 + H * 4 + E * 4) + k * (2 * EFF * (H // 256) * 144 + H * (EFF // 256) * 210)
     kv_bytes = 2 * NKV * HD * 2 * (ctx_pos + tokens // 2)  # K + V rows read per layer, mean position
     per_tok = (BYTES_LAYER + moe_bytes + kv_bytes) * LAYERS + VOCAB * (H // 256) * 210
@@ -299,7 +308,9 @@ def decode_bench(gen, stream, layers, tokens, ctx_pos, cache_ctx=40960):
             "context_position": ctx_pos, "cache_positions": max_ctx, "bytes_per_token": per_tok, "GBps": round(per_tok / ms / 1e6, 1),
             "frac_hbm_peak": round(per_tok / ms / 1e6 / HBM_PEAK_GBS, 4),
             "experts_resident_GB": round(E * LAYERS * stride / 1e9, 1),
-            "launches_per_token": LAYERS * 7 + 5}
+            "launches_per_token": LAYERS * 7 + 5,
+            "long_context": None if long_ms is None else {"context_position": long_pos, "tok_s": round(1e3 / long_ms, 1),
+                                                          "ms_per_token": round(long_ms, 3)}}
 
 
 def attention_bench(stream, lengths=(1024, 4096, 16384, 32768)):
