@@ -181,11 +181,12 @@ def _copy_tail() -> None:
     torch.cuda.synchronize()
 
 
-def _decode_probe(torch, ops, synth, gen, layers: int = 4, tokens: int = 3, pos0: int = 2048) -> None:
+def _decode_probe(torch, ops, synth, gen, layers: int = 4, tokens: int = 3, pos0: int = 2048,
+                  max_ctx: int = 4096) -> None:
     """the calls of bench.py's decode step, eager, on `layers` layers of distinct weights"""
     Q4K, Q6K, H, QD, KVD = 12, 14, 4096, 8192, 512
     E, k, EFF, VOCAB = 128, 8, 1536, 151936
-    NH, NKV, HD, EPS, THETA, max_ctx = 64, 4, 128, 1e-6, 1e6, 4096
+    NH, NKV, HD, EPS, THETA = 64, 4, 128, 1e-6, 1e6
     stride, g_off, u_off, d_off = synth.expert_layout(H, EFF, Q6K)
     L = [dict(q=synth.weights_torch(gen, Q4K, QD, H, "cuda"), k=synth.weights_torch(gen, Q4K, KVD, H, "cuda"),
               v=synth.weights_torch(gen, Q6K, KVD, H, "cuda"), o=synth.weights_torch(gen, Q4K, H, QD, "cuda"),
@@ -260,8 +261,9 @@ def probe(which: str = "qkv", launches: int = 4) -> None:
         _copy_tail()
         print("probe done", flush=True)
         return
-    if which == "decode":
-        _decode_probe(torch, ops, synth, gen)
+    if which in ("decode", "decode_long"):
+        # decode_long: the same step from KV position 32,768 of a 40,960-position cache
+        _decode_probe(torch, ops, synth, gen, **({"pos0": 32768, "max_ctx": 40960} if which == "decode_long" else {}))
         _copy_tail()
         print("probe done", flush=True)
         return
