@@ -30,6 +30,7 @@
 
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
+#include "x_image.hpp"
 
 namespace mnemo {
 // This file is compiled once per workgroup size (MNEMO_GEMV_THREADS) into the namespace
@@ -48,40 +49,7 @@ static_assert(kGemvThreads >= 256 && kGemvThreads <= 1024 && kGemvThreads % 64 =
 constexpr int xpt_for(int kp_max) { return (kp_max + 4 * kGemvThreads - 1) / (4 * kGemvThreads); }
 
 // ------------------------------------------------------------------ x preparation
-// LDS image of x for a padded length kp (multiple of 256):
-//   int8 d1[kp + 128] | uint8 d2[kp + 128] | float u[kp/32] | float s32[kp/32] | float s16[kp/16]
-// The digit planes are stored in 16-byte words, interleaved by 128-column chunk: column c
-// lives in word ((c % 128) / 16) * (kp/128 + 1) + c / 128.  Lane ul reads chunk ul, so the
-// 16-byte reads of one instruction hit consecutive words (no bank conflicts); the +1
-// skew keeps the 4-byte writes of the preparation conflict-free as well.
-struct XLds {
-    int8_t *d1;
-    int8_t *d2;
-    float *u;
-    float *s32;
-    float *s16;
-    int nch1;  // 128-column chunks + 1
-    __device__ XLds(uint8_t *base, int kp)
-        : d1((int8_t *)base), d2((int8_t *)(base + kp + 128)), u((float *)(base + 2 * kp + 256)),
-          s32((float *)(base + 2 * kp + 256 + kp / 8)), s16((float *)(base + 2 * kp + 256 + kp / 4)),
-          nch1(kp / 128 + 1) {}
-    // byte offset of column c (c % 16 == 0 gives a 16-byte aligned word)
-    __device__ __forceinline__ int off(int c) const {
-        return ((((c & 127) >> 4) * nch1 + (c >> 7)) << 4) + (c & 15);
-    }
-};
-
-__host__ __device__ constexpr size_t xlds_bytes(int kp) { return (size_t)2 * kp + 256 + kp / 2; }
-
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    // silu(g) * u, the reference's expression (kernels.cu:686-687)
-    return g / (1.0f + expf(-g)) * u;
-}
-
-template <int XPT>  // float4 of x per thread: kp <= 4 * XPT * kGemvThreads
-struct XRegs {
-    float4 v[XPT];
-};
+// (the image layout, XLds, and build_x are in x_image.hpp: the router builds the same image)
 
 // One 16-byte load per 4 elements from e clamped to n-4 (x may be unaligned; the host
 // rejects n < 4), so the instruction sequence is fixed.
@@ -96,91 +64,6 @@ __device__ __forceinline__ void load_x(const float *__restrict__ x0, const float
         const int ec = min(e, n - 4);
         __builtin_memcpy(&R.v[i], x0 + ec, 16);
         if (XM != 0) __builtin_memcpy(&R2.v[i], x1 + ec, 16);
-    }
-}
-
-__device__ __forceinline__ uint32_t umax_dpp8(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor1, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppXor2, 0xF, 0xF, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowHalfMirror, 0xF, 0xF, false));
-    return v;
-}
-
-// The digit planes and sums of the elements held by tid (one of NT threads); no barrier.
-template <int XPT, int XM, int NT>
-__device__ __forceinline__ void build_x(const XRegs<XPT> &R, const XRegs<XPT> &R2, int n, int kp, const XLds &X,
-                                        int tid) {
-    const int lane = lane_id();
-    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23: adding it rounds to an integer (RNE)
-    const bool ragged = (n & 3) != 0;      // uniform (the host rejects ragged n for XM == 2)
-
-#pragma unroll
-    for (int i = 0; i < XPT; i++) {
-        // computed unconditionally (a load used only under a branch would be sunk into it,
-        // behind the weight loads); only the stores are guarded
-        const int e4 = tid + i * NT;
-        const bool store = 4 * e4 < kp;  // uniform per 8-lane group: kp is a multiple of 256
-        const int e = 4 * e4;
-        float v[4] = {R.v[i].x, R.v[i].y, R.v[i].z, R.v[i].w};
-        if (XM != 0) {
-            const float g[4] = {R2.v[i].x, R2.v[i].y, R2.v[i].z, R2.v[i].w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = XM == 1 ? silu_mul(v[j], g[j]) : v[j] * g[j];
-        }
-        if (ragged) {
-            // element e+j sits at v[j + sh], sh = e - min(e, n-4) (non-zero only in the last
-            // partial group); elements >= n are zero
-            const int sh = e - min(e, n - 4);
-            float t[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int k = min(j + sh, 3);
-                float a = v[3];
-                a = k == 2 ? v[2] : a;
-                a = k == 1 ? v[1] : a;
-                a = k == 0 ? v[0] : a;
-                t[j] = e + j < n ? a : 0.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = t[j];
-        } else if (n != kp) {  // uniform: columns n .. kp-1 of the last super-block are zero
-            const uint32_t keep = e < n ? ~0u : 0u;
-#pragma unroll
-            for (int j = 0; j < 4; j++) v[j] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v[j]) & keep);
-        }
-        // max |v| over the 8 lanes of the sub-block (|v| as float max3 with abs modifiers:
-        // two instructions; non-negative floats order like their bits for the DPP max)
-        const float a4 = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        const float amax = __builtin_bit_cast(float, umax_dpp8(__builtin_bit_cast(uint32_t, a4)));
-        const float u = amax * (1.0f / 32767.0f);
-        const float inv = amax > 0.0f ? 32767.0f * __builtin_amdgcn_rcpf(amax) : 0.0f;
-        // q = rne(v * inv): |v * inv| <= 32767 (1 + 2^-22), so |q| <= 32767.  The low half of
-        // (t + magic) is q in two's complement: byte 1 is the signed digit d1 = q >> 8, byte 0
-        // the unsigned digit d2 = q & 255, and q = 256 d1 + d2.
-        uint32_t b1[4];
-        float s4 = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            b1[j] = __builtin_bit_cast(uint32_t, fmaf(v[j], inv, kMagic));
-            s4 += v[j];
-        }
-        // gather bytes: selector byte k picks byte sel_k of {src0 (4..7), src1 (0..3)}
-        const uint32_t w1 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0C0C0501u) |
-                            __builtin_amdgcn_perm(b1[3], b1[2], 0x05010C0Cu);
-        const uint32_t w2 = __builtin_amdgcn_perm(b1[1], b1[0], 0x0C0C0400u) |
-                            __builtin_amdgcn_perm(b1[3], b1[2], 0x04000C0Cu);
-        const float s16 = sum4(s4);                             // 4 lanes x 4 = 16 elements
-        const float s32 = s16 + dpp_f<kDppRowHalfMirror>(s16);  // 8 lanes = 32 elements
-        if (store) {
-            const int o = X.off(e);
-            *(uint32_t *)(X.d1 + o) = w1;
-            *(uint32_t *)(X.d2 + o) = w2;
-            if ((lane & 7) == 0) {
-                X.u[e >> 5] = u;
-                X.s32[e >> 5] = s32;
-            }
-            if ((lane & 3) == 0) X.s16[e >> 4] = s16;
-        }
     }
 }
 
@@ -779,11 +662,22 @@ __global__ void __launch_bounds__(kGuThreads) gemv_gateup_stage_kernel(GemvArgs 
     uint8_t *buf = smem + (size_t)w * kGuPart;
     const XLds X(smem + (size_t)(kGuThreads / 64) * kGuPart, 4096);
     XRegs<XPT> xr, xr2;
-    load_x<XPT, XM == 2 ? 2 : 0, kGuThreads>(args.x, args.x2, 4096, xr, xr2, threadIdx.x);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    // XM 3: the router's image of x * g, 16-byte words copied into LDS (every thread loads:
+    // clamped, stored only where inside the image)
+    constexpr int kImgWords = (int)(xlds_bytes(4096) / 16);
+    constexpr int kImgPer = (kImgWords + kGuThreads - 1) / kGuThreads;
+    u32x4 im[XM == 3 ? kImgPer : 1];
+    if (XM == 3) {
+#pragma unroll
+        for (int i = 0; i < kImgPer; i++)
+            im[i] = ((const u32x4 *)args.ximg)[min((int)threadIdx.x + kGuThreads * i, kImgWords - 1)];
+    } else {
+        load_x<XPT, XM == 2 ? 2 : 0, kGuThreads>(args.x, args.x2, 4096, xr, xr2, threadIdx.x);
+    }
     int e = E.idx[s];
     e = e >= 0 && e < E.n_experts ? e : 0;  // a dropped slot computes expert 0 (weight 0 in the down)
     const uint8_t *mat = E.table + (size_t)e * E.stride;
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 *gsrc = (const u32x4 *)(mat + E.off[0] + (size_t)r0 * kGuRowBytes);
     const u32x4 *usrc = (const u32x4 *)(mat + E.off[1] + (size_t)r0 * kGuRowBytes);
     u32x4 vg[kGuLoads], vu[kGuLoads];
@@ -803,12 +697,22 @@ __global__ void __launch_bounds__(kGuThreads) gemv_gateup_stage_kernel(GemvArgs 
         ss = sum64_lane63(ss);
         if (lane == 63) part_ss[w] = ss;
     }
-    build_x<XPT, XM == 2 ? 2 : 0, kGuThreads>(xr, xr2, 4096, 4096, X, threadIdx.x);
+    if (XM == 3) {
+        uint8_t *ximg = smem + (size_t)(kGuThreads / 64) * kGuPart;
+#pragma unroll
+        for (int i = 0; i < kImgPer; i++) {
+            const int c = (int)threadIdx.x + kGuThreads * i;
+            if (c < kImgWords) *(u32x4 *)(ximg + 16 * c) = im[i];
+        }
+    } else {
+        build_x<XPT, XM == 2 ? 2 : 0, kGuThreads>(xr, xr2, 4096, 4096, X, threadIdx.x);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < kGuLoads; j++) vu[j] = usrc[64 * j + lane];
     lds_barrier();  // the image (the waves' weights stay in flight)
     float oscale = 1.0f;
+    if (XM == 3) oscale = *args.xscale;
     if (XM == 2) {
         float tot = 0.0f;
 #pragma unroll
@@ -1219,7 +1123,8 @@ int launch_gemv_experts_impl(GemvArgs a, hipStream_t stream) {
         a.experts = 1;
         a.nmat = 0;
         const dim3 g(a.ex.slots * (a.ex.rows / 16)), b(kGuThreads);
-        if (a.x2) hipLaunchKernelGGL((gemv_gateup_stage_kernel<2>), g, b, kGuLds, stream, a);
+        if (a.ximg) hipLaunchKernelGGL((gemv_gateup_stage_kernel<3>), g, b, kGuLds, stream, a);
+        else if (a.x2) hipLaunchKernelGGL((gemv_gateup_stage_kernel<2>), g, b, kGuLds, stream, a);
         else hipLaunchKernelGGL((gemv_gateup_stage_kernel<0>), g, b, kGuLds, stream, a);
         return check_launch("gemv_experts gate/up (staged)");
     }

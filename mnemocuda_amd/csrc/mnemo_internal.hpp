@@ -90,6 +90,10 @@ struct GemvArgs {
     float eps;
     const float *x;
     const float *x2;
+    // expert gate/up with the RMS norm: the image of x * g (x_image.hpp layout) and 1 / rms,
+    // built by the router launch before it (null: the launch builds them itself)
+    const uint8_t *ximg;
+    const float *xscale;
     int experts;  // 0: the static matrices m[]; 1: expert mode (ex)
     GemvExperts ex;
 };

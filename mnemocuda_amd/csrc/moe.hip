@@ -28,6 +28,7 @@
 
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
+#include "x_image.hpp"
 
 namespace mnemo {
 
@@ -39,7 +40,8 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
 int launch_matvec_f32(const float *w, const float *x, float *y, int n_rows, int n_cols, hipStream_t s);
 int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k, hipStream_t s);
 int launch_router_topk(const float *w, const float *x, const float *nw, float eps, unsigned long long *slots, int n,
-                       int n_cols, int k, unsigned long long *cnt, int *idx, float *wts, hipStream_t stream);
+                       int n_cols, int k, unsigned long long *cnt, int *idx, float *wts, uint8_t *img,
+                       float *img_scale, hipStream_t stream);
 
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
@@ -288,12 +290,12 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
 //
 // Workspace: router arrival counter (64 bits) | tagged logit slots [E] (64 bits each) |
 // idx[k] | w[k] | gate/up rows [k][2][eff] | tagged partial slots [k][hidden] (64 bits
-// each, used when the down launch combines through partials) | tile counters [hidden],
-// each 256-byte aligned.  The counter sits at offset 0 whatever the sizes, so a workspace
+// each, used when the down launch combines through partials) | tile counters [hidden] |
+// the router's image of the normed x with 1 / rms (x_image.hpp), each 256-byte aligned.  The counter sits at offset 0 whatever the sizes, so a workspace
 // shared by calls of different shapes never finds other data there.  Zero the workspace
 // once when allocating it; calls keep the counter and slots valid from then on.
 struct MoeDecodeLayout {
-    size_t rcnt, logits, idx, w, gu, partial, cnt, total;
+    size_t rcnt, logits, idx, w, gu, partial, cnt, img, total;
 };
 
 static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
@@ -311,6 +313,7 @@ static MoeDecodeLayout moe_decode_layout(int hidden, int eff, int E, int k) {
     L.gu = take((size_t)k * 2 * eff * 4);
     L.partial = take((size_t)k * hidden * 8);
     L.cnt = take((size_t)hidden * 4);
+    L.img = take(xlds_bytes((hidden + 255) & ~255) + 16);  // the image, then 1 / rms
     L.total = o;
     return L;
 }
@@ -345,14 +348,22 @@ int launch_moe_decode(const float *router_w, const void *experts, size_t expert_
 
     // with norm_w, x is the raw hidden state and both the router and the gate/up launch apply
     // the RMS norm themselves (the reference's separate rms_norm launch, forward.c:800-806)
+    // with the norm, router workgroup 0 also writes the image of x * g and 1 / rms, which the
+    // staged gate/up launch copies instead of building its own (one build instead of one per
+    // workgroup, and no x or norm-weight loads in front of its weight loads)
+    const size_t img_bytes = xlds_bytes((hidden + 255) & ~255);
+    uint8_t *img = norm_w ? w8 + L.img : nullptr;
+    float *img_scale = norm_w ? (float *)(w8 + L.img + img_bytes) : nullptr;
     int rc = launch_router_topk(router_w, x, norm_w, eps, slots, E, hidden, k,
-                                (unsigned long long *)(w8 + L.rcnt), idx, wts, s);
+                                (unsigned long long *)(w8 + L.rcnt), idx, wts, img, img_scale, s);
     if (rc) return rc;
 
     GemvArgs a;
     memset(&a, 0, sizeof a);
     a.x = x;
     a.x2 = norm_w;
+    a.ximg = img;
+    a.xscale = img_scale;
     a.eps = eps;
     a.n_cols = hidden;
     a.ex.table = (const uint8_t *)experts;

@@ -11,6 +11,7 @@
 //                    order as the reference so the bytes match exactly.
 #include "mnemo_common.hpp"
 #include "mnemo_internal.hpp"
+#include "x_image.hpp"
 
 namespace mnemo {
 
@@ -172,7 +173,8 @@ int launch_topk_softmax(const float *scores, int *idx, float *wts, int n, int k,
 // rms_norm_kernel, kernels.cu:692-722) inside every workgroup: each holds all of x.
 template <int T, int V4>
 __device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, const float *__restrict__ x,
-                                              const float *__restrict__ nw, int n_cols, float eps, float *part) {
+                                              const float *__restrict__ nw, int n_cols, float eps, float *part,
+                                              float *img_scale) {
     typedef float fv4 __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x;
     const fv4 *w4 = (const fv4 *)wr, *x4 = (const fv4 *)x, *n4w = (const fv4 *)nw;
@@ -197,6 +199,7 @@ __device__ __forceinline__ float row_dot_norm(const float *__restrict__ wr, cons
     for (int i = 0; i < T / 64; i++) tot += part[i];
     __syncthreads();  // part[] is reused by block_sum
     const float scale = __builtin_amdgcn_rsqf(tot / (float)n_cols + eps);  // rsqrtf, as the reference (kernels.cu:718)
+    if (img_scale && blockIdx.x == 0 && tid == 0) *img_scale = scale;
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < V4; i++) {
@@ -223,7 +226,8 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
                                                         const float *__restrict__ nw, float eps,
                                                         unsigned long long *__restrict__ slots, int n, int n_cols,
                                                         int k, unsigned long long *__restrict__ cnt,
-                                                        int *__restrict__ idx, float *__restrict__ wts, int vec4) {
+                                                        int *__restrict__ idx, float *__restrict__ wts, int vec4,
+                                                        uint8_t *img, float *img_scale) {
     __shared__ float part[T / 64];
     __shared__ unsigned int is_last, tag, stale;
     __shared__ float z[64 * kTopkMaxPerLane];
@@ -240,7 +244,7 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
     unsigned long long old = 0;
     if (tid == 0) stale = 0;  // ordered before its uses by the barrier after the count-in
     if (tid == 0) old = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float v = block_sum<T>(nw ? row_dot_norm<T, V4>(w + (size_t)row * n_cols, x, nw, n_cols, eps, part)
+    const float v = block_sum<T>(nw ? row_dot_norm<T, V4>(w + (size_t)row * n_cols, x, nw, n_cols, eps, part, img_scale)
                                     : row_dot<T, V4>(w + (size_t)row * n_cols, x, n_cols, vec4),
                                  part);
     if (tid == 0) {
@@ -252,6 +256,21 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
         if (is_last)  // {g, n - 1} + 1 + (2^32 - n) = {g + 1, 0}
             __hip_atomic_fetch_add(cnt, (1ull << 32) - (unsigned long long)n, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (img && nw && row == 0) {
+        // after its logit is out: the image of x * g for the gate/up launch that follows, and
+        // (in row_dot_norm) 1 / rms, which multiplies that launch's finished sums; the same
+        // float4 per thread as row_dot_norm's, reloaded from the caches
+        XRegs<V4> R, R2;
+        const int n4 = n_cols / 4;
+#pragma unroll
+        for (int i = 0; i < V4; i++) {
+            const int j = min(tid + i * T, n4 - 1);
+            R.v[i] = ((const float4 *)x)[j];
+            R2.v[i] = ((const float4 *)nw)[j];
+        }
+        const int kp = (n_cols + 255) & ~255;
+        build_x<V4, 2, T>(R, R2, n_cols, kp, XLds(img, kp), tid);
     }
     __syncthreads();
     if (!is_last) return;
@@ -324,7 +343,8 @@ __global__ void __launch_bounds__(T) router_topk_kernel(const float *__restrict_
 }
 
 int launch_router_topk(const float *w, const float *x, const float *nw, float eps, unsigned long long *slots, int n,
-                       int n_cols, int k, unsigned long long *cnt, int *idx, float *wts, hipStream_t stream) {
+                       int n_cols, int k, unsigned long long *cnt, int *idx, float *wts, uint8_t *img,
+                       float *img_scale, hipStream_t stream) {
     constexpr int T = kRouterThreads, kMaxV4 = 8;
     if (!w || !x || !slots || !cnt || !idx || !wts || n <= 0 || n_cols <= 0 || k <= 0 || k > kTopkMaxK ||
         k > n || n > 64 * kTopkMaxPerLane)
@@ -338,13 +358,13 @@ int launch_router_topk(const float *w, const float *x, const float *nw, float ep
     // float4s per thread: the fewest that cover the row
     if (n_cols <= 4 * 2 * T)
         hipLaunchKernelGGL((router_topk_kernel<T, 2>), dim3(n), dim3(T), 0, stream, w, x, nw, eps, slots, n, n_cols, k,
-                           cnt, idx, wts, vec4);
+                           cnt, idx, wts, vec4, img, img_scale);
     else if (n_cols <= 4 * 4 * T)
         hipLaunchKernelGGL((router_topk_kernel<T, 4>), dim3(n), dim3(T), 0, stream, w, x, nw, eps, slots, n, n_cols, k,
-                           cnt, idx, wts, vec4);
+                           cnt, idx, wts, vec4, img, img_scale);
     else
         hipLaunchKernelGGL((router_topk_kernel<T, kMaxV4>), dim3(n), dim3(T), 0, stream, w, x, nw, eps, slots, n,
-                           n_cols, k, cnt, idx, wts, vec4);
+                           n_cols, k, cnt, idx, wts, vec4, img, img_scale);
     return check_launch("router_topk");
 }
 
