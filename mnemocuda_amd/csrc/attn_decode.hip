@@ -627,7 +627,7 @@ int launch_attention_decode_prep(AttnDecodeArgs a, int kv_type, float theta, hip
 //    (whose arguments hold no length) reads it.
 // With at most nsplit chunks every workgroup takes one chunk and the partials are exactly
 // those of attn_chunk_kernel.
-constexpr int kSplitTarget = 256;  // workgroups per launch (one per CU)
+constexpr int kSplitTarget = 512;  // workgroups per launch (two per CU)
 constexpr int kRowsMaxKv = kSplitTarget;
 static int rows_nsplit(int nkv) { return max(1, kSplitTarget / nkv); }
 // partials for nkv * nsplit <= kSplitTarget workgroups, then the header (one int)
