@@ -15,7 +15,7 @@
 //  * O = P V: V goes through LDS so that each lane can gather 8 consecutive positions of
 //    one dim (the MFMA's K direction);
 //  * each chunk writes (max, sum, O) to the workspace; a second launch merges the chunks
-//    per query head (the flash-decoding combine).  Past 4 K positions (blocked V) each
+//    per query head (the flash-decoding combine).  Past 4 K positions (8 K with V rows) each
 //    workgroup walks several chunks and merges them itself, so the partials stay at 64 or
 //    128 per KV head.
 // int8 caches: K and V bytes convert exactly to f16; the per-position K scale multiplies
@@ -117,7 +117,7 @@ constexpr int kPrepHeads = kRows / kChunkWaves;
 constexpr int kTiles = kChunk / 16;  // position tiles = S waves
 static_assert(kChunkWaves == 2 * kTiles && kHd == 32 * (kChunkWaves - kTiles) && kRows % kChunkWaves == 0,
               "4 S waves (16 positions each), 4 O waves (32 dims each), whole query heads per wave");
-// Long sequences (blocked V): past 64 chunks (4 K positions) a workgroup walks the chunks g,
+// Long sequences: past 64 chunks (4 K positions; 128 with V rows) a workgroup walks the chunks g,
 // g + S, g + 2S, ... of its KV head and merges them as it goes (running max, sum and O, the
 // flash-decoding update), so the launch leaves S partials per KV head instead of one per
 // chunk; the next chunk's K (S waves) and V (O waves) loads are issued as soon as the current
@@ -126,9 +126,12 @@ static_assert(kChunkWaves == 2 * kTiles && kHd == 32 * (kChunkWaves - kTiles) &&
 // S = 256 past 384 chunks was slower, 21.6 us at 32 K).  Shorter sequences take one chunk per
 // workgroup, with none of the loop's code.
 constexpr int kLoopChunks = 64;
-__host__ __device__ __forceinline__ int chunk_stride(int nc, bool looping) {
-    if (!looping || nc <= kLoopChunks) return nc;
-    return nc <= 192 ? 64 : 128;
+// looping: 0 never (the entry-point kernel's partials), 1 blocked V, 2 V rows (from 128 chunks
+// on, S = 128: 14.6 against 15.1 us at 16 K, 21.0 against 24.0 at 32 K, but 11.0 against 10.2
+// at 8 K with S = 64)
+__host__ __device__ __forceinline__ int chunk_stride(int nc, int looping) {
+    if (looping == 0 || nc <= (looping == 1 ? kLoopChunks : 2 * kLoopChunks)) return nc;
+    return looping == 1 && nc <= 192 ? 64 : 128;
 }
 
 template <int KV, int VL, bool PREP>
@@ -476,9 +479,9 @@ __global__ void __launch_bounds__(kChunkThreads) attn_chunk_kernel(AttnDecodeArg
     const int pos = a.pos_dev ? *a.pos_dev : a.seq_fixed - 1;
     const int seq = min(pos + 1, a.max_ctx);
     const int nc = (seq + kChunk - 1) / kChunk;
-    const int stride = chunk_stride(nc, VL == kVBlocked);
+    const int stride = chunk_stride(nc, VL == kVBlocked ? 1 : 2);
     if ((int)blockIdx.y >= stride) return;  // the combine reads `stride` partials per KV head
-    if (stride < nc) chunk_body<KV, VL, PREP, VL == kVBlocked>(a, L, pos, seq, nc, stride);
+    if (stride < nc) chunk_body<KV, VL, PREP, true>(a, L, pos, seq, nc, stride);
     else chunk_body<KV, VL, PREP, false>(a, L, pos, seq, nc, stride);
 }
 
@@ -501,7 +504,7 @@ __global__ void __launch_bounds__(kCombThreads) attn_combine_kernel(AttnDecodeAr
     const int kvh = h / a.gqa, hh = h % a.gqa;
     const int seq = min((a.pos_dev ? *a.pos_dev : a.seq_fixed - 1) + 1, a.max_ctx);
     const int nchunks = (seq + kChunk - 1) / kChunk;
-    const int nc = chunk_stride(nchunks, a.loop_split != 0);  // partials per KV head
+    const int nc = chunk_stride(nchunks, a.loop_split);  // partials per KV head
     const float *base = a.ws + (size_t)kvh * a.max_chunks * kPart;
     const int dl = tid % kCombDims, g = tid / kCombDims;
     const int d = (int)blockIdx.y * kCombDims + dl;
@@ -568,7 +571,7 @@ static int check_decode_args(AttnDecodeArgs &a, int kv_type) {
         return set_error(kErrBadArg, "attention_decode: workspace %zu < %zu bytes", a.ws_bytes,
                          attn_decode_workspace_bytes(a.nkv, a.max_ctx));
     a.max_chunks = (a.max_ctx + kChunk - 1) / kChunk;
-    a.loop_split = a.v_layout == kVBlocked;
+    a.loop_split = a.v_layout == kVBlocked ? 1 : 2;
     return 0;
 }
 

@@ -146,7 +146,7 @@ struct AttnDecodeArgs {
     size_t ws_bytes;
     int nh, hd, nkv, gqa;
     int max_ctx, max_chunks;
-    int loop_split;      // decode launches with blocked V: workgroups walk several chunks on long sequences
+    int loop_split;      // decode launches: workgroups walk several chunks on long sequences (1 blocked V, 2 V rows)
     const int *pos_dev;  // sequence length = min(*pos_dev + 1, max_ctx)
     int seq_fixed;       // with pos_dev NULL: the sequence length (a host value)
     float scale;
