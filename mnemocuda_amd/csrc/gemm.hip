@@ -425,6 +425,10 @@ template <int TYPE, bool ATOMIC>
 __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     __shared__ __align__(16) Stage<TYPE> lds[3];
     __shared__ float dlast[kBM], d8last[2][kBN];
+    // Q4_K: the headers of the split's super-blocks (up to kMhSb per row), kept as the loaders
+    // pass them, for the min term after the loop
+    constexpr int kMhSb = 16;
+    __shared__ uint4 mhdr[TYPE == kTypeQ4K ? kBM * kMhSb : 1];
     const int tid = threadIdx.x;
     // the wave index as a scalar, so that every per-wave decision below is a scalar branch
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -460,7 +464,9 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     RawA ra[kPF];
 #pragma unroll
     for (int p = 0; p < kPF; p++) load_step<TYPE>(wrow, arow, min(ks0 + p, last), lp, rw[p], ra[p]);
+    const bool keep_hdr = TYPE == kTypeQ4K && sb1 - sb0 <= kMhSb;  // uniform
     store_step<TYPE>(rw[0], ra[0], ks0, lp, lds[0], lr, ls, true);
+    if (keep_hdr && lp == 0) mhdr[lr * kMhSb] = rw[0].h;
     store_step<TYPE>(rw[1], ra[1], ks0 + 1, lp, lds[1], lr, ls, ks0 + 1 < ks1);
     lds_barrier();
     Frags<TYPE> fr;
@@ -479,6 +485,9 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
                 read_frags<TYPE>(lds[(b + 1) % 3], wi, wj, kh, lane, fr);
                 store_step<TYPE>(rw[(r + 2) % kPF], ra[(r + 2) % kPF], ks + 2, lp, lds[(b + 2) % 3], lr, ls,
                                  ks + 2 < ks1);
+                // (ks + 2 - ks0) % 4 == (p + 2) % 4: a compile-time test
+                if (keep_hdr && lp == 0 && ((p + 2) & 3) == 0 && ks + 2 < ks1)
+                    mhdr[lr * kMhSb + ((ks + 2 - ks0) >> 2)] = rw[(r + 2) % kPF].h;
                 lds_barrier();
             }
         }
@@ -499,8 +508,9 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     }
 
     // Q4_K min term, sum_s -(dmin*m_s)_i * ds_js, added to the absolute accumulator after
-    // the loop (its header reads touch every weight line again; in front of the pipeline
-    // they cost ~2 us more on the M=8192 GEMM).  Windows of 32 sub-blocks
+    // the loop, from the headers the loaders kept in LDS (up to 16 super-blocks per split;
+    // reading them again from memory touched every weight line a second time: M = 8192
+    // 78-80 us against 80-81).  Windows of 32 sub-blocks
     // (4 super-blocks), wave parity kh taking windows kh, kh+2, ...; lane group q = lane/16
     // holds super-block 4w + q of its row / token (K index 8q + s of the MFMA = sub-block s of
     // that super-block).
@@ -513,8 +523,12 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
             uint4 hdr[4], blk[kNB][2];
 #pragma unroll
             for (int a = 0; a < 4; a++) {
-                const uint8_t *rp = g.W + (size_t)min(i0 + wi + 16 * a + (lane & 15), g.M - 1) * wrow_bytes;
-                hdr[a] = valid ? ld16(rp + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
+                if (keep_hdr) {  // the headers the loaders kept (no second pass over the weight lines)
+                    hdr[a] = valid ? mhdr[(wi + 16 * a + (lane & 15)) * kMhSb + (sb - sb0)] : make_uint4(0, 0, 0, 0);
+                } else {
+                    const uint8_t *rp = g.W + (size_t)min(i0 + wi + 16 * a + (lane & 15), g.M - 1) * wrow_bytes;
+                    hdr[a] = valid ? ld16(rp + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
+                }
             }
 #pragma unroll
             for (int b = 0; b < kNB; b++) {
