@@ -425,10 +425,14 @@ template <int TYPE, bool ATOMIC>
 __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     __shared__ __align__(16) Stage<TYPE> lds[3];
     __shared__ float dlast[kBM], d8last[2][kBN];
-    // Q4_K: the headers of the split's super-blocks (up to kMhSb per row), kept as the loaders
-    // pass them, for the min term after the loop
+    // Q4_K min term: the operands of the split's super-blocks (up to kMhSb), kept as the
+    // loaders pass them -- per weight row and super-block the 8 six-bit mins (one byte each)
+    // and dmin, per token and sub-block the f16 ds of its Q8_1 block
     constexpr int kMhSb = 16;
-    __shared__ uint4 mhdr[TYPE == kTypeQ4K ? kBM * kMhSb : 1];
+    constexpr int kQ4 = TYPE == kTypeQ4K;
+    __shared__ uint2 mhm[kQ4 ? kBM * kMhSb : 1];
+    __shared__ uint16_t mhd[kQ4 ? kBM * kMhSb : 1];
+    __shared__ __align__(16) uint16_t dsk[kQ4 ? kBN * kMhSb * 8 : 8];
     const int tid = threadIdx.x;
     // the wave index as a scalar, so that every per-wave decision below is a scalar branch
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -464,10 +468,24 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     RawA ra[kPF];
 #pragma unroll
     for (int p = 0; p < kPF; p++) load_step<TYPE>(wrow, arow, min(ks0 + p, last), lp, rw[p], ra[p]);
-    const bool keep_hdr = TYPE == kTypeQ4K && sb1 - sb0 <= kMhSb;  // uniform
+    const bool keep_min = TYPE == kTypeQ4K && sb1 - sb0 <= kMhSb;  // uniform
+    // step q (relative to ks0) of the split: the loader of a row's first part keeps its mins
+    // and dmin at the super-block's first step, the loader of a sub-block's first values its ds
+    auto keep = [&](const RawW &w, const RawA &a, int q, bool first_step, bool live) {
+        if (!keep_min || !live) return;
+        if (lp == 0 && first_step) {
+            const uint32_t s1 = w.h.z, s2 = w.h.w;  // scale bytes 4-7, 8-11 (get_scale_min_k4)
+            mhm[lr * kMhSb + (q >> 2)] =
+                make_uint2(s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+            mhd[lr * kMhSb + (q >> 2)] = (uint16_t)(w.h.x >> 16);
+        }
+        if (((kVP * lp) & 31) == 0)
+            dsk[lr * kMhSb * 8 + (q >> 2) * 8 + 2 * (q & 3) + ((kVP * lp) >> 5)] = (uint16_t)(a.ds >> 16);
+    };
     store_step<TYPE>(rw[0], ra[0], ks0, lp, lds[0], lr, ls, true);
-    if (keep_hdr && lp == 0) mhdr[lr * kMhSb] = rw[0].h;
+    keep(rw[0], ra[0], 0, true, true);
     store_step<TYPE>(rw[1], ra[1], ks0 + 1, lp, lds[1], lr, ls, ks0 + 1 < ks1);
+    keep(rw[1], ra[1], 1, false, ks0 + 1 < ks1);
     lds_barrier();
     Frags<TYPE> fr;
     read_frags<TYPE>(lds[0], wi, wj, kh, lane, fr);
@@ -486,8 +504,7 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
                 store_step<TYPE>(rw[(r + 2) % kPF], ra[(r + 2) % kPF], ks + 2, lp, lds[(b + 2) % 3], lr, ls,
                                  ks + 2 < ks1);
                 // (ks + 2 - ks0) % 4 == (p + 2) % 4: a compile-time test
-                if (keep_hdr && lp == 0 && ((p + 2) & 3) == 0 && ks + 2 < ks1)
-                    mhdr[lr * kMhSb + ((ks + 2 - ks0) >> 2)] = rw[(r + 2) % kPF].h;
+                keep(rw[(r + 2) % kPF], ra[(r + 2) % kPF], ks + 2 - ks0, ((p + 2) & 3) == 0, ks + 2 < ks1);
                 lds_barrier();
             }
         }
@@ -508,9 +525,9 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     }
 
     // Q4_K min term, sum_s -(dmin*m_s)_i * ds_js, added to the absolute accumulator after
-    // the loop, from the headers the loaders kept in LDS (up to 16 super-blocks per split;
-    // reading them again from memory touched every weight line a second time: M = 8192
-    // 78-80 us against 80-81).  Windows of 32 sub-blocks
+    // the loop, from the operands the loaders kept in LDS (up to 16 super-blocks per split;
+    // reading the headers and the Q8_1 block heads again from memory touched every weight
+    // line a second time and 4096 activation lines per workgroup).  Windows of 32 sub-blocks
     // (4 super-blocks), wave parity kh taking windows kh, kh+2, ...; lane group q = lane/16
     // holds super-block 4w + q of its row / token (K index 8q + s of the MFMA = sub-block s of
     // that super-block).
@@ -521,14 +538,36 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
             const int sb = sb0 + 4 * w + q;
             const bool valid = sb < sb1;
             uint4 hdr[4], blk[kNB][2];
+            if (keep_min) {  // the operands the loaders kept: no second pass over weights or activations
+                const int rs = valid ? sb - sb0 : 0;
+                h8 bd[kNB];
+#pragma unroll
+                for (int b = 0; b < kNB; b++) {
+                    bd[b] = *(const h8 *)&dsk[(wj + 16 * b + (lane & 15)) * kMhSb * 8 + rs * 8];
+                    if (!valid) bd[b] = h8{};
+                }
+#pragma unroll
+                for (int a = 0; a < 4; a++) {
+                    const int row = wi + 16 * a + (lane & 15);
+                    const uint2 mm = mhm[row * kMhSb + rs];
+                    const float dmin = valid ? h2f(mhd[row * kMhSb + rs]) : 0.0f;
+                    h8 hi, lo;
+#pragma unroll
+                    for (int t = 0; t < 8; t++) {
+                        const float v = -dmin * (float)(((t < 4 ? mm.x : mm.y) >> (8 * (t & 3))) & 0xFFu);  // exact
+                        const _Float16 h = (_Float16)v;
+                        hi[t] = h;
+                        lo[t] = (_Float16)(v - (float)h);
+                    }
+#pragma unroll
+                    for (int b = 0; b < kNB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
+                }
+                continue;
+            }
 #pragma unroll
             for (int a = 0; a < 4; a++) {
-                if (keep_hdr) {  // the headers the loaders kept (no second pass over the weight lines)
-                    hdr[a] = valid ? mhdr[(wi + 16 * a + (lane & 15)) * kMhSb + (sb - sb0)] : make_uint4(0, 0, 0, 0);
-                } else {
-                    const uint8_t *rp = g.W + (size_t)min(i0 + wi + 16 * a + (lane & 15), g.M - 1) * wrow_bytes;
-                    hdr[a] = valid ? ld16(rp + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
-                }
+                const uint8_t *rp = g.W + (size_t)min(i0 + wi + 16 * a + (lane & 15), g.M - 1) * wrow_bytes;
+                hdr[a] = valid ? ld16(rp + (size_t)sb * kQ4KBytes) : make_uint4(0, 0, 0, 0);
             }
 #pragma unroll
             for (int b = 0; b < kNB; b++) {

@@ -83,7 +83,10 @@ def test_gemm_zero_scales_and_range(gpu, oracle, type_id):
             assert rel_l2(got[j], ref[j]) < TOL, j
 
 
-@pytest.mark.parametrize("type_id,M,K,N", [(12, 8192, 4096, 512), (12, 1536, 4096, 512), (14, 4096, 1536, 512)])
+@pytest.mark.parametrize("type_id,M,K,N", [(12, 8192, 4096, 512), (12, 1536, 4096, 512), (14, 4096, 1536, 512),
+                                           # 144 tiles, K unsplit: 18 super-blocks per workgroup, more than
+                                           # the min term keeps in LDS (it reads them from memory)
+                                           (12, 2048, 4608, 1152)])
 def test_gemm_baseline_shapes(gpu, oracle, type_id, M, K, N):
     rng = np.random.default_rng(M + N)
     w = synth.weights(rng, type_id, M, K)
