@@ -93,19 +93,33 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
+// The 8 six-bit mins of a Q4_K super-block as bytes, sub-blocks 0-3 / 4-7 (the packed form of
+// get_scale_min_k4, kernels.cu:45-53: m_j = scales[j+4] & 63 for j < 4, else
+// (scales[j+4] >> 4) | ((scales[j] >> 6) << 4)); hdr.z, hdr.w hold scale bytes 4-7, 8-11.
+__device__ __forceinline__ uint2 q4k_mins(const uint4 &hdr) {
+    return make_uint2(hdr.z & 0x3F3F3F3Fu, ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u));
+}
 // Q4_K min-term operand of one super-block: for its 8 sub-blocks, -dmin * m_s as an exact
-// f16 hi + lo pair (dmin is an f16, m a 6-bit integer: 17 significant bits).
-__device__ __forceinline__ void q4k_min_operand(const uint4 &hdr, h8 &hi, h8 &lo) {
-    const float dmin = h2f(hdr.x >> 16);
+// f16 hi + lo pair (dmin is an f16, m a 6-bit integer: 17 significant bits), in packed f16:
+// hi = the product rounded, lo = fma(m, -dmin, -hi), the remainder (at most 6 significant
+// bits, a multiple of dmin's last place: exact, also in the subnormal range)
+__device__ __forceinline__ void q4k_min_operand_m(uint2 mins, uint32_t dmin_bits, h8 &hi, h8 &lo) {
+    const _Float16 nd = -__builtin_bit_cast(_Float16, (uint16_t)dmin_bits);
+    const h2 ndd = {nd, nd};
+    const h2 off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    uint32_t H[4], L[4];
 #pragma unroll
-    for (int s = 0; s < 8; s++) {
-        uint32_t sc, m;
-        q4k_scale_min(hdr.y, hdr.z, hdr.w, s, sc, m);
-        const float v = -dmin * (float)m;  // exact in fp32
-        const _Float16 h = (_Float16)v;
-        hi[s] = h;
-        lo[s] = (_Float16)(v - (float)h);  // the remainder has at most 6 significant bits
+    for (int i = 0; i < 4; i++) {
+        const h2 m = magic_pair(i < 2 ? mins.x : mins.y, (i & 1) ? kSelHi : kSelLo) + off;  // exact
+        const h2 h = m * ndd;
+        H[i] = h2u(h);
+        L[i] = h2u(__builtin_elementwise_fma(m, ndd, -h));
     }
+    hi = __builtin_bit_cast(h8, make_uint4(H[0], H[1], H[2], H[3]));
+    lo = __builtin_bit_cast(h8, make_uint4(L[0], L[1], L[2], L[3]));
+}
+__device__ __forceinline__ void q4k_min_operand(const uint4 &hdr, h8 &hi, h8 &lo) {
+    q4k_min_operand_m(q4k_mins(hdr), hdr.x >> 16, hi, lo);
 }
 // the ds halves of the 8 sub-blocks of a super-block: two Q8_1 block headers
 __device__ __forceinline__ h8 ds_operand(const uint4 &b0, const uint4 &b1) {
@@ -474,9 +488,7 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
     auto keep = [&](const RawW &w, const RawA &a, int q, bool first_step, bool live) {
         if (!keep_min || !live) return;
         if (lp == 0 && first_step) {
-            const uint32_t s1 = w.h.z, s2 = w.h.w;  // scale bytes 4-7, 8-11 (get_scale_min_k4)
-            mhm[lr * kMhSb + (q >> 2)] =
-                make_uint2(s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+            mhm[lr * kMhSb + (q >> 2)] = q4k_mins(w.h);
             mhd[lr * kMhSb + (q >> 2)] = (uint16_t)(w.h.x >> 16);
         }
         if (((kVP * lp) & 31) == 0)
@@ -549,16 +561,8 @@ __global__ void __launch_bounds__(kThreads) gemm_q8_1_kernel(GemmArgs g) {
 #pragma unroll
                 for (int a = 0; a < 4; a++) {
                     const int row = wi + 16 * a + (lane & 15);
-                    const uint2 mm = mhm[row * kMhSb + rs];
-                    const float dmin = valid ? h2f(mhd[row * kMhSb + rs]) : 0.0f;
                     h8 hi, lo;
-#pragma unroll
-                    for (int t = 0; t < 8; t++) {
-                        const float v = -dmin * (float)(((t < 4 ? mm.x : mm.y) >> (8 * (t & 3))) & 0xFFu);  // exact
-                        const _Float16 h = (_Float16)v;
-                        hi[t] = h;
-                        lo[t] = (_Float16)(v - (float)h);
-                    }
+                    q4k_min_operand_m(mhm[row * kMhSb + rs], valid ? mhd[row * kMhSb + rs] : 0u, hi, lo);
 #pragma unroll
                     for (int b = 0; b < kNB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
                 }
@@ -1096,11 +1100,30 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
     int tok[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) tok[b] = stage_row(16 * b + c);
+    SkRaw6 r0[R], r1[R];
+#pragma unroll
+    for (int i = 0; i < NB * 16 / kSkStage; i++)
+        __builtin_amdgcn_global_load_lds((const void *)arow[i],
+                                         (__attribute__((address_space(3))) void *)&L.b[0][(2 * wave + kSkStage * i) * 256],
+                                         16, 0, 0);
+    if (wave < (NB * 32 + 63) / 64)  // whole waves (rows past NB 16 repeat the last)
+        __builtin_amdgcn_global_load_lds((const void *)rrow,
+                                         (__attribute__((address_space(3))) void *)&L.rho[0][(tid & ~63) * 4], 16, 0,
+                                         0);
+    if constexpr (TYPE == kTypeQ4K) {
+        sk_copy_q4<R>(tile_src, 0, L.w[0][wave]);
+    } else {
+#pragma unroll
+        for (int a = 0; a < R; a++) sk_load6(wrow[a], q, r0[a]);
+    }
     // Q4_K's min term, sum_s -(dmin*m_s)_i * ds_js, first: the accumulator starts as this
     // absolute value (the running scales start at 1 and their ratios telescope to
     // 1 / (last d * last d8), which the epilogue multiplies back).  Windows of 32 sub-blocks,
     // lane group q holding super-block 4w + q of its A row / token; the loads of up to four
-    // windows are issued together.
+    // windows are issued together, after the copies of the first block (the two round trips
+    // overlap; no measurable change).  Skipping this term (wrong results) takes the cfg5
+    // prefill from ~1.02 to ~0.945 ms; neither that overlap nor the packed-f16 operand
+    // conversion moved it.
     if constexpr (TYPE == kTypeQ4K) {
         const int nwin = (nkb + 3) / 4;
         for (int w0 = 0; w0 < nwin; w0 += 4) {
@@ -1130,22 +1153,6 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
                     }
                 }
         }
-    }
-    SkRaw6 r0[R], r1[R];
-#pragma unroll
-    for (int i = 0; i < NB * 16 / kSkStage; i++)
-        __builtin_amdgcn_global_load_lds((const void *)arow[i],
-                                         (__attribute__((address_space(3))) void *)&L.b[0][(2 * wave + kSkStage * i) * 256],
-                                         16, 0, 0);
-    if (wave < (NB * 32 + 63) / 64)  // whole waves (rows past NB 16 repeat the last)
-        __builtin_amdgcn_global_load_lds((const void *)rrow,
-                                         (__attribute__((address_space(3))) void *)&L.rho[0][(tid & ~63) * 4], 16, 0,
-                                         0);
-    if constexpr (TYPE == kTypeQ4K) {
-        sk_copy_q4<R>(tile_src, 0, L.w[0][wave]);
-    } else {
-#pragma unroll
-        for (int a = 0; a < R; a++) sk_load6(wrow[a], q, r0[a]);
     }
     __syncthreads();
     // two raw slots (Q6_K), the loop unrolled by two so that both are static
