@@ -966,7 +966,8 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
                                          const uint8_t *const (&tile_src)[sk_q4_copies<R>()],
                                          const _Float16 *const (&arow)[NB * 16 / kSkStage], const float *rrow,
                                          SkLds<TYPE, R> &L, const SkRaw6 (&cur)[R], SkRaw6 (&nxt)[R],
-                                         float (&deff)[R], f4 (&acc)[R][NB]) {
+                                         float (&deff)[R], f4 (&acc)[R][NB], bool late_min,
+                                         uint32_t (&mring)[4][R][2]) {
     // past the end the last block is copied again (into the idle buffers)
     const int kn = min(k + 1, nkb - 1);
     // block k's weights have landed in the wave's LDS area (the memory clobber keeps the
@@ -999,6 +1000,24 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
     for (int a = 0; a < R; a++) {
         if constexpr (TYPE == kTypeQ4K) {
             w4[a] = sk_read_q4<R>(L.w[k & 1][wave], a, c, q);
+            if (late_min) {
+                // the min term's operand of row c: lane group q keeps super-block k when k % 4 == q,
+                // in a ring of four (window order: the newest in slot 0)
+                const bool cap = (k & 3) == q;
+                // the 8 six-bit mins in 48 bits (m_j at bit 6j) and dmin in the top 16
+                const uint2 mn = q4k_mins(w4[a].h);
+                const uint32_t p0 = (mn.x & 0x3Fu) | ((mn.x >> 2) & 0xFC0u) | ((mn.x >> 4) & 0x3F000u) |
+                                    ((mn.x >> 6) & 0xFC0000u) | ((mn.y & 0x3Fu) << 24) | ((mn.y & 0x300u) << 22);
+                const uint32_t p1 = ((mn.y >> 10) & 0xFu) | ((mn.y >> 12) & 0x3F0u) | ((mn.y >> 14) & 0xFC00u) |
+                                    (w4[a].h.x & 0xFFFF0000u);
+                const uint32_t nv[2] = {p0, p1};
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+#pragma unroll
+                    for (int j = 3; j > 0; j--) mring[j][a][i] = cap ? mring[j - 1][a][i] : mring[j][a][i];
+                    mring[0][a][i] = cap ? nv[i] : mring[0][a][i];
+                }
+            }
             d[a] = h2f(w4[a].h.x & 0xFFFFu);
             q4k_scales8(w4[a].h, slo[a], shi[a]);
             if (d[a] == 0.0f) slo[a] = shi[a] = 0u;  // the block's products are zero
@@ -1121,10 +1140,16 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
     // 1 / (last d * last d8), which the epilogue multiplies back).  Windows of 32 sub-blocks,
     // lane group q holding super-block 4w + q of its A row / token; the loads of up to four
     // windows are issued together, after the copies of the first block (the two round trips
-    // overlap; no measurable change).  Skipping this term (wrong results) takes the cfg5
-    // prefill from ~1.02 to ~0.945 ms; neither that overlap nor the packed-f16 operand
-    // conversion moved it.
-    if constexpr (TYPE == kTypeQ4K) {
+    // overlap; no measurable change).  Reading the headers here fetches every weight line of
+    // the tile once more before the main loop.
+    // Q4_K with whole windows and at most four of them (K a multiple of 1024, <= 4096) skips
+    // that: lane group q keeps the mins and dmin of the super-blocks it reads from LDS in the
+    // main loop (64 bits per row and window, four windows), and the term is added to the
+    // absolute values after the loop (cfg5 prefill ~1.04 -> ~1.01 ms, 0 spills at 228 VGPRs;
+    // the same ring unpacked to three dwords spilled 44 VGPRs and was slower).
+    const bool late_min = TYPE == kTypeQ4K && (nkb & 3) == 0 && nkb <= 16;  // uniform
+    uint32_t mring[4][R][2] = {};
+    if (TYPE == kTypeQ4K && !late_min) {
         const int nwin = (nkb + 3) / 4;
         for (int w0 = 0; w0 < nwin; w0 += 4) {
             uint4 hdr[4][R], dsv[4][NB];
@@ -1157,9 +1182,11 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
     __syncthreads();
     // two raw slots (Q6_K), the loop unrolled by two so that both are static
     for (int k = 0; k < nkb; k += 2) {
-        sk_block<TYPE, NB, R>(k, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r0, r1, deff, acc);
+        sk_block<TYPE, NB, R>(k, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r0, r1, deff, acc,
+                              late_min, mring);
         if (k + 1 >= nkb) break;
-        sk_block<TYPE, NB, R>(k + 1, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r1, r0, deff, acc);
+        sk_block<TYPE, NB, R>(k + 1, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r1, r0, deff, acc,
+                              late_min, mring);
     }
 
     // absolute values: the last nonzero d of the rows (from lanes 4q + x) and d8 of the tokens
@@ -1174,6 +1201,31 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
 #pragma unroll
             for (int b = 0; b < NB; b++) acc[a][b][x] *= dr * dt[b];
         }
+    if (late_min) {
+        // the min term on the absolute values: slot j holds window nwin - 1 - j
+        const int nwin = nkb >> 2;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j >= nwin) break;  // uniform
+            const int sb = 4 * (nwin - 1 - j) + q;
+            h8 bd[NB];
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+                bd[b] = __builtin_bit_cast(h8, ld16((const uint8_t *)(g.a_ds + (size_t)tok[b] * (K / 32) + 8 * sb)));
+#pragma unroll
+            for (int a = 0; a < R; a++) {
+                h8 hi, lo;
+                const uint32_t p0 = mring[j][a][0], p1 = mring[j][a][1];
+                const uint2 mn = make_uint2((p0 & 0x3Fu) | ((p0 << 2) & 0x3F00u) | ((p0 << 4) & 0x3F0000u) |
+                                                ((p0 << 6) & 0x3F000000u),
+                                            ((p0 >> 24) & 0x3Fu) | ((p0 >> 22) & 0x300u) | ((p1 << 10) & 0x3C00u) |
+                                                ((p1 << 12) & 0x3F0000u) | ((p1 << 14) & 0x3F000000u));
+                q4k_min_operand_m(mn, p1 >> 16, hi, lo);
+#pragma unroll
+                for (int b = 0; b < NB; b++) acc[a][b] = mfma(lo, bd[b], mfma(hi, bd[b], acc[a][b]));
+            }
+        }
+    }
 
     // D layout: lane holds weight rows 4q + x of each 16-row tile, token column c
 #pragma unroll
