@@ -70,6 +70,12 @@ def _compose_plain(gpu, table, lay, DT, x, idx, w, T, H, EFF, out0):
     # experts of 1-3 full 64-row tiles plus a ragged one
     (130, 256, 256, 2, 1, 14, 0.0),
     (200, 512, 256, 5, 2, 12, 0.5),
+    # Q4_K K in whole 1024-value windows (1-3 of them; the min term formed after the main
+    # loop), and K = 5120 (five windows: the min term before the loop, in two passes)
+    (48, 1024, 1024, 4, 2, 12, 0.5),
+    (24, 2048, 256, 3, 2, 14, 1.1),
+    (70, 3072, 256, 2, 1, 14, 0.0),
+    (16, 5120, 1024, 2, 1, 12, 0.0),
 ])
 def test_moe_prefill_vs_oracle(gpu, oracle, T, H, EFF, E, k, down_type, skew):
     rng = np.random.default_rng(T * 1000 + E)
