@@ -104,6 +104,37 @@ def test_moe_prefill_vs_oracle(gpu, oracle, T, H, EFF, E, k, down_type, skew):
     assert err_o < TOL_ORACLE
 
 
+@pytest.mark.parametrize("H", [512, 2048])
+def test_moe_prefill_zero_d_blocks(gpu, oracle, H):
+    """Gate/up Q4_K blocks with d = 0 (dmin kept, so only the min term survives), scattered
+    and over whole rows, with K below one 1024-value window (min term before the main loop)
+    and K in two whole windows (min term after it, from the headers the loop reads)."""
+    T, EFF, E, k, DT = 96, 256, 4, 2, 14
+    rng = np.random.default_rng(H + 7)
+    table = synth.expert_table(rng, E, H, EFF, DT)
+    lay = synth.expert_layout(H, EFF, DT)
+    stride, _, up_off, down_off = lay
+    nb = H // 256
+    t = table.reshape(E, stride)
+    gu = t[:, :down_off].reshape(E, 2 * EFF * nb, 144)
+    gu[:, :, 0:2][rng.random((E, 2 * EFF * nb)) < 0.15] = 0
+    rows = gu.reshape(E, 2 * EFF, nb, 144)
+    rows[:, 3, :, 0:2] = 0          # every block of gate row 3
+    rows[:, EFF + 10, :, 0:2] = 0   # and of up row 10
+    assert np.shares_memory(rows, t)
+    table = t.reshape(-1)
+    idx, w = synth.zipf_routing(rng, T, E, k, s=0.5)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    out0 = rng.standard_normal((T, H)).astype(np.float32)
+    case(f"moe_prefill zero-d blocks H={H}")
+    out = _run(gpu, dev(table), lay, DT, dev(x), dev(idx), dev(w), T, H, EFF, E, k, dev(out0))
+    got_delta = host(out).astype(np.float64).reshape(T, H) - out0
+    ref_delta = oracle.moe_prefill(table, *lay, DT, x, idx, w, H, EFF, E)
+    err = rel_l2(got_delta, ref_delta)
+    print(f"rel_l2 vs oracle={err:.2e}")
+    assert err < TOL_ORACLE
+
+
 def test_moe_prefill_bad_args(gpu):
     T, H, EFF, E, k = 4, 256, 256, 4, 2
     x = torch.zeros(T * H, device="cuda")
