@@ -809,16 +809,21 @@ int launch_gemm_q8_1(int type, const void *w, const void *act, float *out, int M
 // block are 144 row-contiguous 16-byte chunks copied with global_load_lds (whole cache lines
 // per request, no registers held while they are in flight -- lanes loading their own 8-byte
 // pieces touch 16 rows per instruction and kept the L1 busy at ~3 TB/s in a read test
-// against ~4.8 TB/s for the copies), then read back per lane.  Q6_K blocks are 210 B and
-// only 2-byte aligned, so the lanes load them directly.
-constexpr int kSkThreads = 512;  // 8 waves
-constexpr int kSkWaves = kSkThreads / 64;
-constexpr int kSkTok = kGroupTile;         // token rows per tile: up to 4 column tiles of 16
-constexpr int kSkStage = kSkThreads / 32;  // activation rows staged per pass (32 chunks each)
+// against ~4.8 TB/s for the copies), then read back per lane.  Q6_K blocks (210 B, 2-byte
+// aligned) are copied as dwords (sk_copy_q6).
+constexpr int kSkTok = kGroupTile;  // token rows per tile: up to 4 column tiles of 16
 // weight rows per wave: SwiGLU one gate and one up tile of 16 (same features); grouped two
 // tiles of 16 (Q4_K) or one (Q6_K, whose raw blocks take more registers)
 template <int TYPE, int MODE>
 constexpr int sk_rows_per_wave() { return MODE == 1 || TYPE == kTypeQ4K ? 32 : 16; }
+// waves per workgroup: Q4_K 8 (one workgroup per CU: its double-buffered weight areas fill
+// the LDS), Q6_K 16 (single-buffered weight areas, four waves per SIMD within 128 registers)
+template <int TYPE>
+constexpr int sk_waves() { return TYPE == kTypeQ6K ? 16 : 8; }
+// activation staging passes of a workgroup of W waves (2W rows of 32 chunks per pass); rows
+// past NB 16 repeat the tile's last token into the unused rest of the buffer
+template <int NB, int W>
+constexpr int sk_passes() { return (NB * 16 + 2 * W - 1) / (2 * W); }
 // One block of a 16-row tile is 2304 B = 144 chunks of 16 B.  Every copy instruction is
 // issued by the whole wave (a lane-predicated copy invites the compiler to merge it with its
 // neighbour and derive the wave-uniform LDS address from the wrong lane): chunks 0-127 of
@@ -837,24 +842,58 @@ struct SkRaw6 {
     uint32_t sc[2];  // the lane's scale bytes of halves 0 / 1 (byte grp: scale 8H + 2grp + q/2)
     uint32_t d;      // f16 d
 };
-// vector memory instructions of sk_load6: six 8-byte and one 16-byte unaligned loads (two
-// instructions each: ld8_a2, ld16_a2) and the 2-byte d
-constexpr int kSk6Loads = 15;
+// Q6_K blocks reach the wave through its LDS area by 4-byte copies (lanes loading their own
+// 8-byte pieces touch 16 rows per instruction; with those loads replaced by constants the
+// cfg5 prefill took 0.75 instead of 1.01 ms).  Row r of the 16-row tile occupies dwords
+// 53 r .. 53 r + 52 of the area: the dwords from the one that holds the block's first byte
+// (blocks are 210 B, so every other one starts at 2 mod 4) on, i.e. block byte o sits at
+// area byte 212 r + sh + o with sh = (block offset) & 2.  Dword t = 64 i + lane is moved by
+// copy i; t >= 848 repeats t = 847.  The copies cover bytes 0-207 of each block (the
+// 53rd dword of a 4-byte aligned block reads 2 bytes past it, so it is clamped to the
+// matrix's last full dword); d (bytes 208-209) is loaded by the lanes themselves.
+constexpr int kSk6Dw = 53;
+constexpr int kSk6Copies = 14;
+constexpr int kSk6Area = kSk6Copies * 256;
+// vector memory instructions per block: the copies and the 2-byte d
+constexpr int kSk6Loads = kSk6Copies + 1;
 
-__device__ __forceinline__ void sk_load6(const uint8_t *__restrict__ blk, int q, SkRaw6 &r) {
+// the copies of block k: lane offsets x6[i] = (offset of the dword's row from the tile's
+// first row) + 4 w, lim = the last full dword of the matrix (offsets from the tile's start)
+__device__ __forceinline__ void sk_copy_q6(const uint8_t *tile, const uint32_t (&x6)[kSk6Copies], uint32_t lim,
+                                           int k, uint8_t *dst) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.ql[i] = ld8_a2(blk + 64 * (i >> 1) + 32 * (i & 1) + 8 * q);
+    for (int i = 0; i < kSk6Copies; i++) {
+        const uint32_t o = min((x6[i] + (uint32_t)(kQ6KBytes * k)) & ~3u, lim);
+        __builtin_amdgcn_global_load_lds((const void *)(tile + o),
+                                         (__attribute__((address_space(3))) void *)(dst + 256 * i), 4, 0, 0);
+    }
+}
+
+// the lane's raw values of row c's block from the wave's LDS area (sh: the block's
+// misalignment, 0 or 2 bytes); d arrives separately
+__device__ __forceinline__ void sk_read6(const uint8_t *area, int c, int q, uint32_t sh, SkRaw6 &r) {
+    const uint32_t *a = (const uint32_t *)area + kSk6Dw * c;
+    auto rd8 = [&](int o) {  // block bytes o .. o + 7, o a multiple of 8
+        const uint32_t w0 = a[o >> 2], w1 = a[(o >> 2) + 1], w2 = a[(o >> 2) + 2];
+        return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
+    };
 #pragma unroll
-    for (int H = 0; H < 2; H++) r.qh[H] = ld8_a2(blk + 128 + 32 * H + 8 * q);
+    for (int i = 0; i < 4; i++) r.ql[i] = rd8(64 * (i >> 1) + 32 * (i & 1) + 8 * q);
+#pragma unroll
+    for (int H = 0; H < 2; H++) r.qh[H] = rd8(128 + 32 * H + 8 * q);
     // of the 16 scale bytes the lane needs 8H + 2grp + q/2: bytes q/2, 2 + q/2, .. of each
     // dword, packed per half
-    const uint4 sc = ld16_a2(blk + 192);
+    uint32_t w[5];
+#pragma unroll
+    for (int i = 0; i < 5; i++) w[i] = a[48 + i];
+    uint4 sc;
+    sc.x = __builtin_amdgcn_alignbyte(w[1], w[0], sh);
+    sc.y = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
+    sc.z = __builtin_amdgcn_alignbyte(w[3], w[2], sh);
+    sc.w = __builtin_amdgcn_alignbyte(w[4], w[3], sh);
     const uint32_t sel = 0x06040200u + 0x01010101u * (uint32_t)(q >> 1);
     r.sc[0] = __builtin_amdgcn_perm(sc.y, sc.x, sel);
     r.sc[1] = __builtin_amdgcn_perm(sc.w, sc.z, sel);
-    uint16_t dd;
-    __builtin_memcpy(&dd, blk + 208, 2);
-    r.d = dd;
 }
 
 // Q4_K lane view of a tile's block: the header (d, dmin, scales) and the lane's qs bytes
@@ -920,10 +959,11 @@ __device__ __forceinline__ int sk_slot(int r, int u) { return r * 256 + ((u ^ (r
 
 template <int TYPE, int R>
 struct SkLds {
-    static constexpr int kW = TYPE == kTypeQ4K ? sk_q4_area<R>() : 16;
-    _Float16 b[2][kSkTok * 256];  // staged q8 of one 256-value block, double-buffered
-    float rho[2][kSkTok * 8];     // the rows' scale ratios of that block's 8 sub-blocks
-    uint8_t w[2][kSkWaves][kW];   // Q4_K: each wave's row tiles of one block, double-buffered
+    static constexpr int kW = TYPE == kTypeQ4K ? sk_q4_area<R>() : kSk6Area;
+    static constexpr int kWBufs = TYPE == kTypeQ4K ? 2 : 1;
+    _Float16 b[2][kSkTok * 256];               // staged q8 of one 256-value block, double-buffered
+    float rho[2][kSkTok * 8];                  // the rows' scale ratios of that block's 8 sub-blocks
+    uint8_t w[kWBufs][sk_waves<TYPE>()][kW];   // each wave's row tiles of one block (Q4_K double-buffered)
 };
 
 // the running row scales at a block start: lane c owns A row c of each tile (its running d
@@ -956,27 +996,41 @@ __device__ __forceinline__ void sk_copy_q4(const uint8_t *const (&src)[sk_q4_cop
 }
 
 // One 256-value block k: the activations (and ratios) of block k+1 are copied into the other
-// LDS buffer, the weights of block k+1 into the wave's other LDS area (Q4_K) or registers
-// (Q6_K), then block k is multiplied.  The barrier at the end waits for the activation
-// copies only (they were issued first; memory operations complete in issue order): the
-// weights stay in flight until the next block needs them.
+// LDS buffer, the weights of block k+1 into the wave's other LDS area (Q4_K) or into its
+// single area (Q6_K, once the lanes have read block k out of it), then block k is
+// multiplied.  The barrier at the end waits for the activation copies only (they were issued
+// first; memory operations complete in issue order): the weights stay in flight until the
+// next block needs them.
+// Q6_K copy state of a wave: the 4-byte aligned address at or below its first row, the
+// copies' lane offsets (sk_copy_q6), their clamp, row c's offset and the next block's d
+struct Sk6 {
+    const uint8_t *tile;
+    uint32_t x6[kSk6Copies];
+    uint32_t lim, roff, dn;
+};
 template <int TYPE, int NB, int R>
 __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave, int lane, int tid,
-                                         const uint8_t *const (&wrow)[R],
                                          const uint8_t *const (&tile_src)[sk_q4_copies<R>()],
-                                         const _Float16 *const (&arow)[NB * 16 / kSkStage], const float *rrow,
-                                         SkLds<TYPE, R> &L, const SkRaw6 (&cur)[R], SkRaw6 (&nxt)[R],
-                                         float (&deff)[R], f4 (&acc)[R][NB], bool late_min,
-                                         uint32_t (&mring)[4][R][2]) {
+                                         const _Float16 *const (&arow)[sk_passes<NB, sk_waves<TYPE>()>()],
+                                         const float *rrow, SkLds<TYPE, R> &L, Sk6 &st, float (&deff)[R],
+                                         f4 (&acc)[R][NB], bool late_min, uint32_t (&mring)[4][R][2]) {
+    constexpr int W = sk_waves<TYPE>();
     // past the end the last block is copied again (into the idle buffers)
     const int kn = min(k + 1, nkb - 1);
     // block k's weights have landed in the wave's LDS area (the memory clobber keeps the
     // compiler from moving the LDS reads above the wait)
-    if constexpr (TYPE == kTypeQ4K) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    SkRaw6 cur[R];
+    if constexpr (TYPE == kTypeQ6K) {
+        sk_read6(L.w[0][wave], c, q, (st.roff + (uint32_t)(kQ6KBytes * k)) & 2u, cur[0]);
+        cur[0].d = st.dn;
+        // the reads have returned before the area is refilled below
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
 #pragma unroll
-    for (int i = 0; i < NB * 16 / kSkStage; i++)
+    for (int i = 0; i < sk_passes<NB, W>(); i++)
         __builtin_amdgcn_global_load_lds((const void *)(arow[i] + kn * 256),
-                                         (__attribute__((address_space(3))) void *)&L.b[(k + 1) & 1][(2 * wave + kSkStage * i) * 256],
+                                         (__attribute__((address_space(3))) void *)&L.b[(k + 1) & 1][(2 * wave + 2 * W * i) * 256],
                                          16, 0, 0);
     if (wave < (NB * 32 + 63) / 64)  // the ratios: two 16-byte chunks per row, whole waves
         __builtin_amdgcn_global_load_lds((const void *)(rrow + kn * 8),
@@ -986,8 +1040,10 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
     if constexpr (TYPE == kTypeQ4K) {
         sk_copy_q4<R>(tile_src, kn, L.w[(k + 1) & 1][wave]);
     } else {
-#pragma unroll
-        for (int a = 0; a < R; a++) sk_load6(wrow[a] + (size_t)kn * kQ6KBytes, q, nxt[a]);
+        sk_copy_q6(st.tile, st.x6, st.lim, kn, L.w[0][wave]);
+        uint16_t dd;
+        __builtin_memcpy(&dd, st.tile + st.roff + (size_t)kn * kQ6KBytes + 208, 2);
+        st.dn = dd;
     }
     // keep the loads here, ahead of the multiplication (the scheduler would otherwise sink
     // them past it to save registers, and nothing would be in flight during the MFMAs)
@@ -1067,6 +1123,8 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
                                         int wave, int lane, int tid, int e, int j0, int n_rows, int row_base) {
     constexpr int R = sk_rows_per_wave<TYPE, MODE>() / 16;
     constexpr int H = R / 2;  // SwiGLU: gate tiles 0 .. H-1, up tiles H .. 2H-1
+    constexpr int W = sk_waves<TYPE>();
+    constexpr int P = sk_passes<NB, W>();
     const int q = lane >> 4, c = lane & 15;
     const int K = g.K, nkb = K / 256;
     const int bbytes = TYPE == kTypeQ4K ? kQ4KBytes : kQ6KBytes;
@@ -1076,8 +1134,8 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
 
     // weight row r of tile a (rows past M re-read the last)
     int base;  // SwiGLU: first feature of the wave; grouped: first row
-    if (MODE == 1) base = (blockIdx.x * kSkWaves + wave) * (16 * H);
-    else base = (blockIdx.x * kSkWaves + wave) * (16 * R);
+    if (MODE == 1) base = (blockIdx.x * W + wave) * (16 * H);
+    else base = (blockIdx.x * W + wave) * (16 * R);
     auto row_ptr = [&](int a, int r) {
         if (MODE == 1) return (a < H ? Wm : Wm2) + (size_t)min(base + 16 * (a % H) + r, g.M - 1) * wrow_bytes;
         return Wm + (size_t)min(base + 16 * a + r, g.M - 1) * wrow_bytes;
@@ -1093,18 +1151,35 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
         for (int i = 0; i < 2; i++) tile_src[2 * a + i] = chunk_ptr(a, 64 * i + lane);
     }
     tile_src[2 * R] = lane < 16 * R ? chunk_ptr(lane >> 4, 128 + (lane & 15)) : chunk_ptr(R - 1, 143);
-    // activation staging role: physical slot tid % 32 of rows r = tid/32 + kSkStage i, which
+    // Q6_K copies (one tile of 16 consecutive rows): offsets from the 4-byte aligned address
+    // at or below the first (clamped) row, tb its misalignment
+    Sk6 st;
+    if constexpr (TYPE == kTypeQ6K) {
+        const int r0 = min(base, g.M - 1);
+        const uint8_t *t0 = Wm + (size_t)r0 * wrow_bytes;
+        const uint32_t tb = (uint32_t)(uintptr_t)t0 & 3u;
+        st.tile = t0 - tb;
+        auto rel = [&](int r) { return (uint32_t)((min(base + r, g.M - 1) - r0) * wrow_bytes) + tb; };
+#pragma unroll
+        for (int i = 0; i < kSk6Copies; i++) {
+            const int t = min(64 * i + lane, 16 * kSk6Dw - 1);
+            st.x6[i] = rel(t / kSk6Dw) + 4u * (uint32_t)(t % kSk6Dw);
+        }
+        st.lim = ((uint32_t)((g.M - r0) * wrow_bytes) + tb - 4u) & ~3u;
+        st.roff = rel(c);
+    }
+    // activation staging role: physical slot tid % 32 of rows r = tid/32 + 2W i, which
     // holds the logical slot (tid % 32) ^ (r % 32); ratio staging: threads below 2 NB 16 copy
     // 16-byte chunk tid % 2 of row tid / 2
     const int sr0 = tid >> 5;
-    const _Float16 *arow[NB * 16 / kSkStage];
+    const _Float16 *arow[P];
     auto stage_row = [&](int r) {
         const int j = min(j0 + r, n_rows - 1);
         return MODE == 1 ? g.perm[row_base + j] : row_base + j;
     };
 #pragma unroll
-    for (int i = 0; i < NB * 16 / kSkStage; i++) {
-        const int r = sr0 + kSkStage * i, u = (tid & 31) ^ (r & 31);
+    for (int i = 0; i < P; i++) {
+        const int r = sr0 + 2 * W * i, u = (tid & 31) ^ (r & 31);
         arow[i] = (const _Float16 *)g.A + (size_t)stage_row(r) * K + 8 * u;
     }
     const float *rrow = g.a_rho + (size_t)stage_row(min(tid >> 1, NB * 16 - 1)) * (K / 32) + 4 * (tid & 1);
@@ -1119,11 +1194,10 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
     int tok[NB];
 #pragma unroll
     for (int b = 0; b < NB; b++) tok[b] = stage_row(16 * b + c);
-    SkRaw6 r0[R], r1[R];
 #pragma unroll
-    for (int i = 0; i < NB * 16 / kSkStage; i++)
+    for (int i = 0; i < P; i++)
         __builtin_amdgcn_global_load_lds((const void *)arow[i],
-                                         (__attribute__((address_space(3))) void *)&L.b[0][(2 * wave + kSkStage * i) * 256],
+                                         (__attribute__((address_space(3))) void *)&L.b[0][(2 * wave + 2 * W * i) * 256],
                                          16, 0, 0);
     if (wave < (NB * 32 + 63) / 64)  // whole waves (rows past NB 16 repeat the last)
         __builtin_amdgcn_global_load_lds((const void *)rrow,
@@ -1132,8 +1206,10 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
     if constexpr (TYPE == kTypeQ4K) {
         sk_copy_q4<R>(tile_src, 0, L.w[0][wave]);
     } else {
-#pragma unroll
-        for (int a = 0; a < R; a++) sk_load6(wrow[a], q, r0[a]);
+        sk_copy_q6(st.tile, st.x6, st.lim, 0, L.w[0][wave]);
+        uint16_t dd;
+        __builtin_memcpy(&dd, st.tile + st.roff + 208, 2);
+        st.dn = dd;
     }
     // Q4_K's min term, sum_s -(dmin*m_s)_i * ds_js, first: the accumulator starts as this
     // absolute value (the running scales start at 1 and their ratios telescope to
@@ -1180,14 +1256,15 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
         }
     }
     __syncthreads();
-    // two raw slots (Q6_K), the loop unrolled by two so that both are static
+    // the loop unrolled by two
     for (int k = 0; k < nkb; k += 2) {
-        sk_block<TYPE, NB, R>(k, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r0, r1, deff, acc,
-                              late_min, mring);
+        sk_block<TYPE, NB, R>(k, nkb, q, c, wave, lane, tid, tile_src, arow, rrow, L, st, deff, acc, late_min, mring);
         if (k + 1 >= nkb) break;
-        sk_block<TYPE, NB, R>(k + 1, nkb, q, c, wave, lane, tid, wrow, tile_src, arow, rrow, L, r1, r0, deff, acc,
-                              late_min, mring);
+        sk_block<TYPE, NB, R>(k + 1, nkb, q, c, wave, lane, tid, tile_src, arow, rrow, L, st, deff, acc, late_min,
+                              mring);
     }
+    // the copies issued past the last block land before the workgroup's LDS is released
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // absolute values: the last nonzero d of the rows (from lanes 4q + x) and d8 of the tokens
     float dt[NB];
@@ -1257,11 +1334,12 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
 
 // MODE 1: SwiGLU (gate and up rows of the same features, activation rows gathered through
 // perm[], out[q*ld + f] = silu(gate) * up); MODE 2: the expert-sorted rows themselves.
-// The Q6_K kernel (70 KB of LDS) runs two workgroups per CU when it fits 128 registers: four
-// waves per SIMD instead of two (a few registers spill; 540 -> ~460 us for the cfg5 down GEMM).
-// The Q4_K kernels' 150 KB of LDS allow one workgroup per CU whatever the registers.
+// The Q6_K kernel's 16 waves (124 KB of LDS, one workgroup per CU) run four per SIMD within
+// 128 registers (a few spill).  The Q4_K kernels' 150 KB of LDS allow one 8-wave workgroup
+// per CU whatever the registers.
 template <int TYPE, int MODE>
-__global__ void __launch_bounds__(kSkThreads) __attribute__((amdgpu_waves_per_eu(TYPE == kTypeQ6K ? 4 : 1, 8)))
+__global__ void __launch_bounds__(TYPE == kTypeQ6K ? 1024 : 512)
+    __attribute__((amdgpu_waves_per_eu(TYPE == kTypeQ6K ? 4 : 1, 8)))
 gemm_skinny_kernel(GemmArgs g) {
     __shared__ __align__(16) SkLds<TYPE, sk_rows_per_wave<TYPE, MODE>() / 16> L;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1307,8 +1385,9 @@ int launch_gemm_grouped(int type, int swiglu, const void *experts, size_t expert
         return set_error(kErrUnsupportedType, "grouped gate/up GEMM: Q4_K only (type %d)", type);
 #define MNEMO_SKINNY(T_, M_)                                                                                    \
     do {                                                                                                        \
-        const int rows = sk_rows_per_wave<T_, M_>() / (M_ == 1 ? 2 : 1) * kSkWaves;                            \
-        hipLaunchKernelGGL((gemm_skinny_kernel<T_, M_>), dim3((M + rows - 1) / rows, max_tiles, 1), dim3(kSkThreads), \
+        const int rows = sk_rows_per_wave<T_, M_>() / (M_ == 1 ? 2 : 1) * sk_waves<T_>();                      \
+        hipLaunchKernelGGL((gemm_skinny_kernel<T_, M_>), dim3((M + rows - 1) / rows, max_tiles, 1),            \
+                           dim3(64 * sk_waves<T_>()),                                                          \
                            0, stream, g);                                                                       \
     } while (0)
     if (swiglu) MNEMO_SKINNY(kTypeQ4K, 1);
