@@ -842,37 +842,39 @@ struct SkRaw6 {
     uint32_t sc[2];  // the lane's scale bytes of halves 0 / 1 (byte grp: scale 8H + 2grp + q/2)
     uint32_t d;      // f16 d
 };
-// Q6_K blocks reach the wave through its LDS area by 4-byte copies (lanes loading their own
-// 8-byte pieces touch 16 rows per instruction; with those loads replaced by constants the
-// cfg5 prefill took 0.75 instead of 1.01 ms).  Row r of the 16-row tile occupies dwords
-// 53 r .. 53 r + 52 of the area: the dwords from the one that holds the block's first byte
-// (blocks are 210 B, so every other one starts at 2 mod 4) on, i.e. block byte o sits at
-// area byte 212 r + sh + o with sh = (block offset) & 2.  Dword t = 64 i + lane is moved by
-// copy i; t >= 848 repeats t = 847.  The copies cover bytes 0-207 of each block (the
-// 53rd dword of a 4-byte aligned block reads 2 bytes past it, so it is clamped to the
-// matrix's last full dword); d (bytes 208-209) is loaded by the lanes themselves.
-constexpr int kSk6Dw = 53;
-constexpr int kSk6Copies = 14;
-constexpr int kSk6Area = kSk6Copies * 256;
+// Q6_K blocks reach the wave through its LDS area by 16-byte copies (lanes loading their
+// own 8-byte pieces touch 16 rows per instruction; with those loads replaced by constants the
+// cfg5 prefill took 0.75 instead of 1.01 ms).  A block is 210 B, so every other one starts at
+// 2 mod 4: row r's window starts at the dword that holds the block's first byte (sh = block
+// offset & 2 bytes before it) and occupies chunk slots 15 r .. 15 r + 14 of the area (240 B
+// per row: the 16 rows' reads fall in distinct banks).  Chunks 0-12 are window bytes
+// 16 ch ..; chunk 13 is window bytes 196-211 when sh = 2 (block bytes 194-209) and a repeat of
+// chunk 12 when sh = 0; chunk 14 repeats chunk 12.  So no copy reads past its block, and the
+// block's bytes 0-207 are in the area; d (bytes 208-209) is loaded by the lanes themselves.
+// Slot t = 64 i + lane is written by copy i; slots past 239 repeat row 15's chunk 12.
+constexpr int kSk6Slots = 15;
+constexpr int kSk6Copies = 4;
+constexpr int kSk6Area = kSk6Copies * 1024;
 // vector memory instructions per block: the copies and the 2-byte d
 constexpr int kSk6Loads = kSk6Copies + 1;
 
-// the copies of block k: lane offsets x6[i] = (offset of the dword's row from the tile's
-// first row) + 4 w, lim = the last full dword of the matrix (offsets from the tile's start)
-__device__ __forceinline__ void sk_copy_q6(const uint8_t *tile, const uint32_t (&x6)[kSk6Copies], uint32_t lim,
-                                           int k, uint8_t *dst) {
+// the copies of block k: x6[i] = (offset of the slot's row from the tile's 4-byte aligned
+// start) + window offset of the chunk, bit 0 set for chunk 13 (moved 4 bytes on when sh = 2)
+__device__ __forceinline__ void sk_copy_q6(const uint8_t *tile, const uint32_t (&x6)[kSk6Copies], int k,
+                                           uint8_t *dst) {
 #pragma unroll
     for (int i = 0; i < kSk6Copies; i++) {
-        const uint32_t o = min((x6[i] + (uint32_t)(kQ6KBytes * k)) & ~3u, lim);
+        const uint32_t a = x6[i] + (uint32_t)(kQ6KBytes * k);
+        const uint32_t o = (a & ~3u) + ((a & 1u) ? (a & 2u) << 1 : 0u);
         __builtin_amdgcn_global_load_lds((const void *)(tile + o),
-                                         (__attribute__((address_space(3))) void *)(dst + 256 * i), 4, 0, 0);
+                                         (__attribute__((address_space(3))) void *)(dst + 1024 * i), 16, 0, 0);
     }
 }
 
 // the lane's raw values of row c's block from the wave's LDS area (sh: the block's
 // misalignment, 0 or 2 bytes); d arrives separately
 __device__ __forceinline__ void sk_read6(const uint8_t *area, int c, int q, uint32_t sh, SkRaw6 &r) {
-    const uint32_t *a = (const uint32_t *)area + kSk6Dw * c;
+    const uint32_t *a = (const uint32_t *)area + 4 * kSk6Slots * c;
     auto rd8 = [&](int o) {  // block bytes o .. o + 7, o a multiple of 8
         const uint32_t w0 = a[o >> 2], w1 = a[(o >> 2) + 1], w2 = a[(o >> 2) + 2];
         return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
@@ -882,10 +884,11 @@ __device__ __forceinline__ void sk_read6(const uint8_t *area, int c, int q, uint
 #pragma unroll
     for (int H = 0; H < 2; H++) r.qh[H] = rd8(128 + 32 * H + 8 * q);
     // of the 16 scale bytes the lane needs 8H + 2grp + q/2: bytes q/2, 2 + q/2, .. of each
-    // dword, packed per half
+    // dword, packed per half; window dword 52 (sh = 2 only) is the last of chunk 13
     uint32_t w[5];
 #pragma unroll
-    for (int i = 0; i < 5; i++) w[i] = a[48 + i];
+    for (int i = 0; i < 4; i++) w[i] = a[48 + i];
+    w[4] = a[sh ? 55 : 52];
     uint4 sc;
     sc.x = __builtin_amdgcn_alignbyte(w[1], w[0], sh);
     sc.y = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
@@ -1006,7 +1009,7 @@ __device__ __forceinline__ void sk_copy_q4(const uint8_t *const (&src)[sk_q4_cop
 struct Sk6 {
     const uint8_t *tile;
     uint32_t x6[kSk6Copies];
-    uint32_t lim, roff, dn;
+    uint32_t roff, dn;
 };
 template <int TYPE, int NB, int R>
 __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave, int lane, int tid,
@@ -1040,7 +1043,7 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
     if constexpr (TYPE == kTypeQ4K) {
         sk_copy_q4<R>(tile_src, kn, L.w[(k + 1) & 1][wave]);
     } else {
-        sk_copy_q6(st.tile, st.x6, st.lim, kn, L.w[0][wave]);
+        sk_copy_q6(st.tile, st.x6, kn, L.w[0][wave]);
         uint16_t dd;
         __builtin_memcpy(&dd, st.tile + st.roff + (size_t)kn * kQ6KBytes + 208, 2);
         st.dn = dd;
@@ -1162,10 +1165,10 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
         auto rel = [&](int r) { return (uint32_t)((min(base + r, g.M - 1) - r0) * wrow_bytes) + tb; };
 #pragma unroll
         for (int i = 0; i < kSk6Copies; i++) {
-            const int t = min(64 * i + lane, 16 * kSk6Dw - 1);
-            st.x6[i] = rel(t / kSk6Dw) + 4u * (uint32_t)(t % kSk6Dw);
+            const int t = 64 * i + lane, row = t < 16 * kSk6Slots ? t / kSk6Slots : 15;
+            const int ch = t < 16 * kSk6Slots ? t % kSk6Slots : 12;
+            st.x6[i] = rel(row) + (ch <= 12 ? 16u * (uint32_t)ch : ch == 13 ? 192u + 1u : 192u);
         }
-        st.lim = ((uint32_t)((g.M - r0) * wrow_bytes) + tb - 4u) & ~3u;
         st.roff = rel(c);
     }
     // activation staging role: physical slot tid % 32 of rows r = tid/32 + 2W i, which
@@ -1206,7 +1209,7 @@ __device__ __forceinline__ void sk_tile(const GemmArgs &g, SkLds<TYPE, sk_rows_p
     if constexpr (TYPE == kTypeQ4K) {
         sk_copy_q4<R>(tile_src, 0, L.w[0][wave]);
     } else {
-        sk_copy_q6(st.tile, st.x6, st.lim, 0, L.w[0][wave]);
+        sk_copy_q6(st.tile, st.x6, 0, L.w[0][wave]);
         uint16_t dd;
         __builtin_memcpy(&dd, st.tile + st.roff + 208, 2);
         st.dn = dd;
