@@ -1061,7 +1061,14 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
             w4[a] = sk_read_q4<R>(L.w[k & 1][wave], a, c, q);
             if (late_min) {
                 // the min term's operand of row c: lane group q keeps super-block k when k % 4 == q,
-                // in a ring of four (window order: the newest in slot 0)
+                // in a ring of four (window order: the newest in slot 0), moved up one slot at
+                // each window's first block (a uniform branch)
+                if ((k & 3) == 0) {
+#pragma unroll
+                    for (int i = 0; i < 2; i++)
+#pragma unroll
+                        for (int j = 3; j > 0; j--) mring[j][a][i] = mring[j - 1][a][i];
+                }
                 const bool cap = (k & 3) == q;
                 // the 8 six-bit mins in 48 bits (m_j at bit 6j) and dmin in the top 16
                 const uint2 mn = q4k_mins(w4[a].h);
@@ -1069,13 +1076,8 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
                                     ((mn.x >> 6) & 0xFC0000u) | ((mn.y & 0x3Fu) << 24) | ((mn.y & 0x300u) << 22);
                 const uint32_t p1 = ((mn.y >> 10) & 0xFu) | ((mn.y >> 12) & 0x3F0u) | ((mn.y >> 14) & 0xFC00u) |
                                     (w4[a].h.x & 0xFFFF0000u);
-                const uint32_t nv[2] = {p0, p1};
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-#pragma unroll
-                    for (int j = 3; j > 0; j--) mring[j][a][i] = cap ? mring[j - 1][a][i] : mring[j][a][i];
-                    mring[0][a][i] = cap ? nv[i] : mring[0][a][i];
-                }
+                mring[0][a][0] = cap ? p0 : mring[0][a][0];
+                mring[0][a][1] = cap ? p1 : mring[0][a][1];
             }
             d[a] = h2f(w4[a].h.x & 0xFFFFu);
             q4k_scales8(w4[a].h, slo[a], shi[a]);
