@@ -166,7 +166,9 @@ int mnemo_sample_token_ws(const float *logits, int vocab_size, float temperature
  * [eff][hidden], down Q4_K or Q6_K [hidden][eff] (the reference's expert file layout,
  * src/forward.c:866-872).  topk_idx / topk_w are [n_tokens][k] (cuda_topk_softmax's output
  * per token); ids outside [0, n_experts) are skipped.  hidden, eff % 256 == 0,
- * n_experts <= 512, n_tokens * k <= 4,194,304.  workspace: device memory of at least
+ * n_experts <= 512, n_tokens * k <= 4,194,304.  experts, expert_stride and the three
+ * offsets 4-byte aligned (the weight blocks are copied into LDS by 16-byte DMA from 4-byte
+ * aligned addresses).  workspace: device memory of at least
  * mnemo_moe_prefill_workspace_bytes(...) bytes, 16-byte aligned. */
 size_t mnemo_moe_prefill_workspace_bytes(int n_tokens, int hidden, int eff, int n_experts, int k);
 int mnemo_moe_prefill(const void *experts, size_t expert_stride, size_t gate_off, size_t up_off,

@@ -245,6 +245,11 @@ int launch_moe_prefill(const void *experts, size_t expert_stride, size_t gate_of
         return set_error(kErrUnsupportedType, "moe_prefill: unsupported down type %d", down_type);
     if ((((uintptr_t)ws | (uintptr_t)x | (uintptr_t)out) & 15) != 0)
         return set_error(kErrBadArg, "moe_prefill: workspace, x and out must be 16-byte aligned");
+    // the grouped kernels copy weight blocks into LDS with 16-byte DMA from 4-byte aligned
+    // addresses (Q6_K rows start 2 bytes past one when the row length is odd in blocks, which
+    // the copies absorb)
+    if ((((uintptr_t)experts | expert_stride | gate_off | up_off | down_off) & 3) != 0)
+        return set_error(kErrBadArg, "moe_prefill: the expert table, its stride and offsets must be 4-byte aligned");
     const MoeLayout L = moe_layout(T, hidden, eff, E, k);
     if (ws_bytes < L.total)
         return set_error(kErrBadArg, "moe_prefill: workspace of %zu bytes, need %zu", ws_bytes, L.total);

@@ -149,6 +149,13 @@ def test_moe_prefill_bad_args(gpu):
     ws = torch.zeros(gpu.ops.moe_prefill_workspace_bytes(T, H, EFF, E, k), dtype=torch.uint8, device="cuda")
     with pytest.raises(gpu.MnemoError, match="down type"):
         gpu.ops.moe_prefill(table, *lay, 3, x, idx, w, T, H, EFF, E, k, ws, out)
+    # weight blocks are copied by DMA from 4-byte aligned addresses
+    big = torch.zeros(table.numel() + 16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(gpu.MnemoError, match="4-byte aligned"):
+        gpu.ops.moe_prefill(big[2:], *lay, 14, x, idx, w, T, H, EFF, E, k, ws, out)
+    stride, g_off, u_off, d_off = lay
+    with pytest.raises(gpu.MnemoError, match="4-byte aligned"):
+        gpu.ops.moe_prefill(big, stride, g_off, u_off, d_off + 2, 14, x, idx, w, T, H, EFF, E, k, ws, out)
 
 
 def test_moe_prefill_baseline_shape(gpu):
