@@ -938,14 +938,28 @@ __device__ __forceinline__ h8 sk_operand4(const SkQ4 &r, uint32_t slo, uint32_t 
     return __builtin_bit_cast(h8, make_uint4(q4_scaled(w0, kSelLo, S, N), q4_scaled(w0, kSelHi, S, N),
                                              q4_scaled(w1, kSelLo, S, N), q4_scaled(w1, kSelHi, S, N)));
 }
-// Q6_K: the planes (sc - b)(q - 32) and b(q - 32) of sub-block j
-__device__ __forceinline__ void sk_operand6(const SkRaw6 &r, int j, bool dzero, h8 &a1, h8 &a2) {
+// Q6_K: the two factors of the lane's 4 scales of half H (sc - b and b, b = sc & 1) as f16
+// pairs, for the half's four sub-blocks at once: e6[g/2] / b6[g/2] hold those of sub-blocks
+// 4H + g (g even, g + 1); zero when d is zero
+struct Sk6Scales {
+    uint32_t e6[2], b6[2];
+};
+__device__ __forceinline__ Sk6Scales sk_scales6(const SkRaw6 &r, int H, bool dzero) {
+    Sk6Scales o;
+    const h2 off = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const uint32_t sc = dzero ? 0u : r.sc[H];
+    q8x4_exact(sc & 0xFEFEFEFEu, o.e6[0], o.e6[1]);  // the even parts of the signed bytes
+    const uint32_t b = sc & 0x01010101u;
+    o.b6[0] = h2u(magic_pair(b, kSelLo) + off);
+    o.b6[1] = h2u(magic_pair(b, kSelHi) + off);
+    return o;
+}
+// Q6_K: the planes (sc - b)(q - 32) and b(q - 32) of sub-block j (S: its half's scales)
+__device__ __forceinline__ void sk_operand6(const SkRaw6 &r, const Sk6Scales &S, int j, h8 &a1, h8 &a2) {
     const int H = j >> 2, grp = j & 3;
-    int sc = (int)(int8_t)((r.sc[H] >> (8 * grp)) & 0xFF);
-    if (dzero) sc = 0;
-    const int b1 = sc & 1;
-    const _Float16 e = (_Float16)(float)(sc - b1), bb = (_Float16)(float)b1;
-    const h2 E = {e, e}, B = {bb, bb};
+    const h2 ep = __builtin_bit_cast(h2, S.e6[grp >> 1]);
+    const h2 bp = __builtin_bit_cast(h2, S.b6[grp >> 1]);
+    const h2 E = {ep[grp & 1], ep[grp & 1]}, B = {bp[grp & 1], bp[grp & 1]};
     const uint2 l = r.ql[2 * H + (grp & 1)], hq = r.qh[H];
     const int shl = 4 * (grp >> 1), shh = 2 * grp;
     const uint32_t v0 = ((l.x >> shl) & 0x0F0F0F0Fu) | (((hq.x >> shh) & 0x03030303u) << 4);
@@ -1054,6 +1068,7 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
 
     SkQ4 w4[R];
     uint32_t slo[R], shi[R];
+    Sk6Scales s6[R];
     float d[R];
 #pragma unroll
     for (int a = 0; a < R; a++) {
@@ -1106,9 +1121,10 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
         for (int b = 0; b < NB; b++) bf[b] = *(const h8 *)(bb + sk_slot(16 * b + c, 4 * j + q));
 #pragma unroll
         for (int a = 0; a < R; a++) {
+            if (TYPE == kTypeQ6K && (j & 3) == 0) s6[a] = sk_scales6(cur[a], j >> 2, d[a] == 0.0f);
             h8 a1, a2;
             if constexpr (TYPE == kTypeQ4K) a1 = sk_operand4(w4[a], slo[a], shi[a], j);
-            else sk_operand6(cur[a], j, d[a] == 0.0f, a1, a2);
+            else sk_operand6(cur[a], s6[a], j, a1, a2);
 #pragma unroll
             for (int b = 0; b < NB; b++) {
                 if constexpr (TYPE == kTypeQ4K) acc[a][b] *= rr[b][j >> 2][j & 3];
