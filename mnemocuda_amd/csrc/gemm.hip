@@ -928,10 +928,22 @@ __device__ __forceinline__ void q4k_scales8(const uint4 &h, uint32_t &lo, uint32
 }
 // sub-block j's A operand, sc*q for its 8 values: the pair (1024 + sc) from the scale byte
 // under 0x64, so that (sc, -1024 sc) cost three packed operations
-__device__ __forceinline__ h8 sk_operand4(const SkQ4 &r, uint32_t slo, uint32_t shi, int j) {
-    const uint32_t sel = 0x04000400u + 0x00010001u * (uint32_t)(j & 3);
-    const h2 S = magic_pair(j < 4 ? slo : shi, sel) + h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
-    const h2 N = S * h2{(_Float16)-1024.0f, (_Float16)-1024.0f};
+// the scales of sub-blocks 4H + g as f16 pairs (g = 0, 1 | 2, 3) and their products with -1024
+struct Sk4Scales {
+    h2 s[2], n[2];
+};
+__device__ __forceinline__ Sk4Scales sk_scales4(uint32_t sc4) {
+    Sk4Scales o;
+    const h2 m = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    o.s[0] = magic_pair(sc4, kSelLo) + m;
+    o.s[1] = magic_pair(sc4, kSelHi) + m;
+    o.n[0] = o.s[0] * m;
+    o.n[1] = o.s[1] * m;
+    return o;
+}
+__device__ __forceinline__ h8 sk_operand4(const SkQ4 &r, const Sk4Scales &T, int j) {
+    const _Float16 sj = T.s[(j & 3) >> 1][j & 1], nj = T.n[(j & 3) >> 1][j & 1];
+    const h2 S = {sj, sj}, N = {nj, nj};
     const uint2 c = r.a[j >> 1];
     const int sh = 4 * (j & 1);
     const uint32_t w0 = (c.x >> sh) & 0x0F0F0F0Fu, w1 = (c.y >> sh) & 0x0F0F0F0Fu;
@@ -1069,6 +1081,7 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
     SkQ4 w4[R];
     uint32_t slo[R], shi[R];
     Sk6Scales s6[R];
+    Sk4Scales s4[R];
     float d[R];
 #pragma unroll
     for (int a = 0; a < R; a++) {
@@ -1123,7 +1136,10 @@ __device__ __forceinline__ void sk_block(int k, int nkb, int q, int c, int wave,
         for (int a = 0; a < R; a++) {
             if (TYPE == kTypeQ6K && (j & 3) == 0) s6[a] = sk_scales6(cur[a], j >> 2, d[a] == 0.0f);
             h8 a1, a2;
-            if constexpr (TYPE == kTypeQ4K) a1 = sk_operand4(w4[a], slo[a], shi[a], j);
+            if constexpr (TYPE == kTypeQ4K) {
+                if ((j & 3) == 0) s4[a] = sk_scales4(j < 4 ? slo[a] : shi[a]);
+                a1 = sk_operand4(w4[a], s4[a], j);
+            }
             else sk_operand6(cur[a], s6[a], j, a1, a2);
 #pragma unroll
             for (int b = 0; b < NB; b++) {
