@@ -929,14 +929,17 @@ __device__ __forceinline__ void q4k_scales8(const uint4 &h, uint32_t &lo, uint32
 // sub-block j's A operand, sc*q for its 8 values: the pair (1024 + sc) from the scale byte
 // under 0x64, so that (sc, -1024 sc) cost three packed operations
 // the scales of sub-blocks 4H + g as f16 pairs (g = 0, 1 | 2, 3) and their products with -1024
+// (odd sub-blocks, the high nibbles, are taken in place as bytes 16 q: their pair is
+// (sc / 16, -64 sc), and (1024 + 16 q) * sc / 16 - 64 sc = q * sc in the same exact fma)
 struct Sk4Scales {
     h2 s[2], n[2];
 };
 __device__ __forceinline__ Sk4Scales sk_scales4(uint32_t sc4) {
     Sk4Scales o;
     const h2 m = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    o.s[0] = magic_pair(sc4, kSelLo) + m;
-    o.s[1] = magic_pair(sc4, kSelHi) + m;
+    const h2 f = {(_Float16)1.0f, (_Float16)0.0625f};
+    o.s[0] = (magic_pair(sc4, kSelLo) + m) * f;
+    o.s[1] = (magic_pair(sc4, kSelHi) + m) * f;
     o.n[0] = o.s[0] * m;
     o.n[1] = o.s[1] * m;
     return o;
@@ -945,8 +948,8 @@ __device__ __forceinline__ h8 sk_operand4(const SkQ4 &r, const Sk4Scales &T, int
     const _Float16 sj = T.s[(j & 3) >> 1][j & 1], nj = T.n[(j & 3) >> 1][j & 1];
     const h2 S = {sj, sj}, N = {nj, nj};
     const uint2 c = r.a[j >> 1];
-    const int sh = 4 * (j & 1);
-    const uint32_t w0 = (c.x >> sh) & 0x0F0F0F0Fu, w1 = (c.y >> sh) & 0x0F0F0F0Fu;
+    const uint32_t msk = (j & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    const uint32_t w0 = c.x & msk, w1 = c.y & msk;
     return __builtin_bit_cast(h8, make_uint4(q4_scaled(w0, kSelLo, S, N), q4_scaled(w0, kSelHi, S, N),
                                              q4_scaled(w1, kSelLo, S, N), q4_scaled(w1, kSelHi, S, N)));
 }
