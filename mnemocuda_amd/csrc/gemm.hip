@@ -291,13 +291,18 @@ __device__ __forceinline__ void store_w_q4k(const RawW &r, int ks, int p, Stage<
     q4k_scale_min(r.h.y, r.h.z, r.h.w, j, sc, m);
     const float d = h2f(r.h.x & 0xFFFFu);
     if (d == 0.0f) sc = 0;  // the block's products are zero
-    const _Float16 s = (_Float16)(float)sc, ns = (_Float16)(-1024.0f * (float)sc);
-    const h2 S = {s, s}, N = {ns, ns};
-    const int sh = 4 * (c >> 5);
+    // the pair (sc, -1024 sc) from sc under the 0x64 exponent; high nibbles are taken in
+    // place as the bytes 16 q with (sc / 16, -64 sc): (1024 + 16 q) sc / 16 - 64 sc = q sc
+    const bool hi = (c >> 5) != 0;
+    const h2 F = hi ? h2{(_Float16)0.0625f, (_Float16)0.0625f} : h2{(_Float16)1.0f, (_Float16)1.0f};
+    const h2 mk = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const h2 S = __builtin_elementwise_fma(magic_pair(sc, 0x04000400u), F, F * mk);
+    const h2 N = S * mk;
+    const uint32_t msk = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
     uint32_t o[kVP / 2];
 #pragma unroll
     for (int k = 0; k < kVP / 4; k++) {
-        const uint32_t w = (r.a.w[k] >> sh) & 0x0F0F0F0Fu;
+        const uint32_t w = r.a.w[k] & msk;
         o[2 * k] = q4_scaled(w, kSelLo, S, N);
         o[2 * k + 1] = q4_scaled(w, kSelHi, S, N);
     }
