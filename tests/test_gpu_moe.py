@@ -76,6 +76,9 @@ def _compose_plain(gpu, table, lay, DT, x, idx, w, T, H, EFF, out0):
     (24, 2048, 256, 3, 2, 14, 1.1),
     (70, 3072, 256, 2, 1, 14, 0.0),
     (16, 5120, 1024, 2, 1, 12, 0.0),
+    # Q6_K down rows of 3 blocks (630 B): rows and blocks alternate between 4-byte aligned
+    # and 2 bytes past (the copies' window offsets)
+    (40, 512, 768, 4, 2, 14, 0.5),
 ])
 def test_moe_prefill_vs_oracle(gpu, oracle, T, H, EFF, E, k, down_type, skew):
     rng = np.random.default_rng(T * 1000 + E)
